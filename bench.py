@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X token sampler on the headline workload (configuration 3).
+
+C3: fp32 logits [B=256, V=128256] ~ N(0, 3); per row a 512-token prior-output history drives
+repetition 1.1 / presence 0.5 / frequency 0.3 penalties; then temperature 0.7, top-k 50,
+top-p 0.9 and caller-supplied uniforms (exponential race).  One "step" = one ``vws_sample``
+call over the whole batch with inputs resident in HBM.  Three input sets (rolled copies, 394 MB
+of logits) are rotated so re-reads cannot be served by the 256 MB MALL.
+
+Prints ONE JSON line (rank 0): rows/s, ms per step, the HBM roofline of the dominant kernel
+(algorithmic bytes / its average event-timed duration, peak 8 TB/s) and the CPU baseline (the
+torch restatement of vLLM's sampler, oracle/vllm_torch.py, on a bounded sample of the rows).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "sampled rows/sec + HBM GB/s (% peak), B=256 V=128256 top-k/top-p/penalties"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_args(lib_mod, logits, T, K, P, MP, R, PR, FR, hist, U, out, flags, nkept, ws):
+    a = lib_mod.SampleArgs()
+    a.struct_size = ctypes.sizeof(lib_mod.SampleArgs)
+    B, V = logits.shape
+    a.batch, a.vocab, a.dtype = B, V, lib_mod.DTYPE_F32
+    a.logits, a.logits_row_stride = logits.data_ptr(), logits.stride(0)
+    a.temperature, a.top_k, a.top_p, a.min_p = T.data_ptr(), K.data_ptr(), P.data_ptr(), MP.data_ptr()
+    a.repetition_penalty, a.presence_penalty, a.frequency_penalty = R.data_ptr(), PR.data_ptr(), FR.data_ptr()
+    a.output_ids, a.output_row_stride, a.output_width = hist.data_ptr(), hist.stride(0), hist.shape[1]
+    a.uniforms, a.uniforms_row_stride = U.data_ptr(), U.stride(0)
+    a.sampled, a.row_flags, a.num_kept = out.data_ptr(), flags.data_ptr(), nkept.data_ptr()
+    a.num_logprobs = -1
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    return a
+
+
+def cpu_baseline(w, rows: int, iters: int):
+    """torch CPU restatement of vLLM's sampler on `rows` rows of the workload, all host cores."""
+    import torch
+
+    from oracle import vllm_torch as VT
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sl = slice(0, rows)
+    args = dict(temperature=torch.from_numpy(w.temperature[sl]), top_k=torch.from_numpy(w.top_k[sl]),
+                top_p=torch.from_numpy(w.top_p[sl]), min_p=torch.from_numpy(w.min_p[sl]),
+                repetition=torch.from_numpy(w.repetition[sl]), presence=torch.from_numpy(w.presence[sl]),
+                frequency=torch.from_numpy(w.frequency[sl]),
+                uniforms=torch.from_numpy(w.uniforms[sl]),
+                output_ids=torch.from_numpy(w.output_ids[sl]))
+    x = torch.from_numpy(w.logits_f32()[sl])
+    for _ in range(3):
+        VT.sample(x, **args)
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter_ns()
+        VT.sample(x, **args)
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    med = float(np.median(times))
+    return dict(value=rows / med, unit="rows/s", cores=cores, kind="port",
+                sample=(f"{rows} rows of C3 (V=128256, same seeded inputs), oracle/vllm_torch.py "
+                        f"(vLLM-v1 Sampler op sequence on torch CPU tensors), median of {iters} "
+                        f"after 3 warm-up, torch threads={cores}"),
+                seconds_per_iter=med)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--sets", type=int, default=3, help="rotated input sets (MALL defeat)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=128)
+    ap.add_argument("--cpu-iters", type=int, default=10)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 512 MiB device copy (for PMC byte-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU: the sampler shards by rows and "
+                          "runs no collectives; run with --gpus 1"}), flush=True)
+        sys.exit(2)
+
+    import torch
+
+    from vllm_webgpu_amd import _lib, ops
+    from vllm_webgpu_amd import workloads as W
+
+    t_gen = time.time()
+    w = W.config(args.config)
+    B, V = w.shape
+    log(f"workload {w.name} B={B} V={V} generated in {time.time() - t_gen:.1f}s")
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+
+    logits0 = torch.from_numpy(w.logits_f32()).to(dev)
+    U0 = torch.from_numpy(w.uniforms).to(dev)
+    H0 = torch.from_numpy(w.output_ids).to(dev)
+    T = torch.from_numpy(w.temperature).to(dev)
+    K = torch.from_numpy(w.top_k).to(dev)
+    P = torch.from_numpy(w.top_p).to(dev)
+    MP = torch.from_numpy(w.min_p).to(dev)
+    R = torch.from_numpy(w.repetition).to(dev)
+    PR = torch.from_numpy(w.presence).to(dev)
+    FR = torch.from_numpy(w.frequency).to(dev)
+    sets = []
+    for i in range(args.sets):
+        lg = torch.roll(logits0, shifts=i, dims=0).contiguous()
+        u = torch.roll(U0, shifts=i, dims=0).contiguous()
+        h = torch.roll(H0, shifts=i, dims=0).contiguous()
+        sets.append((lg, u, h))
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    flags = torch.empty(B, dtype=torch.int32, device=dev)
+    nkept = torch.empty(B, dtype=torch.int32, device=dev)
+    ws = ops.workspace(L.vws_sample_workspace_size(B, V, H0.shape[1]), dev)
+    stream = torch.cuda.current_stream()
+    argv = []
+    for lg, u, h in sets:
+        a = build_args(_lib, lg, T, K, P, MP, R, PR, FR, h, u, out, flags, nkept, ws)
+        a.stream = stream.cuda_stream
+        argv.append(a)
+    sample = L.vws_sample
+
+    # correctness spot check of set 0 against the oracle (tokens bit-exact)
+    _lib.check(sample(ctypes.byref(argv[0])))
+    torch.cuda.synchronize()
+    gpu_tok = out.cpu().numpy()
+    gpu_kept = nkept.cpu().numpy()
+    gpu_flags = flags.cpu().numpy().view(np.uint32)
+    from oracle import sampler as O  # checker only
+
+    prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence, w.frequency)
+    ref = O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids)
+    mism = int((ref["token"] != gpu_tok).sum())
+    log(f"parity vs oracle: {mism} token mismatches of {B} rows; "
+        f"|S| mean {gpu_kept.mean():.1f}; near-tie rows {int(((gpu_flags & 3) != 0).sum())}")
+    if mism:
+        print(json.dumps({"error": f"parity failure: {mism} token mismatches"}), flush=True)
+        sys.exit(1)
+
+    for i in range(args.warmup):
+        _lib.check(sample(ctypes.byref(argv[i % len(argv)])))
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` calls, bracketed by synchronisation
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        sample(ctypes.byref(argv[i % len(argv)]))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    st = L.vws_last_error()
+    if st:
+        log(f"last error: {st}")
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    rows_per_s = B * args.steps / (t1 - t0)
+
+    # per-kernel durations with hipEvents on the launch stream (same calls again)
+    ops.profile_begin(4 * args.steps + 8)
+    for i in range(args.steps):
+        sample(ctypes.byref(argv[i % len(argv)]))
+    prof = ops.profile_end()
+    fast_ms = prof["fast"][0] / prof["fast"][1]
+    gen_ms = prof["general"][0] / prof["general"][1] if "general" in prof else 0.0
+
+    alg_bytes = W.algorithmic_bytes(w, gpu_kept)
+    gbps_e2e = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    gbps_fast = alg_bytes / (fast_ms * 1e-3) / 1e9
+    log(f"ms/step {ms_per_step:.4f}  fast kernel {fast_ms * 1e3:.2f} us  general kernel "
+        f"{gen_ms * 1e3:.2f} us  alg bytes {alg_bytes}  e2e {gbps_e2e:.0f} GB/s "
+        f"({gbps_e2e / PEAK_HBM_GBPS:.1%})  fast-kernel {gbps_fast:.0f} GB/s")
+
+    if args.calibrate_copy:
+        a = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1.0)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log("calibration copy: 536870912 bytes read + 536870912 bytes written")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t = time.time()
+        cpu = cpu_baseline(w, args.cpu_rows, args.cpu_iters)
+        log(f"cpu baseline {cpu['value']:.1f} rows/s on {cpu['cores']} cores ({time.time() - t:.1f}s)")
+
+    res = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": ("C3: fp32 logits B=256 V=128256 ~N(0,3); 512-token output history "
+                         "(repetition 1.1, presence 0.5, frequency 0.3); T=0.7, top-k 50, "
+                         "top-p 0.9; caller uniforms [B,V]; 3 rotated input sets"),
+            "global_batch": B, "vocab": V, "parallelism": "none (1 GPU)",
+        },
+        "hbm_gbps_end_to_end": gbps_e2e,
+        "hbm_frac_end_to_end": gbps_e2e / PEAK_HBM_GBPS,
+        "algorithmic_bytes_per_step": alg_bytes,
+        "mean_survivors": float(gpu_kept.mean()),
+        "kernel_us": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
+        "roofline": {
+            "bound": "hbm", "achieved": gbps_fast, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": gbps_fast / PEAK_HBM_GBPS, "traffic": None,
+            "kernel": "vws::fast_kernel<float>",
+        },
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,183 @@
+/*
+ * vws_sampler.h -- C ABI of the MI355X (gfx950) token-sampling library
+ * (vllm_webgpu_amd/_vws.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed as void*.
+ * Nothing here allocates device memory: callers own every buffer, including the workspace.
+ * Work is enqueued on the given stream with no host synchronisation; the return value only
+ * reports argument errors and launch failures.  On error, vws_last_error() gives a
+ * thread-local message.
+ *
+ * Reference interfaces each entry point replaces (paths under the vllm_webgpu reference):
+ *   vws_sample   <- vllm_webgpu/v1/model_runner.py:139-166 (execute_model's host argmax at :145
+ *                   and the sample_tokens() stub at :164-166) and run_inference.py:383-390
+ *                   (greedy / temperature sampling in the CLI); semantics of the vLLM-v1
+ *                   Sampler the plugin delegates to (docs/.../2026-06-29-vllm-webgpu-design.md:451)
+ *   vws_argmax   <- vllm_webgpu/shaders/generic/argmax.wgsl:1-60, dispatched as in
+ *                   tests/test_kernels_sample.py:8-43 (batched here: [B, V] -> [B])
+ *   vws_topk     <- vllm_webgpu/shaders/generic/topk256.wgsl:1-70, dispatched as in
+ *                   tests/test_kernels_sample.py:46-101 (batched, K <= 256 as in topk256, no mask buffer)
+ *   vws_softmax  <- vllm_webgpu/shaders/generic/softmax.wgsl:1-71 (row softmax; here with a
+ *                   per-row temperature as in run_inference.py:386-389, plus max and log-sum)
+ *   vws_apply_penalties <- the vLLM-v1 penalty step the plugin inherits (no WGSL counterpart)
+ */
+#ifndef VWS_SAMPLER_H
+#define VWS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VWS_ABI_VERSION 1
+
+/* status codes */
+#define VWS_OK 0
+#define VWS_ERR_INVALID_ARGUMENT 1
+#define VWS_ERR_UNSUPPORTED_DTYPE 2
+#define VWS_ERR_WORKSPACE_TOO_SMALL 3
+#define VWS_ERR_HIP 4
+#define VWS_ERR_LIMIT 5
+
+/* logits element types */
+#define VWS_DTYPE_F32 0
+#define VWS_DTYPE_BF16 1
+
+/* per-row result flags (vws_sample_args.row_flags) */
+#define VWS_FLAG_TOPP_NEAR_TIE 0x1u  /* top-p cumulative mass within 1e-6 of the threshold */
+#define VWS_FLAG_RACE_NEAR_TIE 0x2u  /* best and second race keys within 1e-6 (relative) */
+#define VWS_FLAG_DEGENERATE 0x4u     /* row maximum not finite: greedy over y = x / T */
+#define VWS_FLAG_GREEDY 0x8u         /* temperature < 1e-5 (or NaN): argmax of penalised x */
+#define VWS_FLAG_GENERAL_PATH 0x100u /* served by the multi-pass kernel (diagnostic only) */
+
+#define VWS_MAX_VOCAB (1 << 19)       /* masses are floor(e * 2^44) summed in 64 bits */
+#define VWS_MAX_LOGPROBS 64
+
+typedef struct vws_sample_args {
+    uint32_t struct_size; /* sizeof(vws_sample_args): ABI guard */
+    int32_t batch;        /* B >= 1 */
+    int32_t vocab;        /* 1 <= V <= VWS_MAX_VOCAB */
+    int32_t dtype;        /* VWS_DTYPE_* */
+    const void* logits;   /* [B, V] with row stride below; read only */
+    int64_t logits_row_stride; /* elements */
+
+    /* Per-row parameters, device arrays of length B.  NULL selects the default:
+     * temperature NULL = every row greedy; top_k NULL/<=0/>=V = off; top_p NULL/>=1 = off;
+     * min_p NULL/0 = off; repetition NULL = 1; presence/frequency NULL = 0. */
+    const float* temperature;
+    const int32_t* top_k;
+    const float* top_p;
+    const float* min_p;
+    const float* repetition_penalty;
+    const float* presence_penalty;
+    const float* frequency_penalty;
+
+    /* Token histories for the penalties: padded int32 [B, width] with the given row stride.
+     * Ids outside [0, V) are padding (vLLM pads with V).  *_lens (device, [B]) may be NULL,
+     * meaning the full width.  Prompt tokens take the repetition penalty only; output tokens
+     * take repetition, frequency (per occurrence) and presence. */
+    const int32_t* prompt_ids;
+    int64_t prompt_row_stride;
+    int32_t prompt_width;
+    const int32_t* prompt_lens;
+    const int32_t* output_ids;
+    int64_t output_row_stride;
+    int32_t output_width;
+    const int32_t* output_lens;
+
+    /* Uniforms in (0, 1), fp32 [B, V] (row stride in elements); read only at surviving
+     * tokens.  Required when temperature is non-NULL. */
+    const float* uniforms;
+    int64_t uniforms_row_stride;
+
+    /* Outputs */
+    int32_t* sampled;    /* [B] token ids */
+    uint32_t* row_flags; /* [B] VWS_FLAG_* or NULL */
+    int32_t* num_kept;   /* [B] tokens left with non-zero probability, or NULL */
+    int32_t num_logprobs;   /* -1: none.  L >= 0: raw (pre-penalty) logprobs */
+    int32_t* logprob_ids;   /* [B, L+1]: sampled id, then top-L ids (value desc, id asc) */
+    float* logprob_vals;    /* [B, L+1] */
+    int32_t* logprob_ranks; /* [B]: #{j : logprob_j >= logprob_sampled} */
+
+    void* workspace; /* device scratch, >= vws_sample_workspace_size(); see vws_workspace_init */
+    size_t workspace_bytes;
+    void* stream; /* hipStream_t */
+} vws_sample_args;
+
+/* ABI version (VWS_ABI_VERSION of the built library). */
+int32_t vws_abi_version(void);
+
+/* Thread-local description of the last error returned on this thread ("" if none). */
+const char* vws_last_error(void);
+
+/* Bytes of workspace vws_sample needs for this shape and history width
+ * (prompt_width + output_width). */
+size_t vws_sample_workspace_size(int32_t batch, int32_t vocab, int32_t history_width);
+
+/* Clears a workspace on `stream` (a fill kernel, safe under graph capture).  Required once
+ * after allocation; vws_sample leaves it clean again for the next call. */
+int vws_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only argument check (no device access): the status vws_sample would return before
+ * launching anything. */
+int vws_validate_sample_args(const vws_sample_args* args);
+
+/* Full sampler: penalties -> temperature -> min-p -> top-k -> top-p -> exponential race,
+ * plus greedy rows and raw logprobs.  Results are identical, bit for bit, to the CPU oracle
+ * in oracle/ for the same inputs. */
+int vws_sample(const vws_sample_args* args);
+
+/* Greedy argmax of each row (lowest index on ties; NaN never selected). */
+int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,
+               int64_t row_stride, int32_t* out_ids, void* stream);
+
+/* Top-k values (as fp32) and ids of each row, ordered (value desc, id asc); 1 <= k <= 256.
+ * Needs vws_topk_workspace_size() bytes of workspace (initialised with vws_workspace_init). */
+size_t vws_topk_workspace_size(int32_t batch, int32_t vocab, int32_t k);
+int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
+             int32_t k, float* out_vals, int32_t* out_ids, void* workspace,
+             size_t workspace_bytes, void* stream);
+
+/* probs = softmax(x / T) per row with the sampler's exp; temperature [B] (NULL = 1).
+ * row_max [B] (= max x / T) and log_sum [B] (= log sum exp(x/T - max)) may be NULL. */
+int vws_softmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,
+                int64_t row_stride, const float* temperature, float* probs, float* row_max,
+                float* log_sum, void* stream);
+
+/* In-place penalties on fp32 logits [B, V] (vLLM-v1 order and arithmetic); history arrays as
+ * in vws_sample_args.  Needs vws_sample_workspace_size(B, V, prompt_width + output_width). */
+int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row_stride,
+                        const float* repetition, const float* presence, const float* frequency,
+                        const int32_t* prompt_ids, int64_t prompt_row_stride, int32_t prompt_width,
+                        const int32_t* prompt_lens, const int32_t* output_ids,
+                        int64_t output_row_stride, int32_t output_width,
+                        const int32_t* output_lens, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Per-kernel timing.  vws_profile_begin(n) makes the next n kernel launches of this library
+ * (on any stream) record a hipEvent pair around themselves; vws_profile_end() waits for those
+ * events, writes the summed milliseconds and launch counts per kernel kind into
+ * ms[VWS_KERNEL_KINDS] / count[VWS_KERNEL_KINDS] and turns recording off. */
+#define VWS_KERNEL_FAST 0      /* single-pass split-row sampler (also the topk operation) */
+#define VWS_KERNEL_GENERAL 1   /* multi-pass sampler */
+#define VWS_KERNEL_ARGMAX 2
+#define VWS_KERNEL_SOFTMAX 3
+#define VWS_KERNEL_PENALTIES 4
+#define VWS_KERNEL_OTHER 5     /* workspace fill, self-test */
+#define VWS_KERNEL_KINDS 6
+int vws_profile_begin(int32_t max_launches);
+int vws_profile_end(double* ms, int32_t* count);
+
+/* Device self-test of the sampler arithmetic: evaluates fn (0 = exp_det, 1 = log_det) at
+ * every fp32 whose order key lies in [key_lo, key_hi] and accumulates the same 64-bit hash
+ * as the CPU oracle's checker into out2[0] and the count into out2[1] (device u64[2],
+ * zeroed by this call). */
+int vws_math_selftest(int32_t fn, uint32_t key_lo, uint32_t key_hi, uint64_t* out2, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VWS_SAMPLER_H */

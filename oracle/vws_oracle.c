@@ -1,0 +1,454 @@
+/*
+ * vws_oracle.c -- CPU oracle for the MI355X token-sampling path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  The product library (vllm_webgpu_amd/_vws.so) neither links nor
+ * loads this file.  Only tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py
+ * use it, and only as the checker.
+ *
+ * What it restates, one row at a time in plain sequential C:
+ *   - greedy argmax, lowest index on ties: vllm_webgpu/v1/model_runner.py:145 (numpy argmax);
+ *     the single-row WGSL kernel vllm_webgpu/shaders/generic/argmax.wgsl:1-60 has the same
+ *     I/O contract; it never selects NaN (strict '>' at :28-31), and neither does this oracle.
+ *   - top-k values/ids, descending: vllm_webgpu/shaders/generic/topk256.wgsl:1-70.
+ *   - online max/normaliser softmax: vllm_webgpu/shaders/generic/softmax.wgsl:26-70.
+ *   - the vLLM-v1 Sampler the plugin delegates sampling to
+ *     (docs/superpowers/specs/2026-06-29-vllm-webgpu-design.md:451; pyproject.toml:10,
+ *     vllm>=0.20, not vendored in the reference): penalties -> temperature -> min-p ->
+ *     top-k -> top-p -> exponential race, and raw logprobs.
+ *
+ * Sampler arithmetic (the definition that makes token ids reproducible bit for bit):
+ *   exp_det / log_det are fixed fp32 operation sequences (Cody-Waite reduction and
+ *   polynomials fitted for this project; every step is an IEEE add, mul or fma), so any
+ *   IEEE-754 machine that runs the same sequence gets the same bits.  Compile with
+ *   -ffp-contract=off.
+ *   top-p uses exact integer masses w = floor(e * 2^44) and exact 64/128-bit sums, so the
+ *   cumulative sum does not depend on summation order.
+ *   min-p keeps a token iff fl(y - max) >= log_det(min_p) (the logit-space form of
+ *   p >= max_p * min_p).
+ *   The exponential race key is e / (0 - log_det(u)); the largest key wins, lowest index on
+ *   equal keys.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define VWO_FLAG_TOPP_NEAR_TIE 0x1u
+#define VWO_FLAG_RACE_NEAR_TIE 0x2u
+#define VWO_FLAG_DEGENERATE 0x4u
+#define VWO_FLAG_GREEDY 0x8u
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---- sampler arithmetic --------------------------------------------------------------- */
+
+/* exp(d) on [-80, 80]; 0 below -80 and for NaN.  Cody-Waite: n = rint(d*log2e),
+ * r = d - n*ln2 with ln2 split into a 16-bit head (n*head is exact) and an fp32 tail,
+ * exp(r) = 1 + r + r^2*Q(r), Q of degree 4 fitted on [-ln2/2, ln2/2] (max rel err 7.5e-9),
+ * then an exact scale by 2^n. */
+float vwo_exp(float d) {
+    if (!(d >= -80.0f)) return 0.0f;
+    if (d > 80.0f) d = 80.0f;
+    if (fabsf(d) < 0x1p-30f) return 1.0f;
+    const float t = d * 0x1.715476p+0f;
+    const float n = rintf(t);
+    float r = fmaf(-n, 0x1.62e4p-1f, d);
+    r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = fmaf(0x1.6d7532p-10f, r, 0x1.120b66p-7f);
+    p = fmaf(p, r, 0x1.5554b8p-5f);
+    p = fmaf(p, r, 0x1.5554dcp-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* log(u) for u > 0: u = 2^e * m, m in [sqrt(1/2), sqrt(2)], f = m - 1 (exact),
+ * log1p(f) = f + f^2*R(f), R of degree 8 fitted on [sqrt(1/2)-1, sqrt(2)-1] (rel err 1e-8),
+ * log(u) = e*ln2 + log1p(f).  log(0) = -inf, log(+inf) = +inf, NaN for u < 0 or NaN. */
+float vwo_log(float u) {
+    if (!(u > 0.0f)) return (u == 0.0f) ? -INFINITY : NAN;
+    if (u == INFINITY) return INFINITY;
+    uint32_t b = f2u(u);
+    int e = 0;
+    if (b < 0x00800000u) { b = f2u(u * 0x1p23f); e = -23; }
+    e += (int)(b >> 23) - 127;
+    uint32_t mb = (b & 0x007FFFFFu) | 0x3F800000u;
+    if (mb > 0x3FB504F3u) { mb -= 0x00800000u; e += 1; }
+    const float f = u2f(mb) - 1.0f;
+    const float f2 = f * f;
+    float R = fmaf(-0x1.4a5298p-4f, f, 0x1.088e82p-3f);
+    R = fmaf(R, f, -0x1.0bb9f2p-3f);
+    R = fmaf(R, f, 0x1.2245c6p-3f);
+    R = fmaf(R, f, -0x1.548f6ep-3f);
+    R = fmaf(R, f, 0x1.99a7bap-3f);
+    R = fmaf(R, f, -0x1.0001f8p-2f);
+    R = fmaf(R, f, 0x1.555548p-2f);
+    R = fmaf(R, f, -0x1.fffffep-2f);
+    const float L = fmaf(f2, R, f);
+    if (e == 0) return L;
+    const float ef = (float)e;
+    return fmaf(ef, 0x1.62e43p-1f, fmaf(ef, -0x1.05c61p-29f, L));
+}
+
+/* floor(e * 2^44) for e in [0, 1] (0 for e <= 0 or NaN). */
+uint64_t vwo_mass(float e) {
+    if (!(e > 0.0f)) return 0;
+    const uint32_t b = f2u(e);
+    const int ex = (int)(b >> 23);
+    const uint64_t mant = ex ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
+    const int sh = (ex ? ex : 1) - 106;
+    if (sh >= 0) return mant << sh;
+    if (sh <= -64) return 0;
+    return mant >> (-sh);
+}
+
+/* Order-preserving key: x < y  <=>  key(x) < key(y); -0 and +0 share a key; NaN -> 0,
+ * below -inf (whose key is 0x007FFFFF). */
+uint32_t vwo_key(float x) {
+    uint32_t b = f2u(x);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0;
+    if (b == 0x80000000u) b = 0;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+/* floor(q * W) exactly, for fp32 q in (0, 1) and W < 2^64. */
+uint64_t vwo_scale_floor(float q, uint64_t W) {
+    const uint32_t b = f2u(q);
+    const int ex = (int)(b >> 23);
+    const uint64_t mq = ex ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
+    const int sh = 150 - (ex ? ex : 1); /* q = mq * 2^-sh, sh >= 24 for q < 1 */
+    const unsigned __int128 prod = (unsigned __int128)mq * (unsigned __int128)W;
+    if (sh >= 128) return 0;
+    return (uint64_t)(prod >> sh);
+}
+
+/* One repetition/frequency/presence penalty step, vLLM-v1 order: repetition on
+ * prompt|output tokens (x>0: x*fl(1/r), else x*r -- the torch fallback form), then
+ * x - f*count, then x - p*(count>0). */
+static inline float apply_pen(float x, int in_prompt, uint32_t cnt, float rep, float inv_rep,
+                              float freq, float pres) {
+    if (in_prompt || cnt > 0) x = (x > 0.0f) ? x * inv_rep : x * rep;
+    x = x - freq * (float)cnt;
+    x = x - pres * (cnt > 0 ? 1.0f : 0.0f);
+    return x;
+}
+
+/* ---- per-row sampler ------------------------------------------------------------------ */
+
+typedef struct {
+    float temperature, top_p, min_p, rep, pres, freq;
+    int32_t top_k, _pad;
+} vwo_params;
+
+typedef struct {
+    int32_t token;
+    uint32_t flags;
+    int32_t n_kept;        /* |S|: tokens with non-zero probability after all truncation */
+    int32_t n_topk;        /* tokens surviving temperature + min-p + top-k */
+    uint64_t mass_total;   /* W over the top-k/min-p survivors */
+    uint64_t threshold;    /* floor(q32 * W) when top-p is active, else 0 */
+    float row_max;         /* m = max y */
+    float kth_y;           /* k-th largest y (or -inf when top-k is off) */
+} vwo_row_out;
+
+static int cmp_u64(const void* a, const void* b) {
+    const uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return (x > y) - (x < y);
+}
+
+/* k-th largest key (with multiplicity) among keys[0..n), 1 <= k <= n. */
+static uint32_t kth_largest_key(const uint32_t* keys, int n, int k) {
+    uint32_t* tmp = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)n);
+    memcpy(tmp, keys, sizeof(uint32_t) * (size_t)n);
+    /* two-level 16-bit radix select, from the top */
+    uint32_t* hist = (uint32_t*)calloc(65536, sizeof(uint32_t));
+    for (int i = 0; i < n; ++i) hist[tmp[i] >> 16]++;
+    int rem = k, hi = 65535;
+    for (; hi >= 0; --hi) { if ((int)hist[hi] >= rem) break; rem -= (int)hist[hi]; }
+    memset(hist, 0, 65536 * sizeof(uint32_t));
+    for (int i = 0; i < n; ++i) if ((tmp[i] >> 16) == (uint32_t)hi) hist[tmp[i] & 0xFFFF]++;
+    int lo = 65535;
+    for (; lo >= 0; --lo) { if ((int)hist[lo] >= rem) break; rem -= (int)hist[lo]; }
+    free(hist);
+    free(tmp);
+    return ((uint32_t)hi << 16) | (uint32_t)lo;
+}
+
+/* Applies penalties to x (length V) in place.  Token ids outside [0, V) are padding. */
+void vwo_apply_penalties_row(float* x, int V, const int32_t* prompt, int np, const int32_t* output,
+                             int no, float rep, float pres, float freq) {
+    uint32_t* cnt = (uint32_t*)calloc((size_t)V, sizeof(uint32_t));
+    uint8_t* inp = (uint8_t*)calloc((size_t)V, 1);
+    for (int i = 0; i < np; ++i) if (prompt[i] >= 0 && prompt[i] < V) inp[prompt[i]] = 1;
+    for (int i = 0; i < no; ++i) if (output[i] >= 0 && output[i] < V) cnt[output[i]]++;
+    const float inv_rep = 1.0f / rep;
+    for (int i = 0; i < V; ++i)
+        if (inp[i] || cnt[i]) x[i] = apply_pen(x[i], inp[i], cnt[i], rep, inv_rep, freq, pres);
+    free(cnt);
+    free(inp);
+}
+
+int32_t vwo_argmax_row(const float* x, int V) {
+    int32_t best = 0;
+    uint32_t bk = 0;
+    for (int i = 0; i < V; ++i) {
+        const uint32_t k = vwo_key(x[i]);
+        if (k > bk) { bk = k; best = i; }
+    }
+    return best;
+}
+
+/* Full sampler on one row.  x0: raw fp32 logits (bf16 inputs are widened exactly by the
+ * caller).  u: uniforms [V] in (0,1).  Logprob outputs (optional, L >= 0): lp_ids/lp_vals have
+ * L+1 entries: [sampled, top1..topL]; *rank = #{j : x0_j >= x0_sampled}. */
+int vwo_sample_row(const float* x0, int V, const int32_t* prompt, int np, const int32_t* output,
+                   int no, const vwo_params* prm, const float* u, int L, int32_t* lp_ids,
+                   float* lp_vals, int32_t* rank, vwo_row_out* out) {
+    memset(out, 0, sizeof(*out));
+    out->kth_y = -INFINITY;
+    float* x = (float*)malloc(sizeof(float) * (size_t)V);
+    memcpy(x, x0, sizeof(float) * (size_t)V);
+    const int has_hist = (np > 0 || no > 0);
+    if (has_hist) vwo_apply_penalties_row(x, V, prompt, np, output, no, prm->rep, prm->pres, prm->freq);
+
+    const float T = prm->temperature;
+    if (!(T >= 1e-5f)) { /* greedy row: argmax of penalised, pre-temperature logits */
+        out->token = vwo_argmax_row(x, V);
+        out->flags = VWO_FLAG_GREEDY;
+        out->n_kept = 1;
+        out->n_topk = 1;
+        goto logprobs;
+    }
+    {
+        float* y = (float*)malloc(sizeof(float) * (size_t)V);
+        uint32_t* ky = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)V);
+        float m = -INFINITY;
+        uint32_t mk = 0;
+        int32_t mi = 0;
+        int nvalid = 0;
+        for (int i = 0; i < V; ++i) {
+            y[i] = x[i] / T;
+            ky[i] = vwo_key(y[i]);
+            if (ky[i]) nvalid++;
+            if (ky[i] > mk) { mk = ky[i]; mi = i; m = y[i]; }
+        }
+        out->row_max = m;
+        if (!(m > -INFINITY && m < INFINITY)) { /* degenerate row: greedy over y */
+            out->token = mi;
+            out->flags = VWO_FLAG_DEGENERATE;
+            out->n_kept = 1;
+            out->n_topk = 1;
+            free(y); free(ky);
+            goto logprobs;
+        }
+        /* min-p (logit-space form) */
+        float lp_min = -INFINITY;
+        if (prm->min_p > 0.0f) lp_min = vwo_log(prm->min_p < 1.0f ? prm->min_p : 1.0f);
+        /* top-k: keep y >= k-th largest y */
+        uint32_t kth = 0;
+        const int k = prm->top_k;
+        if (k > 0 && k < V && k <= nvalid) kth = kth_largest_key(ky, V, k);
+        /* gather survivors of top-k and min-p as packed (key << 32 | idx) */
+        uint64_t* s = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+        int ns = 0;
+        for (int i = 0; i < V; ++i) {
+            if (!ky[i] || ky[i] < kth) continue;
+            if (!((y[i] - m) >= lp_min)) continue;
+            s[ns++] = ((uint64_t)ky[i] << 32) | (uint32_t)i;
+        }
+        if (kth) { for (int i = 0; i < V; ++i) if (ky[i] == kth) { out->kth_y = y[i]; break; } }
+        out->n_topk = ns;
+        qsort(s, (size_t)ns, sizeof(uint64_t), cmp_u64); /* (y asc, idx asc) */
+        uint64_t* w = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(ns ? ns : 1));
+        float* e = (float*)malloc(sizeof(float) * (size_t)(ns ? ns : 1));
+        uint64_t W = 0;
+        for (int j = 0; j < ns; ++j) {
+            const int i = (int)(uint32_t)s[j];
+            e[j] = vwo_exp(y[i] - m);
+            w[j] = vwo_mass(e[j]);
+            W += w[j];
+        }
+        out->mass_total = W;
+        int first = 0; /* first kept position in ascending order */
+        const float q32 = 1.0f - prm->top_p;
+        if (q32 > 0.0f && ns > 0) {
+            const uint64_t thr = vwo_scale_floor(q32 < 1.0f ? q32 : 0x1.fffffep-1f, W);
+            /* q32 >= 1 means top_p <= 0: every token but the last is removed */
+            const int all_but_last = !(q32 < 1.0f);
+            out->threshold = thr;
+            uint64_t C = 0, Cprev = 0;
+            for (first = 0; first < ns - 1; ++first) {
+                const uint64_t Cn = C + w[first];
+                if (!all_but_last && Cn > thr) break;
+                Cprev = Cn;
+                C = Cn;
+            }
+            if (!all_but_last) {
+                const uint64_t tol = (uint64_t)((double)W * 1e-6);
+                const uint64_t Cat = C + w[first];
+                if ((first > 0 && thr - Cprev <= tol) || (Cat > thr && Cat - thr <= tol))
+                    out->flags |= VWO_FLAG_TOPP_NEAR_TIE;
+            }
+        }
+        out->n_kept = ns - first;
+        /* exponential race over the kept tail s[first..ns) */
+        int32_t best = -1;
+        float bkey = 0.0f, skey = -1.0f;
+        for (int j = first; j < ns; ++j) {
+            const int i = (int)(uint32_t)s[j];
+            const float q = 0.0f - vwo_log(u[i]);
+            const float key = e[j] / q;
+            if (!(key >= 0.0f)) continue; /* NaN keys never win */
+            if (best < 0 || key > bkey || (key == bkey && i < best)) {
+                if (best >= 0) skey = (bkey > skey) ? bkey : skey;
+                best = i;
+                bkey = key;
+            } else if (key > skey) {
+                skey = key;
+            }
+        }
+        if (best < 0) best = (int32_t)(uint32_t)s[ns - 1]; /* no valid key: most probable */
+        else if (skey >= 0.0f && (double)skey >= (double)bkey * (1.0 - 1e-6))
+            out->flags |= VWO_FLAG_RACE_NEAR_TIE;
+        out->token = best;
+        free(w); free(e); free(s); free(y); free(ky);
+    }
+logprobs:
+    if (L >= 0 && lp_ids) {
+        double m0 = -INFINITY;
+        for (int i = 0; i < V; ++i) if (x0[i] == x0[i] && x0[i] > m0) m0 = x0[i];
+        double S0 = 0.0;
+        for (int i = 0; i < V; ++i) if (x0[i] == x0[i]) S0 += exp((double)x0[i] - m0);
+        const double lse = m0 + log(S0);
+        const int32_t s = out->token;
+        lp_ids[0] = s;
+        lp_vals[0] = (float)((double)x0[s] - lse);
+        const uint32_t ks = vwo_key(x0[s]);
+        int32_t r = 0;
+        for (int i = 0; i < V; ++i) { const uint32_t kk = vwo_key(x0[i]); if (kk && kk >= ks) r++; }
+        *rank = r;
+        if (L > 0) {
+            /* top-L by (x0 desc, idx asc): sort packed (~key << 32 | idx) ascending */
+            uint64_t* t = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+            for (int i = 0; i < V; ++i) t[i] = ((uint64_t)(~vwo_key(x0[i])) << 32) | (uint32_t)i;
+            qsort(t, (size_t)V, sizeof(uint64_t), cmp_u64);
+            for (int j = 0; j < L && j < V; ++j) {
+                const int i = (int)(uint32_t)t[j];
+                lp_ids[1 + j] = i;
+                lp_vals[1 + j] = (float)((double)x0[i] - lse);
+            }
+            free(t);
+        }
+    }
+    free(x);
+    return 0;
+}
+
+/* Batched driver (rows are independent; OpenMP over rows when built with -fopenmp).
+ * prompt/output: padded [B, *_stride] with ids outside [0, V) ignored; lens may be NULL. */
+int vwo_sample_batch(const float* logits, int B, int V, const int32_t* prompt, int prompt_stride,
+                     const int32_t* prompt_lens, const int32_t* output, int output_stride,
+                     const int32_t* output_lens, const vwo_params* prm, const float* uniforms,
+                     int L, int32_t* lp_ids, float* lp_vals, int32_t* ranks, vwo_row_out* outs) {
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const int np = prompt ? (prompt_lens ? prompt_lens[b] : prompt_stride) : 0;
+        const int no = output ? (output_lens ? output_lens[b] : output_stride) : 0;
+        vwo_sample_row(logits + (size_t)b * V, V, prompt ? prompt + (size_t)b * prompt_stride : NULL, np,
+                       output ? output + (size_t)b * output_stride : NULL, no, &prm[b],
+                       uniforms ? uniforms + (size_t)b * V : NULL, L,
+                       lp_ids ? lp_ids + (size_t)b * (L + 1) : NULL,
+                       lp_vals ? lp_vals + (size_t)b * (L + 1) : NULL, ranks ? ranks + b : NULL,
+                       &outs[b]);
+    }
+    return 0;
+}
+
+/* Top-k values/ids of one row, (value desc, index asc); the topk256.wgsl contract. */
+void vwo_topk_row(const float* x, int V, int k, float* vals, int32_t* ids) {
+    uint64_t* t = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    for (int i = 0; i < V; ++i) t[i] = ((uint64_t)(~vwo_key(x[i])) << 32) | (uint32_t)i;
+    qsort(t, (size_t)V, sizeof(uint64_t), cmp_u64);
+    for (int j = 0; j < k && j < V; ++j) { ids[j] = (int32_t)(uint32_t)t[j]; vals[j] = x[ids[j]]; }
+    free(t);
+}
+
+/* softmax(x / T) of one row with the sampler's exp: p_i = exp_det(fl(x_i/T) - m) / S,
+ * S accumulated in double.  Also returns m and log(S) (so log-sum-exp = m + log S). */
+void vwo_softmax_row(const float* x, int V, float T, float* probs, float* row_max, double* log_sum) {
+    float m = -INFINITY;
+    for (int i = 0; i < V; ++i) { const float y = x[i] / T; if (y > m) m = y; }
+    double S = 0.0;
+    for (int i = 0; i < V; ++i) S += (double)vwo_exp(x[i] / T - m);
+    for (int i = 0; i < V; ++i) probs[i] = (float)((double)vwo_exp(x[i] / T - m) / S);
+    *row_max = m;
+    *log_sum = log(S);
+}
+
+/* ---- exhaustive checks of the arithmetic (pins exp_det/log_det against libm double) --- */
+
+static int64_t ulp_diff(float a, float b) {
+    const int64_t ka = (int64_t)vwo_key(a), kb = (int64_t)vwo_key(b);
+    return ka > kb ? ka - kb : kb - ka;
+}
+
+/* Walks every fp32 d in [lo, hi] with the given bit stride; reports the max ulp error of
+ * exp_det against double exp rounded to fp32, and a 64-bit hash of all outputs. */
+void vwo_check_exp(float lo, float hi, uint32_t stride, int64_t* max_ulp, float* worst,
+                   uint64_t* hash, uint64_t* count) {
+    int64_t mu = 0; float wd = 0.0f; uint64_t h = 0, c = 0;
+    const uint32_t klo = vwo_key(lo), khi = vwo_key(hi);
+#pragma omp parallel
+    {
+        int64_t lmu = 0; float lwd = 0.0f; uint64_t lh = 0, lc = 0;
+#pragma omp for schedule(static)
+        for (int64_t kk = klo; kk <= (int64_t)khi; kk += stride) {
+            const uint32_t key = (uint32_t)kk;
+            const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+            const float d = u2f(bits);
+            const float got = vwo_exp(d);
+            const float want = (d >= -80.0f) ? (float)exp((double)d) : 0.0f;
+            const int64_t du = ulp_diff(got, want);
+            if (du > lmu) { lmu = du; lwd = d; }
+            lh += (uint64_t)f2u(got) * 0x9E3779B97F4A7C15ull ^ (uint64_t)bits;
+            lc++;
+        }
+#pragma omp critical
+        {
+            if (lmu > mu) { mu = lmu; wd = lwd; }
+            h += lh; c += lc;
+        }
+    }
+    *max_ulp = mu; *worst = wd; *hash = h; *count = c;
+}
+
+void vwo_check_log(float lo, float hi, uint32_t stride, int64_t* max_ulp, float* worst,
+                   uint64_t* hash, uint64_t* count) {
+    int64_t mu = 0; float wd = 0.0f; uint64_t h = 0, c = 0;
+    const uint32_t klo = vwo_key(lo), khi = vwo_key(hi);
+#pragma omp parallel
+    {
+        int64_t lmu = 0; float lwd = 0.0f; uint64_t lh = 0, lc = 0;
+#pragma omp for schedule(static)
+        for (int64_t kk = klo; kk <= (int64_t)khi; kk += stride) {
+            const uint32_t key = (uint32_t)kk;
+            const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+            const float uu = u2f(bits);
+            const float got = vwo_log(uu);
+            const float want = (float)log((double)uu);
+            const int64_t du = ulp_diff(got, want);
+            if (du > lmu) { lmu = du; lwd = uu; }
+            lh += (uint64_t)f2u(got) * 0x9E3779B97F4A7C15ull ^ (uint64_t)bits;
+            lc++;
+        }
+#pragma omp critical
+        {
+            if (lmu > mu) { mu = lmu; wd = lwd; }
+            h += lh; c += lc;
+        }
+    }
+    *max_ulp = mu; *worst = wd; *hash = h; *count = c;
+}

@@ -1,0 +1,453 @@
+// vws_capi.hip -- extern "C" entry points of _vws.so: argument validation (pure host code),
+// workspace layout, shape-dependent launch decisions and kernel launches on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "vws_internal.h"
+#include "vws_sampler.h"
+
+namespace vws {
+template <typename T> __global__ void fast_kernel(KArgs);
+template <typename T> __global__ void general_kernel(KArgs);
+template <typename T> __global__ void argmax_kernel(const T*, int64_t, int, int32_t*);
+template <typename T>
+__global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, float*, float*);
+__global__ void penalties_kernel(KArgs, float*);
+__global__ void selftest_kernel(int, uint32_t, uint32_t, unsigned long long*);
+__global__ void fill_u32_kernel(uint32_t*, size_t, uint32_t);
+}  // namespace vws
+
+using namespace vws;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return VWS_OK;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(VWS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return VWS_OK;
+}
+
+struct DeviceInfo {
+    int cus = 0;
+    int fast_blocks_per_cu = 0;
+};
+
+DeviceInfo device_info() {
+    static std::mutex mu;
+    static DeviceInfo cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    DeviceInfo& d = cache[dev];
+    if (d.cus == 0) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) == hipSuccess) d.cus = prop.multiProcessorCount;
+        if (d.cus <= 0) d.cus = 256;
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fast_kernel<float>, kFastThreads, 0) != hipSuccess || n <= 0) n = 4;
+        d.fast_blocks_per_cu = n;
+        (void)hipGetLastError();
+    }
+    return d;
+}
+
+// Parts per row for the single-pass kernel: enough workgroups to fill every slot of the chip
+// once, with at least 4096 elements per part.
+void choose_parts(int B, int V, int esize, int* S, int* part_len) {
+    const DeviceInfo d = device_info();
+    const int slots = d.cus * d.fast_blocks_per_cu;
+    int s = slots / (B > 0 ? B : 1);
+    if (s < 1) s = 1;
+    if (s > kMaxParts) s = kMaxParts;
+    const int max_by_len = V / 4096 > 0 ? V / 4096 : 1;
+    if (s > max_by_len) s = max_by_len;
+    const int min_parts = (V + kPartMax - 1) / kPartMax;  // the slice bitmap covers kPartMax
+    if (s < min_parts) s = min_parts;
+    int len = (V + s - 1) / s;
+    const int align = 64;  // elements; keeps every part start 16-byte aligned
+    len = (len + align - 1) / align * align;
+    if (len > kPartMax) len = kPartMax;
+    (void)esize;
+    s = (V + len - 1) / len;
+    *S = s;
+    *part_len = len;
+}
+
+int esize_of(int dtype) { return dtype == VWS_DTYPE_BF16 ? 2 : 4; }
+
+// ---- optional per-kernel event timing (vws_profile_begin / vws_profile_end) ----
+struct Profiler {
+    std::mutex mu;
+    bool on = false;
+    int cap = 0, n = 0;
+    hipEvent_t* ev = nullptr;
+    int* kind = nullptr;
+};
+Profiler g_prof;
+
+// Records the start event of the next launch; returns the slot or -1.
+int prof_start(hipStream_t s, int kind) {
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    if (!g_prof.on || g_prof.n >= g_prof.cap) return -1;
+    const int i = g_prof.n++;
+    g_prof.kind[i] = kind;
+    (void)hipEventRecord(g_prof.ev[2 * i], s);
+    return i;
+}
+
+void prof_stop(hipStream_t s, int slot) {
+    if (slot < 0) return;
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    (void)hipEventRecord(g_prof.ev[2 * slot + 1], s);
+}
+
+int validate_rows(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_t stride) {
+    if (!logits) return fail(VWS_ERR_INVALID_ARGUMENT, "logits is NULL");
+    if (B < 1) return fail(VWS_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", B);
+    if (V < 1 || V > VWS_MAX_VOCAB)
+        return fail(VWS_ERR_LIMIT, "vocab must be in [1, %d] (got %d)", VWS_MAX_VOCAB, V);
+    if (dtype != VWS_DTYPE_F32 && dtype != VWS_DTYPE_BF16)
+        return fail(VWS_ERR_UNSUPPORTED_DTYPE, "unsupported logits dtype %d", dtype);
+    if (stride < V) return fail(VWS_ERR_INVALID_ARGUMENT, "logits_row_stride %lld < vocab %d", (long long)stride, V);
+    return VWS_OK;
+}
+
+int validate_history(const int32_t* ids, int64_t stride, int32_t width, const char* name) {
+    if (!ids) return VWS_OK;
+    if (width < 0) return fail(VWS_ERR_INVALID_ARGUMENT, "%s_width must be >= 0", name);
+    if (stride < width) return fail(VWS_ERR_INVALID_ARGUMENT, "%s_row_stride < %s_width", name, name);
+    if (width > (1 << 24)) return fail(VWS_ERR_LIMIT, "%s_width too large", name);
+    return VWS_OK;
+}
+
+int validate_sample(const vws_sample_args* a) {
+    if (!a) return fail(VWS_ERR_INVALID_ARGUMENT, "args is NULL");
+    if (a->struct_size != sizeof(vws_sample_args))
+        return fail(VWS_ERR_INVALID_ARGUMENT, "struct_size %u != %zu (ABI mismatch)", a->struct_size, sizeof(vws_sample_args));
+    int st = validate_rows(a->logits, a->dtype, a->batch, a->vocab, a->logits_row_stride);
+    if (st) return st;
+    if (!a->sampled) return fail(VWS_ERR_INVALID_ARGUMENT, "sampled is NULL");
+    if (a->temperature) {
+        if (!a->uniforms) return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms are required when temperature is given");
+        if (a->uniforms_row_stride < a->vocab) return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms_row_stride < vocab");
+    }
+    if (a->num_logprobs < -1 || a->num_logprobs > VWS_MAX_LOGPROBS)
+        return fail(VWS_ERR_LIMIT, "num_logprobs must be in [-1, %d] (got %d)", VWS_MAX_LOGPROBS, a->num_logprobs);
+    if (a->num_logprobs > a->vocab) return fail(VWS_ERR_INVALID_ARGUMENT, "num_logprobs > vocab");
+    if (a->num_logprobs >= 0 && (!a->logprob_ids || !a->logprob_vals || !a->logprob_ranks))
+        return fail(VWS_ERR_INVALID_ARGUMENT, "logprob outputs are NULL while num_logprobs >= 0");
+    if ((st = validate_history(a->prompt_ids, a->prompt_row_stride, a->prompt_width, "prompt"))) return st;
+    if ((st = validate_history(a->output_ids, a->output_row_stride, a->output_width, "output"))) return st;
+    const int hw = (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0);
+    const size_t need = ws_layout(a->batch, a->vocab, hw).total;
+    if (!a->workspace) return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace is NULL (need %zu bytes)", need);
+    if (a->workspace_bytes < need)
+        return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", a->workspace_bytes, need);
+    if (reinterpret_cast<uintptr_t>(a->workspace) & 255u)
+        return fail(VWS_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    return VWS_OK;
+}
+
+KArgs make_kargs(int B, int V, const void* logits, int64_t stride, void* ws, int hw) {
+    KArgs k;
+    std::memset(&k, 0, sizeof(k));
+    k.logits = logits;
+    k.lstride = stride;
+    k.B = B;
+    k.V = V;
+    k.L = -1;
+    const WsLayout w = ws_layout(B, V, hw);
+    char* base = static_cast<char*>(ws);
+    k.row_counter = reinterpret_cast<uint32_t*>(base + w.counter);
+    k.row_state = reinterpret_cast<uint32_t*>(base + w.state);
+    k.part_meta = reinterpret_cast<uint32_t*>(base + w.meta);
+    k.part_list = reinterpret_cast<uint2*>(base + w.list);
+    k.hist_hash = reinterpret_cast<uint32_t*>(base + w.hash);
+    k.hs_row = w.hs_row;
+    return k;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t vws_abi_version(void) { return VWS_ABI_VERSION; }
+
+const char* vws_last_error(void) { return g_err.c_str(); }
+
+size_t vws_sample_workspace_size(int32_t batch, int32_t vocab, int32_t history_width) {
+    if (batch < 1 || vocab < 1 || history_width < 0) return 0;
+    return ws_layout(batch, vocab, history_width).total;
+}
+
+int vws_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+    if (!workspace) return fail(VWS_ERR_INVALID_ARGUMENT, "workspace is NULL");
+    const size_t n = workspace_bytes / 4;
+    if (n == 0) return ok();
+    const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<uint32_t*>(workspace), n, 0u);
+    if (int st = check_launch("vws_workspace_init")) return st;
+    return ok();
+}
+
+int vws_validate_sample_args(const vws_sample_args* args) {
+    const int st = validate_sample(args);
+    return st ? st : ok();
+}
+
+int vws_sample(const vws_sample_args* a) {
+    int st = validate_sample(a);
+    if (st) return st;
+    const int hw = (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0);
+    KArgs k = make_kargs(a->batch, a->vocab, a->logits, a->logits_row_stride, a->workspace, hw);
+    k.temperature = a->temperature;
+    k.top_k = a->top_k;
+    k.top_p = a->top_p;
+    k.min_p = a->min_p;
+    k.rep = a->repetition_penalty;
+    k.pres = a->presence_penalty;
+    k.freq = a->frequency_penalty;
+    k.prompt = a->prompt_ids;
+    k.pstride = a->prompt_row_stride;
+    k.pwidth = a->prompt_ids ? a->prompt_width : 0;
+    k.plens = a->prompt_lens;
+    k.output = a->output_ids;
+    k.ostride = a->output_row_stride;
+    k.owidth = a->output_ids ? a->output_width : 0;
+    k.olens = a->output_lens;
+    k.u = a->uniforms;
+    k.ustride = a->uniforms_row_stride;
+    k.sampled = a->sampled;
+    k.flags = a->row_flags;
+    k.nkept = a->num_kept;
+    k.L = a->num_logprobs;
+    k.lp_ids = a->logprob_ids;
+    k.lp_vals = a->logprob_vals;
+    k.lp_ranks = a->logprob_ranks;
+    k.mode = kModeSample;
+    choose_parts(a->batch, a->vocab, esize_of(a->dtype), &k.S, &k.part_len);
+    hipStream_t s = (hipStream_t)a->stream;
+    const int bp = (a->batch + 7) / 8 * 8;
+    if (a->num_logprobs < 0) {
+        const int ps = prof_start(s, VWS_KERNEL_FAST);
+        if (a->dtype == VWS_DTYPE_F32)
+            hipLaunchKernelGGL(fast_kernel<float>, dim3(bp * k.S), dim3(kFastThreads), 0, s, k);
+        else
+            hipLaunchKernelGGL(fast_kernel<uint16_t>, dim3(bp * k.S), dim3(kFastThreads), 0, s, k);
+        prof_stop(s, ps);
+        if ((st = check_launch("vws_sample (single-pass kernel)"))) return st;
+    }
+    const int pg = prof_start(s, VWS_KERNEL_GENERAL);
+    if (a->dtype == VWS_DTYPE_F32)
+        hipLaunchKernelGGL(general_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
+    else
+        hipLaunchKernelGGL(general_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
+    prof_stop(s, pg);
+    if ((st = check_launch("vws_sample (general kernel)"))) return st;
+    return ok();
+}
+
+int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
+               int32_t* out_ids, void* stream) {
+    int st = validate_rows(logits, dtype, batch, vocab, row_stride);
+    if (st) return st;
+    if (!out_ids) return fail(VWS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    const int ps = prof_start(s, VWS_KERNEL_ARGMAX);
+    if (dtype == VWS_DTYPE_F32)
+        hipLaunchKernelGGL(argmax_kernel<float>, dim3(batch), dim3(1024), 0, s,
+                           static_cast<const float*>(logits), row_stride, vocab, out_ids);
+    else
+        hipLaunchKernelGGL(argmax_kernel<uint16_t>, dim3(batch), dim3(1024), 0, s,
+                           static_cast<const uint16_t*>(logits), row_stride, vocab, out_ids);
+    prof_stop(s, ps);
+    if ((st = check_launch("vws_argmax"))) return st;
+    return ok();
+}
+
+size_t vws_topk_workspace_size(int32_t batch, int32_t vocab, int32_t k) {
+    (void)k;
+    return vws_sample_workspace_size(batch, vocab, 0);
+}
+
+int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
+             int32_t k, float* out_vals, int32_t* out_ids, void* workspace, size_t workspace_bytes,
+             void* stream) {
+    int st = validate_rows(logits, dtype, batch, vocab, row_stride);
+    if (st) return st;
+    if (k < 1 || k > kKMax || k > vocab) return fail(VWS_ERR_LIMIT, "k must be in [1, min(%d, vocab)] (got %d)", kKMax, k);
+    if (!out_vals || !out_ids) return fail(VWS_ERR_INVALID_ARGUMENT, "outputs are NULL");
+    const size_t need = vws_topk_workspace_size(batch, vocab, k);
+    if (!workspace || workspace_bytes < need)
+        return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", workspace_bytes, need);
+    KArgs ka = make_kargs(batch, vocab, logits, row_stride, workspace, 0);
+    ka.mode = kModeTopK;
+    ka.topk_k = k;
+    ka.topk_vals = out_vals;
+    ka.topk_ids = out_ids;
+    choose_parts(batch, vocab, esize_of(dtype), &ka.S, &ka.part_len);
+    hipStream_t s = (hipStream_t)stream;
+    const int bp = (batch + 7) / 8 * 8;
+    const int ps = prof_start(s, VWS_KERNEL_FAST);
+    if (dtype == VWS_DTYPE_F32)
+        hipLaunchKernelGGL(fast_kernel<float>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
+    else
+        hipLaunchKernelGGL(fast_kernel<uint16_t>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
+    prof_stop(s, ps);
+    if ((st = check_launch("vws_topk"))) return st;
+    // rows whose single-pass candidate lists overflowed (ties) are finished exactly here
+    const int pg = prof_start(s, VWS_KERNEL_GENERAL);
+    if (dtype == VWS_DTYPE_F32)
+        hipLaunchKernelGGL(general_kernel<float>, dim3(batch), dim3(kGenThreads), 0, s, ka);
+    else
+        hipLaunchKernelGGL(general_kernel<uint16_t>, dim3(batch), dim3(kGenThreads), 0, s, ka);
+    prof_stop(s, pg);
+    if ((st = check_launch("vws_topk (general kernel)"))) return st;
+    return ok();
+}
+
+int vws_softmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
+                const float* temperature, float* probs, float* row_max, float* log_sum, void* stream) {
+    int st = validate_rows(logits, dtype, batch, vocab, row_stride);
+    if (st) return st;
+    if (!probs) return fail(VWS_ERR_INVALID_ARGUMENT, "probs is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    const int ps = prof_start(s, VWS_KERNEL_SOFTMAX);
+    if (dtype == VWS_DTYPE_F32)
+        hipLaunchKernelGGL(softmax_kernel<float>, dim3(batch), dim3(1024), 0, s,
+                           static_cast<const float*>(logits), row_stride, vocab, temperature, probs,
+                           row_max, log_sum);
+    else
+        hipLaunchKernelGGL(softmax_kernel<uint16_t>, dim3(batch), dim3(1024), 0, s,
+                           static_cast<const uint16_t*>(logits), row_stride, vocab, temperature,
+                           probs, row_max, log_sum);
+    prof_stop(s, ps);
+    if ((st = check_launch("vws_softmax"))) return st;
+    return ok();
+}
+
+int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row_stride,
+                        const float* repetition, const float* presence, const float* frequency,
+                        const int32_t* prompt_ids, int64_t prompt_row_stride, int32_t prompt_width,
+                        const int32_t* prompt_lens, const int32_t* output_ids,
+                        int64_t output_row_stride, int32_t output_width,
+                        const int32_t* output_lens, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+    int st = validate_rows(logits, VWS_DTYPE_F32, batch, vocab, row_stride);
+    if (st) return st;
+    if ((st = validate_history(prompt_ids, prompt_row_stride, prompt_width, "prompt"))) return st;
+    if ((st = validate_history(output_ids, output_row_stride, output_width, "output"))) return st;
+    const int hw = (prompt_ids ? prompt_width : 0) + (output_ids ? output_width : 0);
+    const size_t need = ws_layout(batch, vocab, hw).total;
+    if (!workspace || workspace_bytes < need)
+        return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", workspace_bytes, need);
+    if (hw == 0) return ok();
+    KArgs k = make_kargs(batch, vocab, logits, row_stride, workspace, hw);
+    k.rep = repetition;
+    k.pres = presence;
+    k.freq = frequency;
+    k.prompt = prompt_ids;
+    k.pstride = prompt_row_stride;
+    k.pwidth = prompt_ids ? prompt_width : 0;
+    k.plens = prompt_lens;
+    k.output = output_ids;
+    k.ostride = output_row_stride;
+    k.owidth = output_ids ? output_width : 0;
+    k.olens = output_lens;
+    const int ps = prof_start((hipStream_t)stream, VWS_KERNEL_PENALTIES);
+    hipLaunchKernelGGL(penalties_kernel, dim3(batch), dim3(1024), 0, (hipStream_t)stream, k, logits);
+    prof_stop((hipStream_t)stream, ps);
+    if ((st = check_launch("vws_apply_penalties"))) return st;
+    return ok();
+}
+
+int vws_math_selftest(int32_t fn, uint32_t key_lo, uint32_t key_hi, uint64_t* out2, void* stream) {
+    if (fn != 0 && fn != 1) return fail(VWS_ERR_INVALID_ARGUMENT, "fn must be 0 (exp) or 1 (log)");
+    if (!out2) return fail(VWS_ERR_INVALID_ARGUMENT, "out2 is NULL");
+    if (key_hi < key_lo) return fail(VWS_ERR_INVALID_ARGUMENT, "key_hi < key_lo");
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(out2), (size_t)4, 0u);
+    int st = check_launch("vws_math_selftest (clear)");
+    if (st) return st;
+    hipLaunchKernelGGL(selftest_kernel, dim3(4096), dim3(256), 0, s, fn, key_lo, key_hi,
+                       reinterpret_cast<unsigned long long*>(out2));
+    if ((st = check_launch("vws_math_selftest"))) return st;
+    return ok();
+}
+
+int vws_profile_begin(int32_t max_launches) {
+    if (max_launches < 1 || max_launches > (1 << 20))
+        return fail(VWS_ERR_INVALID_ARGUMENT, "max_launches must be in [1, 2^20]");
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    if (g_prof.on) return fail(VWS_ERR_INVALID_ARGUMENT, "profiling already active");
+    g_prof.ev = new hipEvent_t[2 * (size_t)max_launches];
+    g_prof.kind = new int[max_launches];
+    for (int i = 0; i < 2 * max_launches; ++i) {
+        if (hipEventCreate(&g_prof.ev[i]) != hipSuccess) {
+            for (int j = 0; j < i; ++j) (void)hipEventDestroy(g_prof.ev[j]);
+            delete[] g_prof.ev;
+            delete[] g_prof.kind;
+            g_prof.ev = nullptr;
+            g_prof.kind = nullptr;
+            return fail(VWS_ERR_HIP, "hipEventCreate failed");
+        }
+    }
+    g_prof.cap = max_launches;
+    g_prof.n = 0;
+    g_prof.on = true;
+    return ok();
+}
+
+int vws_profile_end(double* ms, int32_t* count) {
+    std::lock_guard<std::mutex> lock(g_prof.mu);
+    if (!g_prof.on) return fail(VWS_ERR_INVALID_ARGUMENT, "profiling is not active");
+    for (int k = 0; k < VWS_KERNEL_KINDS; ++k) {
+        if (ms) ms[k] = 0.0;
+        if (count) count[k] = 0;
+    }
+    int st = VWS_OK;
+    for (int i = 0; i < g_prof.n; ++i) {
+        float t = 0.0f;
+        if (hipEventSynchronize(g_prof.ev[2 * i + 1]) != hipSuccess ||
+            hipEventElapsedTime(&t, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]) != hipSuccess) {
+            st = fail(VWS_ERR_HIP, "event timing failed");
+            continue;
+        }
+        const int k = g_prof.kind[i];
+        if (ms) ms[k] += (double)t;
+        if (count) count[k] += 1;
+    }
+    for (int i = 0; i < 2 * g_prof.cap; ++i) (void)hipEventDestroy(g_prof.ev[i]);
+    delete[] g_prof.ev;
+    delete[] g_prof.kind;
+    g_prof.ev = nullptr;
+    g_prof.kind = nullptr;
+    g_prof.on = false;
+    g_prof.cap = g_prof.n = 0;
+    return st ? st : ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,347 @@
+// vws_device.h -- device-side building blocks of the gfx950 sampler: the sampler arithmetic
+// (bit-exact fp32 exp/log, order keys, integer masses), wave64 primitives and a wave-level
+// radix select over LDS-resident keys.
+//
+// The arithmetic below is the project's definition of exp_det / log_det: fixed sequences of
+// IEEE fp32 add/mul/fma that give the same bits on any IEEE machine.  The file must be
+// compiled with -ffp-contract=off so that no multiply-add is fused behind our back.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vws {
+
+constexpr int kWave = 64;
+constexpr float kSamplingEps = 1e-5f;
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// exp(d) for d in [-80, 80] (clamped above), 0 below -80 and for NaN.  Cody-Waite
+// reduction n = rint(d * log2 e), r = d - n * ln2 with a 16-bit head of ln2 (n * head is
+// exact) and an fp32 tail; exp(r) = 1 + r + r^2 Q(r) with Q of degree 4 fitted for this
+// project on [-ln2/2, ln2/2]; exact scaling by 2^n.  Max error 1 ulp (checked on every fp32).
+__device__ __forceinline__ float exp_det(float d) {
+    if (!(d >= -80.0f)) return 0.0f;
+    if (d > 80.0f) d = 80.0f;
+    if (__builtin_fabsf(d) < 0x1p-30f) return 1.0f;
+    const float t = d * 0x1.715476p+0f;
+    const float n = __builtin_rintf(t);
+    float r = __builtin_fmaf(-n, 0x1.62e4p-1f, d);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = __builtin_fmaf(0x1.6d7532p-10f, r, 0x1.120b66p-7f);
+    p = __builtin_fmaf(p, r, 0x1.5554b8p-5f);
+    p = __builtin_fmaf(p, r, 0x1.5554dcp-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+// log(u) for u > 0: u = 2^e m with m in [sqrt(1/2), sqrt(2)], f = m - 1 (exact),
+// log1p(f) = f + f^2 R(f) with R of degree 8 fitted for this project, log u = e ln2 + log1p(f).
+// log(0) = -inf, log(+inf) = +inf, NaN otherwise.  Max error 1 ulp (checked on every fp32).
+__device__ __forceinline__ float log_det(float u) {
+    if (!(u > 0.0f)) return (u == 0.0f) ? -__builtin_inff() : __builtin_nanf("");
+    if (u == __builtin_inff()) return u;
+    uint32_t b = f2u(u);
+    int e = 0;
+    if (b < 0x00800000u) { b = f2u(u * 0x1p23f); e = -23; }
+    e += (int)(b >> 23) - 127;
+    uint32_t mb = (b & 0x007FFFFFu) | 0x3F800000u;
+    if (mb > 0x3FB504F3u) { mb -= 0x00800000u; e += 1; }
+    const float f = u2f(mb) - 1.0f;
+    const float f2 = f * f;
+    float R = __builtin_fmaf(-0x1.4a5298p-4f, f, 0x1.088e82p-3f);
+    R = __builtin_fmaf(R, f, -0x1.0bb9f2p-3f);
+    R = __builtin_fmaf(R, f, 0x1.2245c6p-3f);
+    R = __builtin_fmaf(R, f, -0x1.548f6ep-3f);
+    R = __builtin_fmaf(R, f, 0x1.99a7bap-3f);
+    R = __builtin_fmaf(R, f, -0x1.0001f8p-2f);
+    R = __builtin_fmaf(R, f, 0x1.555548p-2f);
+    R = __builtin_fmaf(R, f, -0x1.fffffep-2f);
+    const float L = __builtin_fmaf(f2, R, f);
+    if (e == 0) return L;
+    const float ef = (float)e;
+    return __builtin_fmaf(ef, 0x1.62e43p-1f, __builtin_fmaf(ef, -0x1.05c61p-29f, L));
+}
+
+// floor(e * 2^44) for e in [0, 1]; 0 for e <= 0 or NaN.
+__device__ __forceinline__ uint64_t mass_of(float e) {
+    if (!(e > 0.0f)) return 0;
+    const uint32_t b = f2u(e);
+    const int ex = (int)(b >> 23);
+    const uint64_t mant = ex ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
+    const int sh = (ex ? ex : 1) - 106;
+    if (sh >= 0) return mant << sh;
+    if (sh <= -64) return 0;
+    return mant >> (-sh);
+}
+
+// Order-preserving key: x < y <=> key(x) < key(y); -0 and +0 share a key; NaN -> 0.
+__device__ __forceinline__ uint32_t key_of(float x) {
+    uint32_t b = f2u(x);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0;
+    if (b == 0x80000000u) b = 0;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Inverse of key_of on keys >= 1 (key 0 maps to a NaN).
+__device__ __forceinline__ float val_of(uint32_t k) {
+    return u2f((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// floor(q * W) for fp32 q in (0, 1) and W < 2^64, exact (128-bit product).
+__device__ __forceinline__ uint64_t scale_floor(float q, uint64_t W) {
+    const uint32_t b = f2u(q);
+    const int ex = (int)(b >> 23);
+    const uint64_t mq = ex ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
+    const int sh = 150 - (ex ? ex : 1);
+    const uint64_t lo = mq * W;
+    const uint64_t hi = __umul64hi(mq, W);
+    if (sh >= 128) return 0;
+    if (sh >= 64) return hi >> (sh - 64);
+    if (sh == 0) return lo;
+    return (lo >> sh) | (hi << (64 - sh));
+}
+
+// vLLM-v1 penalty step: repetition on prompt|output tokens (x > 0: x * fl(1/r), else x * r),
+// then x - f * count, then x - p * (count > 0).
+__device__ __forceinline__ float apply_penalty(float x, bool in_prompt, uint32_t cnt, float rep,
+                                               float inv_rep, float freq, float pres) {
+    if (in_prompt || cnt > 0) x = (x > 0.0f) ? x * inv_rep : x * rep;
+    x = x - freq * (float)cnt;
+    x = x - pres * (cnt > 0 ? 1.0f : 0.0f);
+    return x;
+}
+
+// Greedy rows: temperature < 1e-5 or NaN.
+__device__ __forceinline__ bool is_greedy(float T) { return !(T >= kSamplingEps); }
+
+// ---- wave64 primitives ------------------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ int lane_prefix(uint64_t mask) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t t = __shfl_up(v, o, kWave);
+        if (l >= o) v += t;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = __shfl_xor(v, o, kWave); v = v > t ? v : t; }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = __shfl_xor(v, o, kWave); v = v < t ? v : t; }
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = __shfl_xor(v, o, kWave); v = v > t ? v : t; }
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = __shfl_xor(v, o, kWave); v = v < t ? v : t; }
+    return v;
+}
+
+// k-th largest key (1-based, counting multiplicity) among keys[0..n) in LDS, computed by one
+// whole wave with a 4 x 8-bit radix select.  hist: 256 words of wave-private LDS.
+// Requires 1 <= k <= n.
+__device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t* keys, int n, int k,
+                                                     uint32_t* hist) {
+    const int lane = lane_id();
+    uint32_t prefix = 0, pmask = 0;
+    uint32_t rem = (uint32_t)k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = lane; b < 256; b += kWave) hist[b] = 0;
+        wave_sync();
+        for (int i = lane; i < n; i += kWave) {
+            const uint32_t kk = keys[i];
+            if ((kk & pmask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+        }
+        wave_sync();
+        // lane l owns bins 255-4l .. 252-4l (descending key order)
+        const uint32_t c0 = hist[255 - 4 * lane], c1 = hist[254 - 4 * lane];
+        const uint32_t c2 = hist[253 - 4 * lane], c3 = hist[252 - 4 * lane];
+        const uint32_t s = c0 + c1 + c2 + c3;
+        const uint32_t incl = wave_incl_scan(s);
+        const uint32_t excl = incl - s;
+        const uint64_t hit = __ballot(excl < rem && rem <= incl);
+        const int L = __ffsll((unsigned long long)hit) - 1;
+        uint32_t bin = 0, r = rem - excl;
+        if (r <= c0) bin = 255 - 4 * lane;
+        else if ((r -= c0) <= c1) bin = 254 - 4 * lane;
+        else if ((r -= c1) <= c2) bin = 253 - 4 * lane;
+        else { r -= c2; bin = 252 - 4 * lane; }
+        bin = __shfl(bin, L, kWave);
+        rem = __shfl(r, L, kWave);
+        prefix |= bin << shift;
+        pmask |= 255u << shift;
+        wave_sync();
+    }
+    return prefix;
+}
+
+// k-th largest key (1-based, with multiplicity) of at most 256 keys held 4 per lane by one
+// whole wave (missing entries passed as 0): an in-register bitonic sort into descending order
+// across the wave (element e = 4 * lane + i), then a read of element k - 1.
+__device__ __forceinline__ uint32_t wave_kth_largest_256(uint32_t v0, uint32_t v1, uint32_t v2,
+                                                         uint32_t v3, int k) {
+    const int lane = lane_id();
+    uint32_t v[4] = {v0, v1, v2, v3};
+#pragma unroll
+    for (int size = 2; size <= 256; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 4) {
+                const int lstride = stride >> 2;
+                const bool upper = (lane & lstride) != 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int e = 4 * lane + i;
+                    const bool desc = (e & size) == 0;
+                    const uint32_t o = __shfl_xor(v[i], lstride, kWave);
+                    const uint32_t hi = v[i] > o ? v[i] : o, lo = v[i] > o ? o : v[i];
+                    // the lower element of a pair keeps the larger key in a descending block
+                    v[i] = (upper != desc) ? hi : lo;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if ((i & stride) == 0) {
+                        const int e = 4 * lane + i;
+                        const bool desc = (e & size) == 0;
+                        const uint32_t x = v[i], y = v[i + stride];
+                        const bool swap = desc ? (x < y) : (x > y);
+                        v[i] = swap ? y : x;
+                        v[i + stride] = swap ? x : y;
+                    }
+                }
+            }
+        }
+    }
+    const int src = (k - 1) >> 2, sel = (k - 1) & 3;
+    const uint32_t r0 = __shfl(v[0], src, kWave), r1 = __shfl(v[1], src, kWave);
+    const uint32_t r2 = __shfl(v[2], src, kWave), r3 = __shfl(v[3], src, kWave);
+    return sel == 0 ? r0 : sel == 1 ? r1 : sel == 2 ? r2 : r3;
+}
+
+// Number of keys >= t among keys[0..n) (one whole wave).
+__device__ __forceinline__ int wave_count_ge(const uint32_t* keys, int n, uint32_t t) {
+    int c = 0;
+    for (int i = lane_id(); i < n; i += kWave) c += (keys[i] >= t) ? 1 : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, kWave);
+    return c;
+}
+
+// ---- logits element access --------------------------------------------------------------
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    static constexpr int kVec = 4;  // elements per 16-byte load
+    __device__ __forceinline__ static float load1(const float* p) { return *p; }
+    __device__ __forceinline__ static void load_vec(const float* p, float* out) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    }
+};
+template <> struct Elem<uint16_t> {  // bfloat16 bit patterns, widened exactly
+    static constexpr int kVec = 8;
+    __device__ __forceinline__ static float load1(const uint16_t* p) { return u2f((uint32_t)(*p) << 16); }
+    __device__ __forceinline__ static void load_vec(const uint16_t* p, float* out) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i] = u2f(w[i] << 16);
+            out[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+        }
+    }
+};
+
+// A row slice [lo, hi) seen as chunks of kVec elements: chunk 0 is the unaligned head
+// (elements before the first 16-byte boundary), chunks 1..nbody are aligned vectors and chunk
+// nbody+1 is the tail.  Elements outside the slice read as NaN, which every consumer ignores.
+template <typename T> struct Slice {
+    const T* row;
+    int lo, hi;      // element range
+    int a;           // first aligned element (>= lo, <= hi)
+    int nbody;       // aligned vectors
+    __device__ __forceinline__ void init(const T* row_, int lo_, int hi_) {
+        row = row_; lo = lo_; hi = hi_;
+        const uintptr_t addr = reinterpret_cast<uintptr_t>(row + lo);
+        const int mis = (int)((addr & 15u) / sizeof(T));
+        int head = mis ? (Elem<T>::kVec - mis) : 0;
+        if (head > hi - lo) head = hi - lo;
+        a = lo + head;
+        nbody = (hi - a) / Elem<T>::kVec;
+    }
+    __device__ int nchunks() const { return nbody + 2; }
+    // Aligned vector vi of the body with the index clamped into range (nbody >= 1), so the load
+    // is unconditional and can stay in flight; vectors with vi >= nbody repeat the last vector
+    // and must be discarded by the consumer (their element index is >= body_end()).
+    __device__ __forceinline__ int load_body(int vi, float* out) const {
+        constexpr int V = Elem<T>::kVec;
+        const int vc = vi < nbody ? vi : nbody - 1;
+        Elem<T>::load_vec(row + a + vc * V, out);
+        return a + vi * V;
+    }
+    __device__ __forceinline__ int body_end() const { return a + nbody * Elem<T>::kVec; }
+    // Unaligned head (which = 0) or tail (which = 1) elements as one NaN-padded chunk.
+    __device__ __forceinline__ int load_edge(int which, float* out) const {
+        constexpr int V = Elem<T>::kVec;
+        const int i0 = which == 0 ? lo : a + nbody * V;
+        const int end = which == 0 ? a : hi;
+#pragma unroll
+        for (int j = 0; j < V; ++j) out[j] = (i0 + j < end) ? Elem<T>::load1(row + i0 + j) : __builtin_nanf("");
+        return i0;
+    }
+    // Loads chunk c into out[kVec]; returns the index of out[0].
+    __device__ __forceinline__ int load(int c, float* out) const {
+        constexpr int V = Elem<T>::kVec;
+        const float nan = __builtin_nanf("");
+        if (c >= 1 && c <= nbody) {
+            const int i0 = a + (c - 1) * V;
+            Elem<T>::load_vec(row + i0, out);
+            return i0;
+        }
+        const int i0 = (c == 0) ? lo : a + nbody * V;
+        const int end = (c == 0) ? a : hi;
+#pragma unroll
+        for (int j = 0; j < V; ++j) out[j] = (c <= nbody + 1 && i0 + j < end) ? Elem<T>::load1(row + i0 + j) : nan;
+        return i0;
+    }
+};
+
+}  // namespace vws

@@ -1,0 +1,108 @@
+// vws_internal.h -- kernel argument block and workspace layout shared by the launchers
+// (vws_capi.hip) and the kernels (vws_sample.hip, vws_ops.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vws {
+
+// Fast path (split-row streaming top-k): shape constants.
+constexpr int kFastThreads = 256;                 // 4 waves per part
+constexpr int kFastWaves = kFastThreads / 64;
+constexpr int kCapW = 512;                        // candidate slots per wave (LDS)
+constexpr int kKMax = 256;                        // largest k the fast path serves
+constexpr int kPartCap = 512;                     // list entries a part may publish
+constexpr int kMergeCap = kFastWaves * kCapW;     // entries the last part can merge
+constexpr int kKeepCap = 256;                     // survivors the fast epilogue resolves
+constexpr int kHashSlots = 1024;                  // history slots per part (LDS)
+constexpr int kHashFill = 768;                    // max unique history tokens per part
+constexpr int kPartMax = 32768;                   // elements per part (LDS bitmap of the slice)
+constexpr int kMaxParts = 16;                    // VWS_MAX_VOCAB / kPartMax = 16
+
+// General path (one workgroup per row, multi-pass).
+constexpr int kGenThreads = 1024;
+constexpr int kGenWaves = kGenThreads / 64;
+constexpr int kBuckets = 4096;                    // d-buckets of width 1/128 over d in [0, 32)
+constexpr int kGatherCap = 2048;                  // boundary-bucket entries resolved in LDS
+constexpr int kLpCapW = 192;                      // per-wave top-L candidate slots
+
+// Row states written by the fast path for the general path.
+constexpr uint32_t kRowNeedsGeneral = 1u;
+
+enum Mode : int { kModeSample = 0, kModeTopK = 1 };
+
+struct KArgs {
+    const void* logits;
+    int64_t lstride;
+    int B, V;
+    const float* temperature;
+    const int32_t* top_k;
+    const float* top_p;
+    const float* min_p;
+    const float* rep;
+    const float* pres;
+    const float* freq;
+    const int32_t* prompt;
+    int64_t pstride;
+    int pwidth;
+    const int32_t* plens;
+    const int32_t* output;
+    int64_t ostride;
+    int owidth;
+    const int32_t* olens;
+    const float* u;
+    int64_t ustride;
+    int32_t* sampled;
+    uint32_t* flags;
+    int32_t* nkept;
+    int L;
+    int32_t* lp_ids;
+    float* lp_vals;
+    int32_t* lp_ranks;
+    // workspace views
+    uint32_t* row_counter;  // [B]
+    uint32_t* row_state;    // [B]
+    uint32_t* part_meta;    // [B * kMaxParts * 4]: count, kth key, status, 0
+    uint2* part_list;       // [B * kMaxParts * kPartCap]: (key, index)
+    uint32_t* hist_hash;    // [B * hs_row * 3]: token+1, count | prompt<<31, penalised bits
+    int hs_row;             // history hash slots per row (power of two) or 0
+    int S;                  // parts per row
+    int part_len;           // elements per part (multiple of 64)
+    int mode;               // Mode
+    int topk_k;             // k for kModeTopK
+    float* topk_vals;       // [B, k]
+    int32_t* topk_ids;      // [B, k]
+};
+
+// Workspace layout (bytes, 256-aligned sections).
+struct WsLayout {
+    size_t counter, state, meta, list, hash, total;
+    int hs_row;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline int hash_slots_for(int history_width) {
+    if (history_width <= 0) return 0;
+    int s = 64;
+    while (s < 2 * history_width) s <<= 1;
+    return s;
+}
+
+inline WsLayout ws_layout(int B, int V, int history_width) {
+    (void)V;
+    WsLayout w{};
+    size_t off = 0;
+    w.counter = off; off = align256(off + sizeof(uint32_t) * (size_t)B);
+    w.state = off;   off = align256(off + sizeof(uint32_t) * (size_t)B);
+    w.meta = off;    off = align256(off + sizeof(uint32_t) * 4 * (size_t)B * kMaxParts);
+    w.list = off;    off = align256(off + sizeof(uint2) * (size_t)B * kMaxParts * kPartCap);
+    w.hs_row = hash_slots_for(history_width);
+    w.hash = off;    off = align256(off + sizeof(uint32_t) * 3 * (size_t)B * (size_t)w.hs_row);
+    w.total = off;
+    return w;
+}
+
+}  // namespace vws

@@ -1,0 +1,194 @@
+// vws_ops.hip -- the standalone row operations of the library: batched argmax (the argmax.wgsl
+// contract), row softmax with temperature (softmax.wgsl), in-place penalties, and the device
+// self-test of the sampler arithmetic.
+#include "vws_device.h"
+#include "vws_internal.h"
+#include "vws_sampler.h"
+
+namespace vws {
+
+constexpr int kOpThreads = 1024;
+constexpr int kOpWaves = kOpThreads / 64;
+
+__device__ __forceinline__ uint64_t op_block_max(uint64_t v, uint64_t* red) {
+    v = wave_max_u64(v);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t t = 0;
+#pragma unroll
+    for (int i = 0; i < kOpWaves; ++i) t = t > red[i] ? t : red[i];
+    return t;
+}
+
+__device__ __forceinline__ double op_block_sum_f64(double v, double* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    __syncthreads();
+    if (lane_id() == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < kOpWaves; ++i) t += red[i];
+    return t;
+}
+
+// One workgroup per row; (key << 32 | 0x7FFFFFFF - index) max = largest value, lowest index.
+template <typename T>
+__global__ __launch_bounds__(kOpThreads) void argmax_kernel(const T* logits, int64_t stride, int V,
+                                                             int32_t* out) {
+    __shared__ uint64_t red[kOpWaves];
+    const int r = blockIdx.x;
+    Slice<T> sl;
+    sl.init(logits + (size_t)r * stride, 0, V);
+    constexpr int VEC = Elem<T>::kVec;
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
+        float v[VEC];
+        const int i0 = sl.load(c, v);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const uint64_t pk = ((uint64_t)key_of(v[j]) << 32) | (uint32_t)(0x7FFFFFFF - (i0 + j));
+            best = best > pk ? best : pk;
+        }
+    }
+    best = op_block_max(best, red);
+    if (threadIdx.x == 0) {
+        int32_t tok = (int32_t)(0x7FFFFFFF - (uint32_t)(best & 0xFFFFFFFFu));
+        if ((best >> 32) == 0u || tok >= V) tok = 0;  // every element NaN
+        out[r] = tok;
+    }
+}
+
+// probs = exp_det(x/T - m) / S, m = max x/T, S = sum exp_det(x/T - m); one workgroup per row.
+template <typename T>
+__global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, int64_t stride, int V,
+                                                              const float* temperature, float* probs,
+                                                              float* row_max, float* log_sum) {
+    __shared__ uint64_t red[kOpWaves];
+    __shared__ double redd[kOpWaves];
+    const int r = blockIdx.x;
+    const float Tt = temperature ? temperature[r] : 1.0f;
+    Slice<T> sl;
+    sl.init(logits + (size_t)r * stride, 0, V);
+    constexpr int VEC = Elem<T>::kVec;
+    uint64_t mk = 0;
+    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
+        float v[VEC];
+        sl.load(c, v);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[j] / Tt); mk = mk > k ? mk : k; }
+    }
+    mk = op_block_max(mk, red);
+    const float m = val_of((uint32_t)mk);
+    double s = 0.0;
+    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
+        float v[VEC];
+        sl.load(c, v);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) if (v[j] == v[j]) s += (double)exp_det(v[j] / Tt - m);
+    }
+    const double S = op_block_sum_f64(s, redd);
+    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
+        float v[VEC];
+        const int i0 = sl.load(c, v);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const int i = i0 + j;
+            const bool inside = (c == 0) ? (i < sl.a) : (c <= sl.nbody ? true : i < V);
+            if (c <= sl.nbody + 1 && inside && i < V)
+                probs[(size_t)r * V + i] = (float)((double)exp_det(v[j] / Tt - m) / S);
+        }
+    }
+    if (threadIdx.x == 0) {
+        if (row_max) row_max[r] = m;
+        if (log_sum) log_sum[r] = (float)log(S);
+    }
+}
+
+// In-place vLLM-v1 penalties on fp32 rows: one workgroup per row, history deduplicated in a
+// per-row hash in the workspace.
+__global__ __launch_bounds__(kOpThreads) void penalties_kernel(KArgs a, float* logits) {
+    const int r = blockIdx.x;
+    const float rep = a.rep ? a.rep[r] : 1.0f;
+    const float pres = a.pres ? a.pres[r] : 0.0f;
+    const float freq = a.freq ? a.freq[r] : 0.0f;
+    const float inv_rep = 1.0f / rep;
+    const int np = a.prompt ? (a.plens ? min(max(a.plens[r], 0), a.pwidth) : a.pwidth) : 0;
+    const int no = a.output ? (a.olens ? min(max(a.olens[r], 0), a.owidth) : a.owidth) : 0;
+    const int hs = a.hs_row;
+    if (hs == 0 || (np == 0 && no == 0)) return;
+    uint32_t* hkey = a.hist_hash + (size_t)r * (size_t)hs * 3;
+    uint32_t* hval = hkey + hs;
+    for (int i = threadIdx.x; i < hs; i += kOpThreads) { hkey[i] = 0u; hval[i] = 0u; }
+    __threadfence();
+    __syncthreads();
+    auto insert = [&](int t, uint32_t inc) {
+        uint32_t s = ((uint32_t)t * 2654435761u) & (uint32_t)(hs - 1);
+        for (int probe = 0; probe < hs; ++probe) {
+            const uint32_t prev = atomicCAS(&hkey[s], 0u, (uint32_t)t + 1u);
+            if (prev == 0u || prev == (uint32_t)t + 1u) {
+                if (inc & 0x80000000u) atomicOr(&hval[s], 0x80000000u);
+                else atomicAdd(&hval[s], inc);
+                return;
+            }
+            s = (s + 1u) & (uint32_t)(hs - 1);
+        }
+    };
+    for (int i = threadIdx.x; i < np; i += kOpThreads) {
+        const int t = a.prompt[(size_t)r * a.pstride + i];
+        if (t >= 0 && t < a.V) insert(t, 0x80000000u);
+    }
+    for (int i = threadIdx.x; i < no; i += kOpThreads) {
+        const int t = a.output[(size_t)r * a.ostride + i];
+        if (t >= 0 && t < a.V) insert(t, 1u);
+    }
+    __threadfence();
+    __syncthreads();
+    float* row = logits + (size_t)r * a.lstride;
+    for (int s = threadIdx.x; s < hs; s += kOpThreads) {
+        const uint32_t kk = __hip_atomic_load(&hkey[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!kk) continue;
+        const uint32_t v = __hip_atomic_load(&hval[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int t = (int)kk - 1;
+        row[t] = apply_penalty(row[t], (v >> 31) != 0u, v & 0x7FFFFFFFu, rep, inv_rep, freq, pres);
+    }
+}
+
+// Hash of f(x) over every fp32 x whose order key lies in [klo, khi]; same accumulation as the
+// CPU oracle's checker (sum over inputs of bits(f(x)) * golden ^ bits(x)).
+__global__ __launch_bounds__(256) void selftest_kernel(int fn, uint32_t klo, uint32_t khi,
+                                                       unsigned long long* out) {
+    __shared__ uint64_t red[4][2];
+    uint64_t h = 0, c = 0;
+    const uint64_t n = (uint64_t)khi - klo + 1ull;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const uint32_t key = klo + (uint32_t)i;
+        const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+        const float x = u2f(bits);
+        const float y = fn == 0 ? exp_det(x) : log_det(x);
+        h += ((uint64_t)f2u(y) * 0x9E3779B97F4A7C15ull) ^ (uint64_t)bits;
+        c++;
+    }
+    h = wave_sum_u64(h);
+    c = wave_sum_u64(c);
+    if (lane_id() == 0) { red[threadIdx.x >> 6][0] = h; red[threadIdx.x >> 6][1] = c; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t th = 0, tc = 0;
+        for (int w = 0; w < 4; ++w) { th += red[w][0]; tc += red[w][1]; }
+        atomicAdd(&out[0], (unsigned long long)th);
+        atomicAdd(&out[1], (unsigned long long)tc);
+    }
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+template __global__ void argmax_kernel<float>(const float*, int64_t, int, int32_t*);
+template __global__ void argmax_kernel<uint16_t>(const uint16_t*, int64_t, int, int32_t*);
+template __global__ void softmax_kernel<float>(const float*, int64_t, int, const float*, float*, float*, float*);
+template __global__ void softmax_kernel<uint16_t>(const uint16_t*, int64_t, int, const float*, float*, float*, float*);
+
+}  // namespace vws

@@ -1,0 +1,250 @@
+"""torch-facing wrappers of the gfx950 sampler library (device tensors in, device tensors out).
+
+Every function enqueues work on torch's current HIP stream and returns without synchronising.
+Inputs stay on the GPU; nothing here falls back to a CPU implementation -- if ``_vws.so`` is
+missing or the tensors are not on a ROCm device, the call raises.
+
+Reference interfaces these replace (paths under the vllm_webgpu reference):
+``sample`` <- ``vllm_webgpu/v1/model_runner.py:139-166`` and ``run_inference.py:383-390``;
+``argmax`` <- ``shaders/generic/argmax.wgsl``; ``topk`` <- ``shaders/generic/topk256.wgsl``;
+``softmax`` <- ``shaders/generic/softmax.wgsl``.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_ws_lock = threading.Lock()
+_ws_cache: dict[int, torch.Tensor] = {}
+
+
+def _stream_ptr() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    raise TypeError(f"logits dtype {t.dtype} is not supported (float32 or bfloat16)")
+
+
+def _check_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a ROCm device tensor (got {t.device})")
+
+
+def _row_param(x, B: int, dtype, device, name: str) -> torch.Tensor | None:
+    if x is None:
+        return None
+    if not torch.is_tensor(x):
+        x = torch.full((B,), x, dtype=dtype)
+    x = x.to(device=device, dtype=dtype).contiguous()
+    if x.shape != (B,):
+        raise ValueError(f"{name} must have shape ({B},), got {tuple(x.shape)}")
+    return x
+
+
+def _history(ids, lens, B: int, device, name: str):
+    if ids is None:
+        return None, 0, 0, None
+    ids = ids.to(device=device, dtype=torch.int32)
+    if ids.dim() != 2 or ids.shape[0] != B:
+        raise ValueError(f"{name} must be [B, width] (got {tuple(ids.shape)})")
+    if ids.stride(1) != 1:
+        ids = ids.contiguous()
+    if lens is not None:
+        lens = lens.to(device=device, dtype=torch.int32).contiguous()
+    return ids, ids.stride(0), ids.shape[1], lens
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Per-device scratch buffer, grown on demand and cleared once on the current stream.
+
+    Calls that share a device share this buffer: run them in stream order (one stream), as the
+    sampler kernels leave it clean for the next call but do not guard concurrent use.
+    """
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        ws = _ws_cache.get(idx)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=f"cuda:{idx}")
+            _lib.check(_lib.lib().vws_workspace_init(ws.data_ptr(), ws.numel(), _stream_ptr()))
+            _ws_cache[idx] = ws
+        return ws
+
+
+@dataclass
+class SampleResult:
+    sampled: torch.Tensor                # [B] int32
+    flags: torch.Tensor                  # [B] int32 (VWS_FLAG_* bits; uint32 on the device)
+    num_kept: torch.Tensor               # [B] int32
+    logprob_ids: torch.Tensor | None     # [B, L+1] int32
+    logprob_vals: torch.Tensor | None    # [B, L+1] float32
+    logprob_ranks: torch.Tensor | None   # [B] int32
+
+
+def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p=None,
+           repetition_penalty=None, presence_penalty=None, frequency_penalty=None,
+           prompt_ids=None, prompt_lens=None, output_ids=None, output_lens=None,
+           uniforms: torch.Tensor | None = None, num_logprobs: int | None = None) -> SampleResult:
+    """Samples one token per row of ``logits`` [B, V] (float32 or bfloat16, on the GPU).
+
+    Per-row parameters are scalars or [B] tensors; ``None`` means off (temperature None = every
+    row greedy).  Histories are padded int32 [B, W] (ids outside [0, V) are padding).
+    ``uniforms`` [B, V] float32 in (0, 1) drive the exponential race and are required whenever
+    ``temperature`` is given.
+    """
+    _check_device(logits, "logits")
+    if logits.dim() != 2:
+        raise ValueError("logits must be [B, V]")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    B, V = logits.shape
+    dev = logits.device
+    T = _row_param(temperature, B, torch.float32, dev, "temperature")
+    K = _row_param(top_k, B, torch.int32, dev, "top_k")
+    P = _row_param(top_p, B, torch.float32, dev, "top_p")
+    MP = _row_param(min_p, B, torch.float32, dev, "min_p")
+    R = _row_param(repetition_penalty, B, torch.float32, dev, "repetition_penalty")
+    PR = _row_param(presence_penalty, B, torch.float32, dev, "presence_penalty")
+    FR = _row_param(frequency_penalty, B, torch.float32, dev, "frequency_penalty")
+    pid, pstride, pwidth, plens = _history(prompt_ids, prompt_lens, B, dev, "prompt_ids")
+    oid, ostride, owidth, olens = _history(output_ids, output_lens, B, dev, "output_ids")
+    U = None
+    if uniforms is not None:
+        _check_device(uniforms, "uniforms")
+        U = uniforms if uniforms.dtype == torch.float32 else uniforms.float()
+        if U.stride(1) != 1:
+            U = U.contiguous()
+        if U.shape != (B, V):
+            raise ValueError(f"uniforms must be [{B}, {V}]")
+    sampled = torch.empty(B, dtype=torch.int32, device=dev)
+    flags = torch.empty(B, dtype=torch.int32, device=dev)
+    nkept = torch.empty(B, dtype=torch.int32, device=dev)
+    L = -1 if num_logprobs is None else int(num_logprobs)
+    lp_ids = lp_vals = ranks = None
+    if L >= 0:
+        lp_ids = torch.empty((B, L + 1), dtype=torch.int32, device=dev)
+        lp_vals = torch.empty((B, L + 1), dtype=torch.float32, device=dev)
+        ranks = torch.empty(B, dtype=torch.int32, device=dev)
+    L_lib = _lib.lib()
+    nbytes = L_lib.vws_sample_workspace_size(B, V, pwidth + owidth)
+    ws = workspace(nbytes, dev)
+    a = _lib.SampleArgs()
+    a.struct_size = ctypes.sizeof(_lib.SampleArgs)
+    a.batch, a.vocab, a.dtype = B, V, _dtype_code(logits)
+    a.logits, a.logits_row_stride = logits.data_ptr(), logits.stride(0)
+    a.temperature, a.top_k, a.top_p, a.min_p = _ptr(T), _ptr(K), _ptr(P), _ptr(MP)
+    a.repetition_penalty, a.presence_penalty, a.frequency_penalty = _ptr(R), _ptr(PR), _ptr(FR)
+    a.prompt_ids, a.prompt_row_stride, a.prompt_width, a.prompt_lens = _ptr(pid), pstride, pwidth, _ptr(plens)
+    a.output_ids, a.output_row_stride, a.output_width, a.output_lens = _ptr(oid), ostride, owidth, _ptr(olens)
+    a.uniforms = _ptr(U)
+    a.uniforms_row_stride = U.stride(0) if U is not None else 0
+    a.sampled, a.row_flags, a.num_kept = sampled.data_ptr(), flags.data_ptr(), nkept.data_ptr()
+    a.num_logprobs = L
+    a.logprob_ids, a.logprob_vals, a.logprob_ranks = _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.stream = _stream_ptr()
+    _lib.check(L_lib.vws_sample(ctypes.byref(a)))
+    # keep the argument tensors alive until the work is enqueued (it is, on return)
+    return SampleResult(sampled, flags, nkept, lp_ids, lp_vals, ranks)
+
+
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """[B, V] -> [B] int32 argmax (lowest index on ties, NaN never selected)."""
+    _check_device(logits, "logits")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    B, V = logits.shape
+    out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _lib.check(_lib.lib().vws_argmax(logits.data_ptr(), _dtype_code(logits), B, V, logits.stride(0),
+                                     out.data_ptr(), _stream_ptr()))
+    return out
+
+
+def topk(logits: torch.Tensor, k: int):
+    """[B, V] -> (values [B, k] float32, ids [B, k] int32), ordered (value desc, id asc)."""
+    _check_device(logits, "logits")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    B, V = logits.shape
+    vals = torch.empty((B, k), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((B, k), dtype=torch.int32, device=logits.device)
+    L = _lib.lib()
+    ws = workspace(L.vws_topk_workspace_size(B, V, k), logits.device)
+    _lib.check(L.vws_topk(logits.data_ptr(), _dtype_code(logits), B, V, logits.stride(0), k,
+                          vals.data_ptr(), ids.data_ptr(), ws.data_ptr(), ws.numel(), _stream_ptr()))
+    return vals, ids
+
+
+def softmax(logits: torch.Tensor, temperature=None):
+    """softmax(x / T) per row -> (probs [B, V] f32, row_max [B] f32, log_sum [B] f32)."""
+    _check_device(logits, "logits")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    B, V = logits.shape
+    T = _row_param(temperature, B, torch.float32, logits.device, "temperature")
+    probs = torch.empty((B, V), dtype=torch.float32, device=logits.device)
+    rm = torch.empty(B, dtype=torch.float32, device=logits.device)
+    ls = torch.empty(B, dtype=torch.float32, device=logits.device)
+    _lib.check(_lib.lib().vws_softmax(logits.data_ptr(), _dtype_code(logits), B, V, logits.stride(0),
+                                      _ptr(T), probs.data_ptr(), rm.data_ptr(), ls.data_ptr(),
+                                      _stream_ptr()))
+    return probs, rm, ls
+
+
+def apply_penalties(logits: torch.Tensor, repetition_penalty=None, presence_penalty=None,
+                    frequency_penalty=None, prompt_ids=None, prompt_lens=None, output_ids=None,
+                    output_lens=None) -> torch.Tensor:
+    """In-place vLLM-v1 penalties on float32 logits [B, V]; returns ``logits``."""
+    _check_device(logits, "logits")
+    if logits.dtype != torch.float32 or logits.stride(1) != 1:
+        raise ValueError("apply_penalties needs contiguous-row float32 logits")
+    B, V = logits.shape
+    dev = logits.device
+    R = _row_param(repetition_penalty, B, torch.float32, dev, "repetition_penalty")
+    PR = _row_param(presence_penalty, B, torch.float32, dev, "presence_penalty")
+    FR = _row_param(frequency_penalty, B, torch.float32, dev, "frequency_penalty")
+    pid, pstride, pwidth, plens = _history(prompt_ids, prompt_lens, B, dev, "prompt_ids")
+    oid, ostride, owidth, olens = _history(output_ids, output_lens, B, dev, "output_ids")
+    L = _lib.lib()
+    ws = workspace(L.vws_sample_workspace_size(B, V, pwidth + owidth), dev)
+    _lib.check(L.vws_apply_penalties(logits.data_ptr(), B, V, logits.stride(0), _ptr(R), _ptr(PR),
+                                     _ptr(FR), _ptr(pid), pstride, pwidth, _ptr(plens), _ptr(oid),
+                                     ostride, owidth, _ptr(olens), ws.data_ptr(), ws.numel(),
+                                     _stream_ptr()))
+    return logits
+
+
+def math_selftest(fn: int, key_lo: int, key_hi: int) -> tuple[int, int]:
+    """Device hash of exp_det (fn=0) or log_det (fn=1) over an order-key range; synchronises."""
+    out = torch.zeros(2, dtype=torch.int64, device="cuda")
+    _lib.check(_lib.lib().vws_math_selftest(fn, key_lo, key_hi, out.data_ptr(), _stream_ptr()))
+    h, c = out.cpu().tolist()
+    return h & (2**64 - 1), c
+
+
+def profile_begin(max_launches: int) -> None:
+    """Records a hipEvent pair around each of the next ``max_launches`` library kernel launches."""
+    _lib.check(_lib.lib().vws_profile_begin(max_launches))
+
+
+def profile_end() -> dict:
+    """Waits for the recorded events; returns {kind: (total_ms, launches)} and stops recording."""
+    n = len(_lib.KERNEL_KINDS)
+    ms = (ctypes.c_double * n)()
+    cnt = (ctypes.c_int32 * n)()
+    _lib.check(_lib.lib().vws_profile_end(ctypes.cast(ms, ctypes.c_void_p),
+                                          ctypes.cast(cnt, ctypes.c_void_p)))
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(_lib.KERNEL_KINDS) if cnt[i]}
