@@ -1,0 +1,139 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point that
+``include/vws_sampler.h`` declares, reports its ABI version and workspace sizes, and its host
+argument validation returns the documented status codes.  No compute call is made here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from vllm_webgpu_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vws_sampler.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(_lib.LIB_PATH):
+        subprocess.run(["make", "-s", "-j4", "-C", os.path.join(ROOT, "vllm_webgpu_amd", "csrc")],
+                       check=True)
+    return _lib.lib()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(vws_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.EXPORTED)
+
+
+def test_exports_every_declared_symbol(L):
+    for name in _declared():
+        assert getattr(L, name) is not None, name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (vws_\w+)", out))
+    assert set(_declared()) <= exported
+
+
+def test_abi_constants_match_header(L):
+    text = open(HEADER).read()
+
+    def define(name):
+        body = re.search(rf"#define {name}\s+([^/\n]+)", text).group(1).strip()
+        m = re.fullmatch(r"\(\s*(\d+)\s*<<\s*(\d+)\s*\)", body)
+        return (int(m.group(1)) << int(m.group(2))) if m else int(body.rstrip("u"), 0)
+
+    assert L.vws_abi_version() == _lib.ABI_VERSION == define("VWS_ABI_VERSION")
+    assert define("VWS_ERR_INVALID_ARGUMENT") == _lib.ERR_INVALID_ARGUMENT
+    assert define("VWS_ERR_UNSUPPORTED_DTYPE") == _lib.ERR_UNSUPPORTED_DTYPE
+    assert define("VWS_ERR_WORKSPACE_TOO_SMALL") == _lib.ERR_WORKSPACE_TOO_SMALL
+    assert define("VWS_ERR_LIMIT") == _lib.ERR_LIMIT
+    assert define("VWS_MAX_VOCAB") == _lib.MAX_VOCAB
+    assert define("VWS_MAX_LOGPROBS") == _lib.MAX_LOGPROBS
+
+
+def test_workspace_sizes(L):
+    a = L.vws_sample_workspace_size(256, 128256, 512)
+    b = L.vws_sample_workspace_size(256, 128256, 0)
+    assert a > b > 0 and a % 256 == 0 and b % 256 == 0
+    assert L.vws_sample_workspace_size(512, 128256, 0) > b
+    assert L.vws_sample_workspace_size(0, 100, 0) == 0
+    assert L.vws_sample_workspace_size(4, 100, -1) == 0
+    assert L.vws_topk_workspace_size(8, 1000, 50) > 0
+
+
+FAKE = 0x10000          # host-side stand-in addresses: validation never dereferences them
+
+
+def _args(L, **over):
+    a = _lib.SampleArgs()
+    a.struct_size = ctypes.sizeof(_lib.SampleArgs)
+    a.batch, a.vocab, a.dtype = 4, 1000, _lib.DTYPE_F32
+    a.logits, a.logits_row_stride = FAKE, 1000
+    a.temperature = FAKE
+    a.uniforms, a.uniforms_row_stride = FAKE, 1000
+    a.sampled = FAKE
+    a.num_logprobs = -1
+    a.workspace = 0x100000
+    a.workspace_bytes = L.vws_sample_workspace_size(4, 1000, 0)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def _status(L, a):
+    return L.vws_validate_sample_args(ctypes.byref(a))
+
+
+def test_valid_args_pass(L):
+    assert _status(L, _args(L)) == _lib.OK
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(logits=None), _lib.ERR_INVALID_ARGUMENT, "logits is NULL"),
+    (dict(batch=0), _lib.ERR_INVALID_ARGUMENT, "batch"),
+    (dict(vocab=0), _lib.ERR_LIMIT, "vocab"),
+    (dict(vocab=(1 << 19) + 1, logits_row_stride=(1 << 19) + 1), _lib.ERR_LIMIT, "vocab"),
+    (dict(dtype=7), _lib.ERR_UNSUPPORTED_DTYPE, "dtype"),
+    (dict(logits_row_stride=999), _lib.ERR_INVALID_ARGUMENT, "stride"),
+    (dict(sampled=None), _lib.ERR_INVALID_ARGUMENT, "sampled"),
+    (dict(uniforms=None), _lib.ERR_INVALID_ARGUMENT, "uniforms"),
+    (dict(uniforms_row_stride=10), _lib.ERR_INVALID_ARGUMENT, "uniforms_row_stride"),
+    (dict(num_logprobs=65), _lib.ERR_LIMIT, "num_logprobs"),
+    (dict(num_logprobs=-2), _lib.ERR_LIMIT, "num_logprobs"),
+    (dict(num_logprobs=5), _lib.ERR_INVALID_ARGUMENT, "logprob outputs"),
+    (dict(prompt_ids=FAKE, prompt_width=-1), _lib.ERR_INVALID_ARGUMENT, "prompt_width"),
+    (dict(output_ids=FAKE, output_width=8, output_row_stride=4), _lib.ERR_INVALID_ARGUMENT,
+     "output_row_stride"),
+    (dict(workspace=None), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+    (dict(workspace_bytes=256), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+    (dict(workspace=0x100010), _lib.ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(struct_size=8), _lib.ERR_INVALID_ARGUMENT, "struct_size"),
+])
+def test_invalid_args_rejected(L, over, code, msg):
+    assert _status(L, _args(L, **over)) == code
+    assert msg in _lib.last_error()
+
+
+def test_history_grows_the_required_workspace(L):
+    a = _args(L, output_ids=FAKE, output_width=512, output_row_stride=512)
+    assert _status(L, a) == _lib.ERR_WORKSPACE_TOO_SMALL
+    a.workspace_bytes = L.vws_sample_workspace_size(4, 1000, 512)
+    assert _status(L, a) == _lib.OK
+
+
+def test_greedy_batches_need_no_uniforms(L):
+    assert _status(L, _args(L, temperature=None, uniforms=None)) == _lib.OK
+
+
+def test_errors_raise_with_library_text(L):
+    assert _status(L, _args(L, dtype=9)) != 0
+    with pytest.raises(_lib.VwsError, match="unsupported logits dtype 9"):
+        _lib.check(_lib.ERR_UNSUPPORTED_DTYPE)
