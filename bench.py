@@ -88,8 +88,8 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--sets", type=int, default=3, help="rotated input sets (MALL defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=128)
-    ap.add_argument("--cpu-iters", type=int, default=10)
+    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--cpu-iters", type=int, default=30)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 512 MiB device copy (for PMC byte-counter calibration)")
     args = ap.parse_args()
