@@ -160,8 +160,8 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
  * (on any stream) record a hipEvent pair around themselves; vws_profile_end() waits for those
  * events, writes the summed milliseconds and launch counts per kernel kind into
  * ms[VWS_KERNEL_KINDS] / count[VWS_KERNEL_KINDS] and turns recording off. */
-#define VWS_KERNEL_FAST 0      /* single-pass split-row sampler (also the topk operation) */
-#define VWS_KERNEL_GENERAL 1   /* multi-pass sampler */
+#define VWS_KERNEL_SAMPLE 0    /* the sampling kernel of vws_sample (one workgroup per row) */
+#define VWS_KERNEL_TOPK 1      /* the kernels of vws_topk */
 #define VWS_KERNEL_ARGMAX 2
 #define VWS_KERNEL_SOFTMAX 3
 #define VWS_KERNEL_PENALTIES 4

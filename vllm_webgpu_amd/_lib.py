@@ -42,7 +42,7 @@ EXPORTED = (
     "vws_profile_begin", "vws_profile_end",
 )
 
-KERNEL_KINDS = ("fast", "general", "argmax", "softmax", "penalties", "other")
+KERNEL_KINDS = ("sample", "topk", "argmax", "softmax", "penalties", "other")
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

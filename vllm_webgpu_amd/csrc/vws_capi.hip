@@ -14,6 +14,7 @@
 namespace vws {
 template <typename T> __global__ void fast_kernel(KArgs);
 template <typename T> __global__ void general_kernel(KArgs);
+template <typename T> __global__ void row_kernel(KArgs);
 template <typename T> __global__ void argmax_kernel(const T*, int64_t, int, int32_t*);
 template <typename T>
 __global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, float*, float*);
@@ -248,25 +249,14 @@ int vws_sample(const vws_sample_args* a) {
     k.lp_vals = a->logprob_vals;
     k.lp_ranks = a->logprob_ranks;
     k.mode = kModeSample;
-    choose_parts(a->batch, a->vocab, esize_of(a->dtype), &k.S, &k.part_len);
     hipStream_t s = (hipStream_t)a->stream;
-    const int bp = (a->batch + 7) / 8 * 8;
-    if (a->num_logprobs < 0) {
-        const int ps = prof_start(s, VWS_KERNEL_FAST);
-        if (a->dtype == VWS_DTYPE_F32)
-            hipLaunchKernelGGL(fast_kernel<float>, dim3(bp * k.S), dim3(kFastThreads), 0, s, k);
-        else
-            hipLaunchKernelGGL(fast_kernel<uint16_t>, dim3(bp * k.S), dim3(kFastThreads), 0, s, k);
-        prof_stop(s, ps);
-        if ((st = check_launch("vws_sample (single-pass kernel)"))) return st;
-    }
-    const int pg = prof_start(s, VWS_KERNEL_GENERAL);
+    const int ps = prof_start(s, VWS_KERNEL_SAMPLE);
     if (a->dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(general_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
+        hipLaunchKernelGGL(row_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
     else
-        hipLaunchKernelGGL(general_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
-    prof_stop(s, pg);
-    if ((st = check_launch("vws_sample (general kernel)"))) return st;
+        hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
+    prof_stop(s, ps);
+    if ((st = check_launch("vws_sample"))) return st;
     return ok();
 }
 
@@ -311,7 +301,7 @@ int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, in
     choose_parts(batch, vocab, esize_of(dtype), &ka.S, &ka.part_len);
     hipStream_t s = (hipStream_t)stream;
     const int bp = (batch + 7) / 8 * 8;
-    const int ps = prof_start(s, VWS_KERNEL_FAST);
+    const int ps = prof_start(s, VWS_KERNEL_TOPK);
     if (dtype == VWS_DTYPE_F32)
         hipLaunchKernelGGL(fast_kernel<float>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
     else
@@ -319,7 +309,7 @@ int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, in
     prof_stop(s, ps);
     if ((st = check_launch("vws_topk"))) return st;
     // rows whose single-pass candidate lists overflowed (ties) are finished exactly here
-    const int pg = prof_start(s, VWS_KERNEL_GENERAL);
+    const int pg = prof_start(s, VWS_KERNEL_TOPK);
     if (dtype == VWS_DTYPE_F32)
         hipLaunchKernelGGL(general_kernel<float>, dim3(batch), dim3(kGenThreads), 0, s, ka);
     else

@@ -256,6 +256,24 @@ __device__ __forceinline__ uint32_t wave_kth_largest_256(uint32_t v0, uint32_t v
     return sel == 0 ? r0 : sel == 1 ? r1 : sel == 2 ? r2 : r3;
 }
 
+// One key per lane sorted descending across the wave (bitonic network): lane i gets the i-th
+// largest key.
+__device__ __forceinline__ uint32_t wave_sort_desc64(uint32_t v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint32_t o = __shfl_xor(v, stride, kWave);
+            const bool desc = (lane & size) == 0;
+            const bool upper = (lane & stride) != 0;
+            const uint32_t hi = v > o ? v : o, lo = v > o ? o : v;
+            v = (upper != desc) ? hi : lo;
+        }
+    }
+    return v;
+}
+
 // Number of keys >= t among keys[0..n) (one whole wave).
 __device__ __forceinline__ int wave_count_ge(const uint32_t* keys, int n, uint32_t t) {
     int c = 0;

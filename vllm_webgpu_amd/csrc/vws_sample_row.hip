@@ -1,0 +1,669 @@
+// vws_sample_row.hip -- the sampling kernel: one workgroup of 1024 threads per row.
+//
+// Greedy rows and top-k rows (k <= 256) are finished in one streaming pass over the row:
+//   1. the history ids are loaded, then the first two iterations of logits (8 x 16-byte loads
+//      per lane each) are put in flight;
+//   2. the history goes into an LDS hash (count, prompt flag);
+//   3. a threshold is seeded from the first iteration: the lane maxima of its 32 values are
+//      sorted per wave, the 16 largest of every wave are pooled and the m-th largest of the
+//      pool (m = 3k x the sampled fraction of the row) becomes the starting threshold;
+//   4. the row is streamed once, double-buffered; an element at or above the threshold goes to
+//      its wave's LDS candidate buffer (history tokens are penalised on the spot when no penalty
+//      can raise a logit; otherwise their penalised values are gathered up front and their
+//      stream positions skipped).  A full buffer is cut to its exact top-k by a radix select,
+//      which raises the threshold for every wave;
+//   5. the k-th largest candidate is selected.  It is exact when every element at or above it
+//      was kept, i.e. when it is not below any threshold used; a seeded pass that fails this
+//      check is streamed again without the seed;
+//   6. survivors of temperature, top-k and min-p get their exact integer masses and race keys
+//      (uniforms are fetched for the candidates while the k-th value is selected); top-p is
+//      cut on the exact prefix sums and the race is reduced across the survivors.
+// Every other row (top-k off or k > 256, logprobs requested, candidate or hash overflow,
+// degenerate maxima, temperature ties across a threshold) runs the multi-pass path of
+// vws_general.h in the same workgroup, so one launch serves the whole batch.
+#include "vws_general.h"
+
+namespace vws {
+
+constexpr int kRowThreads = kGenThreads;     // 1024
+constexpr int kRowWaves = kGenWaves;         // 16
+constexpr int kRowCap = 512;                 // candidate slots per wave
+constexpr int kRowHash = 2048;               // history hash slots
+constexpr int kRowHashFill = 1536;           // unique history tokens served in LDS
+constexpr int kRowKeep = 256;                // survivors finished here
+constexpr int kSeedPerWave = 16;             // lane maxima each wave contributes to the seed pool
+
+struct RowSmem {
+    uint32_t ckey[kRowWaves][kRowCap];
+    int32_t cidx[kRowWaves][kRowCap];
+    uint32_t rhist[kRowWaves][256];          // per-wave radix-select scratch
+    uint32_t hkey[kRowHash];                 // history token + 1 (0 = empty)
+    uint32_t hval[kRowHash];                 // output count | prompt flag << 31
+    float hpen[kRowHash];                    // penalised value (gather mode)
+    uint64_t sck[kRowKeep];                  // survivors: key(y) << 32 | index
+    uint64_t sw[kRowKeep];                   // exact mass
+    float srk[kRowKeep];                     // race key
+    uint32_t seedk[kRowWaves * kSeedPerWave];
+    uint64_t red[kRowWaves][8];
+    int cnt[kRowWaves];
+    uint32_t tauw[kRowWaves];
+    uint32_t tau, status, nhash, nkeep;
+    uint32_t bc[8];
+};
+
+union RowShared {
+    GenSmem g;
+    RowSmem f;
+};
+
+__device__ __forceinline__ uint32_t rhash_slot(int t) {
+    return ((uint32_t)t * 2654435761u) >> (32 - 11);  // kRowHash = 2048
+}
+
+__device__ __forceinline__ void rhash_insert(RowSmem& sm, int t, uint32_t inc) {
+    uint32_t s = rhash_slot(t);
+    for (int probe = 0; probe < kRowHash; ++probe) {
+        const uint32_t prev = atomicCAS(&sm.hkey[s], 0u, (uint32_t)t + 1u);
+        if (prev == 0u && atomicAdd(&sm.nhash, 1u) >= (uint32_t)kRowHashFill) atomicOr(&sm.status, 1u);
+        if (prev == 0u || prev == (uint32_t)t + 1u) {
+            if (inc & 0x80000000u) atomicOr(&sm.hval[s], 0x80000000u);
+            else atomicAdd(&sm.hval[s], inc);
+            return;
+        }
+        s = (s + 1u) & (kRowHash - 1);
+    }
+    atomicOr(&sm.status, 1u);
+}
+
+// count | prompt << 31 of history token t, 0 when absent
+__device__ __forceinline__ uint32_t rhash_value(const RowSmem& sm, int t) {
+    uint32_t s = rhash_slot(t);
+    for (int probe = 0; probe < kRowHash; ++probe) {
+        const uint32_t k = sm.hkey[s];
+        if (k == (uint32_t)t + 1u) return sm.hval[s];
+        if (k == 0u) return 0u;
+        s = (s + 1u) & (kRowHash - 1);
+    }
+    return 0u;
+}
+
+// The race over the kept survivors and the diagnostics of the top-p cut.
+struct RowRace {
+    uint64_t best = 0;     // (key bits << 32) | (0x7FFFFFFF - index), 0 = none
+    uint64_t last = 0;     // max (key(y) << 32 | index) over kept survivors
+    uint64_t cprev = 0;    // largest cumulative mass among removed survivors
+    uint64_t cat = ~0ull;  // smallest cumulative mass among kept survivors
+    uint32_t second = 0;   // key bits + 1 of the best non-winning key, 0 = none
+    uint32_t nkept = 0;
+    __device__ __forceinline__ void add_key(float key, int idx) {
+        if (!(key >= 0.0f)) return;  // NaN keys never win
+        const uint64_t pk = ((uint64_t)f2u(key) << 32) | (uint32_t)(0x7FFFFFFF - idx);
+        if (pk > best) {
+            if (best) { const uint32_t o = (uint32_t)(best >> 32) + 1u; second = second > o ? second : o; }
+            best = pk;
+        } else {
+            const uint32_t o = f2u(key) + 1u;
+            second = second > o ? second : o;
+        }
+    }
+    __device__ __forceinline__ void merge(const RowRace& o) {
+        const uint64_t hi = best > o.best ? best : o.best;
+        const uint64_t lo = best > o.best ? o.best : best;
+        const uint32_t l = lo ? (uint32_t)(lo >> 32) + 1u : 0u;
+        second = second > o.second ? second : o.second;
+        second = second > l ? second : l;
+        best = hi;
+        last = last > o.last ? last : o.last;
+        cprev = cprev > o.cprev ? cprev : o.cprev;
+        cat = cat < o.cat ? cat : o.cat;
+        nkept += o.nkept;
+    }
+    __device__ __forceinline__ void shfl_merge(int off) {
+        RowRace o;
+        o.best = __shfl_xor(best, off, kWave);
+        o.last = __shfl_xor(last, off, kWave);
+        o.cprev = __shfl_xor(cprev, off, kWave);
+        o.cat = __shfl_xor(cat, off, kWave);
+        o.second = __shfl_xor(second, off, kWave);
+        o.nkept = __shfl_xor(nkept, off, kWave);
+        merge(o);
+    }
+};
+
+// Position of candidate t in the per-wave buffers (w < 0 when t is past the end).
+__device__ __forceinline__ void cand_locate(const RowSmem& sm, int t, int& w, int& e) {
+    w = -1;
+    e = 0;
+    int off = 0;
+#pragma unroll
+    for (int i = 0; i < kRowWaves; ++i) {
+        const int c = sm.cnt[i];
+        if (w < 0 && t < off + c) { w = i; e = t - off; }
+        off += c;
+    }
+}
+
+// LDS of the row kernel: the single-pass state and the general path's state share it.
+__shared__ RowShared g_row_sh;
+
+// Cuts wave w's candidate buffer (cnt entries) to its exact top-k, all ties included, in place,
+// and raises the shared threshold to the k-th key.  Returns (k-th key << 32) | new count.
+// Compaction is rare, so it lives out of line and the unrolled streaming loop stays small.
+__device__ __noinline__ uint64_t row_compact(int w, int cnt, int k) {
+    RowSmem& sm = g_row_sh.f;
+    uint32_t* ck = sm.ckey[w];
+    int32_t* ci = sm.cidx[w];
+    const int lane = lane_id();
+    const uint32_t kth = wave_kth_largest(ck, cnt, k, sm.rhist[w]);
+    int out = 0;
+    for (int base = 0; base < cnt; base += kWave) {
+        const int i = base + lane;
+        bool keep = false;
+        uint32_t kk = 0;
+        int32_t ii = 0;
+        if (i < cnt) { kk = ck[i]; ii = ci[i]; keep = kk >= kth; }
+        const uint64_t bal = __ballot(keep);
+        if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
+        out += __popcll(bal);
+        wave_sync();
+    }
+    if (lane == 0) atomicMax(&sm.tau, kth);
+    wave_sync();
+    return ((uint64_t)kth << 32) | (uint32_t)out;
+}
+
+// Per-wave candidate buffer of the row kernel: every element of the wave's share at or above
+// the wave's threshold; the threshold only rises (own compactions, other waves' via sm.tau).
+struct RowCand {
+    int w, k, cnt;        // wave-uniform
+    uint32_t tau;         // threshold key
+    float tauf;           // its value form (-inf when every non-NaN value passes)
+    bool ovf;             // ties overflowed the buffer
+    __device__ __forceinline__ void init(int w_, int k_) {
+        w = w_; k = k_; cnt = 0; tau = 0u; tauf = -__builtin_inff(); ovf = false;
+    }
+    __device__ __forceinline__ void set_tau(uint32_t t) {
+        if (t > tau) {
+            tau = t;
+            tauf = (tau > 0x007FFFFFu) ? val_of(tau) : -__builtin_inff();
+        }
+    }
+    __device__ __forceinline__ void refresh() {
+        set_tau(__builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(&g_row_sh.f.tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)));
+    }
+    // Appends (kk, idx) from the lanes where c holds; wave-uniform call.
+    __device__ __forceinline__ void append(bool c, uint32_t kk, int32_t idx) {
+        uint64_t bal = __ballot(c);
+        if (!bal || ovf) return;
+        int n = __popcll(bal);
+        if (cnt + n > kRowCap) {
+            const uint64_t rc = row_compact(w, cnt, k);
+            cnt = __builtin_amdgcn_readfirstlane((uint32_t)rc);
+            set_tau(__builtin_amdgcn_readfirstlane((uint32_t)(rc >> 32)));
+            c = c && kk >= tau;
+            bal = __ballot(c);
+            n = __popcll(bal);
+            if (cnt + n > kRowCap) { ovf = true; return; }
+        }
+        if (c) {
+            const int pos = cnt + lane_prefix(bal);
+            g_row_sh.f.ckey[w][pos] = kk;
+            g_row_sh.f.cidx[w][pos] = idx;
+        }
+        cnt += n;
+        wave_sync();
+    }
+};
+
+// Serves greedy and top-k rows; returns false when the row must take the general path (nothing
+// has been written for it then).
+// Defaults read in place of a missing per-row parameter array, so every parameter is one
+// unconditional scalar load: T, top_p, min_p, repetition, presence, frequency.
+__device__ float kRowDefaultsF[8] = {0.0f, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+// top_k (0 = off), and a length that clamps to the history width (absent lengths = full width)
+__device__ int32_t kRowDefaultsI[4] = {0, 0x7FFFFFFF, 0, 0};
+// Stand-in source for loads that have nothing to read (no history, no aligned body).  These
+// arrays are never written; they are not const so that they live in the global address space,
+// like the arrays they stand in for, and selecting between the two keeps global loads.
+__device__ uint4 kRowDummy[4] = {};
+
+// Per-row parameters, all issued as scalar loads before the first one is used.  Scalar loads
+// complete on their own counter, so waiting for them never waits for the logits in flight.
+__device__ __forceinline__ RowP row_params_scalar(const KArgs& a, int r) {
+    const float* pT = a.temperature ? a.temperature + r : &kRowDefaultsF[0];
+    const float* pP = a.top_p ? a.top_p + r : &kRowDefaultsF[1];
+    const float* pM = a.min_p ? a.min_p + r : &kRowDefaultsF[2];
+    const float* pR = a.rep ? a.rep + r : &kRowDefaultsF[3];
+    const float* pS = a.pres ? a.pres + r : &kRowDefaultsF[4];
+    const float* pF = a.freq ? a.freq + r : &kRowDefaultsF[5];
+    const int32_t* pK = a.top_k ? a.top_k + r : &kRowDefaultsI[0];
+    const int32_t* pPL = a.plens ? a.plens + r : &kRowDefaultsI[1];
+    const int32_t* pOL = a.olens ? a.olens + r : &kRowDefaultsI[1];
+    RowP p;
+    int pl, ol;
+    // scalar loads on the scalar counter; the compiler would otherwise issue vector loads, and
+    // waiting for those would also wait for every logits load issued before them
+    asm volatile(
+        "s_load_dword %0, %9, 0x0\n\t"
+        "s_load_dword %1, %10, 0x0\n\t"
+        "s_load_dword %2, %11, 0x0\n\t"
+        "s_load_dword %3, %12, 0x0\n\t"
+        "s_load_dword %4, %13, 0x0\n\t"
+        "s_load_dword %5, %14, 0x0\n\t"
+        "s_load_dword %6, %15, 0x0\n\t"
+        "s_load_dword %7, %16, 0x0\n\t"
+        "s_load_dword %8, %17, 0x0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(p.T), "=&s"(p.top_p), "=&s"(p.min_p), "=&s"(p.rep), "=&s"(p.pres), "=&s"(p.freq),
+          "=&s"(p.k), "=&s"(pl), "=&s"(ol)
+        : "s"(pT), "s"(pP), "s"(pM), "s"(pR), "s"(pS), "s"(pF), "s"(pK), "s"(pPL), "s"(pOL)
+        : "memory");
+    p.greedy = is_greedy(p.T);
+    p.inv_rep = 1.0f / p.rep;
+    p.np = a.prompt ? min(max(pl, 0), a.pwidth) : 0;
+    p.no = a.output ? min(max(ol, 0), a.owidth) : 0;
+    const bool identity = (p.rep == 1.0f && p.pres == 0.0f && p.freq == 0.0f);
+    p.has_hist = (p.np > 0 || p.no > 0) && !identity;
+    return p;
+}
+
+// Serves greedy and top-k rows; returns false when the row must take the general path (nothing
+// has been written for it then).
+template <typename T>
+__device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
+    constexpr int NT = kRowThreads;
+    constexpr int VEC = Elem<T>::kVec;
+    constexpr int U = 32 / VEC;  // 16-byte loads in flight per lane per iteration
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int V = a.V;
+    const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+
+    // 1. loads in the order they are consumed, none behind a branch (a load that only some
+    //    paths issue makes the wait for everything before it conservative):
+    //    history ids (clamped to the row width), the first two iterations of logits, then the
+    //    parameters as scalar loads.
+    const int32_t* prow = (a.prompt && a.pwidth > 0) ? a.prompt + (size_t)r * a.pstride
+                                                     : reinterpret_cast<const int32_t*>(kRowDummy);
+    const int32_t* orow = (a.output && a.owidth > 0) ? a.output + (size_t)r * a.ostride
+                                                     : reinterpret_cast<const int32_t*>(kRowDummy);
+    const int hp_raw = prow[(a.prompt && a.pwidth > 0) ? min(tid, a.pwidth - 1) : 0];
+    const int ho_raw = orow[(a.output && a.owidth > 0) ? min(tid, a.owidth - 1) : 0];
+    Slice<T> sl;
+    sl.init(row, 0, V);
+    const int nbody = sl.nbody;
+    const int nit = (nbody + NT * U - 1) / (NT * U);
+    const T* body = nbody > 0 ? row + sl.a : reinterpret_cast<const T*>(kRowDummy);
+    const int vlast = nbody > 0 ? nbody - 1 : 0;
+    float A[U][VEC], Bq[U][VEC];
+    // vectors past the body repeat the last one; consumers skip them (vi >= nbody)
+    auto load_iter = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const int vi = (it * U + q) * NT + tid;
+            Elem<T>::load_vec(body + (size_t)min(vi, vlast) * VEC, buf[q]);
+        }
+    };
+    load_iter(A, 0);
+    load_iter(Bq, 1);
+    const RowP prm = row_params_scalar(a, r);
+    const int k = fast_k(a, prm);
+    if (k == 0) return false;
+    const bool hh = prm.has_hist;
+    // penalties that never raise a logit let history candidates be found by their raw value
+    const bool mono = prm.rep >= 1.0f && prm.pres >= 0.0f && prm.freq >= 0.0f;
+    const bool gather = hh && !mono;
+    const int32_t* pr = hh && prm.np > 0 ? prow : nullptr;
+    const int32_t* ou = hh && prm.no > 0 ? orow : nullptr;
+
+    // 2. LDS state and the history hash
+    if (tid == 0) { sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
+    if (hh) {
+        for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
+    }
+    __syncthreads();
+    if (hh) {
+        if (tid < prm.np && hp_raw >= 0 && hp_raw < V) rhash_insert(sm, hp_raw, 0x80000000u);
+        if (tid < prm.no && ho_raw >= 0 && ho_raw < V) rhash_insert(sm, ho_raw, 1u);
+        if (pr) {
+            for (int i = NT + tid; i < prm.np; i += NT) {
+                const int t = pr[i];
+                if (t >= 0 && t < V) rhash_insert(sm, t, 0x80000000u);
+            }
+        }
+        if (ou) {
+            for (int i = NT + tid; i < prm.no; i += NT) {
+                const int t = ou[i];
+                if (t >= 0 && t < V) rhash_insert(sm, t, 1u);
+            }
+        }
+    }
+
+    // 3. seed threshold from the first iteration
+    const int sample = nbody > 0 ? min(NT * U, nbody) * VEC : 0;
+    const int m_seed = sample > 0 ? (int)(((int64_t)3 * k * sample + V - 1) / V) : 0;
+    const bool seeded = sample > 0 && m_seed <= kRowWaves * kSeedPerWave;
+    if (seeded) {
+        float mx = __builtin_nanf("");  // fmaxf ignores NaN; clamped duplicate loads are skipped
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const bool ok = q * NT + tid < nbody;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) mx = ok ? fmaxf(mx, A[q][j]) : mx;
+        }
+        const uint32_t sk = wave_sort_desc64(key_of(mx));
+        if (lane < kSeedPerWave) sm.seedk[wave * kSeedPerWave + lane] = sk;
+    }
+    __syncthreads();  // also publishes the hash
+    if (seeded && wave == 0) {
+        const uint32_t t0 = wave_kth_largest_256(sm.seedk[4 * lane], sm.seedk[4 * lane + 1],
+                                                 sm.seedk[4 * lane + 2], sm.seedk[4 * lane + 3], m_seed);
+        if (lane == 0) sm.bc[0] = t0;
+    }
+    if (gather && sm.status == 0u) {
+        for (int s = tid; s < kRowHash; s += NT) {
+            const uint32_t kk = sm.hkey[s];
+            if (kk) {
+                const uint32_t v = sm.hval[s];
+                sm.hpen[s] = apply_penalty(Elem<T>::load1(row + (kk - 1u)), (v >> 31) != 0u,
+                                           v & 0x7FFFFFFFu, prm.rep, prm.inv_rep, prm.freq, prm.pres);
+            }
+        }
+    }
+    __syncthreads();
+    if (sm.status != 0u) return false;
+    uint32_t seed = seeded ? sm.bc[0] : 0u;
+
+    // 4. stream; 5. the k-th largest candidate, checked against every threshold used.  A seeded
+    //    pass whose k-th candidate lies below a threshold is streamed again without the seed.
+    RowCand cb;
+    auto slot = [&](float v, int idx, bool valid) __attribute__((always_inline)) {
+        bool c = valid && v >= cb.tauf;
+        if (__ballot(c) == 0ull) return;
+        if (hh && c) {
+            const uint32_t hv = rhash_value(sm, idx);
+            if (hv != 0u) {
+                if (gather) {
+                    c = false;
+                } else {
+                    v = apply_penalty(v, (hv >> 31) != 0u, hv & 0x7FFFFFFFu, prm.rep, prm.inv_rep,
+                                      prm.freq, prm.pres);
+                    c = v >= cb.tauf;
+                }
+            }
+        }
+        cb.append(c, key_of(v), idx);
+    };
+    auto examine = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
+        cb.refresh();
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const int vi = (it * U + q) * NT + tid;
+            const int i0 = sl.a + vi * VEC;
+            const bool ok = vi < nbody;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) slot(buf[q][j], i0 + j, ok);
+        }
+    };
+    const bool sampling = !prm.greedy;
+    float ureg = 0.5f;
+    uint32_t kth = 0, mk = 0, tmax = 0;
+    int total = 0;
+    for (int attempt = 0;; ++attempt) {
+        if (attempt > 0) {
+            __syncthreads();
+            if (tid == 0) sm.tau = 0u;
+            __syncthreads();
+            load_iter(A, 0);
+            load_iter(Bq, 1);
+        }
+        cb.init(wave, k);
+        cb.set_tau(seed);
+        if (gather) {
+            constexpr int per = kRowHash / kRowWaves;
+            for (int s0 = wave * per; s0 < (wave + 1) * per; s0 += kWave) {
+                const int s = s0 + lane;
+                const uint32_t kk = sm.hkey[s];
+                const uint32_t pk = kk ? key_of(sm.hpen[s]) : 0u;
+                cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)kk - 1);
+            }
+        }
+        {   // unaligned head (thread 0) and tail (thread 1): fewer than 2 vectors in total
+            float v[VEC];
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
+            int i0 = 0;
+            if (tid <= 1) i0 = sl.load_edge(tid, v);
+            const int end = tid == 0 ? sl.a : V;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) slot(v[j], i0 + j, tid <= 1 && i0 + j < end);
+        }
+        for (int it = 0; it < nit && !cb.ovf; it += 2) {
+            examine(A, it);
+            load_iter(A, it + 2);
+            if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
+            load_iter(Bq, it + 3);
+        }
+
+        if (lane == 0) { sm.cnt[wave] = cb.ovf ? (1 << 28) : cb.cnt; sm.tauw[wave] = cb.tau; }
+        if (tid == 0) { sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
+        __syncthreads();
+        total = 0;
+        tmax = seed;
+#pragma unroll
+        for (int w = 0; w < kRowWaves; ++w) {
+            total += sm.cnt[w];
+            tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
+        }
+        if (total >= (1 << 28)) return false;  // ties overflowed a buffer
+        // the uniform of candidate tid is in flight while the k-th value is found
+        int cw, ce;
+        cand_locate(sm, tid, cw, ce);
+        uint32_t ck = 0;
+        if (cw >= 0) {
+            ck = sm.ckey[cw][ce];
+            if (sampling) ureg = a.u[(size_t)r * a.ustride + sm.cidx[cw][ce]];
+        }
+        uint32_t mxw = ck;
+        for (int t = NT + tid; t < total; t += NT) {
+            int w2, e2;
+            cand_locate(sm, t, w2, e2);
+            const uint32_t c2 = sm.ckey[w2][e2];
+            mxw = mxw > c2 ? mxw : c2;
+        }
+        mxw = wave_max_u32(mxw);
+        if (lane == 0) atomicMax(&sm.bc[2], mxw);
+        if (wave == 0) {
+            uint32_t kk = 0;
+            if (total >= k) {
+                if (total <= 256) {
+                    uint32_t v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        int w2, e2;
+                        cand_locate(sm, 4 * lane + i, w2, e2);
+                        v[i] = w2 >= 0 ? sm.ckey[w2][e2] : 0u;
+                    }
+                    kk = wave_kth_largest_256(v[0], v[1], v[2], v[3], k);
+                } else {
+                    kk = wave_kth_largest_multi(&sm.ckey[0][0], kRowCap, sm.cnt, kRowWaves, k, sm.rhist[0]);
+                }
+            }
+            if (lane == 0) sm.bc[1] = kk;
+        }
+        __syncthreads();
+        kth = sm.bc[1];
+        mk = sm.bc[2];
+        const bool seeded_run = seed != 0u;
+        const bool exact = seeded_run ? (total >= k && kth >= tmax) : (kth == 0u || kth >= tmax);
+        if (exact) break;
+        if (!seeded_run || attempt > 0) return false;
+        seed = 0u;
+    }
+
+    if (!sampling) {
+        // greedy: lowest index at the maximum of the penalised logits (0 when every value is NaN)
+        int best = 0x7FFFFFFF;
+        for (int t = tid; t < total; t += NT) {
+            int w2, e2;
+            cand_locate(sm, t, w2, e2);
+            if (sm.ckey[w2][e2] == mk && sm.cidx[w2][e2] < best) best = sm.cidx[w2][e2];
+        }
+        best = (int)wave_min_u32((uint32_t)best);
+        if (lane == 0) atomicMin(&sm.bc[3], (uint32_t)best);
+        __syncthreads();
+        if (tid == 0) {
+            a.sampled[r] = (mk != 0u) ? (int32_t)sm.bc[3] : 0;
+            if (a.flags) a.flags[r] = VWS_FLAG_GREEDY;
+            if (a.nkept) a.nkept[r] = 1;
+        }
+        return true;
+    }
+
+    // 6. survivors of temperature + top-k + min-p
+    const float Tt = prm.T;
+    const float m = mk ? val_of(mk) / Tt : __builtin_nanf("");
+    if (!(m > -__builtin_inff() && m < __builtin_inff())) return false;  // degenerate row
+    const float kth_y = kth ? val_of(kth) / Tt : -__builtin_inff();
+    // an element below a threshold may still tie with the k-th value after the division by T
+    if (tmax > 0x007FFFFFu && val_of(tmax - 1u) / Tt >= kth_y) return false;
+    const float lp_min = (prm.min_p > 0.0f) ? log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)
+                                            : -__builtin_inff();
+    uint64_t wsum = 0;
+    for (int base = 0; base < total; base += NT) {
+        const int t = base + tid;
+        bool keep = false;
+        float y = 0.0f, uu = ureg;
+        int32_t ii = 0;
+        if (t < total) {
+            int w2, e2;
+            cand_locate(sm, t, w2, e2);
+            y = val_of(sm.ckey[w2][e2]) / Tt;
+            ii = sm.cidx[w2][e2];
+            keep = key_of(y) != 0u && y >= kth_y && (y - m) >= lp_min;
+            if (base > 0 && keep) uu = a.u[(size_t)r * a.ustride + ii];
+        }
+        const uint64_t bal = __ballot(keep);
+        uint32_t off = 0;
+        if (lane == 0 && bal) off = atomicAdd(&sm.nkeep, (uint32_t)__popcll(bal));
+        off = __shfl(off, 0, kWave);
+        if (keep) {
+            const uint32_t pos = off + (uint32_t)lane_prefix(bal);
+            if (pos < (uint32_t)kRowKeep) {
+                const float e = exp_det(y - m);
+                const uint64_t w = mass_of(e);
+                sm.sck[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)ii;
+                sm.sw[pos] = w;
+                sm.srk[pos] = e / (0.0f - log_det(uu));
+                wsum += w;
+            }
+        }
+    }
+    wsum = wave_sum_u64(wsum);
+    if (lane == 0) sm.red[wave][7] = wsum;  // slot 7: the race reduction below reuses 0..5
+    __syncthreads();
+    uint64_t W = 0;
+#pragma unroll
+    for (int w = 0; w < kRowWaves; ++w) W += sm.red[w][7];
+    const int n = (int)sm.nkeep;
+    if (n > kRowKeep) return false;
+
+    // 7. top-p over exact masses (C_j = sum of w_i over survivors i <= j in (y, index) order),
+    //    then the race among the kept survivors
+    const float q32 = 1.0f - prm.top_p;
+    const bool topp = q32 > 0.0f;
+    const bool abl = topp && !(q32 < 1.0f);  // top_p <= 0: only the last survivor is kept
+    const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
+    const int nw = (n + kWave - 1) / kWave;
+    RowRace rs;
+    if (wave < nw) {
+        const int j = tid;
+        if (j < n) {
+            const uint64_t cj = sm.sck[j];
+            bool removed = false;
+            uint64_t C = 0;
+            if (topp) {
+                for (int i = 0; i < n; ++i) C += (sm.sck[i] <= cj) ? sm.sw[i] : 0ull;
+                removed = abl ? (C != W) : (C <= thr && C != W);
+            }
+            if (removed) {
+                rs.cprev = C;
+            } else {
+                rs.cat = C;
+                rs.nkept = 1;
+                rs.last = cj;
+                rs.add_key(sm.srk[j], (int)(uint32_t)cj);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) rs.shfl_merge(off);
+        if (lane == 0) {
+            sm.red[wave][0] = rs.best; sm.red[wave][1] = rs.last; sm.red[wave][2] = rs.cprev;
+            sm.red[wave][3] = rs.cat; sm.red[wave][4] = rs.second; sm.red[wave][5] = rs.nkept;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        RowRace t;
+        for (int w = 0; w < nw; ++w) {
+            RowRace o;
+            o.best = sm.red[w][0]; o.last = sm.red[w][1]; o.cprev = sm.red[w][2]; o.cat = sm.red[w][3];
+            o.second = (uint32_t)sm.red[w][4]; o.nkept = (uint32_t)sm.red[w][5];
+            t.merge(o);
+        }
+        int32_t tok;
+        uint32_t fl = 0;
+        if (t.best) {
+            tok = (int32_t)(0x7FFFFFFF - (uint32_t)(t.best & 0xFFFFFFFFu));
+            const float bk = u2f((uint32_t)(t.best >> 32));
+            if (t.second) {
+                const float sk = u2f(t.second - 1u);
+                if ((double)sk >= (double)bk * (1.0 - 1e-6)) fl |= VWS_FLAG_RACE_NEAR_TIE;
+            }
+        } else {
+            tok = (int32_t)(uint32_t)(t.last & 0xFFFFFFFFu);
+        }
+        if (topp && !abl) {
+            const uint64_t tol = (uint64_t)((double)W * 1e-6);
+            if ((n - (int)t.nkept > 0 && thr - t.cprev <= tol) || (t.cat > thr && t.cat - thr <= tol))
+                fl |= VWS_FLAG_TOPP_NEAR_TIE;
+        }
+        a.sampled[r] = tok;
+        if (a.flags) a.flags[r] = fl;
+        if (a.nkept) a.nkept[r] = (int32_t)t.nkept;
+    }
+    return true;
+}
+
+// The general path runs in a function of its own so that its register allocation (it needs
+// more than the 128 VGPRs a 1024-thread workgroup allows and spills) stays out of the
+// single-pass loop.  The kernel hands it the address of its kernarg segment (a callee has no
+// register of its own for it); the launch arguments are read from there into scalar registers.
+template <typename T>
+__device__ __noinline__ void row_general(int r, uint64_t kernarg) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the kernarg segment exists only in the device pass
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
+    using KArgsConst = const KArgs __attribute__((address_space(4)));
+    const KArgs a = *(KArgsConst*)(((uint64_t)hi << 32) | lo);
+    const RowP prm = row_params(a, r);
+    general_row<T>(a, g_row_sh.g, r, prm);
+#else
+    (void)r;
+    (void)kernarg;
+#endif
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void row_kernel(KArgs a) {
+    const int r = blockIdx.x;
+    if (r >= a.B) return;
+    if (row_fast<T>(a, g_row_sh.f, r)) return;
+    __syncthreads();
+    row_general<T>(r, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr());
+}
+
+template __global__ void row_kernel<float>(KArgs);
+template __global__ void row_kernel<uint16_t>(KArgs);
+
+}  // namespace vws
