@@ -124,6 +124,14 @@ __device__ __forceinline__ bool is_greedy(float T) { return !(T >= kSamplingEps)
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// Lane id computed at the point of use: the volatile asm is re-executed rather than kept live,
+// so loops that need the lane's position do not hold a long-lived per-lane register for it.
+__device__ __forceinline__ int lane_now() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 __device__ __forceinline__ int lane_prefix(uint64_t mask) {
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                           __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
@@ -293,6 +301,11 @@ template <> struct Elem<float> {
         const float4 v = *reinterpret_cast<const float4*>(p);
         out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
     }
+    // the kVec elements of 16 loaded bytes
+    __device__ __forceinline__ static void from_words(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                      float* out) {
+        out[0] = u2f(w0); out[1] = u2f(w1); out[2] = u2f(w2); out[3] = u2f(w3);
+    }
 };
 template <> struct Elem<uint16_t> {  // bfloat16 bit patterns, widened exactly
     static constexpr int kVec = 8;
@@ -306,7 +319,22 @@ template <> struct Elem<uint16_t> {  // bfloat16 bit patterns, widened exactly
             out[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
         }
     }
+    __device__ __forceinline__ static void from_words(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                      float* out) {
+        const uint32_t w[4] = {w0, w1, w2, w3};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i] = u2f(w[i] << 16);
+            out[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+        }
+    }
 };
+
+// Buffer resource over `bytes` bytes at p (raw addressing): loads past the end return zero and
+// never fault, and one 32-bit lane offset plus a scalar offset addresses every load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 
 // A row slice [lo, hi) seen as chunks of kVec elements: chunk 0 is the unaligned head
 // (elements before the first 16-byte boundary), chunks 1..nbody are aligned vectors and chunk

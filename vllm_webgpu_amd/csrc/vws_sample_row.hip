@@ -49,6 +49,9 @@ struct RowSmem {
     uint32_t tauw[kRowWaves];
     uint32_t tau, status, nhash, nkeep;
     uint32_t bc[8];
+    // penalty context of the row for the out-of-line fix-up: mode 0 none, 1 penalise, 2 drop
+    uint32_t pmode;
+    float prep, pinv, ppres, pfreq;
 };
 
 union RowShared {
@@ -146,10 +149,54 @@ __device__ __forceinline__ void cand_locate(const RowSmem& sm, int t, int& w, in
 // LDS of the row kernel: the single-pass state and the general path's state share it.
 __shared__ RowShared g_row_sh;
 
-// Cuts wave w's candidate buffer (cnt entries) to its exact top-k, all ties included, in place,
-// and raises the shared threshold to the k-th key.  Returns (k-th key << 32) | new count.
-// Compaction is rare, so it lives out of line and the unrolled streaming loop stays small.
-__device__ __noinline__ uint64_t row_compact(int w, int cnt, int k) {
+// Applies the penalties to wave w's candidates [from, cnt), in place, and returns the new count.
+// Candidates enter the buffer by their raw value; with penalties that never raise a logit
+// (mode 1) the raw value bounds the penalised one from above, so nothing is missed and the key
+// is corrected here.  In mode 2 (a penalty may raise a logit) the penalised history values were
+// added up front with bit 31 of the index set; stream entries of history tokens are dropped.
+__device__ __noinline__ int row_fixup(int w, int from, int cnt) {
+    RowSmem& sm = g_row_sh.f;
+    const uint32_t mode = sm.pmode;
+    if (mode == 0u || from >= cnt) return cnt;
+    uint32_t* ck = sm.ckey[w];
+    int32_t* ci = sm.cidx[w];
+    const int lane = lane_id();
+    int out = from;
+    for (int base = from; base < cnt; base += kWave) {
+        const int i = base + lane;
+        bool keep = false;
+        uint32_t kk = 0;
+        int32_t ii = 0;
+        if (i < cnt) {
+            kk = ck[i];
+            ii = ci[i];
+            keep = true;
+            if (ii < 0) {
+                ii &= 0x7FFFFFFF;  // added up front, already penalised
+            } else {
+                const uint32_t hv = rhash_value(sm, ii);
+                if (hv != 0u) {
+                    if (mode == 2u) keep = false;
+                    else kk = key_of(apply_penalty(val_of(kk), (hv >> 31) != 0u, hv & 0x7FFFFFFFu,
+                                                   sm.prep, sm.pinv, sm.pfreq, sm.ppres));
+                }
+            }
+        }
+        const uint64_t bal = __ballot(keep);
+        if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
+        out += __popcll(bal);
+        wave_sync();
+    }
+    return out;
+}
+
+// Penalises wave w's unfixed candidates [nfix, cnt), then cuts the buffer to its exact top-k,
+// all ties included, in place, and raises the shared threshold to the k-th key.  Returns
+// (k-th key << 32) | new count (k-th key 0 when fewer than k candidates remain).  Compaction is
+// rare, so it lives out of line and the unrolled streaming loop stays small.
+__device__ __noinline__ uint64_t row_compact(int w, int nfix, int cnt, int k) {
+    cnt = row_fixup(w, nfix, cnt);
+    if (cnt <= k) return (uint64_t)(uint32_t)cnt;
     RowSmem& sm = g_row_sh.f;
     uint32_t* ck = sm.ckey[w];
     int32_t* ci = sm.cidx[w];
@@ -176,11 +223,12 @@ __device__ __noinline__ uint64_t row_compact(int w, int cnt, int k) {
 // the wave's threshold; the threshold only rises (own compactions, other waves' via sm.tau).
 struct RowCand {
     int w, k, cnt;        // wave-uniform
+    int nfix;             // entries [0, nfix) carry penalised keys
     uint32_t tau;         // threshold key
     float tauf;           // its value form (-inf when every non-NaN value passes)
     bool ovf;             // ties overflowed the buffer
     __device__ __forceinline__ void init(int w_, int k_) {
-        w = w_; k = k_; cnt = 0; tau = 0u; tauf = -__builtin_inff(); ovf = false;
+        w = w_; k = k_; cnt = 0; nfix = 0; tau = 0u; tauf = -__builtin_inff(); ovf = false;
     }
     __device__ __forceinline__ void set_tau(uint32_t t) {
         if (t > tau) {
@@ -198,8 +246,9 @@ struct RowCand {
         if (!bal || ovf) return;
         int n = __popcll(bal);
         if (cnt + n > kRowCap) {
-            const uint64_t rc = row_compact(w, cnt, k);
+            const uint64_t rc = row_compact(w, nfix, cnt, k);
             cnt = __builtin_amdgcn_readfirstlane((uint32_t)rc);
+            nfix = cnt;
             set_tau(__builtin_amdgcn_readfirstlane((uint32_t)(rc >> 32)));
             c = c && kk >= tau;
             bal = __ballot(c);
@@ -214,19 +263,22 @@ struct RowCand {
         cnt += n;
         wave_sync();
     }
+    // penalised keys for every candidate (once, after the stream)
+    __device__ __forceinline__ void finish() {
+        if (nfix < cnt) cnt = __builtin_amdgcn_readfirstlane((uint32_t)row_fixup(w, nfix, cnt));
+        nfix = cnt;
+    }
 };
 
 // Serves greedy and top-k rows; returns false when the row must take the general path (nothing
 // has been written for it then).
 // Defaults read in place of a missing per-row parameter array, so every parameter is one
-// unconditional scalar load: T, top_p, min_p, repetition, presence, frequency.
+// unconditional scalar load: T, top_p, min_p, repetition, presence, frequency.  The arrays are
+// never written; they are not const so that they live in the global address space, like the
+// arrays they stand in for, and the pointer select between the two stays global.
 __device__ float kRowDefaultsF[8] = {0.0f, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 // top_k (0 = off), and a length that clamps to the history width (absent lengths = full width)
 __device__ int32_t kRowDefaultsI[4] = {0, 0x7FFFFFFF, 0, 0};
-// Stand-in source for loads that have nothing to read (no history, no aligned body).  These
-// arrays are never written; they are not const so that they live in the global address space,
-// like the arrays they stand in for, and selecting between the two keeps global loads.
-__device__ uint4 kRowDummy[4] = {};
 
 // Per-row parameters, all issued as scalar loads before the first one is used.  Scalar loads
 // complete on their own counter, so waiting for them never waits for the logits in flight.
@@ -275,33 +327,41 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     constexpr int NT = kRowThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int U = 32 / VEC;  // 16-byte loads in flight per lane per iteration
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int V = a.V;
     const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+    // position of this lane in the workgroup, recomputed where the streaming loop needs it
+    auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
 
     // 1. loads in the order they are consumed, none behind a branch (a load that only some
     //    paths issue makes the wait for everything before it conservative):
     //    history ids (clamped to the row width), the first two iterations of logits, then the
     //    parameters as scalar loads.
-    const int32_t* prow = (a.prompt && a.pwidth > 0) ? a.prompt + (size_t)r * a.pstride
-                                                     : reinterpret_cast<const int32_t*>(kRowDummy);
-    const int32_t* orow = (a.output && a.owidth > 0) ? a.output + (size_t)r * a.ostride
-                                                     : reinterpret_cast<const int32_t*>(kRowDummy);
-    const int hp_raw = prow[(a.prompt && a.pwidth > 0) ? min(tid, a.pwidth - 1) : 0];
-    const int ho_raw = orow[(a.output && a.owidth > 0) ? min(tid, a.owidth - 1) : 0];
+    //    Buffer loads: a row's loads share one lane offset (the iteration and vector go in the
+    //    scalar offset), and loads past the end read zeros, so nothing is clamped.
+    const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
+    const int32_t* prow = has_p ? a.prompt + (size_t)r * a.pstride : nullptr;
+    const int32_t* orow = has_o ? a.output + (size_t)r * a.ostride : nullptr;
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(has_p ? (const void*)prow : (const void*)row,
+                                                 has_p ? 4u * (uint32_t)a.pwidth : 0u);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(has_o ? (const void*)orow : (const void*)row,
+                                                 has_o ? 4u * (uint32_t)a.owidth : 0u);
+    const int hp_raw = __builtin_amdgcn_raw_buffer_load_b32(prs, 4u * (uint32_t)tid, 0u, 0);
+    const int ho_raw = __builtin_amdgcn_raw_buffer_load_b32(ors, 4u * (uint32_t)tid, 0u, 0);
     Slice<T> sl;
     sl.init(row, 0, V);
     const int nbody = sl.nbody;
     const int nit = (nbody + NT * U - 1) / (NT * U);
-    const T* body = nbody > 0 ? row + sl.a : reinterpret_cast<const T*>(kRowDummy);
-    const int vlast = nbody > 0 ? nbody - 1 : 0;
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + sl.a, 16u * (uint32_t)nbody);
     float A[U][VEC], Bq[U][VEC];
-    // vectors past the body repeat the last one; consumers skip them (vi >= nbody)
+    // vectors past the body read zeros; consumers skip them (vi >= nbody)
     auto load_iter = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < U; ++q) {
-            const int vi = (it * U + q) * NT + tid;
-            Elem<T>::load_vec(body + (size_t)min(vi, vlast) * VEC, buf[q]);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+                lrs, 16u * (uint32_t)tid_now(), 16u * (uint32_t)((it * U + q) * NT), 0);
+            Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
     load_iter(A, 0);
@@ -317,7 +377,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const int32_t* ou = hh && prm.no > 0 ? orow : nullptr;
 
     // 2. LDS state and the history hash
-    if (tid == 0) { sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
+    if (tid == 0) {
+        sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu;
+        sm.pmode = !hh ? 0u : (gather ? 2u : 1u);
+        sm.prep = prm.rep; sm.pinv = prm.inv_rep; sm.ppres = prm.pres; sm.pfreq = prm.freq;
+    }
     if (hh) {
         for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
     }
@@ -378,27 +442,16 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     //    pass whose k-th candidate lies below a threshold is streamed again without the seed.
     RowCand cb;
     auto slot = [&](float v, int idx, bool valid) __attribute__((always_inline)) {
-        bool c = valid && v >= cb.tauf;
+        const bool c = valid && v >= cb.tauf;
         if (__ballot(c) == 0ull) return;
-        if (hh && c) {
-            const uint32_t hv = rhash_value(sm, idx);
-            if (hv != 0u) {
-                if (gather) {
-                    c = false;
-                } else {
-                    v = apply_penalty(v, (hv >> 31) != 0u, hv & 0x7FFFFFFFu, prm.rep, prm.inv_rep,
-                                      prm.freq, prm.pres);
-                    c = v >= cb.tauf;
-                }
-            }
-        }
-        cb.append(c, key_of(v), idx);
+        cb.append(c, key_of(v), idx);  // raw value; penalties are applied by RowCand::finish
     };
     auto examine = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
         cb.refresh();
+        const int t = tid_now();
 #pragma unroll
         for (int q = 0; q < U; ++q) {
-            const int vi = (it * U + q) * NT + tid;
+            const int vi = (it * U + q) * NT + t;
             const int i0 = sl.a + vi * VEC;
             const bool ok = vi < nbody;
 #pragma unroll
@@ -425,7 +478,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 const int s = s0 + lane;
                 const uint32_t kk = sm.hkey[s];
                 const uint32_t pk = kk ? key_of(sm.hpen[s]) : 0u;
-                cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)kk - 1);
+                cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)((kk - 1u) | 0x80000000u));
             }
         }
         {   // unaligned head (thread 0) and tail (thread 1): fewer than 2 vectors in total
@@ -445,6 +498,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             load_iter(Bq, it + 3);
         }
 
+        if (!cb.ovf) cb.finish();
         if (lane == 0) { sm.cnt[wave] = cb.ovf ? (1 << 28) : cb.cnt; sm.tauw[wave] = cb.tau; }
         if (tid == 0) { sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
         __syncthreads();
