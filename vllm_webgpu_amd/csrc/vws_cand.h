@@ -121,8 +121,8 @@ __device__ __forceinline__ uint32_t wave_kth_largest_multi(const uint32_t* base,
         else if ((r -= c0) <= c1) bin = 254 - 4 * lane;
         else if ((r -= c1) <= c2) bin = 253 - 4 * lane;
         else { r -= c2; bin = 252 - 4 * lane; }
-        bin = __shfl(bin, L, kWave);
-        rem = __shfl(r, L, kWave);
+        bin = __builtin_amdgcn_readlane(bin, L);  // L is wave-uniform
+        rem = __builtin_amdgcn_readlane(r, L);
         prefix |= bin << shift;
         pmask |= 255u << shift;
         wave_sync();

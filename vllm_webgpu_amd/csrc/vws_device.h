@@ -142,6 +142,33 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
+// v of lane (lane ^ s) for s in {1, 2, 4, 8, 16, 32}, on the VALU: DPP moves inside a row of
+// 16 (xor 4 and xor 8 as compositions of mirrors), permlane swaps across rows and halves.
+// Cheaper than an LDS-crossbar shuffle; s is a compile-time constant after unrolling.
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v, int s) {
+    switch (s) {
+    case 1: return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    case 2: return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    case 4:  // row_half_mirror (l ^ 7), then quad_perm [3,2,1,0] (l ^ 3)
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false), 0x1B,
+                                        0xF, 0xF, false);
+    case 8:  // row_mirror (l ^ 15), then row_half_mirror (l ^ 7)
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false), 0x141,
+                                        0xF, 0xF, false);
+    case 16: {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane_id() & 16) ? p[0] : p[1];
+    }
+    default: {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane_id() & 32) ? p[0] : p[1];
+    }
+    }
+}
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v, int s) {
+    return ((uint64_t)lane_xor((uint32_t)(v >> 32), s) << 32) | lane_xor((uint32_t)v, s);
+}
+
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
     const int l = lane_id();
 #pragma unroll
@@ -154,31 +181,31 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = __shfl_xor(v, o, kWave); v = v > t ? v : t; }
+    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = lane_xor(v, o); v = v > t ? v : t; }
     return v;
 }
 
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = __shfl_xor(v, o, kWave); v = v < t ? v : t; }
+    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = lane_xor(v, o); v = v < t ? v : t; }
     return v;
 }
 
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    for (int o = 32; o > 0; o >>= 1) v += lane_xor64(v, o);
     return v;
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = __shfl_xor(v, o, kWave); v = v > t ? v : t; }
+    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = lane_xor64(v, o); v = v > t ? v : t; }
     return v;
 }
 
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = __shfl_xor(v, o, kWave); v = v < t ? v : t; }
+    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = lane_xor64(v, o); v = v < t ? v : t; }
     return v;
 }
 
@@ -211,8 +238,8 @@ __device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t* keys, int n
         else if ((r -= c0) <= c1) bin = 254 - 4 * lane;
         else if ((r -= c1) <= c2) bin = 253 - 4 * lane;
         else { r -= c2; bin = 252 - 4 * lane; }
-        bin = __shfl(bin, L, kWave);
-        rem = __shfl(r, L, kWave);
+        bin = __builtin_amdgcn_readlane(bin, L);  // L is wave-uniform
+        rem = __builtin_amdgcn_readlane(r, L);
         prefix |= bin << shift;
         pmask |= 255u << shift;
         wave_sync();
@@ -238,7 +265,7 @@ __device__ __forceinline__ uint32_t wave_kth_largest_256(uint32_t v0, uint32_t v
                 for (int i = 0; i < 4; ++i) {
                     const int e = 4 * lane + i;
                     const bool desc = (e & size) == 0;
-                    const uint32_t o = __shfl_xor(v[i], lstride, kWave);
+                    const uint32_t o = lane_xor(v[i], lstride);
                     const uint32_t hi = v[i] > o ? v[i] : o, lo = v[i] > o ? o : v[i];
                     // the lower element of a pair keeps the larger key in a descending block
                     v[i] = (upper != desc) ? hi : lo;
@@ -259,8 +286,8 @@ __device__ __forceinline__ uint32_t wave_kth_largest_256(uint32_t v0, uint32_t v
         }
     }
     const int src = (k - 1) >> 2, sel = (k - 1) & 3;
-    const uint32_t r0 = __shfl(v[0], src, kWave), r1 = __shfl(v[1], src, kWave);
-    const uint32_t r2 = __shfl(v[2], src, kWave), r3 = __shfl(v[3], src, kWave);
+    const uint32_t r0 = __builtin_amdgcn_readlane(v[0], src), r1 = __builtin_amdgcn_readlane(v[1], src);
+    const uint32_t r2 = __builtin_amdgcn_readlane(v[2], src), r3 = __builtin_amdgcn_readlane(v[3], src);
     return sel == 0 ? r0 : sel == 1 ? r1 : sel == 2 ? r2 : r3;
 }
 
@@ -272,7 +299,7 @@ __device__ __forceinline__ uint32_t wave_sort_desc64(uint32_t v) {
     for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint32_t o = __shfl_xor(v, stride, kWave);
+            const uint32_t o = lane_xor(v, stride);
             const bool desc = (lane & size) == 0;
             const bool upper = (lane & stride) != 0;
             const uint32_t hi = v > o ? v : o, lo = v > o ? o : v;
@@ -287,7 +314,7 @@ __device__ __forceinline__ int wave_count_ge(const uint32_t* keys, int n, uint32
     int c = 0;
     for (int i = lane_id(); i < n; i += kWave) c += (keys[i] >= t) ? 1 : 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, kWave);
+    for (int o = 32; o > 0; o >>= 1) c += lane_xor(c, o);
     return c;
 }
 

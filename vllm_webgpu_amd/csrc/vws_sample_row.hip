@@ -7,20 +7,22 @@
 //   3. a threshold is seeded from the first iteration: the lane maxima of its 32 values are
 //      sorted per wave, the 16 largest of every wave are pooled and the m-th largest of the
 //      pool (m = 3k x the sampled fraction of the row) becomes the starting threshold;
-//   4. the row is streamed once, double-buffered; an element at or above the threshold goes to
-//      its wave's LDS candidate buffer (history tokens are penalised on the spot when no penalty
-//      can raise a logit; otherwise their penalised values are gathered up front and their
-//      stream positions skipped).  A full buffer is cut to its exact top-k by a radix select,
+//   4. the row is streamed once, double-buffered, with buffer loads; an element at or above
+//      the threshold goes to its wave's LDS candidate buffer by its raw value.  Penalties are
+//      applied to the buffered candidates (when a buffer is compacted and once after the
+//      stream): penalties that never raise a logit keep raw >= penalised, so nothing is missed;
+//      otherwise the penalised history values are added up front and the stream entries of
+//      history tokens dropped.  A full buffer is cut to its exact top-k by a radix select,
 //      which raises the threshold for every wave;
 //   5. the k-th largest candidate is selected.  It is exact when every element at or above it
-//      was kept, i.e. when it is not below any threshold used; a seeded pass that fails this
-//      check is streamed again without the seed;
+//      was kept, i.e. when it is not below any threshold used (a seed above the k-th value
+//      fails this check and sends the row to the general path);
 //   6. survivors of temperature, top-k and min-p get their exact integer masses and race keys
-//      (uniforms are fetched for the candidates while the k-th value is selected); top-p is
+//      (each wave fetches its candidates' uniforms as soon as its stream ends); top-p is
 //      cut on the exact prefix sums and the race is reduced across the survivors.
-// Every other row (top-k off or k > 256, logprobs requested, candidate or hash overflow,
-// degenerate maxima, temperature ties across a threshold) runs the multi-pass path of
-// vws_general.h in the same workgroup, so one launch serves the whole batch.
+// Every other row (top-k off or k > 256, logprobs requested, candidate or hash overflow, a
+// seed above the k-th value, degenerate maxima, temperature ties across a threshold) runs the
+// multi-pass path of vws_general.h in the same workgroup, so one launch serves the whole batch.
 #include "vws_general.h"
 
 namespace vws {
@@ -36,6 +38,7 @@ constexpr int kSeedPerWave = 16;             // lane maxima each wave contribute
 struct RowSmem {
     uint32_t ckey[kRowWaves][kRowCap];
     int32_t cidx[kRowWaves][kRowCap];
+    float cu[kRowWaves][kRowCap];            // uniforms of the candidates (sampled rows)
     uint32_t rhist[kRowWaves][256];          // per-wave radix-select scratch
     uint32_t hkey[kRowHash];                 // history token + 1 (0 = empty)
     uint32_t hval[kRowHash];                 // output count | prompt flag << 31
@@ -123,12 +126,12 @@ struct RowRace {
     }
     __device__ __forceinline__ void shfl_merge(int off) {
         RowRace o;
-        o.best = __shfl_xor(best, off, kWave);
-        o.last = __shfl_xor(last, off, kWave);
-        o.cprev = __shfl_xor(cprev, off, kWave);
-        o.cat = __shfl_xor(cat, off, kWave);
-        o.second = __shfl_xor(second, off, kWave);
-        o.nkept = __shfl_xor(nkept, off, kWave);
+        o.best = lane_xor64(best, off);
+        o.last = lane_xor64(last, off);
+        o.cprev = lane_xor64(cprev, off);
+        o.cat = lane_xor64(cat, off);
+        o.second = lane_xor(second, off);
+        o.nkept = lane_xor(nkept, off);
         merge(o);
     }
 };
@@ -459,66 +462,60 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         }
     };
     const bool sampling = !prm.greedy;
-    float ureg = 0.5f;
-    uint32_t kth = 0, mk = 0, tmax = 0;
-    int total = 0;
-    for (int attempt = 0;; ++attempt) {
-        if (attempt > 0) {
-            __syncthreads();
-            if (tid == 0) sm.tau = 0u;
-            __syncthreads();
-            load_iter(A, 0);
-            load_iter(Bq, 1);
+    cb.init(wave, k);
+    cb.set_tau(seed);
+    if (gather) {
+        constexpr int per = kRowHash / kRowWaves;
+        for (int s0 = wave * per; s0 < (wave + 1) * per; s0 += kWave) {
+            const int s = s0 + lane;
+            const uint32_t kk = sm.hkey[s];
+            const uint32_t pk = kk ? key_of(sm.hpen[s]) : 0u;
+            cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)((kk - 1u) | 0x80000000u));
         }
-        cb.init(wave, k);
-        cb.set_tau(seed);
-        if (gather) {
-            constexpr int per = kRowHash / kRowWaves;
-            for (int s0 = wave * per; s0 < (wave + 1) * per; s0 += kWave) {
-                const int s = s0 + lane;
-                const uint32_t kk = sm.hkey[s];
-                const uint32_t pk = kk ? key_of(sm.hpen[s]) : 0u;
-                cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)((kk - 1u) | 0x80000000u));
-            }
-        }
-        {   // unaligned head (thread 0) and tail (thread 1): fewer than 2 vectors in total
-            float v[VEC];
+    }
+    for (int it = 0; it < nit && !cb.ovf; it += 2) {
+        examine(A, it);
+        load_iter(A, it + 2);
+        if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
+        load_iter(Bq, it + 3);
+    }
+    {   // unaligned head (thread 0) and tail (thread 1), fewer than 2 vectors in total; handled
+        // last, where waiting for their loads holds up nothing
+        float v[VEC];
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
-            int i0 = 0;
-            if (tid <= 1) i0 = sl.load_edge(tid, v);
-            const int end = tid == 0 ? sl.a : V;
+        for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
+        int i0 = 0;
+        if (tid <= 1) i0 = sl.load_edge(tid, v);
+        const int end = tid == 0 ? sl.a : V;
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) slot(v[j], i0 + j, tid <= 1 && i0 + j < end);
+        for (int j = 0; j < VEC; ++j) slot(v[j], i0 + j, tid <= 1 && i0 + j < end);
+    }
+    if (!cb.ovf) {
+        cb.finish();
+        // the uniforms of this wave's candidates, fetched while other waves still stream
+        if (sampling) {
+            for (int e = lane; e < cb.cnt; e += kWave)
+                sm.cu[wave][e] = a.u[(size_t)r * a.ustride + sm.cidx[wave][e]];
         }
-        for (int it = 0; it < nit && !cb.ovf; it += 2) {
-            examine(A, it);
-            load_iter(A, it + 2);
-            if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
-            load_iter(Bq, it + 3);
-        }
+    }
 
-        if (!cb.ovf) cb.finish();
-        if (lane == 0) { sm.cnt[wave] = cb.ovf ? (1 << 28) : cb.cnt; sm.tauw[wave] = cb.tau; }
-        if (tid == 0) { sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
-        __syncthreads();
-        total = 0;
-        tmax = seed;
+    // 5. the k-th largest candidate.  It is exact when it is not below any threshold used;
+    //    otherwise (a seed above the k-th value, tie overflow) the row takes the general path.
+    if (lane == 0) { sm.cnt[wave] = cb.ovf ? (1 << 28) : cb.cnt; sm.tauw[wave] = cb.tau; }
+    if (tid == 0) { sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
+    __syncthreads();
+    int total = 0;
+    uint32_t tmax = seed;
 #pragma unroll
-        for (int w = 0; w < kRowWaves; ++w) {
-            total += sm.cnt[w];
-            tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
-        }
-        if (total >= (1 << 28)) return false;  // ties overflowed a buffer
-        // the uniform of candidate tid is in flight while the k-th value is found
+    for (int w = 0; w < kRowWaves; ++w) {
+        total += sm.cnt[w];
+        tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
+    }
+    if (total >= (1 << 28)) return false;  // ties overflowed a buffer
+    {
         int cw, ce;
         cand_locate(sm, tid, cw, ce);
-        uint32_t ck = 0;
-        if (cw >= 0) {
-            ck = sm.ckey[cw][ce];
-            if (sampling) ureg = a.u[(size_t)r * a.ustride + sm.cidx[cw][ce]];
-        }
-        uint32_t mxw = ck;
+        uint32_t mxw = cw >= 0 ? sm.ckey[cw][ce] : 0u;
         for (int t = NT + tid; t < total; t += NT) {
             int w2, e2;
             cand_locate(sm, t, w2, e2);
@@ -527,33 +524,30 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         }
         mxw = wave_max_u32(mxw);
         if (lane == 0) atomicMax(&sm.bc[2], mxw);
-        if (wave == 0) {
-            uint32_t kk = 0;
-            if (total >= k) {
-                if (total <= 256) {
-                    uint32_t v[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        int w2, e2;
-                        cand_locate(sm, 4 * lane + i, w2, e2);
-                        v[i] = w2 >= 0 ? sm.ckey[w2][e2] : 0u;
-                    }
-                    kk = wave_kth_largest_256(v[0], v[1], v[2], v[3], k);
-                } else {
-                    kk = wave_kth_largest_multi(&sm.ckey[0][0], kRowCap, sm.cnt, kRowWaves, k, sm.rhist[0]);
-                }
-            }
-            if (lane == 0) sm.bc[1] = kk;
-        }
-        __syncthreads();
-        kth = sm.bc[1];
-        mk = sm.bc[2];
-        const bool seeded_run = seed != 0u;
-        const bool exact = seeded_run ? (total >= k && kth >= tmax) : (kth == 0u || kth >= tmax);
-        if (exact) break;
-        if (!seeded_run || attempt > 0) return false;
-        seed = 0u;
     }
+    if (wave == 0) {
+        uint32_t kk = 0;
+        if (total >= k) {
+            if (total <= 256) {
+                uint32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    int w2, e2;
+                    cand_locate(sm, 4 * lane + i, w2, e2);
+                    v[i] = w2 >= 0 ? sm.ckey[w2][e2] : 0u;
+                }
+                kk = wave_kth_largest_256(v[0], v[1], v[2], v[3], k);
+            } else {
+                kk = wave_kth_largest_multi(&sm.ckey[0][0], kRowCap, sm.cnt, kRowWaves, k, sm.rhist[0]);
+            }
+        }
+        if (lane == 0) sm.bc[1] = kk;
+    }
+    __syncthreads();
+    const uint32_t kth = sm.bc[1];
+    const uint32_t mk = sm.bc[2];
+    const bool exact = seed != 0u ? (total >= k && kth >= tmax) : (kth == 0u || kth >= tmax);
+    if (!exact) return false;
 
     if (!sampling) {
         // greedy: lowest index at the maximum of the penalised logits (0 when every value is NaN)
@@ -587,20 +581,20 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     for (int base = 0; base < total; base += NT) {
         const int t = base + tid;
         bool keep = false;
-        float y = 0.0f, uu = ureg;
+        float y = 0.0f, uu = 0.5f;
         int32_t ii = 0;
         if (t < total) {
             int w2, e2;
             cand_locate(sm, t, w2, e2);
             y = val_of(sm.ckey[w2][e2]) / Tt;
             ii = sm.cidx[w2][e2];
+            uu = sm.cu[w2][e2];
             keep = key_of(y) != 0u && y >= kth_y && (y - m) >= lp_min;
-            if (base > 0 && keep) uu = a.u[(size_t)r * a.ustride + ii];
         }
         const uint64_t bal = __ballot(keep);
         uint32_t off = 0;
         if (lane == 0 && bal) off = atomicAdd(&sm.nkeep, (uint32_t)__popcll(bal));
-        off = __shfl(off, 0, kWave);
+        off = __builtin_amdgcn_readlane(off, 0);
         if (keep) {
             const uint32_t pos = off + (uint32_t)lane_prefix(bal);
             if (pos < (uint32_t)kRowKeep) {
