@@ -623,42 +623,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const bool abl = topp && !(q32 < 1.0f);  // top_p <= 0: only the last survivor is kept
     const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
     const int nw = (n + kWave - 1) / kWave;
-    RowRace rs;
-    if (wave < nw) {
-        const int j = tid;
-        if (j < n) {
-            const uint64_t cj = sm.sck[j];
-            bool removed = false;
-            uint64_t C = 0;
-            if (topp) {
-                for (int i = 0; i < n; ++i) C += (sm.sck[i] <= cj) ? sm.sw[i] : 0ull;
-                removed = abl ? (C != W) : (C <= thr && C != W);
-            }
-            if (removed) {
-                rs.cprev = C;
-            } else {
-                rs.cat = C;
-                rs.nkept = 1;
-                rs.last = cj;
-                rs.add_key(sm.srk[j], (int)(uint32_t)cj);
-            }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) rs.shfl_merge(off);
-        if (lane == 0) {
-            sm.red[wave][0] = rs.best; sm.red[wave][1] = rs.last; sm.red[wave][2] = rs.cprev;
-            sm.red[wave][3] = rs.cat; sm.red[wave][4] = rs.second; sm.red[wave][5] = rs.nkept;
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        RowRace t;
-        for (int w = 0; w < nw; ++w) {
-            RowRace o;
-            o.best = sm.red[w][0]; o.last = sm.red[w][1]; o.cprev = sm.red[w][2]; o.cat = sm.red[w][3];
-            o.second = (uint32_t)sm.red[w][4]; o.nkept = (uint32_t)sm.red[w][5];
-            t.merge(o);
-        }
+    // token, flags and survivor count from the merged race of the row
+    auto emit = [&](const RowRace& t) __attribute__((always_inline)) {
         int32_t tok;
         uint32_t fl = 0;
         if (t.best) {
@@ -679,6 +645,75 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         a.sampled[r] = tok;
         if (a.flags) a.flags[r] = fl;
         if (a.nkept) a.nkept[r] = (int32_t)t.nkept;
+    };
+    // survivor j's cumulative mass C_j given, its share of the race
+    auto race_of = [&](int j, uint64_t cj, uint64_t C) __attribute__((always_inline)) {
+        RowRace rs;
+        if (j < n) {
+            const bool removed = topp && (abl ? (C != W) : (C <= thr && C != W));
+            if (removed) {
+                rs.cprev = C;
+            } else {
+                rs.cat = C;
+                rs.nkept = 1;
+                rs.last = cj;
+                rs.add_key(sm.srk[j], (int)(uint32_t)cj);
+            }
+        }
+        return rs;
+    };
+    if (nw == 1) {
+        // up to 64 survivors: one per lane of wave 0; the other survivors' keys and masses are
+        // read with readlane, so the cumulative sums need no LDS round trips
+        if (wave != 0) return true;
+        const uint64_t cj = lane < n ? sm.sck[lane] : ~0ull;
+        const uint64_t wj = lane < n ? sm.sw[lane] : 0ull;
+        uint64_t C = 0;
+        if (topp) {
+            const uint32_t chi = (uint32_t)(cj >> 32), clo = (uint32_t)cj;
+            const uint32_t whi = (uint32_t)(wj >> 32), wlo = (uint32_t)wj;
+            for (int i = 0; i < n; ++i) {
+                // readlane returns int: widen through uint32_t (no sign extension)
+                const uint64_t ci = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(chi, i) << 32) |
+                                    (uint32_t)__builtin_amdgcn_readlane(clo, i);
+                const uint64_t wi = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(whi, i) << 32) |
+                                    (uint32_t)__builtin_amdgcn_readlane(wlo, i);
+                C += (ci <= cj) ? wi : 0ull;
+            }
+        }
+        RowRace rs = race_of(lane, cj, C);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) rs.shfl_merge(off);
+        if (lane == 0) emit(rs);
+        return true;
+    }
+    RowRace rs;
+    if (wave < nw) {
+        const int j = tid;
+        uint64_t cj = 0, C = 0;
+        if (j < n) {
+            cj = sm.sck[j];
+            if (topp)
+                for (int i = 0; i < n; ++i) C += (sm.sck[i] <= cj) ? sm.sw[i] : 0ull;
+        }
+        rs = race_of(j, cj, C);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) rs.shfl_merge(off);
+        if (lane == 0) {
+            sm.red[wave][0] = rs.best; sm.red[wave][1] = rs.last; sm.red[wave][2] = rs.cprev;
+            sm.red[wave][3] = rs.cat; sm.red[wave][4] = rs.second; sm.red[wave][5] = rs.nkept;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        RowRace t;
+        for (int w = 0; w < nw; ++w) {
+            RowRace o;
+            o.best = sm.red[w][0]; o.last = sm.red[w][1]; o.cprev = sm.red[w][2]; o.cat = sm.red[w][3];
+            o.second = (uint32_t)sm.red[w][4]; o.nkept = (uint32_t)sm.red[w][5];
+            t.merge(o);
+        }
+        emit(t);
     }
     return true;
 }
