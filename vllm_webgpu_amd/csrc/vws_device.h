@@ -179,33 +179,42 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
     return v;
 }
 
+// Butterfly over the wave with op(a, b), strides 32 .. 1 written out (each stride is a
+// constant, so lane_xor is a fixed DPP / permlane sequence).
+#define VWS_BUTTERFLY(v, XOR, OP)          \
+    do {                                   \
+        v = OP(v, XOR(v, 32));             \
+        v = OP(v, XOR(v, 16));             \
+        v = OP(v, XOR(v, 8));              \
+        v = OP(v, XOR(v, 4));              \
+        v = OP(v, XOR(v, 2));              \
+        v = OP(v, XOR(v, 1));              \
+    } while (0)
+
+__device__ __forceinline__ uint32_t vws_max32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t vws_min32(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint64_t vws_max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t vws_min64(uint64_t a, uint64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint64_t vws_add64(uint64_t a, uint64_t b) { return a + b; }
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = lane_xor(v, o); v = v > t ? v : t; }
+    VWS_BUTTERFLY(v, lane_xor, vws_max32);
     return v;
 }
-
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint32_t t = lane_xor(v, o); v = v < t ? v : t; }
+    VWS_BUTTERFLY(v, lane_xor, vws_min32);
     return v;
 }
-
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += lane_xor64(v, o);
+    VWS_BUTTERFLY(v, lane_xor64, vws_add64);
     return v;
 }
-
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = lane_xor64(v, o); v = v > t ? v : t; }
+    VWS_BUTTERFLY(v, lane_xor64, vws_max64);
     return v;
 }
-
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) { const uint64_t t = lane_xor64(v, o); v = v < t ? v : t; }
+    VWS_BUTTERFLY(v, lane_xor64, vws_min64);
     return v;
 }
 

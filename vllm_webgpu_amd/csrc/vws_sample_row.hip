@@ -33,22 +33,25 @@ constexpr int kRowCap = 512;                 // candidate slots per wave
 constexpr int kRowHash = 2048;               // history hash slots
 constexpr int kRowHashFill = 1536;           // unique history tokens served in LDS
 constexpr int kRowKeep = 256;                // survivors finished here
+constexpr int kRowPack = kRowThreads;        // candidates finished here (more: general path)
 constexpr int kSeedPerWave = 16;             // lane maxima each wave contributes to the seed pool
 
 struct RowSmem {
     uint32_t ckey[kRowWaves][kRowCap];
     int32_t cidx[kRowWaves][kRowCap];
-    float cu[kRowWaves][kRowCap];            // uniforms of the candidates (sampled rows)
+    alignas(16) uint32_t pkey[kRowPack];     // all candidates of the row, packed in any order
+    int32_t pidx[kRowPack];
+    float pu[kRowPack];                      // their uniforms (sampled rows)
     uint32_t rhist[kRowWaves][256];          // per-wave radix-select scratch
     uint32_t hkey[kRowHash];                 // history token + 1 (0 = empty)
     uint32_t hval[kRowHash];                 // output count | prompt flag << 31
     float hpen[kRowHash];                    // penalised value (gather mode)
-    uint64_t sck[kRowKeep];                  // survivors: key(y) << 32 | index
-    uint64_t sw[kRowKeep];                   // exact mass
+    alignas(16) uint64_t sck[kRowKeep];      // survivors: key(y) << 32 | index
+    alignas(16) uint64_t sw[kRowKeep];       // exact mass
     float srk[kRowKeep];                     // race key
+    uint32_t npack;                          // candidates packed so far
     uint32_t seedk[kRowWaves * kSeedPerWave];
     uint64_t red[kRowWaves][8];
-    int cnt[kRowWaves];
     uint32_t tauw[kRowWaves];
     uint32_t tau, status, nhash, nkeep;
     uint32_t bc[8];
@@ -101,6 +104,7 @@ struct RowRace {
     uint64_t cat = ~0ull;  // smallest cumulative mass among kept survivors
     uint32_t second = 0;   // key bits + 1 of the best non-winning key, 0 = none
     uint32_t nkept = 0;
+    uint32_t nrem = 0;     // survivors removed by top-p
     __device__ __forceinline__ void add_key(float key, int idx) {
         if (!(key >= 0.0f)) return;  // NaN keys never win
         const uint64_t pk = ((uint64_t)f2u(key) << 32) | (uint32_t)(0x7FFFFFFF - idx);
@@ -123,6 +127,7 @@ struct RowRace {
         cprev = cprev > o.cprev ? cprev : o.cprev;
         cat = cat < o.cat ? cat : o.cat;
         nkept += o.nkept;
+        nrem += o.nrem;
     }
     __device__ __forceinline__ void shfl_merge(int off) {
         RowRace o;
@@ -132,22 +137,10 @@ struct RowRace {
         o.cat = lane_xor64(cat, off);
         o.second = lane_xor(second, off);
         o.nkept = lane_xor(nkept, off);
+        o.nrem = lane_xor(nrem, off);
         merge(o);
     }
 };
-
-// Position of candidate t in the per-wave buffers (w < 0 when t is past the end).
-__device__ __forceinline__ void cand_locate(const RowSmem& sm, int t, int& w, int& e) {
-    w = -1;
-    e = 0;
-    int off = 0;
-#pragma unroll
-    for (int i = 0; i < kRowWaves; ++i) {
-        const int c = sm.cnt[i];
-        if (w < 0 && t < off + c) { w = i; e = t - off; }
-        off += c;
-    }
-}
 
 // LDS of the row kernel: the single-pass state and the general path's state share it.
 __shared__ RowShared g_row_sh;
@@ -381,7 +374,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
 
     // 2. LDS state and the history hash
     if (tid == 0) {
-        sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu;
+        sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.npack = 0u; sm.bc[4] = 0u;
         sm.pmode = !hh ? 0u : (gather ? 2u : 1u);
         sm.prep = prm.rep; sm.pinv = prm.inv_rep; sm.ppres = prm.pres; sm.pfreq = prm.freq;
     }
@@ -490,58 +483,56 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) slot(v[j], i0 + j, tid <= 1 && i0 + j < end);
     }
+    // each wave packs its candidates (penalised keys, indices, uniforms) into the row's arrays
+    // as soon as its own stream ends, while other waves are still streaming
     if (!cb.ovf) {
         cb.finish();
-        // the uniforms of this wave's candidates, fetched while other waves still stream
-        if (sampling) {
-            for (int e = lane; e < cb.cnt; e += kWave)
-                sm.cu[wave][e] = a.u[(size_t)r * a.ustride + sm.cidx[wave][e]];
-        }
-    }
-
-    // 5. the k-th largest candidate.  It is exact when it is not below any threshold used;
-    //    otherwise (a seed above the k-th value, tie overflow) the row takes the general path.
-    if (lane == 0) { sm.cnt[wave] = cb.ovf ? (1 << 28) : cb.cnt; sm.tauw[wave] = cb.tau; }
-    if (tid == 0) { sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; }
-    __syncthreads();
-    int total = 0;
-    uint32_t tmax = seed;
-#pragma unroll
-    for (int w = 0; w < kRowWaves; ++w) {
-        total += sm.cnt[w];
-        tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
-    }
-    if (total >= (1 << 28)) return false;  // ties overflowed a buffer
-    {
-        int cw, ce;
-        cand_locate(sm, tid, cw, ce);
-        uint32_t mxw = cw >= 0 ? sm.ckey[cw][ce] : 0u;
-        for (int t = NT + tid; t < total; t += NT) {
-            int w2, e2;
-            cand_locate(sm, t, w2, e2);
-            const uint32_t c2 = sm.ckey[w2][e2];
-            mxw = mxw > c2 ? mxw : c2;
-        }
-        mxw = wave_max_u32(mxw);
-        if (lane == 0) atomicMax(&sm.bc[2], mxw);
-    }
-    if (wave == 0) {
-        uint32_t kk = 0;
-        if (total >= k) {
-            if (total <= 256) {
-                uint32_t v[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    int w2, e2;
-                    cand_locate(sm, 4 * lane + i, w2, e2);
-                    v[i] = w2 >= 0 ? sm.ckey[w2][e2] : 0u;
-                }
-                kk = wave_kth_largest_256(v[0], v[1], v[2], v[3], k);
-            } else {
-                kk = wave_kth_largest_multi(&sm.ckey[0][0], kRowCap, sm.cnt, kRowWaves, k, sm.rhist[0]);
+        uint32_t b = 0;
+        if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)cb.cnt);
+        const int pbase = __builtin_amdgcn_readlane(b, 0);
+        if (pbase + cb.cnt <= kRowPack) {
+            for (int e = lane; e < cb.cnt; e += kWave) {
+                const int32_t ii = sm.cidx[wave][e];
+                sm.pkey[pbase + e] = sm.ckey[wave][e];
+                sm.pidx[pbase + e] = ii;
+                if (sampling) sm.pu[pbase + e] = a.u[(size_t)r * a.ustride + ii];
             }
         }
-        if (lane == 0) sm.bc[1] = kk;
+    }
+    if (lane == 0) {
+        sm.tauw[wave] = cb.tau;
+        if (cb.ovf) atomicOr(&sm.status, 2u);
+    }
+    __syncthreads();
+    const int total = (int)sm.npack;
+    if (sm.status != 0u || total > kRowPack) return false;  // tie overflow, too many candidates
+
+    // 5. the k-th largest candidate key.  Candidate t (packed order) goes to thread t, which
+    //    counts the keys above it, sixteen per step with 128-bit LDS reads: the candidate whose
+    //    count brackets k holds the k-th key, the one with none above holds the maximum.  The
+    //    k-th key is exact when it is not below any threshold used; otherwise (a seed above
+    //    the k-th value) the row takes the general path.
+    uint32_t tmax = seed;
+#pragma unroll
+    for (int w = 0; w < kRowWaves; ++w) tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
+    const bool mine = tid < total;
+    const uint32_t myk = mine ? sm.pkey[tid] : 0u;
+    if (tid == 0) { sm.bc[1] = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
+    __syncthreads();
+    if (wave * kWave < total) {
+        uint32_t gt = 0, ge = 0;
+        const uint4* p4 = reinterpret_cast<const uint4*>(sm.pkey);
+        int j = 0;
+        for (; j + 16 <= total; j += 16) {
+            const uint4 a0 = p4[j / 4], a1 = p4[j / 4 + 1], a2 = p4[j / 4 + 2], a3 = p4[j / 4 + 3];
+            const uint32_t v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                    a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { gt += v[i] > myk; ge += v[i] >= myk; }
+        }
+        for (; j < total; ++j) { const uint32_t kj = sm.pkey[j]; gt += kj > myk; ge += kj >= myk; }
+        if (mine && gt == 0u) sm.bc[2] = myk;                               // the maximum
+        if (mine && gt < (uint32_t)k && (uint32_t)k <= ge) sm.bc[1] = myk;  // the k-th key
     }
     __syncthreads();
     const uint32_t kth = sm.bc[1];
@@ -551,14 +542,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
 
     if (!sampling) {
         // greedy: lowest index at the maximum of the penalised logits (0 when every value is NaN)
-        int best = 0x7FFFFFFF;
-        for (int t = tid; t < total; t += NT) {
-            int w2, e2;
-            cand_locate(sm, t, w2, e2);
-            if (sm.ckey[w2][e2] == mk && sm.cidx[w2][e2] < best) best = sm.cidx[w2][e2];
-        }
-        best = (int)wave_min_u32((uint32_t)best);
-        if (lane == 0) atomicMin(&sm.bc[3], (uint32_t)best);
+        const uint32_t best = wave_min_u32((mine && myk == mk) ? (uint32_t)sm.pidx[tid] : 0x7FFFFFFFu);
+        if (lane == 0 && best != 0x7FFFFFFFu) atomicMin(&sm.bc[3], best);
         __syncthreads();
         if (tid == 0) {
             a.sampled[r] = (mk != 0u) ? (int32_t)sm.bc[3] : 0;
@@ -568,7 +553,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         return true;
     }
 
-    // 6. survivors of temperature + top-k + min-p
+    // 6. survivors of temperature + top-k + min-p: exact masses and race keys, compacted into
+    //    the survivor arrays (any order)
     const float Tt = prm.T;
     const float m = mk ? val_of(mk) / Tt : __builtin_nanf("");
     if (!(m > -__builtin_inff() && m < __builtin_inff())) return false;  // degenerate row
@@ -577,18 +563,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     if (tmax > 0x007FFFFFu && val_of(tmax - 1u) / Tt >= kth_y) return false;
     const float lp_min = (prm.min_p > 0.0f) ? log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)
                                             : -__builtin_inff();
-    uint64_t wsum = 0;
-    for (int base = 0; base < total; base += NT) {
-        const int t = base + tid;
+    if (wave * kWave < total) {
         bool keep = false;
-        float y = 0.0f, uu = 0.5f;
-        int32_t ii = 0;
-        if (t < total) {
-            int w2, e2;
-            cand_locate(sm, t, w2, e2);
-            y = val_of(sm.ckey[w2][e2]) / Tt;
-            ii = sm.cidx[w2][e2];
-            uu = sm.cu[w2][e2];
+        float y = 0.0f;
+        if (mine) {
+            y = val_of(myk) / Tt;
             keep = key_of(y) != 0u && y >= kth_y && (y - m) >= lp_min;
         }
         const uint64_t bal = __ballot(keep);
@@ -599,121 +578,113 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             const uint32_t pos = off + (uint32_t)lane_prefix(bal);
             if (pos < (uint32_t)kRowKeep) {
                 const float e = exp_det(y - m);
-                const uint64_t w = mass_of(e);
-                sm.sck[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)ii;
-                sm.sw[pos] = w;
-                sm.srk[pos] = e / (0.0f - log_det(uu));
-                wsum += w;
+                sm.sck[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.pidx[tid];
+                sm.sw[pos] = mass_of(e);
+                sm.srk[pos] = e / (0.0f - log_det(sm.pu[tid]));
             }
         }
     }
-    wsum = wave_sum_u64(wsum);
-    if (lane == 0) sm.red[wave][7] = wsum;  // slot 7: the race reduction below reuses 0..5
     __syncthreads();
-    uint64_t W = 0;
-#pragma unroll
-    for (int w = 0; w < kRowWaves; ++w) W += sm.red[w][7];
     const int n = (int)sm.nkeep;
-    if (n > kRowKeep) return false;
+    if (n == 0 || n > kRowKeep) return false;
 
-    // 7. top-p over exact masses (C_j = sum of w_i over survivors i <= j in (y, index) order),
-    //    then the race among the kept survivors
+    // 7. top-p over exact masses: survivor j (thread j) sums w_i over survivors i <= j in
+    //    (y, index) order, four per step with 128-bit LDS reads; then the race among the kept
+    //    survivors, reduced across the wave and the waves
     const float q32 = 1.0f - prm.top_p;
     const bool topp = q32 > 0.0f;
     const bool abl = topp && !(q32 < 1.0f);  // top_p <= 0: only the last survivor is kept
+    const int nws = (n + kWave - 1) / kWave;
+    if (wave >= nws) return true;
+    const bool mys = tid < n;
+    const uint64_t myck = mys ? sm.sck[tid] : ~0ull;
+    uint64_t C = 0, W = 0;
+    {
+        const uint4* c4 = reinterpret_cast<const uint4*>(sm.sck);
+        const uint4* w4 = reinterpret_cast<const uint4*>(sm.sw);
+        int j = 0;
+        for (; j + 4 <= n; j += 4) {
+            const uint4 c0 = c4[j / 2], c1 = c4[j / 2 + 1], v0 = w4[j / 2], v1 = w4[j / 2 + 1];
+            const uint64_t ck[4] = {((uint64_t)c0.y << 32) | c0.x, ((uint64_t)c0.w << 32) | c0.z,
+                                    ((uint64_t)c1.y << 32) | c1.x, ((uint64_t)c1.w << 32) | c1.z};
+            const uint64_t wv[4] = {((uint64_t)v0.y << 32) | v0.x, ((uint64_t)v0.w << 32) | v0.z,
+                                    ((uint64_t)v1.y << 32) | v1.x, ((uint64_t)v1.w << 32) | v1.z};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { W += wv[i]; C += ck[i] <= myck ? wv[i] : 0ull; }
+        }
+        for (; j < n; ++j) { const uint64_t wj = sm.sw[j]; W += wj; C += sm.sck[j] <= myck ? wj : 0ull; }
+    }
     const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
-    const int nw = (n + kWave - 1) / kWave;
-    // token, flags and survivor count from the merged race of the row
-    auto emit = [&](const RowRace& t) __attribute__((always_inline)) {
+    RowRace rs;
+    if (mys) {
+        const bool removed = topp && (abl ? (C != W) : (C <= thr && C != W));
+        if (removed) {
+            rs.cprev = C;
+            rs.nrem = 1;
+        } else {
+            rs.cat = C;
+            rs.nkept = 1;
+            rs.last = myck;
+            rs.add_key(sm.srk[tid], (int)(uint32_t)myck);
+        }
+    }
+    rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
+    rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);
+    if (nws > 1) {
+        if (lane == 0) {
+            sm.red[wave][0] = rs.best; sm.red[wave][1] = rs.last; sm.red[wave][2] = rs.cprev;
+            sm.red[wave][3] = rs.cat; sm.red[wave][4] = rs.second;
+            sm.red[wave][5] = ((uint64_t)rs.nrem << 32) | rs.nkept;
+        }
+        // only the waves that hold survivors are still here (the others have left, so no
+        // workgroup barrier): each of them counts itself in, and wave 0 waits for all of them.
+        // Every one of these waves reaches the increment; the wait is bounded all the same.
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane == 0) {
+            __hip_atomic_fetch_add(&sm.bc[4], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (wave == 0) {
+                for (int spin = 0; spin < (1 << 22); ++spin) {
+                    if (__hip_atomic_load(&sm.bc[4], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >=
+                        (uint32_t)nws) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+        }
+        if (wave != 0) return true;
+        wave_sync();
+        if (lane == 0) {
+            for (int w = 1; w < nws; ++w) {
+                RowRace o;
+                o.best = sm.red[w][0]; o.last = sm.red[w][1]; o.cprev = sm.red[w][2]; o.cat = sm.red[w][3];
+                o.second = (uint32_t)sm.red[w][4]; o.nkept = (uint32_t)sm.red[w][5];
+                o.nrem = (uint32_t)(sm.red[w][5] >> 32);
+                rs.merge(o);
+            }
+        }
+    } else if (wave != 0) {
+        return true;
+    }
+    if (lane == 0) {
         int32_t tok;
         uint32_t fl = 0;
-        if (t.best) {
-            tok = (int32_t)(0x7FFFFFFF - (uint32_t)(t.best & 0xFFFFFFFFu));
-            const float bk = u2f((uint32_t)(t.best >> 32));
-            if (t.second) {
-                const float sk = u2f(t.second - 1u);
+        if (rs.best) {
+            tok = (int32_t)(0x7FFFFFFF - (uint32_t)(rs.best & 0xFFFFFFFFu));
+            const float bk = u2f((uint32_t)(rs.best >> 32));
+            if (rs.second) {
+                const float sk = u2f(rs.second - 1u);
                 if ((double)sk >= (double)bk * (1.0 - 1e-6)) fl |= VWS_FLAG_RACE_NEAR_TIE;
             }
         } else {
-            tok = (int32_t)(uint32_t)(t.last & 0xFFFFFFFFu);
+            tok = (int32_t)(uint32_t)(rs.last & 0xFFFFFFFFu);
         }
         if (topp && !abl) {
             const uint64_t tol = (uint64_t)((double)W * 1e-6);
-            if ((n - (int)t.nkept > 0 && thr - t.cprev <= tol) || (t.cat > thr && t.cat - thr <= tol))
+            if ((rs.nrem > 0u && thr - rs.cprev <= tol) || (rs.cat > thr && rs.cat - thr <= tol))
                 fl |= VWS_FLAG_TOPP_NEAR_TIE;
         }
         a.sampled[r] = tok;
         if (a.flags) a.flags[r] = fl;
-        if (a.nkept) a.nkept[r] = (int32_t)t.nkept;
-    };
-    // survivor j's cumulative mass C_j given, its share of the race
-    auto race_of = [&](int j, uint64_t cj, uint64_t C) __attribute__((always_inline)) {
-        RowRace rs;
-        if (j < n) {
-            const bool removed = topp && (abl ? (C != W) : (C <= thr && C != W));
-            if (removed) {
-                rs.cprev = C;
-            } else {
-                rs.cat = C;
-                rs.nkept = 1;
-                rs.last = cj;
-                rs.add_key(sm.srk[j], (int)(uint32_t)cj);
-            }
-        }
-        return rs;
-    };
-    if (nw == 1) {
-        // up to 64 survivors: one per lane of wave 0; the other survivors' keys and masses are
-        // read with readlane, so the cumulative sums need no LDS round trips
-        if (wave != 0) return true;
-        const uint64_t cj = lane < n ? sm.sck[lane] : ~0ull;
-        const uint64_t wj = lane < n ? sm.sw[lane] : 0ull;
-        uint64_t C = 0;
-        if (topp) {
-            const uint32_t chi = (uint32_t)(cj >> 32), clo = (uint32_t)cj;
-            const uint32_t whi = (uint32_t)(wj >> 32), wlo = (uint32_t)wj;
-            for (int i = 0; i < n; ++i) {
-                // readlane returns int: widen through uint32_t (no sign extension)
-                const uint64_t ci = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(chi, i) << 32) |
-                                    (uint32_t)__builtin_amdgcn_readlane(clo, i);
-                const uint64_t wi = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(whi, i) << 32) |
-                                    (uint32_t)__builtin_amdgcn_readlane(wlo, i);
-                C += (ci <= cj) ? wi : 0ull;
-            }
-        }
-        RowRace rs = race_of(lane, cj, C);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) rs.shfl_merge(off);
-        if (lane == 0) emit(rs);
-        return true;
-    }
-    RowRace rs;
-    if (wave < nw) {
-        const int j = tid;
-        uint64_t cj = 0, C = 0;
-        if (j < n) {
-            cj = sm.sck[j];
-            if (topp)
-                for (int i = 0; i < n; ++i) C += (sm.sck[i] <= cj) ? sm.sw[i] : 0ull;
-        }
-        rs = race_of(j, cj, C);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) rs.shfl_merge(off);
-        if (lane == 0) {
-            sm.red[wave][0] = rs.best; sm.red[wave][1] = rs.last; sm.red[wave][2] = rs.cprev;
-            sm.red[wave][3] = rs.cat; sm.red[wave][4] = rs.second; sm.red[wave][5] = rs.nkept;
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        RowRace t;
-        for (int w = 0; w < nw; ++w) {
-            RowRace o;
-            o.best = sm.red[w][0]; o.last = sm.red[w][1]; o.cprev = sm.red[w][2]; o.cat = sm.red[w][3];
-            o.second = (uint32_t)sm.red[w][4]; o.nkept = (uint32_t)sm.red[w][5];
-            t.merge(o);
-        }
-        emit(t);
+        if (a.nkept) a.nkept[r] = (int32_t)rs.nkept;
     }
     return true;
 }
