@@ -17,6 +17,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -78,6 +79,22 @@ def cpu_baseline(w, rows: int, iters: int):
                         f"(vLLM-v1 Sampler op sequence on torch CPU tensors), median of {iters} "
                         f"after 3 warm-up, torch threads={cores}"),
                 seconds_per_iter=med)
+
+
+def pmc_traffic_bytes(config: int):
+    """HBM bytes per row_kernel launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (copy-calibrated); None when no summary covers this workload."""
+    if config != 3:
+        return None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "sample_c3_b256_v128256.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"^\| `void vws::row_kernel<float>\(vws::KArgs\)` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
+                  text, re.M)
+    return None if m is None else float(m.group(1)) * 1e6
 
 
 def main():
@@ -160,24 +177,30 @@ def main():
     torch.cuda.synchronize()
 
     # timed region: exactly `steps` calls, bracketed by synchronisation
+    # hipEvents on the launch stream bracket the same region: it holds only sampling-kernel
+    # launches (the input sets rotate by pointer), so region time / steps is the kernel's
+    # average launch duration, back-to-back dispatch gaps included.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     for i in range(args.steps):
         sample(ctypes.byref(argv[i % len(argv)]))
+    ev1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    kern_ms = ev0.elapsed_time(ev1) / args.steps
     st = L.vws_last_error()
     if st:
         log(f"last error: {st}")
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     rows_per_s = B * args.steps / (t1 - t0)
 
-    # per-kernel durations with hipEvents on the launch stream (same calls again)
+    # one hipEvent pair around each launch (same calls again): adds the event packets' cost
     ops.profile_begin(4 * args.steps + 8)
     for i in range(args.steps):
         sample(ctypes.byref(argv[i % len(argv)]))
     prof = ops.profile_end()
-    kern_ms = prof["sample"][0] / prof["sample"][1]
 
     alg_bytes = W.algorithmic_bytes(w, gpu_kept)
     gbps_e2e = alg_bytes / (ms_per_step * 1e-3) / 1e9
@@ -224,10 +247,11 @@ def main():
         "hbm_frac_end_to_end": gbps_e2e / PEAK_HBM_GBPS,
         "algorithmic_bytes_per_step": alg_bytes,
         "mean_survivors": float(gpu_kept.mean()),
-        "kernel_us": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
+        "kernel_us": {"sample": kern_ms * 1e3},
+        "kernel_us_event_pairs": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": gbps_kern / PEAK_HBM_GBPS, "traffic": None,
+            "frac": gbps_kern / PEAK_HBM_GBPS, "traffic": pmc_traffic_bytes(args.config),
             "kernel": "vws::row_kernel<float>",
         },
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},

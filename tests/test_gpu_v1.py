@@ -1,0 +1,160 @@
+"""GPU parity of the vLLM-v1 front end: ``Sampler.forward`` and the model runner's
+``execute_model`` / ``sample_tokens`` loop against the CPU oracle on the same inputs.
+
+Every random row is seeded, so the uniforms the sampler draws can be redrawn here from
+generators with the same seeds and handed to the oracle; tokens must then agree bit for bit and
+raw logprobs within rtol 1e-5."""
+from types import SimpleNamespace as NS
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler as O
+from vllm_webgpu_amd import workloads as W
+from vllm_webgpu_amd.v1.model_runner import ROCmModelRunner
+from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
+from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_uniforms
+
+pytestmark = pytest.mark.gpu
+
+
+def _gens(B, dev, base):
+    return {i: torch.Generator(device=dev).manual_seed(base + i) for i in range(B)}
+
+
+def _metadata(w, dev, gens, num_logprobs):
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    hist = t(w.output_ids) if w.output_ids is not None else None
+    no_pen = hist is None
+    greedy = ~(w.temperature >= np.float32(1e-5))
+    return SamplingMetadata(
+        temperature=None if greedy.all() else t(w.temperature), all_greedy=bool(greedy.all()),
+        all_random=not greedy.any(), top_p=t(w.top_p), top_k=t(w.top_k), generators=gens,
+        max_num_logprobs=num_logprobs, no_penalties=no_pen, prompt_token_ids=None,
+        frequency_penalties=t(w.frequency), presence_penalties=t(w.presence),
+        repetition_penalties=t(w.repetition), output_token_ids=[], min_p=t(w.min_p),
+        output_token_ids_tensor=hist)
+
+
+@pytest.mark.parametrize("cfg,scale,L", [(2, 0.25, None), (3, 0.05, None), (4, 0.05, None),
+                                         (5, 0.05, 20)])
+def test_sampler_forward_matches_oracle(cuda, cfg, scale, L):
+    w = W.config(cfg, scale=scale)
+    B, V = w.shape
+    if w.dtype == "bf16":
+        logits = torch.from_numpy(w.logits.view(np.int16)).to(cuda).view(torch.bfloat16)
+    else:
+        logits = torch.from_numpy(w.logits).to(cuda)
+    out = Sampler()(logits, _metadata(w, cuda, _gens(B, cuda, 7000), L))
+    u = draw_uniforms(B, V, _gens(B, cuda, 7000), cuda).cpu().numpy()
+    prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
+                        w.frequency)
+    ref = O.sample(w.logits_f32(), prm, u, output_ids=w.output_ids, num_logprobs=L)
+    tok = out.sampled_token_ids.cpu().numpy()
+    assert tok.shape == (B, 1) and tok.dtype == np.int32
+    bad = np.nonzero(tok[:, 0] != ref["token"])[0]
+    assert bad.size == 0, f"rows {bad[:8]}: gpu {tok[bad[:8], 0]} oracle {ref['token'][bad[:8]]}"
+    if L is None:
+        assert out.logprobs_tensors is None
+    else:
+        lp = out.logprobs_tensors
+        np.testing.assert_array_equal(lp.logprob_token_ids.cpu().numpy(), ref["lp_ids"])
+        np.testing.assert_array_equal(lp.selected_token_ranks.cpu().numpy(), ref["ranks"])
+        np.testing.assert_allclose(lp.logprobs.cpu().numpy(), ref["lp_vals"], rtol=1e-5, atol=1e-6)
+
+
+class _FakeModel:
+    """Deterministic logits per step (seeded), kept for the oracle check."""
+
+    def __init__(self, V, dev):
+        self.vocab_size, self.dev, self.step, self.history = V, dev, 0, []
+
+    def forward(self, input_ids, positions, scheduler_output):
+        rng = np.random.default_rng(900 + self.step)
+        x = rng.normal(0.0, 3.0, (input_ids.shape[0], self.vocab_size)).astype(np.float32)
+        # make recent inputs likely again so the penalties matter
+        ids = input_ids.cpu().numpy()
+        x[np.arange(len(ids)), ids % self.vocab_size] += 6.0
+        self.step += 1
+        self.history.append(x)
+        return torch.from_numpy(x).to(self.dev)
+
+
+def _sp(**kw):
+    base = dict(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0,
+                presence_penalty=0.0, frequency_penalty=0.0, seed=None, logprobs=None)
+    base.update(kw)
+    return NS(**base)
+
+
+def test_runner_steps_match_oracle(cuda):
+    V = 4096
+    model = _FakeModel(V, cuda)
+    runner = ROCmModelRunner(None, cuda, model, max_num_reqs=8, max_prompt_len=64,
+                             max_output_len=32)
+    params = {
+        "g": _sp(temperature=0.0, repetition_penalty=1.5),
+        "k": _sp(temperature=0.8, top_k=20, seed=11, presence_penalty=0.4),
+        "p": _sp(temperature=1.0, top_p=0.9, repetition_penalty=1.3, presence_penalty=0.2,
+                 frequency_penalty=0.1, seed=12),
+        "m": _sp(temperature=0.6, min_p=0.1, logprobs=5, seed=13, frequency_penalty=0.5),
+        "late": _sp(temperature=0.9, top_k=50, top_p=0.8, seed=14, repetition_penalty=1.2),
+    }
+    prompts = {"g": [1, 2, 3], "k": [5, 5, 9, 4000], "p": [17], "m": [2, 3, 5, 7, 11, 13],
+               "late": [100, 200]}
+    mirror = {r: torch.Generator(device=cuda).manual_seed(params[r].seed)
+              for r in params if params[r].seed is not None}
+    outputs = {r: [] for r in params}
+    active = []
+    for step in range(6):
+        new = ["g", "k", "p", "m"] if step == 0 else (["late"] if step == 3 else [])
+        finished = {"k"} if step == 3 else set()
+        active = [r for r in active if r not in finished] + new
+        so = NS(scheduled_new_reqs=[NS(req_id=r, prompt_token_ids=prompts[r],
+                                       sampling_params=params[r]) for r in new],
+                finished_req_ids=finished, num_scheduled_tokens={r: 1 for r in active})
+        assert runner.execute_model(so) is None
+        mro = runner.sample_tokens(None)
+        assert mro.req_ids == active
+        assert [len(t) for t in mro.sampled_token_ids] == [1] * len(active)
+
+        B = len(active)
+        u = np.full((B, V), 0.5, np.float32)
+        for i, r in enumerate(active):
+            if r in mirror:
+                row = torch.empty(V, dtype=torch.float32, device=cuda).uniform_(generator=mirror[r])
+                u[i] = row.clamp_(min=2.0 ** -24).cpu().numpy()
+        sps = [params[r] for r in active]
+        prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
+                            [s.top_p for s in sps], [s.min_p for s in sps],
+                            [s.repetition_penalty for s in sps], [s.presence_penalty for s in sps],
+                            [s.frequency_penalty for s in sps])
+        pw = max(len(prompts[r]) for r in active)
+        ow = max(1, max(len(outputs[r]) for r in active))
+        pr = np.full((B, pw), V, np.int32)
+        ou = np.full((B, ow), V, np.int32)
+        for i, r in enumerate(active):
+            pr[i, :len(prompts[r])] = prompts[r]
+            ou[i, :len(outputs[r])] = outputs[r]
+        L = 5 if any(params[r].logprobs for r in active) else None
+        ref = O.sample(model.history[-1], prm, u, prompt_ids=pr, output_ids=ou, num_logprobs=L)
+        got = [t[0] for t in mro.sampled_token_ids]
+        assert got == ref["token"].tolist(), f"step {step}: {got} vs {ref['token'].tolist()}"
+        if L is None:
+            assert mro.logprobs is None
+        else:
+            assert mro.logprobs.logprob_token_ids == ref["lp_ids"].tolist()
+            assert mro.logprobs.sampled_token_ranks == ref["ranks"].tolist()
+            np.testing.assert_allclose(np.array(mro.logprobs.logprobs), ref["lp_vals"], rtol=1e-5,
+                                       atol=1e-6)
+        for r, tok in zip(active, got):
+            outputs[r].append(tok)
+    # the device history table agrees with the host lists
+    b = runner.input_batch
+    for r in active:
+        st = b.requests[r]
+        n = len(outputs[r])
+        assert b.output_ids[st.slot, :n].tolist() == outputs[r] and st.output_token_ids == outputs[r]
+        assert int(b.output_lens[st.slot]) == n

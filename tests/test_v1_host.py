@@ -1,0 +1,141 @@
+"""Host logic of the vLLM-v1 front end (no GPU): metadata packing from the persistent batch,
+device-side history appends (exercised on CPU tensors), uniform draws, padding, and the loud
+failures the sampler owes its callers (no CPU fallback, unsupported processors refused)."""
+from types import SimpleNamespace as NS
+
+import pytest
+import torch
+
+from vllm_webgpu_amd.v1.model_runner import InputBatch, ROCmModelRunner, WebGPUModelRunner
+from vllm_webgpu_amd.v1.outputs import LogprobsTensors, ModelRunnerOutput, SamplerOutput
+from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
+from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_uniforms, pad_output_ids
+
+V = 100
+
+
+def sp(**kw):
+    base = dict(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition_penalty=1.0,
+                presence_penalty=0.0, frequency_penalty=0.0, seed=None, logprobs=None)
+    base.update(kw)
+    return NS(**base)
+
+
+def test_pad_output_ids_ragged():
+    ids, lens = pad_output_ids([[1, 2, 3], [], [7]], V, torch.device("cpu"))
+    assert ids.dtype == torch.int32 and ids.tolist() == [[1, 2, 3], [V, V, V], [7, V, V]]
+    assert lens.tolist() == [3, 0, 1]
+    ids, lens = pad_output_ids([[], []], V, torch.device("cpu"))
+    assert ids.shape == (2, 1) and ids.eq(V).all() and lens.tolist() == [0, 0]
+
+
+def test_draw_uniforms_open_interval_and_seeded_rows():
+    g1 = torch.Generator().manual_seed(5)
+    u = draw_uniforms(3, 5000, {1: g1}, torch.device("cpu"))
+    assert u.dtype == torch.float32 and u.shape == (3, 5000)
+    assert float(u.min()) > 0.0 and float(u.max()) < 1.0
+    g2 = torch.Generator().manual_seed(5)
+    u2 = draw_uniforms(3, 5000, {1: g2}, torch.device("cpu"))
+    assert torch.equal(u[1], u2[1])          # seeded row reproducible
+    assert not torch.equal(u[0], u2[0])      # unseeded rows are fresh draws
+
+
+def test_input_batch_metadata_fields():
+    b = InputBatch(4, 8, 6, V, torch.device("cpu"))
+    b.add_request("a", [1, 2, 3], sp(temperature=0.0))
+    b.add_request("b", [4, 5], sp(temperature=0.7, top_k=20, top_p=0.9, seed=11, logprobs=3,
+                                  repetition_penalty=1.2))
+    b.add_request("c", [6], sp(temperature=1.0, top_k=-1, min_p=0.05, logprobs=1))
+    m = b.make_sampling_metadata(["c", "a", "b"])
+    assert isinstance(m, SamplingMetadata)
+    assert not m.all_greedy and not m.all_random
+    assert m.temperature.tolist() == pytest.approx([1.0, 0.0, 0.7])
+    assert m.top_k.tolist() == [0, 0, 20]           # -1 normalised to "off"
+    assert m.top_p.tolist() == pytest.approx([1.0, 1.0, 0.9])
+    assert m.min_p.tolist() == pytest.approx([0.05, 0.0, 0.0])
+    assert m.max_num_logprobs == 3
+    assert set(m.generators) == {2}                 # only the seeded random row
+    assert not m.no_penalties
+    assert m.prompt_token_ids.tolist()[1] == [1, 2, 3]   # widest prompt: 3 columns
+    assert m.prompt_token_ids.tolist()[0] == [6, V, V]
+    assert m.output_token_ids_tensor.eq(V).all() and m.output_token_lens.tolist() == [0, 0, 0]
+
+
+def test_input_batch_all_greedy_and_off_switches():
+    b = InputBatch(2, 4, 4, V, torch.device("cpu"))
+    b.add_request("a", [1], sp(temperature=0.0))
+    b.add_request("b", [2], sp(temperature=1e-6))
+    m = b.make_sampling_metadata(["a", "b"])
+    assert m.all_greedy and m.temperature is None
+    assert m.top_k is None and m.top_p is None and m.min_p is None
+    assert m.no_penalties and m.prompt_token_ids is None and m.output_token_ids_tensor is None
+    assert m.max_num_logprobs is None
+
+
+def test_input_batch_append_and_slot_reuse():
+    b = InputBatch(2, 4, 3, V, torch.device("cpu"))
+    b.add_request("a", [1], sp(repetition_penalty=1.1))
+    b.add_request("b", [2], sp(repetition_penalty=1.1))
+    with pytest.raises(RuntimeError):
+        b.add_request("c", [3], sp())
+    for step in range(4):   # the table holds 3 ids: the 4th append is dropped, not wrapped
+        b.append_sampled(["b", "a"], torch.tensor([10 + step, 20 + step], dtype=torch.int32))
+    sa, sb = b.requests["a"].slot, b.requests["b"].slot
+    assert b.output_ids[sa].tolist() == [20, 21, 22] and b.output_ids[sb].tolist() == [10, 11, 12]
+    assert b.output_lens[sa].item() == 3
+    b.remove_request("a")
+    b.add_request("c", [9, 9], sp())
+    assert b.requests["c"].slot == sa
+    assert b.output_ids[sa].eq(V).all() and b.output_lens[sa].item() == 0
+    assert b.prompt_ids[sa].tolist()[:3] == [9, 9, V]
+    with pytest.raises(ValueError):
+        b.add_request("d", [1] * 5, sp())          # longer than max_prompt_len
+    with pytest.raises(ValueError):
+        b.add_request("c", [1], sp())              # duplicate id
+
+
+def test_sampler_refuses_cpu_logits_and_unsupported_processors():
+    s = Sampler()
+    b = InputBatch(1, 2, 2, V, torch.device("cpu"))
+    b.add_request("a", [1], sp())
+    m = b.make_sampling_metadata(["a"])
+    with pytest.raises(ValueError, match="ROCm device"):
+        s(torch.zeros(1, V), m)                    # no host fallback
+    m.allowed_token_ids_mask = torch.zeros(1, V, dtype=torch.bool)
+    with pytest.raises(NotImplementedError):
+        s(torch.zeros(1, V), m)
+    with pytest.raises(NotImplementedError):
+        Sampler(logprobs_mode="processed_logprobs")
+
+
+def test_runner_without_model_and_grammar():
+    r = WebGPUModelRunner(None, device="cpu")
+    assert r is not None and WebGPUModelRunner is ROCmModelRunner
+    assert r.execute_model(NS()) is None and r.sample_tokens(None) is None
+    with pytest.raises(NotImplementedError):
+        r.load_model()
+    assert r.supported_worker_tasks() == ("generate",)
+
+
+def test_output_containers():
+    lp = LogprobsTensors(torch.tensor([[3, 1, 2]], dtype=torch.int32),
+                         torch.tensor([[-1.5, -0.5, -1.0]]), torch.tensor([3], dtype=torch.int32))
+    lists = lp.tolists()
+    assert lists.logprob_token_ids == [[3, 1, 2]] and lists.sampled_token_ranks == [3]
+    out = SamplerOutput(sampled_token_ids=torch.tensor([[3]], dtype=torch.int32), logprobs_tensors=lp)
+    assert out.sampled_token_ids.shape == (1, 1)
+    mro = ModelRunnerOutput(req_ids=["x"], req_id_to_index={"x": 0}, sampled_token_ids=[[3]],
+                            logprobs=lists)
+    assert mro.req_id_to_index["x"] == 0
+
+
+def test_platform_routes_to_worker():
+    from vllm_webgpu_amd.platform import WORKER_CLS, MI355XPlatform, WebGPUPlatform
+    cfg = NS(parallel_config=NS(worker_cls="auto", distributed_executor_backend=None))
+    WebGPUPlatform.check_and_update_config(cfg)
+    assert cfg.parallel_config.worker_cls == WORKER_CLS
+    assert cfg.parallel_config.distributed_executor_backend == "uni"
+    mod, cls = WORKER_CLS.rsplit(".", 1)
+    import importlib
+    assert getattr(importlib.import_module(mod), cls) is not None
+    assert MI355XPlatform.is_pin_memory_available()

@@ -1,0 +1,274 @@
+"""Model runner: caches device logits in ``execute_model`` and samples them in ``sample_tokens``.
+
+Mirrors the sampling half of ``WebGPUModelRunner`` (``vllm_webgpu/v1/model_runner.py:54-176``):
+same method names (``execute_model``, ``sample_tokens``, ``supported_worker_tasks``,
+``reset_mm_cache``, ``reset_encoder_cache``), same ``_last_logits`` cache (``:63,140``), same
+decode-only batching rule (``:129-137``: the last token of each request, position = length - 1).
+Where the reference argmaxes numpy logits on the host and returns ``None`` from
+``sample_tokens`` (``:145,164-166``), this runner keeps the logits on the GPU, builds a vLLM-v1
+``SamplingMetadata`` from a persistent batch and calls the device ``Sampler``.
+
+The persistent batch (``InputBatch``) holds every running request's prompt and generated ids in
+device tables padded with ``vocab_size``; each step gathers the scheduled rows and, after
+sampling, appends the sampled ids on the device, so histories are never re-uploaded.  Host
+copies of the generated ids (needed by ``SamplingMetadata.output_token_ids`` and the engine)
+come from the one device-to-host copy of the sampled ids per step.
+
+Building the model and its weights is outside this package: ``model`` is any object with the
+reference model's ``forward(input_ids, positions, scheduler_output) -> logits [B, V]``
+(``vllm_webgpu/models/llama.py:222-237``) that returns a ROCm-device tensor.
+"""
+from __future__ import annotations
+
+import logging
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+
+from .outputs import ModelRunnerOutput
+from .sample.metadata import SamplingMetadata
+from .sample.sampler import Sampler
+
+logger = logging.getLogger(__name__)
+
+_SAMPLING_EPS = 1e-5
+
+
+def _param(sp: Any, name: str, default):
+    v = getattr(sp, name, default) if sp is not None else default
+    return default if v is None else v
+
+
+@dataclass
+class CachedRequestState:
+    req_id: str
+    prompt_token_ids: list[int]
+    sampling_params: Any
+    generator: torch.Generator | None
+    slot: int
+    output_token_ids: list[int] = field(default_factory=list)
+
+    @property
+    def num_tokens(self) -> int:
+        return len(self.prompt_token_ids) + len(self.output_token_ids)
+
+
+class InputBatch:
+    """Persistent per-request sampling state, resident on the device between steps.
+
+    Slots are reused as requests finish.  ``prompt_ids[slot]`` / ``output_ids[slot]`` hold the
+    request's ids padded with ``vocab_size`` (the padding id the sampler ignores);
+    ``output_lens[slot]`` counts the generated ids.
+    """
+
+    def __init__(self, max_num_reqs: int, max_prompt_len: int, max_output_len: int,
+                 vocab_size: int, device: torch.device) -> None:
+        self.max_num_reqs = max_num_reqs
+        self.max_prompt_len = max_prompt_len
+        self.max_output_len = max_output_len
+        self.vocab_size = vocab_size
+        self.device = device
+        self.prompt_ids = torch.full((max_num_reqs, max(max_prompt_len, 1)), vocab_size,
+                                     dtype=torch.int32, device=device)
+        self.output_ids = torch.full((max_num_reqs, max(max_output_len, 1)), vocab_size,
+                                     dtype=torch.int32, device=device)
+        self.output_lens = torch.zeros(max_num_reqs, dtype=torch.int32, device=device)
+        self.requests: dict[str, CachedRequestState] = {}
+        self._free = list(range(max_num_reqs - 1, -1, -1))
+
+    def add_request(self, req_id: str, prompt_token_ids: list[int], sampling_params: Any) -> int:
+        if req_id in self.requests:
+            raise ValueError(f"request {req_id!r} is already in the batch")
+        if len(prompt_token_ids) > self.max_prompt_len:
+            raise ValueError(f"prompt of {len(prompt_token_ids)} tokens exceeds "
+                             f"max_prompt_len={self.max_prompt_len}")
+        if not self._free:
+            raise RuntimeError(f"batch is full ({self.max_num_reqs} requests)")
+        slot = self._free.pop()
+        seed = _param(sampling_params, "seed", None)
+        gen = None
+        if seed is not None:
+            gen = torch.Generator(device=self.device)
+            gen.manual_seed(int(seed))
+        self.requests[req_id] = CachedRequestState(req_id, list(prompt_token_ids),
+                                                   sampling_params, gen, slot)
+        row = torch.full((self.prompt_ids.shape[1],), self.vocab_size, dtype=torch.int32)
+        if prompt_token_ids:
+            row[:len(prompt_token_ids)] = torch.as_tensor(prompt_token_ids, dtype=torch.int32)
+        self.prompt_ids[slot].copy_(row, non_blocking=False)
+        self.output_ids[slot].fill_(self.vocab_size)
+        self.output_lens[slot] = 0
+        return slot
+
+    def remove_request(self, req_id: str) -> None:
+        st = self.requests.pop(req_id, None)
+        if st is not None:
+            self._free.append(st.slot)
+
+    def make_sampling_metadata(self, req_ids: list[str]) -> SamplingMetadata:
+        states = [self.requests[r] for r in req_ids]
+        dev = self.device
+        B = len(states)
+        sps = [s.sampling_params for s in states]
+        temp = [float(_param(sp, "temperature", 1.0)) for sp in sps]
+        greedy = [t < _SAMPLING_EPS for t in temp]
+        top_k = [int(_param(sp, "top_k", 0)) for sp in sps]
+        top_k = [0 if k < 0 else k for k in top_k]            # -1 and 0 both mean "off"
+        top_p = [float(_param(sp, "top_p", 1.0)) for sp in sps]
+        min_p = [float(_param(sp, "min_p", 0.0)) for sp in sps]
+        rep = [float(_param(sp, "repetition_penalty", 1.0)) for sp in sps]
+        pres = [float(_param(sp, "presence_penalty", 0.0)) for sp in sps]
+        freq = [float(_param(sp, "frequency_penalty", 0.0)) for sp in sps]
+        lps = [_param(sp, "logprobs", None) for sp in sps]
+        lps = [int(x) for x in lps if x is not None]
+
+        def t(x, dtype):
+            return torch.tensor(x, dtype=dtype).to(dev, non_blocking=True)
+
+        all_greedy = all(greedy)
+        no_penalties = all(r == 1.0 for r in rep) and not any(pres) and not any(freq)
+        slots = t([s.slot for s in states], torch.int64)
+        # gather only the populated columns: the kernel reads every history column it is given
+        pw = max(1, max((len(s.prompt_token_ids) for s in states), default=1))
+        ow = max(1, min(self.output_ids.shape[1],
+                        max((len(s.output_token_ids) for s in states), default=1)))
+        # Rows that are not random draw uniforms too (one [B, V] draw), but the kernel ignores them.
+        gens = {i: s.generator for i, s in enumerate(states)
+                if s.generator is not None and not greedy[i]}
+        return SamplingMetadata(
+            temperature=None if all_greedy else t(temp, torch.float32),
+            all_greedy=all_greedy,
+            all_random=not any(greedy),
+            top_p=None if all(p >= 1.0 for p in top_p) else t(top_p, torch.float32),
+            top_k=None if not any(top_k) else t(top_k, torch.int32),
+            generators=gens,
+            max_num_logprobs=max(lps) if lps else None,
+            no_penalties=no_penalties,
+            prompt_token_ids=None if no_penalties else self.prompt_ids[:, :pw].index_select(0, slots),
+            frequency_penalties=t(freq, torch.float32),
+            presence_penalties=t(pres, torch.float32),
+            repetition_penalties=t(rep, torch.float32),
+            output_token_ids=[s.output_token_ids for s in states],
+            min_p=None if not any(min_p) else t(min_p, torch.float32),
+            output_token_ids_tensor=(None if no_penalties
+                                    else self.output_ids[:, :ow].index_select(0, slots)),
+            output_token_lens=None if no_penalties else self.output_lens.index_select(0, slots),
+        ) if B else None
+
+    def append_sampled(self, req_ids: list[str], sampled: torch.Tensor) -> None:
+        """Appends ``sampled`` (int32 [B] on the device) to the output tables, on the device."""
+        if not req_ids:
+            return
+        slots = torch.tensor([self.requests[r].slot for r in req_ids], dtype=torch.int64,
+                             device=self.device)
+        pos = self.output_lens.index_select(0, slots).long()
+        ok = pos < self.output_ids.shape[1]
+        self.output_ids[slots[ok], pos[ok]] = sampled.to(torch.int32)[ok]
+        self.output_lens.index_add_(0, slots, ok.to(torch.int32))
+
+
+class ROCmModelRunner:
+    """Runner for one MI355X: model forward -> cached device logits -> device sampler."""
+
+    def __init__(self, vllm_config: Any, device: torch.device | str | None = None,
+                 model: Any = None, max_num_reqs: int = 1024, max_prompt_len: int = 8192,
+                 max_output_len: int = 8192, vocab_size: int | None = None) -> None:
+        self.vllm_config = vllm_config
+        self.device = torch.device(device if device is not None else "cuda")
+        self.model = model
+        self.sampler = Sampler()
+        self._last_logits: torch.Tensor | None = None
+        self._last_req_ids: list[str] = []
+        self._max = (max_num_reqs, max_prompt_len, max_output_len)
+        self._vocab_size = vocab_size
+        self.input_batch: InputBatch | None = None
+
+    # -- state ---------------------------------------------------------------------------
+    def _batch(self, vocab_size: int) -> InputBatch:
+        if self.input_batch is None:
+            self.input_batch = InputBatch(*self._max, vocab_size, self.device)
+        elif self.input_batch.vocab_size != vocab_size:
+            raise ValueError(f"vocab size changed from {self.input_batch.vocab_size} to {vocab_size}")
+        return self.input_batch
+
+    def _update_states(self, scheduler_output: Any, vocab_size: int) -> list[str]:
+        batch = self._batch(vocab_size)
+        for rid in getattr(scheduler_output, "finished_req_ids", ()) or ():
+            batch.remove_request(rid)
+        for nr in getattr(scheduler_output, "scheduled_new_reqs", ()) or ():
+            batch.add_request(nr.req_id, list(nr.prompt_token_ids or []), nr.sampling_params)
+        order = list(getattr(scheduler_output, "num_scheduled_tokens", {}) or {})
+        if not order:
+            cached = getattr(scheduler_output, "scheduled_cached_reqs", None)
+            order = list(getattr(cached, "req_ids", []) or [])
+            order += [nr.req_id for nr in getattr(scheduler_output, "scheduled_new_reqs", ()) or ()]
+        return order
+
+    def load_model(self) -> None:
+        if self.model is None:
+            raise NotImplementedError("model construction is not part of the sampling package; "
+                                      "pass a model object with forward(input_ids, positions, "
+                                      "scheduler_output) -> device logits")
+
+    # -- steps -----------------------------------------------------------------------------
+    def execute_model(self, scheduler_output: Any) -> None:
+        """Runs the model on the scheduled requests and caches the logits (returns ``None``;
+        ``sample_tokens`` produces the step's output)."""
+        if self.model is None:
+            return None
+        try:
+            vocab = self._vocab_size or getattr(self.model, "vocab_size")
+            req_ids = self._update_states(scheduler_output, vocab)
+            if not req_ids:
+                self._last_logits, self._last_req_ids = None, []
+                return None
+            reqs = [self.input_batch.requests[r] for r in req_ids]
+            last = [(s.output_token_ids or s.prompt_token_ids)[-1:] for s in reqs]
+            input_ids = torch.tensor([x[0] if x else 0 for x in last], dtype=torch.int32)
+            positions = torch.tensor([s.num_tokens - 1 for s in reqs], dtype=torch.int32)
+            logits = self.model.forward(input_ids.to(self.device), positions.to(self.device),
+                                        scheduler_output)
+            if logits.shape != (len(req_ids), vocab):
+                raise ValueError(f"model returned logits {tuple(logits.shape)}, expected "
+                                 f"({len(req_ids)}, {vocab})")
+            self._last_logits, self._last_req_ids = logits, req_ids
+            return None
+        except Exception as e:
+            logger.exception("execute_model failed: %s", e)
+            raise
+
+    def sample_tokens(self, grammar_output: Any) -> ModelRunnerOutput | None:
+        """Samples the cached logits; one device-to-host copy of the sampled ids per step."""
+        if self._last_logits is None:
+            return None
+        if grammar_output is not None and getattr(grammar_output, "grammar_bitmask", None) is not None:
+            raise NotImplementedError("structured-output bitmasks are not applied by the device sampler")
+        req_ids, logits = self._last_req_ids, self._last_logits
+        self._last_logits = None
+        batch = self.input_batch
+        md = batch.make_sampling_metadata(req_ids)
+        out = self.sampler(logits, md)
+        sampled = out.sampled_token_ids[:, 0]
+        batch.append_sampled(req_ids, sampled)
+        ids = sampled.tolist()
+        for r, tok in zip(req_ids, ids):
+            batch.requests[r].output_token_ids.append(tok)
+        lp = out.logprobs_tensors.tolists() if out.logprobs_tensors is not None else None
+        return ModelRunnerOutput(req_ids=list(req_ids),
+                                 req_id_to_index={r: i for i, r in enumerate(req_ids)},
+                                 sampled_token_ids=[[t] for t in ids], logprobs=lp,
+                                 prompt_logprobs_dict={}, pooler_output=[])
+
+    def supported_worker_tasks(self) -> tuple[str, ...]:
+        return ("generate",)
+
+    def reset_mm_cache(self) -> None:
+        pass
+
+    def reset_encoder_cache(self) -> None:
+        pass
+
+
+# Drop-in name of the reference class this runner replaces (vllm_webgpu/v1/model_runner.py:54).
+WebGPUModelRunner = ROCmModelRunner

@@ -1,0 +1,47 @@
+"""``SamplingMetadata``: the per-step batch of sampling parameters, in vLLM-v1's shape.
+
+The reference has no sampling metadata of its own: its runner argmaxes on the host
+(``vllm_webgpu/v1/model_runner.py:145``) and leaves everything else to vLLM's sampler
+(``docs/superpowers/specs/2026-06-29-vllm-webgpu-design.md:451``).  The fields below are vLLM-v1's
+(``vllm/v1/sample/metadata.py``), plus ``min_p`` as a tensor (vLLM-v1 carries it inside its
+built-in min-p logits processor) and ``output_token_ids_tensor``, an optional padded device copy
+of ``output_token_ids`` that a persistent batch can keep resident between steps.
+
+Conventions the kernels rely on:
+
+* ``temperature`` is float32 ``[B]``; rows with ``temperature < 1e-5`` are greedy.  ``None``
+  means every row is greedy (``all_greedy``).
+* ``top_k`` int32 ``[B]`` (``<= 0`` or ``>= V`` is off), ``top_p`` / ``min_p`` float32 ``[B]``
+  (``1.0`` / ``0.0`` are off).  ``None`` turns the step off for the whole batch.
+* ``prompt_token_ids`` int32/int64 ``[B, P]`` padded with ``vocab_size`` (vLLM pads with V); any
+  id outside ``[0, V)`` is padding.
+* ``generators`` maps a row index to the ``torch.Generator`` of a seeded request; the uniforms of
+  that row are drawn from it, the others from torch's default generator.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass
+class SamplingMetadata:
+    temperature: torch.Tensor | None
+    all_greedy: bool
+    all_random: bool
+    top_p: torch.Tensor | None
+    top_k: torch.Tensor | None
+    generators: dict[int, torch.Generator]
+    max_num_logprobs: int | None
+    no_penalties: bool
+    prompt_token_ids: torch.Tensor | None
+    frequency_penalties: torch.Tensor | None
+    presence_penalties: torch.Tensor | None
+    repetition_penalties: torch.Tensor | None
+    output_token_ids: list[list[int]]
+    min_p: torch.Tensor | None = None
+    allowed_token_ids_mask: torch.Tensor | None = None
+    bad_words_token_ids: dict[int, list[list[int]]] = field(default_factory=dict)
+    output_token_ids_tensor: torch.Tensor | None = None
+    output_token_lens: torch.Tensor | None = None

@@ -1,0 +1,98 @@
+"""``Sampler``: vLLM-v1's sampling layer as one call into the gfx950 library.
+
+Reference anchors: the reference samples greedily on the host
+(``vllm_webgpu/v1/model_runner.py:139-159``, ``logits.argmax(axis=-1)``) and otherwise defers to
+vLLM's CPU sampler (``docs/superpowers/specs/2026-06-29-vllm-webgpu-design.md:451``).  This class
+keeps vLLM-v1's ``Sampler.forward(logits, sampling_metadata) -> SamplerOutput`` signature and its
+order of operations -- raw logprobs of the unprocessed logits, penalties, greedy argmax of the
+penalised logits, temperature, min-p, top-k, top-p, exponential race, logprob gather -- but runs
+all of it in a single stream-ordered kernel launch (``vws_sample``) on device-resident logits.
+
+Random rows consume caller-side uniforms ``u`` in (0, 1) drawn here with torch's generators
+(the request's own generator for seeded rows), and the race key is ``p / (-ln u)``: an
+exponential race, as vLLM's ``random_sample`` (``probs / q.exponential_()``).
+
+There is no host fallback: without the HIP library, or for logits that are not on a ROCm device,
+``forward`` raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from ... import ops
+from ..outputs import LogprobsTensors, SamplerOutput
+from .metadata import SamplingMetadata
+
+_U_MIN = 2.0 ** -24   # smallest uniform handed to the race: -ln(u) stays finite and positive
+
+
+def draw_uniforms(B: int, V: int, generators: dict[int, torch.Generator],
+                  device: torch.device) -> torch.Tensor:
+    """float32 ``[B, V]`` uniforms in (0, 1); row ``i`` comes from ``generators[i]`` if present."""
+    u = torch.rand((B, V), dtype=torch.float32, device=device)
+    for i, g in generators.items():
+        u[i].uniform_(generator=g)
+    return u.clamp_(min=_U_MIN)
+
+
+def pad_output_ids(output_token_ids: list[list[int]], vocab_size: int,
+                   device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Packs ragged output histories into int32 ``[B, W]`` padded with ``vocab_size`` (+ lengths)."""
+    B = len(output_token_ids)
+    W = max((len(t) for t in output_token_ids), default=0)
+    host = torch.full((B, max(W, 1)), vocab_size, dtype=torch.int32,
+                      pin_memory=torch.cuda.is_available())
+    lens = torch.empty(B, dtype=torch.int32, pin_memory=torch.cuda.is_available())
+    for i, t in enumerate(output_token_ids):
+        if t:
+            host[i, :len(t)] = torch.as_tensor(t, dtype=torch.int32)
+        lens[i] = len(t)
+    return host.to(device, non_blocking=True), lens.to(device, non_blocking=True)
+
+
+class Sampler:
+    """vLLM-v1 ``Sampler`` facade over ``vws_sample``."""
+
+    def __init__(self, logprobs_mode: str = "raw_logprobs") -> None:
+        if logprobs_mode != "raw_logprobs":
+            raise NotImplementedError(
+                f"logprobs_mode {logprobs_mode!r}: only 'raw_logprobs' (log-softmax of the "
+                "unprocessed logits) is computed by the device sampler")
+        self.logprobs_mode = logprobs_mode
+
+    def __call__(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata) -> SamplerOutput:
+        return self.forward(logits, sampling_metadata)
+
+    def forward(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata) -> SamplerOutput:
+        m = sampling_metadata
+        if m.allowed_token_ids_mask is not None or m.bad_words_token_ids:
+            raise NotImplementedError(
+                "allowed-token masks and bad-words lists are not applied by the device sampler")
+        if logits.dim() != 2:
+            raise ValueError(f"logits must be [num_reqs, vocab] (got {tuple(logits.shape)})")
+        B, V = logits.shape
+        dev = logits.device
+
+        temperature = None if m.all_greedy else m.temperature
+        uniforms = None
+        if temperature is not None:
+            uniforms = draw_uniforms(B, V, m.generators, dev)
+
+        penalties = {}
+        if not m.no_penalties:
+            out_ids, out_lens = m.output_token_ids_tensor, m.output_token_lens
+            if out_ids is None and any(m.output_token_ids):
+                out_ids, out_lens = pad_output_ids(m.output_token_ids, V, dev)
+            penalties = dict(repetition_penalty=m.repetition_penalties,
+                             presence_penalty=m.presence_penalties,
+                             frequency_penalty=m.frequency_penalties,
+                             prompt_ids=m.prompt_token_ids, output_ids=out_ids,
+                             output_lens=out_lens)
+
+        res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
+                         min_p=m.min_p, uniforms=uniforms, num_logprobs=m.max_num_logprobs,
+                         **penalties)
+        lp = None
+        if m.max_num_logprobs is not None:
+            lp = LogprobsTensors(res.logprob_ids, res.logprob_vals, res.logprob_ranks)
+        return SamplerOutput(sampled_token_ids=res.sampled.unsqueeze(-1), logprobs_tensors=lp)
