@@ -113,7 +113,9 @@ int32_t vws_abi_version(void);
 const char* vws_last_error(void);
 
 /* Bytes of workspace vws_sample needs for this shape and history width
- * (prompt_width + output_width). */
+ * (prompt_width + output_width): the history hash of rows served by the multi-pass path,
+ * B x (power of two >= 2 x history_width, at least 64) x 12 bytes.  0 without a history, in
+ * which case `workspace` may be NULL. */
 size_t vws_sample_workspace_size(int32_t batch, int32_t vocab, int32_t history_width);
 
 /* Clears a workspace on `stream` (a fill kernel, safe under graph capture).  Required once

@@ -61,15 +61,21 @@ def test_abi_constants_match_header(L):
 
 def test_workspace_sizes(L):
     a = L.vws_sample_workspace_size(256, 128256, 512)
-    b = L.vws_sample_workspace_size(256, 128256, 0)
-    assert a > b > 0 and a % 256 == 0 and b % 256 == 0
-    assert L.vws_sample_workspace_size(512, 128256, 0) > b
+    # history hash only: 256 rows x 1024 slots (power of two >= 2 x 512) x 3 words
+    assert a == 256 * 1024 * 12
+    assert L.vws_sample_workspace_size(256, 128256, 0) == 0       # no history: no workspace
+    assert L.vws_sample_workspace_size(512, 128256, 512) == 2 * a
+    assert L.vws_sample_workspace_size(4, 100, 1) == 4 * 64 * 12  # at least 64 slots
     assert L.vws_sample_workspace_size(0, 100, 0) == 0
     assert L.vws_sample_workspace_size(4, 100, -1) == 0
-    assert L.vws_topk_workspace_size(8, 1000, 50) > 0
+    t = L.vws_topk_workspace_size(8, 1000, 50)
+    assert t > 0 and t % 256 == 0
 
 
 FAKE = 0x10000          # host-side stand-in addresses: validation never dereferences them
+
+
+HIST = dict(output_ids=FAKE, output_width=8, output_row_stride=8)   # needs a workspace
 
 
 def _args(L, **over):
@@ -112,9 +118,9 @@ def test_valid_args_pass(L):
     (dict(prompt_ids=FAKE, prompt_width=-1), _lib.ERR_INVALID_ARGUMENT, "prompt_width"),
     (dict(output_ids=FAKE, output_width=8, output_row_stride=4), _lib.ERR_INVALID_ARGUMENT,
      "output_row_stride"),
-    (dict(workspace=None), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
-    (dict(workspace_bytes=256), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
-    (dict(workspace=0x100010), _lib.ERR_INVALID_ARGUMENT, "aligned"),
+    (dict(HIST, workspace=None), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+    (dict(HIST, workspace_bytes=256), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+    (dict(HIST, workspace=0x100010, workspace_bytes=1 << 20), _lib.ERR_INVALID_ARGUMENT, "aligned"),
     (dict(struct_size=8), _lib.ERR_INVALID_ARGUMENT, "struct_size"),
 ])
 def test_invalid_args_rejected(L, over, code, msg):
@@ -127,6 +133,10 @@ def test_history_grows_the_required_workspace(L):
     assert _status(L, a) == _lib.ERR_WORKSPACE_TOO_SMALL
     a.workspace_bytes = L.vws_sample_workspace_size(4, 1000, 512)
     assert _status(L, a) == _lib.OK
+
+
+def test_no_history_needs_no_workspace(L):
+    assert _status(L, _args(L, workspace=None, workspace_bytes=0)) == _lib.OK
 
 
 def test_greedy_batches_need_no_uniforms(L):

@@ -162,7 +162,8 @@ int validate_sample(const vws_sample_args* a) {
     if ((st = validate_history(a->prompt_ids, a->prompt_row_stride, a->prompt_width, "prompt"))) return st;
     if ((st = validate_history(a->output_ids, a->output_row_stride, a->output_width, "output"))) return st;
     const int hw = (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0);
-    const size_t need = ws_layout(a->batch, a->vocab, hw).total;
+    const size_t need = ws_layout(a->batch, a->vocab, hw, false).total;
+    if (need == 0) return VWS_OK;
     if (!a->workspace) return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace is NULL (need %zu bytes)", need);
     if (a->workspace_bytes < need)
         return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", a->workspace_bytes, need);
@@ -171,7 +172,7 @@ int validate_sample(const vws_sample_args* a) {
     return VWS_OK;
 }
 
-KArgs make_kargs(int B, int V, const void* logits, int64_t stride, void* ws, int hw) {
+KArgs make_kargs(int B, int V, const void* logits, int64_t stride, void* ws, int hw, bool parts) {
     KArgs k;
     std::memset(&k, 0, sizeof(k));
     k.logits = logits;
@@ -179,13 +180,15 @@ KArgs make_kargs(int B, int V, const void* logits, int64_t stride, void* ws, int
     k.B = B;
     k.V = V;
     k.L = -1;
-    const WsLayout w = ws_layout(B, V, hw);
+    const WsLayout w = ws_layout(B, V, hw, parts);
     char* base = static_cast<char*>(ws);
-    k.row_counter = reinterpret_cast<uint32_t*>(base + w.counter);
-    k.row_state = reinterpret_cast<uint32_t*>(base + w.state);
-    k.part_meta = reinterpret_cast<uint32_t*>(base + w.meta);
-    k.part_list = reinterpret_cast<uint2*>(base + w.list);
-    k.hist_hash = reinterpret_cast<uint32_t*>(base + w.hash);
+    if (parts) {
+        k.row_counter = reinterpret_cast<uint32_t*>(base + w.counter);
+        k.row_state = reinterpret_cast<uint32_t*>(base + w.state);
+        k.part_meta = reinterpret_cast<uint32_t*>(base + w.meta);
+        k.part_list = reinterpret_cast<uint2*>(base + w.list);
+    }
+    k.hist_hash = w.hs_row ? reinterpret_cast<uint32_t*>(base + w.hash) : nullptr;
     k.hs_row = w.hs_row;
     return k;
 }
@@ -200,7 +203,7 @@ const char* vws_last_error(void) { return g_err.c_str(); }
 
 size_t vws_sample_workspace_size(int32_t batch, int32_t vocab, int32_t history_width) {
     if (batch < 1 || vocab < 1 || history_width < 0) return 0;
-    return ws_layout(batch, vocab, history_width).total;
+    return ws_layout(batch, vocab, history_width, false).total;
 }
 
 int vws_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
@@ -223,7 +226,7 @@ int vws_sample(const vws_sample_args* a) {
     int st = validate_sample(a);
     if (st) return st;
     const int hw = (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0);
-    KArgs k = make_kargs(a->batch, a->vocab, a->logits, a->logits_row_stride, a->workspace, hw);
+    KArgs k = make_kargs(a->batch, a->vocab, a->logits, a->logits_row_stride, a->workspace, hw, false);
     k.temperature = a->temperature;
     k.top_k = a->top_k;
     k.top_p = a->top_p;
@@ -280,7 +283,8 @@ int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, 
 
 size_t vws_topk_workspace_size(int32_t batch, int32_t vocab, int32_t k) {
     (void)k;
-    return vws_sample_workspace_size(batch, vocab, 0);
+    if (batch < 1 || vocab < 1) return 0;
+    return ws_layout(batch, vocab, 0, true).total;
 }
 
 int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
@@ -293,7 +297,7 @@ int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, in
     const size_t need = vws_topk_workspace_size(batch, vocab, k);
     if (!workspace || workspace_bytes < need)
         return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", workspace_bytes, need);
-    KArgs ka = make_kargs(batch, vocab, logits, row_stride, workspace, 0);
+    KArgs ka = make_kargs(batch, vocab, logits, row_stride, workspace, 0, true);
     ka.mode = kModeTopK;
     ka.topk_k = k;
     ka.topk_vals = out_vals;
@@ -351,11 +355,11 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
     if ((st = validate_history(prompt_ids, prompt_row_stride, prompt_width, "prompt"))) return st;
     if ((st = validate_history(output_ids, output_row_stride, output_width, "output"))) return st;
     const int hw = (prompt_ids ? prompt_width : 0) + (output_ids ? output_width : 0);
-    const size_t need = ws_layout(batch, vocab, hw).total;
-    if (!workspace || workspace_bytes < need)
+    const size_t need = ws_layout(batch, vocab, hw, false).total;
+    if (need && (!workspace || workspace_bytes < need))
         return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", workspace_bytes, need);
     if (hw == 0) return ok();
-    KArgs k = make_kargs(batch, vocab, logits, row_stride, workspace, hw);
+    KArgs k = make_kargs(batch, vocab, logits, row_stride, workspace, hw, false);
     k.rep = repetition;
     k.pres = presence;
     k.freq = frequency;

@@ -91,14 +91,19 @@ inline int hash_slots_for(int history_width) {
     return s;
 }
 
-inline WsLayout ws_layout(int B, int V, int history_width) {
+// Workspace sections.  Sampling and the penalty op keep only the history hash of the multi-pass
+// path (B x hs_row x 3 words, zero between calls); the split top-k op also needs its per-row
+// counters, row states and part lists (parts = true).
+inline WsLayout ws_layout(int B, int V, int history_width, bool parts) {
     (void)V;
     WsLayout w{};
     size_t off = 0;
-    w.counter = off; off = align256(off + sizeof(uint32_t) * (size_t)B);
-    w.state = off;   off = align256(off + sizeof(uint32_t) * (size_t)B);
-    w.meta = off;    off = align256(off + sizeof(uint32_t) * 4 * (size_t)B * kMaxParts);
-    w.list = off;    off = align256(off + sizeof(uint2) * (size_t)B * kMaxParts * kPartCap);
+    if (parts) {
+        w.counter = off; off = align256(off + sizeof(uint32_t) * (size_t)B);
+        w.state = off;   off = align256(off + sizeof(uint32_t) * (size_t)B);
+        w.meta = off;    off = align256(off + sizeof(uint32_t) * 4 * (size_t)B * kMaxParts);
+        w.list = off;    off = align256(off + sizeof(uint2) * (size_t)B * kMaxParts * kPartCap);
+    }
     w.hs_row = hash_slots_for(history_width);
     w.hash = off;    off = align256(off + sizeof(uint32_t) * 3 * (size_t)B * (size_t)w.hs_row);
     w.total = off;
