@@ -42,6 +42,7 @@ struct RowSmem {
     alignas(16) uint32_t pkey[kRowPack];     // all candidates of the row, packed in any order
     int32_t pidx[kRowPack];
     float pu[kRowPack];                      // their uniforms (sampled rows)
+    uint32_t crank[kRowPack];                // rank of each packed candidate (partial sums)
     uint32_t rhist[kRowWaves][256];          // per-wave radix-select scratch
     uint32_t hkey[kRowHash];                 // history token + 1 (0 = empty)
     uint32_t hval[kRowHash];                 // output count | prompt flag << 31
@@ -381,6 +382,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     if (hh) {
         for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
     }
+    sm.pkey[tid] = 0u;   // unpacked slots keep key 0, which ranks below every candidate
+    sm.crank[tid] = 0u;
     __syncthreads();
     if (hh) {
         if (tid < prm.np && hp_raw >= 0 && hp_raw < V) rhash_insert(sm, hp_raw, 0x80000000u);
@@ -485,6 +488,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     // each wave packs its candidates (penalised keys, indices, uniforms) into the row's arrays
     // as soon as its own stream ends, while other waves are still streaming
+    // The uniform of each lane's first candidate is only loaded here; it is stored after the
+    // rank count, so that its latency overlaps the count.
+    float u_first = 0.0f;
+    int u_slot = -1;
     if (!cb.ovf) {
         cb.finish();
         uint32_t b = 0;
@@ -495,7 +502,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 const int32_t ii = sm.cidx[wave][e];
                 sm.pkey[pbase + e] = sm.ckey[wave][e];
                 sm.pidx[pbase + e] = ii;
-                if (sampling) sm.pu[pbase + e] = a.u[(size_t)r * a.ustride + ii];
+                if (sampling) {
+                    const float uv = a.u[(size_t)r * a.ustride + ii];
+                    if (e == lane) { u_first = uv; u_slot = pbase + e; }
+                    else sm.pu[pbase + e] = uv;
+                }
             }
         }
     }
@@ -518,21 +529,38 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const bool mine = tid < total;
     const uint32_t myk = mine ? sm.pkey[tid] : 0u;
     if (tid == 0) { sm.bc[1] = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
-    __syncthreads();
-    if (wave * kWave < total) {
-        uint32_t gt = 0, ge = 0;
-        const uint4* p4 = reinterpret_cast<const uint4*>(sm.pkey);
-        int j = 0;
-        for (; j + 16 <= total; j += 16) {
-            const uint4 a0 = p4[j / 4], a1 = p4[j / 4 + 1], a2 = p4[j / 4 + 2], a3 = p4[j / 4 + 3];
-            const uint32_t v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                                    a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    {
+        // The rank of candidate c is the number of candidates before it in (key desc, packed
+        // position asc) order, so ranks are distinct: rank 0 holds the maximum and rank k-1 the
+        // k-th largest key.  Waves split the count as (group of 64 candidates, range of keys)
+        // pairs, 16 keys per step with 128-bit LDS reads, and add their partial ranks into
+        // LDS.  Slots past the packed candidates hold key 0 and never count.
+        const int ngrp = (total + kWave - 1) / kWave;
+        const int nspl = ngrp > 0 ? kRowWaves / ngrp : 0;
+        if (wave < ngrp * nspl) {
+            const int g = wave % ngrp, sp = wave / ngrp;
+            const int c = g * kWave + lane;
+            const uint32_t kc = sm.pkey[c];
+            const int chunk = (((total + nspl - 1) / nspl) + 15) & ~15;
+            const int j0 = sp * chunk, j1 = min(j0 + chunk, (total + 15) & ~15);
+            const uint4* p4 = reinterpret_cast<const uint4*>(sm.pkey);
+            uint32_t cnt = 0;
+            for (int j = j0; j < j1; j += 16) {
+                const uint4 a0 = p4[j / 4], a1 = p4[j / 4 + 1], a2 = p4[j / 4 + 2], a3 = p4[j / 4 + 3];
+                const uint32_t v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                        a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
 #pragma unroll
-            for (int i = 0; i < 16; ++i) { gt += v[i] > myk; ge += v[i] >= myk; }
+                for (int i = 0; i < 16; ++i) cnt += v[i] > kc - (uint32_t)(j + i < c);
+            }
+            if (c < total && cnt) atomicAdd(&sm.crank[c], cnt);
         }
-        for (; j < total; ++j) { const uint32_t kj = sm.pkey[j]; gt += kj > myk; ge += kj >= myk; }
-        if (mine && gt == 0u) sm.bc[2] = myk;                               // the maximum
-        if (mine && gt < (uint32_t)k && (uint32_t)k <= ge) sm.bc[1] = myk;  // the k-th key
+    }
+    if (u_slot >= 0) sm.pu[u_slot] = u_first;
+    __syncthreads();
+    if (mine) {
+        const uint32_t rk = sm.crank[tid];
+        if (rk == 0u) sm.bc[2] = myk;                    // the maximum
+        if (rk == (uint32_t)k - 1u) sm.bc[1] = myk;      // the k-th largest key
     }
     __syncthreads();
     const uint32_t kth = sm.bc[1];
