@@ -49,7 +49,8 @@ struct RowSmem {
     float hpen[kRowHash];                    // penalised value (gather mode)
     alignas(16) uint64_t sck[kRowKeep];      // survivors: key(y) << 32 | index
     alignas(16) uint64_t sw[kRowKeep];       // exact mass
-    float srk[kRowKeep];                     // race key
+    float se[kRowKeep];                      // exp(y - max)
+    uint32_t spos[kRowKeep];                 // packed position (for the uniform)
     uint32_t npack;                          // candidates packed so far
     uint32_t seedk[kRowWaves * kSeedPerWave];
     uint64_t red[kRowWaves][8];
@@ -445,14 +446,20 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         if (__ballot(c) == 0ull) return;
         cb.append(c, key_of(v), idx);  // raw value; penalties are applied by RowCand::finish
     };
+    // One vector (VEC elements per lane) at a time: the lane maximum against the threshold
+    // decides for the whole wave whether any element of the vector is examined one by one.
     auto examine = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
         cb.refresh();
         const int t = tid_now();
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const int vi = (it * U + q) * NT + t;
-            const int i0 = sl.a + vi * VEC;
             const bool ok = vi < nbody;
+            float mq = buf[q][0];
+#pragma unroll
+            for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
+            if (__ballot(ok && mq >= cb.tauf) == 0ull) continue;
+            const int i0 = sl.a + vi * VEC;
 #pragma unroll
             for (int j = 0; j < VEC; ++j) slot(buf[q][j], i0 + j, ok);
         }
@@ -488,8 +495,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     // each wave packs its candidates (penalised keys, indices, uniforms) into the row's arrays
     // as soon as its own stream ends, while other waves are still streaming
-    // The uniform of each lane's first candidate is only loaded here; it is stored after the
-    // rank count, so that its latency overlaps the count.
+    // The uniform of each lane's first candidate is only loaded here; it is stored just before
+    // the survivors are published, so that its latency overlaps the rank count.
     float u_first = 0.0f;
     int u_slot = -1;
     if (!cb.ovf) {
@@ -555,7 +562,6 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             if (c < total && cnt) atomicAdd(&sm.crank[c], cnt);
         }
     }
-    if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
     if (mine) {
         const uint32_t rk = sm.crank[tid];
@@ -608,10 +614,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 const float e = exp_det(y - m);
                 sm.sck[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.pidx[tid];
                 sm.sw[pos] = mass_of(e);
-                sm.srk[pos] = e / (0.0f - log_det(sm.pu[tid]));
+                sm.se[pos] = e;
+                sm.spos[pos] = (uint32_t)tid;
             }
         }
     }
+    if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
     const int n = (int)sm.nkeep;
     if (n == 0 || n > kRowKeep) return false;
@@ -653,7 +661,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             rs.cat = C;
             rs.nkept = 1;
             rs.last = myck;
-            rs.add_key(sm.srk[tid], (int)(uint32_t)myck);
+            rs.add_key(sm.se[tid] / (0.0f - log_det(sm.pu[sm.spos[tid]])), (int)(uint32_t)myck);
         }
     }
     rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
