@@ -256,6 +256,33 @@ __device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t* keys, int n
     return prefix;
 }
 
+// The four largest keys of the wave (one key per lane, counted with multiplicity): lane i < 4
+// receives the (i+1)-th largest, the other lanes 0.
+__device__ __forceinline__ uint32_t wave_top4(uint32_t v) {
+    const int lane = lane_id();
+    uint32_t mine = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t mk = wave_max_u32(v);
+        const uint64_t at = __ballot(v == mk);  // never empty: mk is some lane's key
+        if (lane == (int)__builtin_ctzll(at)) v = 0u;
+        if (lane == i) mine = mk;
+    }
+    return mine;
+}
+
+// The m-th largest of the wave's keys (one per lane, 1 <= m <= 64), in every lane: the largest
+// x with at least m keys >= x, decided bit by bit from the top.
+__device__ __forceinline__ uint32_t wave_mth_largest64(uint32_t v, int m) {
+    uint32_t ans = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t cand = ans | (1u << b);
+        if (__popcll(__ballot(v >= cand)) >= m) ans = cand;
+    }
+    return ans;
+}
+
 // k-th largest key (1-based, with multiplicity) of at most 256 keys held 4 per lane by one
 // whole wave (missing entries passed as 0): an in-register bitonic sort into descending order
 // across the wave (element e = 4 * lane + i), then a read of element k - 1.

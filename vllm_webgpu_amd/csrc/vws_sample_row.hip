@@ -407,6 +407,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const int sample = nbody > 0 ? min(NT * U, nbody) * VEC : 0;
     const int m_seed = sample > 0 ? (int)(((int64_t)3 * k * sample + V - 1) / V) : 0;
     const bool seeded = sample > 0 && m_seed <= kRowWaves * kSeedPerWave;
+    // m <= 64: the pool is every wave's 4 largest lane maxima, and every wave selects the m-th
+    // largest of it for itself; otherwise the 16 largest of every wave, selected by wave 0
+    const bool small_pool = m_seed <= kRowWaves * 4;
     if (seeded) {
         float mx = __builtin_nanf("");  // fmaxf ignores NaN; clamped duplicate loads are skipped
 #pragma unroll
@@ -415,16 +418,26 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) mx = ok ? fmaxf(mx, A[q][j]) : mx;
         }
-        const uint32_t sk = wave_sort_desc64(key_of(mx));
-        if (lane < kSeedPerWave) sm.seedk[wave * kSeedPerWave + lane] = sk;
+        if (small_pool) {
+            const uint32_t t4 = wave_top4(key_of(mx));
+            if (lane < 4) sm.seedk[wave * 4 + lane] = t4;
+        } else {
+            const uint32_t sk = wave_sort_desc64(key_of(mx));
+            if (lane < kSeedPerWave) sm.seedk[wave * kSeedPerWave + lane] = sk;
+        }
     }
     __syncthreads();  // also publishes the hash
-    if (seeded && wave == 0) {
+    // the hash is complete here; a row whose history overflowed it takes the general path
+    if (sm.status & 1u) return false;
+    uint32_t seed = 0u;
+    if (seeded && small_pool) {
+        seed = wave_mth_largest64(sm.seedk[lane], m_seed);
+    } else if (seeded && wave == 0) {
         const uint32_t t0 = wave_kth_largest_256(sm.seedk[4 * lane], sm.seedk[4 * lane + 1],
                                                  sm.seedk[4 * lane + 2], sm.seedk[4 * lane + 3], m_seed);
         if (lane == 0) sm.bc[0] = t0;
     }
-    if (gather && sm.status == 0u) {
+    if (gather) {
         for (int s = tid; s < kRowHash; s += NT) {
             const uint32_t kk = sm.hkey[s];
             if (kk) {
@@ -434,9 +447,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             }
         }
     }
-    __syncthreads();
-    if (sm.status != 0u) return false;
-    uint32_t seed = seeded ? sm.bc[0] : 0u;
+    if (gather || (seeded && !small_pool)) {
+        __syncthreads();
+        if (seeded && !small_pool) seed = sm.bc[0];
+    }
 
     // 4. stream; 5. the k-th largest candidate, checked against every threshold used.  A seeded
     //    pass whose k-th candidate lies below a threshold is streamed again without the seed.
