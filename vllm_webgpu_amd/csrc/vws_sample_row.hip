@@ -43,6 +43,8 @@ struct RowSmem {
     int32_t pidx[kRowPack];
     float pu[kRowPack];                      // their uniforms (sampled rows)
     uint32_t crank[kRowPack];                // rank of each packed candidate (partial sums)
+    uint64_t sC[kRowKeep];                   // survivors' cumulative masses (partial sums)
+    uint64_t sW;                             // total mass of the survivors
     uint32_t rhist[kRowWaves][256];          // per-wave radix-select scratch
     uint32_t hkey[kRowHash];                 // history token + 1 (0 = empty)
     uint32_t hval[kRowHash];                 // output count | prompt flag << 31
@@ -385,6 +387,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     sm.pkey[tid] = 0u;   // unpacked slots keep key 0, which ranks below every candidate
     sm.crank[tid] = 0u;
+    if (tid < kRowKeep) sm.sC[tid] = 0ull;
+    if (tid == 0) sm.sW = 0ull;
     __syncthreads();
     if (hh) {
         if (tid < prm.np && hp_raw >= 0 && hp_raw < V) rhash_insert(sm, hp_raw, 0x80000000u);
@@ -549,11 +553,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     for (int w = 0; w < kRowWaves; ++w) tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
     const bool mine = tid < total;
     const uint32_t myk = mine ? sm.pkey[tid] : 0u;
-    if (tid == 0) { sm.bc[1] = 0u; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
+    if (tid == 0) { sm.bc[1] = 0xFFFFFFFFu; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
     {
-        // The rank of candidate c is the number of candidates before it in (key desc, packed
-        // position asc) order, so ranks are distinct: rank 0 holds the maximum and rank k-1 the
-        // k-th largest key.  Waves split the count as (group of 64 candidates, range of keys)
+        // The rank of candidate c is the number of candidate keys above its own: rank 0 holds
+        // the maximum, and the k-th largest key is the smallest key of rank < k (ties with it
+        // share its rank).  Waves split the count as (group of 64 candidates, range of keys)
         // pairs, 16 keys per step with 128-bit LDS reads, and add their partial ranks into
         // LDS.  Slots past the packed candidates hold key 0 and never count.
         const int ngrp = (total + kWave - 1) / kWave;
@@ -571,7 +575,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 const uint32_t v[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
                                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
 #pragma unroll
-                for (int i = 0; i < 16; ++i) cnt += v[i] > kc - (uint32_t)(j + i < c);
+                for (int i = 0; i < 16; ++i) cnt += v[i] > kc;
             }
             if (c < total && cnt) atomicAdd(&sm.crank[c], cnt);
         }
@@ -579,11 +583,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     __syncthreads();
     if (mine) {
         const uint32_t rk = sm.crank[tid];
-        if (rk == 0u) sm.bc[2] = myk;                    // the maximum
-        if (rk == (uint32_t)k - 1u) sm.bc[1] = myk;      // the k-th largest key
+        if (rk == 0u) sm.bc[2] = myk;                          // the maximum
+        if (rk < (uint32_t)k) atomicMin(&sm.bc[1], myk);       // the k-th largest key
     }
     __syncthreads();
-    const uint32_t kth = sm.bc[1];
+    const uint32_t kth = total >= k ? sm.bc[1] : 0u;
     const uint32_t mk = sm.bc[2];
     const bool exact = seed != 0u ? (total >= k && kth >= tmax) : (kth == 0u || kth >= tmax);
     if (!exact) return false;
@@ -622,48 +626,54 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         uint32_t off = 0;
         if (lane == 0 && bal) off = atomicAdd(&sm.nkeep, (uint32_t)__popcll(bal));
         off = __builtin_amdgcn_readlane(off, 0);
+        uint64_t mw = 0ull;
         if (keep) {
             const uint32_t pos = off + (uint32_t)lane_prefix(bal);
             if (pos < (uint32_t)kRowKeep) {
                 const float e = exp_det(y - m);
+                mw = mass_of(e);
                 sm.sck[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.pidx[tid];
-                sm.sw[pos] = mass_of(e);
+                sm.sw[pos] = mw;
                 sm.se[pos] = e;
                 sm.spos[pos] = (uint32_t)tid;
             }
         }
+        mw = wave_sum_u64(mw);
+        if (lane == 0 && mw) atomicAdd(&sm.sW, mw);
     }
     if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
     const int n = (int)sm.nkeep;
     if (n == 0 || n > kRowKeep) return false;
 
-    // 7. top-p over exact masses: survivor j (thread j) sums w_i over survivors i <= j in
-    //    (y, index) order, four per step with 128-bit LDS reads; then the race among the kept
-    //    survivors, reduced across the wave and the waves
+    // 7. top-p over exact masses: the cumulative mass of every survivor, then the race among
+    //    the kept survivors, reduced across the wave and the waves
     const float q32 = 1.0f - prm.top_p;
     const bool topp = q32 > 0.0f;
     const bool abl = topp && !(q32 < 1.0f);  // top_p <= 0: only the last survivor is kept
     const int nws = (n + kWave - 1) / kWave;
+    {
+        // C_j = sum of w_i over the survivors i <= j in (y, index) order.  Waves split the sums
+        // as (group of 64 survivors, range of survivors) pairs and add them into LDS.
+        const int nsp = min(kRowWaves / nws, (n + 15) / 16);
+        if (wave < nws * nsp) {
+            const int g = wave % nws, sp = wave / nws;
+            const int j = g * kWave + lane;
+            const uint64_t ckj = j < n ? sm.sck[j] : 0ull;
+            const int chunk = (n + nsp - 1) / nsp;
+            const int i0 = sp * chunk, i1 = min(n, i0 + chunk);
+            uint64_t part = 0ull;
+#pragma unroll 4
+            for (int i = i0; i < i1; ++i) part += sm.sck[i] <= ckj ? sm.sw[i] : 0ull;
+            if (j < n && part) atomicAdd(&sm.sC[j], part);
+        }
+    }
+    __syncthreads();
     if (wave >= nws) return true;
     const bool mys = tid < n;
     const uint64_t myck = mys ? sm.sck[tid] : ~0ull;
-    uint64_t C = 0, W = 0;
-    {
-        const uint4* c4 = reinterpret_cast<const uint4*>(sm.sck);
-        const uint4* w4 = reinterpret_cast<const uint4*>(sm.sw);
-        int j = 0;
-        for (; j + 4 <= n; j += 4) {
-            const uint4 c0 = c4[j / 2], c1 = c4[j / 2 + 1], v0 = w4[j / 2], v1 = w4[j / 2 + 1];
-            const uint64_t ck[4] = {((uint64_t)c0.y << 32) | c0.x, ((uint64_t)c0.w << 32) | c0.z,
-                                    ((uint64_t)c1.y << 32) | c1.x, ((uint64_t)c1.w << 32) | c1.z};
-            const uint64_t wv[4] = {((uint64_t)v0.y << 32) | v0.x, ((uint64_t)v0.w << 32) | v0.z,
-                                    ((uint64_t)v1.y << 32) | v1.x, ((uint64_t)v1.w << 32) | v1.z};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { W += wv[i]; C += ck[i] <= myck ? wv[i] : 0ull; }
-        }
-        for (; j < n; ++j) { const uint64_t wj = sm.sw[j]; W += wj; C += sm.sck[j] <= myck ? wj : 0ull; }
-    }
+    const uint64_t C = mys ? sm.sC[tid] : 0ull;
+    const uint64_t W = sm.sW;
     const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
     RowRace rs;
     if (mys) {
