@@ -35,6 +35,7 @@ constexpr int kRowHashFill = 1536;           // unique history tokens served in 
 constexpr int kRowKeep = 256;                // survivors finished here
 constexpr int kRowPack = kRowThreads;        // candidates finished here (more: general path)
 constexpr int kSeedPerWave = 16;             // lane maxima each wave contributes to the seed pool
+constexpr int kLoadNT = 2;                   // buffer-load cache policy: non-temporal
 
 struct RowSmem {
     uint32_t ckey[kRowWaves][kRowCap];
@@ -355,12 +356,14 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const int nit = (nbody + NT * U - 1) / (NT * U);
     const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + sl.a, 16u * (uint32_t)nbody);
     float A[U][VEC], Bq[U][VEC];
-    // vectors past the body read zeros; consumers skip them (vi >= nbody)
+    // Vectors past the body read zeros; consumers skip them (vi >= nbody).  The loads are
+    // non-temporal (nt): the row is read once, and streaming it with the default policy evicts
+    // the kernel's own code and small operands from L2 and the infinity cache.
     auto load_iter = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-                lrs, 16u * (uint32_t)tid_now(), 16u * (uint32_t)((it * U + q) * NT), 0);
+                lrs, 16u * (uint32_t)tid_now(), 16u * (uint32_t)((it * U + q) * NT), kLoadNT);
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
@@ -476,7 +479,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             float mq = buf[q][0];
 #pragma unroll
             for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
-            if (__ballot(ok && mq >= cb.tauf) == 0ull) continue;
+            if (__builtin_expect(__ballot(ok && mq >= cb.tauf) == 0ull, 1)) continue;
             const int i0 = sl.a + vi * VEC;
 #pragma unroll
             for (int j = 0; j < VEC; ++j) slot(buf[q][j], i0 + j, ok);
