@@ -34,18 +34,29 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_args(lib_mod, logits, T, K, P, MP, R, PR, FR, hist, U, out, flags, nkept, ws):
+def build_args(lib_mod, logits, T, K, P, MP, R, PR, FR, hist, U, out, flags, nkept, ws,
+               lp=None):
+    """vws_sample_args over device tensors; ``hist``/``U`` may be None, ``lp`` = (L, ids, vals,
+    ranks) requests logprobs."""
+    import torch
+
     a = lib_mod.SampleArgs()
     a.struct_size = ctypes.sizeof(lib_mod.SampleArgs)
     B, V = logits.shape
-    a.batch, a.vocab, a.dtype = B, V, lib_mod.DTYPE_F32
+    a.batch, a.vocab = B, V
+    a.dtype = lib_mod.DTYPE_BF16 if logits.dtype == torch.bfloat16 else lib_mod.DTYPE_F32
     a.logits, a.logits_row_stride = logits.data_ptr(), logits.stride(0)
     a.temperature, a.top_k, a.top_p, a.min_p = T.data_ptr(), K.data_ptr(), P.data_ptr(), MP.data_ptr()
     a.repetition_penalty, a.presence_penalty, a.frequency_penalty = R.data_ptr(), PR.data_ptr(), FR.data_ptr()
-    a.output_ids, a.output_row_stride, a.output_width = hist.data_ptr(), hist.stride(0), hist.shape[1]
-    a.uniforms, a.uniforms_row_stride = U.data_ptr(), U.stride(0)
+    if hist is not None:
+        a.output_ids, a.output_row_stride, a.output_width = hist.data_ptr(), hist.stride(0), hist.shape[1]
+    if U is not None:
+        a.uniforms, a.uniforms_row_stride = U.data_ptr(), U.stride(0)
     a.sampled, a.row_flags, a.num_kept = out.data_ptr(), flags.data_ptr(), nkept.data_ptr()
     a.num_logprobs = -1
+    if lp is not None:
+        a.num_logprobs = lp[0]
+        a.logprob_ids, a.logprob_vals, a.logprob_ranks = lp[1].data_ptr(), lp[2].data_ptr(), lp[3].data_ptr()
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     return a
 
@@ -127,9 +138,12 @@ def main():
     dev = torch.device("cuda:0")
     L = _lib.lib()
 
-    logits0 = torch.from_numpy(w.logits_f32()).to(dev)
-    U0 = torch.from_numpy(w.uniforms).to(dev)
-    H0 = torch.from_numpy(w.output_ids).to(dev)
+    if w.dtype == "bf16":
+        logits0 = torch.from_numpy(w.logits.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        logits0 = torch.from_numpy(w.logits).to(dev)
+    U0 = torch.from_numpy(w.uniforms).to(dev) if w.uniforms is not None else None
+    H0 = torch.from_numpy(w.output_ids).to(dev) if w.output_ids is not None else None
     T = torch.from_numpy(w.temperature).to(dev)
     K = torch.from_numpy(w.top_k).to(dev)
     P = torch.from_numpy(w.top_p).to(dev)
@@ -140,17 +154,23 @@ def main():
     sets = []
     for i in range(args.sets):
         lg = torch.roll(logits0, shifts=i, dims=0).contiguous()
-        u = torch.roll(U0, shifts=i, dims=0).contiguous()
-        h = torch.roll(H0, shifts=i, dims=0).contiguous()
+        u = torch.roll(U0, shifts=i, dims=0).contiguous() if U0 is not None else None
+        h = torch.roll(H0, shifts=i, dims=0).contiguous() if H0 is not None else None
         sets.append((lg, u, h))
     out = torch.empty(B, dtype=torch.int32, device=dev)
     flags = torch.empty(B, dtype=torch.int32, device=dev)
     nkept = torch.empty(B, dtype=torch.int32, device=dev)
-    ws = ops.workspace(L.vws_sample_workspace_size(B, V, H0.shape[1]), dev)
+    ws = ops.workspace(L.vws_sample_workspace_size(B, V, 0 if H0 is None else H0.shape[1]), dev)
+    lp = None
+    if w.num_logprobs is not None:
+        nl = w.num_logprobs
+        lp = (nl, torch.empty((B, nl + 1), dtype=torch.int32, device=dev),
+              torch.empty((B, nl + 1), dtype=torch.float32, device=dev),
+              torch.empty(B, dtype=torch.int32, device=dev))
     stream = torch.cuda.current_stream()
     argv = []
     for lg, u, h in sets:
-        a = build_args(_lib, lg, T, K, P, MP, R, PR, FR, h, u, out, flags, nkept, ws)
+        a = build_args(_lib, lg, T, K, P, MP, R, PR, FR, h, u, out, flags, nkept, ws, lp)
         a.stream = stream.cuda_stream
         argv.append(a)
     sample = L.vws_sample
@@ -164,7 +184,8 @@ def main():
     from oracle import sampler as O  # checker only
 
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence, w.frequency)
-    ref = O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids)
+    ref = O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids,
+                   num_logprobs=w.num_logprobs)
     mism = int((ref["token"] != gpu_tok).sum())
     log(f"parity vs oracle: {mism} token mismatches of {B} rows; "
         f"|S| mean {gpu_kept.mean():.1f}; near-tie rows {int(((gpu_flags & 3) != 0).sum())}")
@@ -225,7 +246,7 @@ def main():
         log(f"cpu baseline {cpu['value']:.1f} rows/s on {cpu['cores']} cores ({time.time() - t:.1f}s)")
 
     res = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == 3 else f"sampled rows/sec + HBM GB/s (% peak), {w.name}",
         "value": rows_per_s,
         "unit": "rows/s",
         "n_gpus": 1,
@@ -235,12 +256,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16" if w.dtype == "bf16" else "f32",
         "data": "synthetic",
         "config": {
             "workload": ("C3: fp32 logits B=256 V=128256 ~N(0,3); 512-token output history "
                          "(repetition 1.1, presence 0.5, frequency 0.3); T=0.7, top-k 50, "
-                         "top-p 0.9; caller uniforms [B,V]; 3 rotated input sets"),
+                         "top-p 0.9; caller uniforms [B,V]; 3 rotated input sets")
+            if args.config == 3 else f"{w.name}; {args.sets} rotated input sets",
             "global_batch": B, "vocab": V, "parallelism": "none (1 GPU)",
         },
         "hbm_gbps_end_to_end": gbps_e2e,
@@ -252,7 +274,8 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": gbps_kern / PEAK_HBM_GBPS, "traffic": pmc_traffic_bytes(args.config),
-            "kernel": "vws::row_kernel<float>",
+            "kernel": ("vws::row_kernel<unsigned short>" if w.dtype == "bf16"
+                       else "vws::row_kernel<float>"),
         },
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
     }
