@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 1
+#define VWS_ABI_VERSION 2
 
 /* status codes */
 #define VWS_OK 0
@@ -87,6 +87,22 @@ typedef struct vws_sample_args {
     int32_t output_width;
     const int32_t* output_lens;
 
+    /* vLLM-v1 logits processors, applied before the penalties (raw logprobs never see them).
+     * allowed_mask: uint32 [B, ceil(V/32)] words with the given row stride, bit (t & 31) of word
+     * t >> 5 set = token t allowed, others become -inf (allowed_token_ids); NULL = all allowed.
+     * adjust_ids / adjust_vals: padded [B, width] (shared row stride) sparse per-row list:
+     * value -inf bans the token (bad words, min-tokens stop ids), a finite value is added to
+     * its logit (logit bias; at most one finite entry per token and row).  Ids outside [0, V)
+     * are padding; adjust_lens (device [B]) may be NULL, meaning the full width.  Rows with an
+     * allowed mask are served by the multi-pass path. */
+    const uint32_t* allowed_mask;
+    int64_t allowed_row_stride;
+    const int32_t* adjust_ids;
+    const float* adjust_vals;
+    int64_t adjust_row_stride;
+    int32_t adjust_width;
+    const int32_t* adjust_lens;
+
     /* Uniforms in (0, 1), fp32 [B, V] (row stride in elements); read only at surviving
      * tokens.  Required when temperature is non-NULL. */
     const float* uniforms;
@@ -113,9 +129,9 @@ int32_t vws_abi_version(void);
 const char* vws_last_error(void);
 
 /* Bytes of workspace vws_sample needs for this shape and history width
- * (prompt_width + output_width): the history hash of rows served by the multi-pass path,
- * B x (power of two >= 2 x history_width, at least 64) x 12 bytes.  0 without a history, in
- * which case `workspace` may be NULL. */
+ * (prompt_width + output_width + adjust_width): the history hash of rows served by the
+ * multi-pass path, B x (power of two >= 2 x history_width, at least 64) x 16 bytes.  0 without
+ * a history, in which case `workspace` may be NULL. */
 size_t vws_sample_workspace_size(int32_t batch, int32_t vocab, int32_t history_width);
 
 /* Clears a workspace on `stream` (a fill kernel, safe under graph capture).  Required once

@@ -67,7 +67,9 @@ def lib() -> ctypes.CDLL:
             L.vwo_scale_floor.argtypes = [ctypes.c_float, ctypes.c_uint64]
             L.vwo_scale_floor.restype = ctypes.c_uint64
             L.vwo_sample_batch.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P, P,
-                                           ctypes.c_int, P, P, P, ctypes.c_int, P, P, P, P]
+                                           ctypes.c_int, P, P, ctypes.c_int, P, P, ctypes.c_int,
+                                           P, P, P, ctypes.c_int, P, P, P, P]
+            L.vwo_apply_adjustments_row.argtypes = [P, ctypes.c_int, P, P, P, ctypes.c_int]
             L.vwo_apply_penalties_row.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int,
                                                   ctypes.c_float, ctypes.c_float, ctypes.c_float]
             L.vwo_argmax_row.argtypes = [P, ctypes.c_int]
@@ -164,6 +166,21 @@ def softmax(x: np.ndarray, temperature: float = 1.0):
     return probs, rm, ls
 
 
+def apply_adjustments(x: np.ndarray, allowed=None, adjust_ids=None, adjust_vals=None) -> np.ndarray:
+    """Copy of x [B,V] after the logits processors (allowed bitmask, bans, logit bias)."""
+    x = np.array(x, dtype=np.float32, copy=True).reshape(-1, x.shape[-1])
+    B, V = x.shape
+    al = None if allowed is None else np.ascontiguousarray(allowed, np.uint32)
+    ai = None if adjust_ids is None else np.ascontiguousarray(adjust_ids, np.int32)
+    av = None if adjust_vals is None else np.ascontiguousarray(adjust_vals, np.float32)
+    for b in range(B):
+        lib().vwo_apply_adjustments_row(_ptr(x[b]), V, None if al is None else _ptr(al[b]),
+                                        None if ai is None else _ptr(ai[b]),
+                                        None if av is None else _ptr(av[b]),
+                                        0 if ai is None else ai.shape[1])
+    return x
+
+
 def apply_penalties(x: np.ndarray, prompt_ids=None, output_ids=None, repetition=1.0,
                     presence=0.0, frequency=0.0) -> np.ndarray:
     """Penalised copy of x [B,V]; *_ids: padded int32 [B, W] (ids outside [0,V) are padding)."""
@@ -198,11 +215,16 @@ def make_params(B, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repetition=1.
 def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None = None,
            prompt_ids: np.ndarray | None = None, output_ids: np.ndarray | None = None,
            prompt_lens: np.ndarray | None = None, output_lens: np.ndarray | None = None,
-           num_logprobs: int | None = None) -> dict:
+           num_logprobs: int | None = None, allowed: np.ndarray | None = None,
+           adjust_ids: np.ndarray | None = None, adjust_vals: np.ndarray | None = None,
+           adjust_lens: np.ndarray | None = None) -> dict:
     """Samples every row of fp32 ``logits`` [B, V].
 
     ``params``: PARAMS_DTYPE [B] (see make_params).  ``uniforms``: fp32 [B, V] in (0, 1).
     History arrays: padded int32 [B, W]; ids outside [0, V) are padding (vLLM pads with V).
+    Logits processors (before the penalties): ``allowed`` uint32 [B, ceil(V/32)] bitmask (bit
+    set = allowed, None = all); ``adjust_ids`` int32 / ``adjust_vals`` fp32 [B, Wa]: value
+    -inf bans the token, a finite value is added (logit bias).
     Returns dict(token, flags, n_kept, n_topk, mass_total, threshold, row_max, kth_y,
     [lp_ids, lp_vals, ranks]).
     """
@@ -224,9 +246,18 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
         lp_ids = np.zeros((B, L + 1), np.int32)
         lp_vals = np.zeros((B, L + 1), np.float32)
         ranks = np.zeros(B, np.int32)
+    al = None if allowed is None else np.ascontiguousarray(allowed, np.uint32)
+    ai = None if adjust_ids is None else np.ascontiguousarray(adjust_ids, np.int32)
+    av = None if adjust_vals is None else np.ascontiguousarray(adjust_vals, np.float32)
+    an = None if adjust_lens is None else np.ascontiguousarray(adjust_lens, np.int32)
+    if ai is not None:
+        assert av is not None and av.shape == ai.shape
     lib().vwo_sample_batch(_ptr(x), B, V, _ptr(pr), 0 if pr is None else pr.shape[1], _ptr(pl),
-                           _ptr(po), 0 if po is None else po.shape[1], _ptr(ol), _ptr(prm),
-                           _ptr(u), L, _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks), _ptr(outs))
+                           _ptr(po), 0 if po is None else po.shape[1], _ptr(ol),
+                           _ptr(al), 0 if al is None else al.shape[1],
+                           _ptr(ai), _ptr(av), 0 if ai is None else ai.shape[1], _ptr(an),
+                           _ptr(prm), _ptr(u), L, _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks),
+                           _ptr(outs))
     res = {name: outs[name].copy() for name in ROW_OUT_DTYPE.names}
     if L >= 0:
         res.update(lp_ids=lp_ids, lp_vals=lp_vals, ranks=ranks)

@@ -13,8 +13,9 @@
  *   - online max/normaliser softmax: vllm_webgpu/shaders/generic/softmax.wgsl:26-70.
  *   - the vLLM-v1 Sampler the plugin delegates sampling to
  *     (docs/superpowers/specs/2026-06-29-vllm-webgpu-design.md:451; pyproject.toml:10,
- *     vllm>=0.20, not vendored in the reference): penalties -> temperature -> min-p ->
- *     top-k -> top-p -> exponential race, and raw logprobs.
+ *     vllm>=0.20, not vendored in the reference): logits processors (allowed-token mask,
+ *     bans, logit bias) -> penalties -> temperature -> min-p -> top-k -> top-p ->
+ *     exponential race, and raw logprobs.
  *
  * Sampler arithmetic (the definition that makes token ids reproducible bit for bit):
  *   exp_det / log_det are fixed fp32 operation sequences (Cody-Waite reduction and
@@ -177,6 +178,28 @@ static uint32_t kth_largest_key(const uint32_t* keys, int n, int k) {
     return ((uint32_t)hi << 16) | (uint32_t)lo;
 }
 
+/* vLLM-v1's logits processors that run before the penalties, in place on x (length V):
+ * tokens whose bit is clear in `allowed` (V bits, NULL = all allowed) and tokens listed with
+ * value -inf (bad words, min-tokens stop ids) become -inf; a token listed with a finite value
+ * gets x + value (logit bias; at most one finite entry per token).  Ids outside [0, V) are
+ * padding. */
+void vwo_apply_adjustments_row(float* x, int V, const uint32_t* allowed, const int32_t* ids,
+                               const float* vals, int n) {
+    if (allowed)
+        for (int i = 0; i < V; ++i)
+            if (!((allowed[i >> 5] >> (i & 31)) & 1u)) x[i] = -INFINITY;
+    uint8_t* ban = n > 0 ? (uint8_t*)calloc((size_t)V, 1) : NULL;
+    for (int j = 0; j < n; ++j)
+        if (ids[j] >= 0 && ids[j] < V && vals[j] == -INFINITY) ban[ids[j]] = 1;
+    for (int j = 0; j < n; ++j) {
+        const int t = ids[j];
+        if (t < 0 || t >= V || ban[t] || vals[j] == -INFINITY) continue;
+        x[t] = x[t] + vals[j];
+    }
+    for (int t = 0; n > 0 && t < V; ++t) if (ban[t]) x[t] = -INFINITY;
+    free(ban);
+}
+
 /* Applies penalties to x (length V) in place.  Token ids outside [0, V) are padding. */
 void vwo_apply_penalties_row(float* x, int V, const int32_t* prompt, int np, const int32_t* output,
                              int no, float rep, float pres, float freq) {
@@ -205,12 +228,14 @@ int32_t vwo_argmax_row(const float* x, int V) {
  * caller).  u: uniforms [V] in (0,1).  Logprob outputs (optional, L >= 0): lp_ids/lp_vals have
  * L+1 entries: [sampled, top1..topL]; *rank = #{j : x0_j >= x0_sampled}. */
 int vwo_sample_row(const float* x0, int V, const int32_t* prompt, int np, const int32_t* output,
-                   int no, const vwo_params* prm, const float* u, int L, int32_t* lp_ids,
+                   int no, const uint32_t* allowed, const int32_t* adj_ids, const float* adj_vals,
+                   int na, const vwo_params* prm, const float* u, int L, int32_t* lp_ids,
                    float* lp_vals, int32_t* rank, vwo_row_out* out) {
     memset(out, 0, sizeof(*out));
     out->kth_y = -INFINITY;
     float* x = (float*)malloc(sizeof(float) * (size_t)V);
     memcpy(x, x0, sizeof(float) * (size_t)V);
+    if (allowed || na > 0) vwo_apply_adjustments_row(x, V, allowed, adj_ids, adj_vals, na);
     const int has_hist = (np > 0 || no > 0);
     if (has_hist) vwo_apply_penalties_row(x, V, prompt, np, output, no, prm->rep, prm->pres, prm->freq);
 
@@ -351,14 +376,20 @@ logprobs:
  * prompt/output: padded [B, *_stride] with ids outside [0, V) ignored; lens may be NULL. */
 int vwo_sample_batch(const float* logits, int B, int V, const int32_t* prompt, int prompt_stride,
                      const int32_t* prompt_lens, const int32_t* output, int output_stride,
-                     const int32_t* output_lens, const vwo_params* prm, const float* uniforms,
+                     const int32_t* output_lens, const uint32_t* allowed, int allowed_stride,
+                     const int32_t* adj_ids, const float* adj_vals, int adj_stride,
+                     const int32_t* adj_lens, const vwo_params* prm, const float* uniforms,
                      int L, int32_t* lp_ids, float* lp_vals, int32_t* ranks, vwo_row_out* outs) {
 #pragma omp parallel for schedule(dynamic, 1)
     for (int b = 0; b < B; ++b) {
         const int np = prompt ? (prompt_lens ? prompt_lens[b] : prompt_stride) : 0;
         const int no = output ? (output_lens ? output_lens[b] : output_stride) : 0;
+        const int na = adj_ids ? (adj_lens ? adj_lens[b] : adj_stride) : 0;
         vwo_sample_row(logits + (size_t)b * V, V, prompt ? prompt + (size_t)b * prompt_stride : NULL, np,
-                       output ? output + (size_t)b * output_stride : NULL, no, &prm[b],
+                       output ? output + (size_t)b * output_stride : NULL, no,
+                       allowed ? allowed + (size_t)b * allowed_stride : NULL,
+                       adj_ids ? adj_ids + (size_t)b * adj_stride : NULL,
+                       adj_vals ? adj_vals + (size_t)b * adj_stride : NULL, na, &prm[b],
                        uniforms ? uniforms + (size_t)b * V : NULL, L,
                        lp_ids ? lp_ids + (size_t)b * (L + 1) : NULL,
                        lp_vals ? lp_vals + (size_t)b * (L + 1) : NULL, ranks ? ranks + b : NULL,

@@ -54,9 +54,31 @@ def first_argmax(x):
     return int(np.nonzero(ok & (x == m))[0][0])
 
 
-def sample_row(x0, T, k, p, min_p, rep, pres, freq, u, prompt=None, output=None):
+def process(x, allowed=None, adj_ids=None, adj_vals=None):
+    """vLLM-v1 logits processors ahead of the penalties: disallowed tokens (``allowed`` is a
+    bool [V] here) and tokens listed with -inf become -inf, a token listed with a finite value
+    gets it added in fp32.  Ids outside [0, V) are padding."""
+    x = np.asarray(x, np.float32).copy()
+    V = x.size
+    if allowed is not None:
+        x[~np.asarray(allowed, bool)] = -np.inf
+    if adj_ids is not None:
+        ids = np.asarray(adj_ids)
+        vals = np.asarray(adj_vals, np.float32)
+        ok = (ids >= 0) & (ids < V)
+        banned = set(int(t) for t, v in zip(ids[ok], vals[ok]) if v == -np.inf)
+        for t, v in zip(ids[ok], vals[ok]):
+            if int(t) not in banned:
+                x[t] = np.float32(x[t] + v)
+        for t in banned:
+            x[t] = -np.inf
+    return x
+
+
+def sample_row(x0, T, k, p, min_p, rep, pres, freq, u, prompt=None, output=None, allowed=None,
+               adj_ids=None, adj_vals=None):
     """Returns dict(token, n_kept, margin_ok) for one row."""
-    x = penalise(x0, prompt, output, rep, pres, freq)
+    x = penalise(process(x0, allowed, adj_ids, adj_vals), prompt, output, rep, pres, freq)
     V = x.size
     T = np.float32(T)
     if not (T >= EPS_GREEDY):

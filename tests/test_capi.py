@@ -61,11 +61,11 @@ def test_abi_constants_match_header(L):
 
 def test_workspace_sizes(L):
     a = L.vws_sample_workspace_size(256, 128256, 512)
-    # history hash only: 256 rows x 1024 slots (power of two >= 2 x 512) x 3 words
-    assert a == 256 * 1024 * 12
+    # history hash only: 256 rows x 1024 slots (power of two >= 2 x 512) x 4 words
+    assert a == 256 * 1024 * 16
     assert L.vws_sample_workspace_size(256, 128256, 0) == 0       # no history: no workspace
     assert L.vws_sample_workspace_size(512, 128256, 512) == 2 * a
-    assert L.vws_sample_workspace_size(4, 100, 1) == 4 * 64 * 12  # at least 64 slots
+    assert L.vws_sample_workspace_size(4, 100, 1) == 4 * 64 * 16  # at least 64 slots
     assert L.vws_sample_workspace_size(0, 100, 0) == 0
     assert L.vws_sample_workspace_size(4, 100, -1) == 0
     t = L.vws_topk_workspace_size(8, 1000, 50)
@@ -122,6 +122,11 @@ def test_valid_args_pass(L):
     (dict(HIST, workspace_bytes=256), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
     (dict(HIST, workspace=0x100010, workspace_bytes=1 << 20), _lib.ERR_INVALID_ARGUMENT, "aligned"),
     (dict(struct_size=8), _lib.ERR_INVALID_ARGUMENT, "struct_size"),
+    (dict(adjust_ids=FAKE, adjust_width=4, adjust_row_stride=4), _lib.ERR_INVALID_ARGUMENT,
+     "adjust_vals"),
+    (dict(adjust_ids=FAKE, adjust_vals=FAKE, adjust_width=8, adjust_row_stride=4),
+     _lib.ERR_INVALID_ARGUMENT, "adjust_row_stride"),
+    (dict(allowed_mask=FAKE, allowed_row_stride=31), _lib.ERR_INVALID_ARGUMENT, "allowed_row_stride"),
 ])
 def test_invalid_args_rejected(L, over, code, msg):
     assert _status(L, _args(L, **over)) == code
@@ -133,6 +138,14 @@ def test_history_grows_the_required_workspace(L):
     assert _status(L, a) == _lib.ERR_WORKSPACE_TOO_SMALL
     a.workspace_bytes = L.vws_sample_workspace_size(4, 1000, 512)
     assert _status(L, a) == _lib.OK
+
+
+def test_processor_lists_grow_the_required_workspace(L):
+    a = _args(L, adjust_ids=FAKE, adjust_vals=FAKE, adjust_width=100, adjust_row_stride=100)
+    assert _status(L, a) == _lib.ERR_WORKSPACE_TOO_SMALL
+    a.workspace_bytes = L.vws_sample_workspace_size(4, 1000, 100)
+    assert _status(L, a) == _lib.OK
+    assert _status(L, _args(L, allowed_mask=FAKE, allowed_row_stride=32)) == _lib.OK
 
 
 def test_no_history_needs_no_workspace(L):

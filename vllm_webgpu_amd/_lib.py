@@ -14,7 +14,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2
@@ -61,6 +61,9 @@ class SampleArgs(ctypes.Structure):
         ("repetition_penalty", _P), ("presence_penalty", _P), ("frequency_penalty", _P),
         ("prompt_ids", _P), ("prompt_row_stride", _I64), ("prompt_width", _I32), ("prompt_lens", _P),
         ("output_ids", _P), ("output_row_stride", _I64), ("output_width", _I32), ("output_lens", _P),
+        ("allowed_mask", _P), ("allowed_row_stride", _I64),
+        ("adjust_ids", _P), ("adjust_vals", _P), ("adjust_row_stride", _I64), ("adjust_width", _I32),
+        ("adjust_lens", _P),
         ("uniforms", _P), ("uniforms_row_stride", _I64),
         ("sampled", _P), ("row_flags", _P), ("num_kept", _P),
         ("num_logprobs", _I32), ("logprob_ids", _P), ("logprob_vals", _P), ("logprob_ranks", _P),

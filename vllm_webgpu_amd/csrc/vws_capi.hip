@@ -143,6 +143,12 @@ int validate_history(const int32_t* ids, int64_t stride, int32_t width, const ch
     return VWS_OK;
 }
 
+// History entries a row can put into the hash: prompt, output and processor tokens.
+int sample_history_width(const vws_sample_args* a) {
+    return (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0) +
+           (a->adjust_ids ? a->adjust_width : 0);
+}
+
 int validate_sample(const vws_sample_args* a) {
     if (!a) return fail(VWS_ERR_INVALID_ARGUMENT, "args is NULL");
     if (a->struct_size != sizeof(vws_sample_args))
@@ -161,7 +167,11 @@ int validate_sample(const vws_sample_args* a) {
         return fail(VWS_ERR_INVALID_ARGUMENT, "logprob outputs are NULL while num_logprobs >= 0");
     if ((st = validate_history(a->prompt_ids, a->prompt_row_stride, a->prompt_width, "prompt"))) return st;
     if ((st = validate_history(a->output_ids, a->output_row_stride, a->output_width, "output"))) return st;
-    const int hw = (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0);
+    if ((st = validate_history(a->adjust_ids, a->adjust_row_stride, a->adjust_width, "adjust"))) return st;
+    if (a->adjust_ids && !a->adjust_vals) return fail(VWS_ERR_INVALID_ARGUMENT, "adjust_vals is NULL while adjust_ids is set");
+    if (a->allowed_mask && a->allowed_row_stride < (int64_t)(a->vocab + 31) / 32)
+        return fail(VWS_ERR_INVALID_ARGUMENT, "allowed_row_stride < ceil(vocab / 32) words");
+    const int hw = sample_history_width(a);
     const size_t need = ws_layout(a->batch, a->vocab, hw, false).total;
     if (need == 0) return VWS_OK;
     if (!a->workspace) return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace is NULL (need %zu bytes)", need);
@@ -225,7 +235,7 @@ int vws_validate_sample_args(const vws_sample_args* args) {
 int vws_sample(const vws_sample_args* a) {
     int st = validate_sample(a);
     if (st) return st;
-    const int hw = (a->prompt_ids ? a->prompt_width : 0) + (a->output_ids ? a->output_width : 0);
+    const int hw = sample_history_width(a);
     KArgs k = make_kargs(a->batch, a->vocab, a->logits, a->logits_row_stride, a->workspace, hw, false);
     k.temperature = a->temperature;
     k.top_k = a->top_k;
@@ -242,6 +252,13 @@ int vws_sample(const vws_sample_args* a) {
     k.ostride = a->output_row_stride;
     k.owidth = a->output_ids ? a->output_width : 0;
     k.olens = a->output_lens;
+    k.allowed = a->allowed_mask;
+    k.astride = a->allowed_row_stride;
+    k.adj_ids = a->adjust_ids;
+    k.adj_vals = a->adjust_vals;
+    k.adjstride = a->adjust_row_stride;
+    k.adjwidth = a->adjust_ids ? a->adjust_width : 0;
+    k.adjlens = a->adjust_lens;
     k.u = a->uniforms;
     k.ustride = a->uniforms_row_stride;
     k.sampled = a->sampled;

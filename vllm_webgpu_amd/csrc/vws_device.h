@@ -117,6 +117,21 @@ __device__ __forceinline__ float apply_penalty(float x, bool in_prompt, uint32_t
     return x;
 }
 
+// History hash value word: output occurrences (bits 0-28), a logit bias present (bit 29),
+// banned by a logits processor (bit 30), token in the prompt (bit 31).
+constexpr uint32_t kHCount = 0x1FFFFFFFu;
+constexpr uint32_t kHBias = 1u << 29;
+constexpr uint32_t kHBan = 1u << 30;
+constexpr uint32_t kHPrompt = 1u << 31;
+
+// A token of the row's hash: the logits processors (ban, else logit bias), then the penalties.
+__device__ __forceinline__ float apply_hashed(float x, uint32_t hv, float bias, float rep,
+                                              float inv_rep, float freq, float pres) {
+    if (hv & kHBan) x = -__builtin_inff();
+    else if (hv & kHBias) x = x + bias;
+    return apply_penalty(x, (hv & kHPrompt) != 0u, hv & kHCount, rep, inv_rep, freq, pres);
+}
+
 // Greedy rows: temperature < 1e-5 or NaN.
 __device__ __forceinline__ bool is_greedy(float T) { return !(T >= kSamplingEps); }
 

@@ -58,13 +58,19 @@ __device__ __forceinline__ uint32_t ghash_slot(int t, int hs) {
     return ((uint32_t)t * 2654435761u) & (uint32_t)(hs - 1);
 }
 
-__device__ __forceinline__ void ghash_insert(uint32_t* hkey, uint32_t* hval, int hs, int t, uint32_t inc) {
+// inc: 1 counts an output occurrence; otherwise kHPrompt, kHBan or kHBias (with its bias) is set
+__device__ __forceinline__ void ghash_insert(uint32_t* hkey, uint32_t* hval, uint32_t* hadj, int hs,
+                                             int t, uint32_t inc, float bias = 0.0f) {
     uint32_t s = ghash_slot(t, hs);
     for (int probe = 0; probe < hs; ++probe) {
         const uint32_t prev = atomicCAS(&hkey[s], 0u, (uint32_t)t + 1u);
         if (prev == 0u || prev == (uint32_t)t + 1u) {
-            if (inc & 0x80000000u) atomicOr(&hval[s], 0x80000000u);
-            else atomicAdd(&hval[s], inc);
+            if (inc == 1u) {
+                atomicAdd(&hval[s], 1u);
+            } else {
+                if (inc & kHBias) __hip_atomic_store(&hadj[s], f2u(bias), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                atomicOr(&hval[s], inc);
+            }
             return;
         }
         s = (s + 1u) & (uint32_t)(hs - 1);
@@ -216,11 +222,14 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
     sl.init(row, 0, V);
     const int nch = sl.nchunks();
     const int nit = (nch + 2 * NT - 1) / (2 * NT);
-    const bool hh = prm.has_hist;
+    const bool hh = prm.need_hash;
     const int hs = a.hs_row;
-    uint32_t* hkey = a.hist_hash + (size_t)r * (size_t)hs * 3;
+    uint32_t* hkey = a.hist_hash + (size_t)r * (size_t)hs * 4;
     uint32_t* hval = hkey + hs;
     uint32_t* hpen = hval + hs;
+    uint32_t* hadj = hpen + hs;
+    const uint32_t* mrow = a.allowed ? a.allowed + (size_t)r * a.astride : nullptr;
+    const int nmw = (V + 31) / 32;
     const int L = a.L;
 
     // ---- history: hash in the workspace + bitmap of positions in LDS
@@ -230,22 +239,34 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
         for (int i = tid; i < hs; i += NT) { hkey[i] = 0u; hval[i] = 0u; hpen[i] = 0u; }
         __threadfence();
         __syncthreads();
-        if (prm.np > 0) {
+        if (prm.has_hist && prm.np > 0) {
             const int32_t* pr = a.prompt + (size_t)r * a.pstride;
             for (int i = tid; i < prm.np; i += NT) {
                 const int t = pr[i];
                 if (t >= 0 && t < V) {
-                    ghash_insert(hkey, hval, hs, t, 0x80000000u);
+                    ghash_insert(hkey, hval, hadj, hs, t, kHPrompt);
                     atomicOr(&sm.bitmap[t >> 5], 1u << (t & 31));
                 }
             }
         }
-        if (prm.no > 0) {
+        if (prm.has_hist && prm.no > 0) {
             const int32_t* ou = a.output + (size_t)r * a.ostride;
             for (int i = tid; i < prm.no; i += NT) {
                 const int t = ou[i];
                 if (t >= 0 && t < V) {
-                    ghash_insert(hkey, hval, hs, t, 1u);
+                    ghash_insert(hkey, hval, hadj, hs, t, 1u);
+                    atomicOr(&sm.bitmap[t >> 5], 1u << (t & 31));
+                }
+            }
+        }
+        if (prm.na > 0) {
+            const int32_t* ai = a.adj_ids + (size_t)r * a.adjstride;
+            const float* av = a.adj_vals + (size_t)r * a.adjstride;
+            for (int i = tid; i < prm.na; i += NT) {
+                const int t = ai[i];
+                if (t >= 0 && t < V) {
+                    const float bv = av[i];
+                    ghash_insert(hkey, hval, hadj, hs, t, bv == -__builtin_inff() ? kHBan : kHBias, bv);
                     atomicOr(&sm.bitmap[t >> 5], 1u << (t & 31));
                 }
             }
@@ -257,23 +278,35 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             if (kk) {
                 const uint32_t v = __hip_atomic_load(&hval[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const float raw = Elem<T>::load1(row + (kk - 1u));
-                const float pen = apply_penalty(raw, (v >> 31) != 0u, v & 0x7FFFFFFFu, prm.rep,
-                                                prm.inv_rep, prm.freq, prm.pres);
+                const float bias = u2f(__hip_atomic_load(&hadj[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                const float pen = apply_hashed(raw, v, bias, prm.rep, prm.inv_rep, prm.freq, prm.pres);
                 __hip_atomic_store(&hpen[s], f2u(pen), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         __threadfence();
         __syncthreads();
     }
+    // processed values of a chunk: hashed tokens (processors, then penalties), then the
+    // allowed-token mask (masked tokens are -inf whatever the hash did to them)
     auto finalize = [&](float* v, int i0) {
-        if (!hh) return;
-        const uint32_t w = (uint32_t)i0 >> 5, sh = (uint32_t)i0 & 31u;
-        const uint64_t win = (uint64_t)sm.bitmap[w] | ((uint64_t)sm.bitmap[w + 1] << 32);
-        const uint32_t bits = (uint32_t)(win >> sh) & ((1u << VEC) - 1u);
-        if (bits) {
+        if (hh) {
+            const uint32_t w = (uint32_t)i0 >> 5, sh = (uint32_t)i0 & 31u;
+            const uint64_t win = (uint64_t)sm.bitmap[w] | ((uint64_t)sm.bitmap[w + 1] << 32);
+            const uint32_t bits = (uint32_t)(win >> sh) & ((1u << VEC) - 1u);
+            if (bits) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j)
+                    if ((bits >> j) & 1u) v[j] = ghash_pen(hkey, hpen, hs, i0 + j, v[j]);
+            }
+        }
+        if (mrow) {
+            const int w = i0 >> 5, sh = i0 & 31;
+            const uint64_t win = (uint64_t)mrow[w < nmw ? w : nmw - 1] |
+                                 ((uint64_t)(w + 1 < nmw ? mrow[w + 1] : 0u) << 32);
+            const uint32_t bits = (uint32_t)(win >> sh);
 #pragma unroll
             for (int j = 0; j < VEC; ++j)
-                if (((bits >> j) & 1u) && v[j] == v[j]) v[j] = ghash_pen(hkey, hpen, hs, i0 + j, v[j]);
+                if (!((bits >> j) & 1u) && i0 + j < V) v[j] = -__builtin_inff();
         }
     };
     // every pass visits the same chunks in the same order: 2 chunks per thread per iteration

@@ -52,6 +52,13 @@ struct KArgs {
     int64_t ostride;
     int owidth;
     const int32_t* olens;
+    const uint32_t* allowed;   // [B, astride] words, bit set = token allowed (or null)
+    int64_t astride;
+    const int32_t* adj_ids;    // [B, adjstride] sparse processor list (or null)
+    const float* adj_vals;
+    int64_t adjstride;
+    int adjwidth;
+    const int32_t* adjlens;
     const float* u;
     int64_t ustride;
     int32_t* sampled;
@@ -66,7 +73,7 @@ struct KArgs {
     uint32_t* row_state;    // [B]
     uint32_t* part_meta;    // [B * kMaxParts * 4]: count, kth key, status, 0
     uint2* part_list;       // [B * kMaxParts * kPartCap]: (key, index)
-    uint32_t* hist_hash;    // [B * hs_row * 3]: token+1, count | prompt<<31, penalised bits
+    uint32_t* hist_hash;    // [B * hs_row * 4]: token+1, count | flags, penalised bits, bias
     int hs_row;             // history hash slots per row (power of two) or 0
     int S;                  // parts per row
     int part_len;           // elements per part (multiple of 64)
@@ -92,7 +99,7 @@ inline int hash_slots_for(int history_width) {
 }
 
 // Workspace sections.  Sampling and the penalty op keep only the history hash of the multi-pass
-// path (B x hs_row x 3 words, zero between calls); the split top-k op also needs its per-row
+// path (B x hs_row x 4 words); the split top-k op also needs its per-row
 // counters, row states and part lists (parts = true).
 inline WsLayout ws_layout(int B, int V, int history_width, bool parts) {
     (void)V;
@@ -105,7 +112,7 @@ inline WsLayout ws_layout(int B, int V, int history_width, bool parts) {
         w.list = off;    off = align256(off + sizeof(uint2) * (size_t)B * kMaxParts * kPartCap);
     }
     w.hs_row = hash_slots_for(history_width);
-    w.hash = off;    off = align256(off + sizeof(uint32_t) * 3 * (size_t)B * (size_t)w.hs_row);
+    w.hash = off;    off = align256(off + sizeof(uint32_t) * 4 * (size_t)B * (size_t)w.hs_row);
     w.total = off;
     return w;
 }

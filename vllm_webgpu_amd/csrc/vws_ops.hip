@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kOpThreads) void penalties_kernel(KArgs a, float* l
     const int no = a.output ? (a.olens ? min(max(a.olens[r], 0), a.owidth) : a.owidth) : 0;
     const int hs = a.hs_row;
     if (hs == 0 || (np == 0 && no == 0)) return;
-    uint32_t* hkey = a.hist_hash + (size_t)r * (size_t)hs * 3;
+    uint32_t* hkey = a.hist_hash + (size_t)r * (size_t)hs * 4;
     uint32_t* hval = hkey + hs;
     for (int i = threadIdx.x; i < hs; i += kOpThreads) { hkey[i] = 0u; hval[i] = 0u; }
     __threadfence();

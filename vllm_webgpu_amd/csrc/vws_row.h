@@ -11,7 +11,10 @@ namespace vws {
 struct RowP {
     float T, top_p, min_p, rep, pres, freq, inv_rep;
     int k, np, no;
-    bool greedy, has_hist;
+    int na;          // logits-processor entries (bans, logit bias) of the row
+    bool greedy;
+    bool has_hist;   // penalties apply: a history and not every penalty the identity
+    bool need_hash;  // the row's hash holds history or processor tokens
 };
 
 __device__ __forceinline__ RowP row_params(const KArgs& a, int r) {
@@ -30,18 +33,21 @@ __device__ __forceinline__ RowP row_params(const KArgs& a, int r) {
     // vLLM skips the penalty step when every penalty is the identity; the result is the same
     const bool identity = (p.rep == 1.0f && p.pres == 0.0f && p.freq == 0.0f);
     p.has_hist = (p.np > 0 || p.no > 0) && !identity;
+    p.na = a.adj_ids ? (a.adjlens ? min(max(a.adjlens[r], 0), a.adjwidth) : a.adjwidth) : 0;
     if (a.mode == kModeTopK) {
         p.greedy = false;
         p.has_hist = false;
+        p.na = 0;
         p.k = a.topk_k;
     }
+    p.need_hash = p.has_hist || p.na > 0;
     return p;
 }
 
 // k served by the single-pass kernel for this row, or 0 when the row needs the general kernel.
 __device__ __forceinline__ int fast_k(const KArgs& a, const RowP& p) {
     if (a.mode == kModeTopK) return a.topk_k;
-    if (a.L >= 0) return 0;
+    if (a.L >= 0 || a.allowed) return 0;
     if (p.greedy) return 1;
     if (p.k > 0 && p.k < a.V && p.k <= kKMax) return p.k;
     return 0;

@@ -47,9 +47,10 @@ struct RowSmem {
     uint64_t sC[kRowKeep];                   // survivors' cumulative masses (partial sums)
     uint64_t sW;                             // total mass of the survivors
     uint32_t rhist[kRowWaves][256];          // per-wave radix-select scratch
-    uint32_t hkey[kRowHash];                 // history token + 1 (0 = empty)
-    uint32_t hval[kRowHash];                 // output count | prompt flag << 31
-    float hpen[kRowHash];                    // penalised value (gather mode)
+    uint32_t hkey[kRowHash];                 // history / processor token + 1 (0 = empty)
+    uint32_t hval[kRowHash];                 // output count | kHBias | kHBan | kHPrompt
+    float hpen[kRowHash];                    // processed value (gather mode)
+    float hadj[kRowHash];                    // logit bias (kHBias)
     alignas(16) uint64_t sck[kRowKeep];      // survivors: key(y) << 32 | index
     alignas(16) uint64_t sw[kRowKeep];       // exact mass
     float se[kRowKeep];                      // exp(y - max)
@@ -59,6 +60,7 @@ struct RowSmem {
     uint64_t red[kRowWaves][8];
     uint32_t tauw[kRowWaves];
     uint32_t tau, status, nhash, nkeep;
+    uint32_t adjraise;                       // a positive logit bias was inserted
     uint32_t bc[8];
     // penalty context of the row for the out-of-line fix-up: mode 0 none, 1 penalise, 2 drop
     uint32_t pmode;
@@ -74,14 +76,19 @@ __device__ __forceinline__ uint32_t rhash_slot(int t) {
     return ((uint32_t)t * 2654435761u) >> (32 - 11);  // kRowHash = 2048
 }
 
-__device__ __forceinline__ void rhash_insert(RowSmem& sm, int t, uint32_t inc) {
+// inc: 1 counts an output occurrence; otherwise kHPrompt, kHBan or kHBias (with its bias) is set
+__device__ __forceinline__ void rhash_insert(RowSmem& sm, int t, uint32_t inc, float bias = 0.0f) {
     uint32_t s = rhash_slot(t);
     for (int probe = 0; probe < kRowHash; ++probe) {
         const uint32_t prev = atomicCAS(&sm.hkey[s], 0u, (uint32_t)t + 1u);
         if (prev == 0u && atomicAdd(&sm.nhash, 1u) >= (uint32_t)kRowHashFill) atomicOr(&sm.status, 1u);
         if (prev == 0u || prev == (uint32_t)t + 1u) {
-            if (inc & 0x80000000u) atomicOr(&sm.hval[s], 0x80000000u);
-            else atomicAdd(&sm.hval[s], inc);
+            if (inc == 1u) {
+                atomicAdd(&sm.hval[s], 1u);
+            } else {
+                if (inc & kHBias) sm.hadj[s] = bias;  // one finite entry per token and row
+                atomicOr(&sm.hval[s], inc);
+            }
             return;
         }
         s = (s + 1u) & (kRowHash - 1);
@@ -89,16 +96,16 @@ __device__ __forceinline__ void rhash_insert(RowSmem& sm, int t, uint32_t inc) {
     atomicOr(&sm.status, 1u);
 }
 
-// count | prompt << 31 of history token t, 0 when absent
-__device__ __forceinline__ uint32_t rhash_value(const RowSmem& sm, int t) {
+// slot of token t in the row's hash, -1 when absent
+__device__ __forceinline__ int rhash_find(const RowSmem& sm, int t) {
     uint32_t s = rhash_slot(t);
     for (int probe = 0; probe < kRowHash; ++probe) {
         const uint32_t k = sm.hkey[s];
-        if (k == (uint32_t)t + 1u) return sm.hval[s];
-        if (k == 0u) return 0u;
+        if (k == (uint32_t)t + 1u) return (int)s;
+        if (k == 0u) return -1;
         s = (s + 1u) & (kRowHash - 1);
     }
-    return 0u;
+    return -1;
 }
 
 // The race over the kept survivors and the diagnostics of the top-p cut.
@@ -150,11 +157,12 @@ struct RowRace {
 // LDS of the row kernel: the single-pass state and the general path's state share it.
 __shared__ RowShared g_row_sh;
 
-// Applies the penalties to wave w's candidates [from, cnt), in place, and returns the new count.
-// Candidates enter the buffer by their raw value; with penalties that never raise a logit
-// (mode 1) the raw value bounds the penalised one from above, so nothing is missed and the key
-// is corrected here.  In mode 2 (a penalty may raise a logit) the penalised history values were
-// added up front with bit 31 of the index set; stream entries of history tokens are dropped.
+// Applies the logits processors and penalties to wave w's candidates [from, cnt), in place, and
+// returns the new count.  Candidates enter the buffer by their raw value; when nothing can raise
+// a logit (mode 1: bans, non-positive biases, penalties with r >= 1, f >= 0, p >= 0) the raw
+// value bounds the processed one from above, so nothing is missed and the key is corrected
+// here.  In mode 2 (something may raise a logit) the processed values of the hashed tokens were
+// added up front with bit 31 of the index set; stream entries of hashed tokens are dropped.
 __device__ __noinline__ int row_fixup(int w, int from, int cnt) {
     RowSmem& sm = g_row_sh.f;
     const uint32_t mode = sm.pmode;
@@ -175,11 +183,11 @@ __device__ __noinline__ int row_fixup(int w, int from, int cnt) {
             if (ii < 0) {
                 ii &= 0x7FFFFFFF;  // added up front, already penalised
             } else {
-                const uint32_t hv = rhash_value(sm, ii);
-                if (hv != 0u) {
+                const int hs = rhash_find(sm, ii);
+                if (hs >= 0) {
                     if (mode == 2u) keep = false;
-                    else kk = key_of(apply_penalty(val_of(kk), (hv >> 31) != 0u, hv & 0x7FFFFFFFu,
-                                                   sm.prep, sm.pinv, sm.pfreq, sm.ppres));
+                    else kk = key_of(apply_hashed(val_of(kk), sm.hval[hs], sm.hadj[hs], sm.prep,
+                                                  sm.pinv, sm.pfreq, sm.ppres));
                 }
             }
         }
@@ -293,24 +301,26 @@ __device__ __forceinline__ RowP row_params_scalar(const KArgs& a, int r) {
     const int32_t* pK = a.top_k ? a.top_k + r : &kRowDefaultsI[0];
     const int32_t* pPL = a.plens ? a.plens + r : &kRowDefaultsI[1];
     const int32_t* pOL = a.olens ? a.olens + r : &kRowDefaultsI[1];
+    const int32_t* pAL = a.adjlens ? a.adjlens + r : &kRowDefaultsI[1];
     RowP p;
-    int pl, ol;
+    int pl, ol, al;
     // scalar loads on the scalar counter; the compiler would otherwise issue vector loads, and
     // waiting for those would also wait for every logits load issued before them
     asm volatile(
-        "s_load_dword %0, %9, 0x0\n\t"
-        "s_load_dword %1, %10, 0x0\n\t"
-        "s_load_dword %2, %11, 0x0\n\t"
-        "s_load_dword %3, %12, 0x0\n\t"
-        "s_load_dword %4, %13, 0x0\n\t"
-        "s_load_dword %5, %14, 0x0\n\t"
-        "s_load_dword %6, %15, 0x0\n\t"
-        "s_load_dword %7, %16, 0x0\n\t"
-        "s_load_dword %8, %17, 0x0\n\t"
+        "s_load_dword %0, %10, 0x0\n\t"
+        "s_load_dword %1, %11, 0x0\n\t"
+        "s_load_dword %2, %12, 0x0\n\t"
+        "s_load_dword %3, %13, 0x0\n\t"
+        "s_load_dword %4, %14, 0x0\n\t"
+        "s_load_dword %5, %15, 0x0\n\t"
+        "s_load_dword %6, %16, 0x0\n\t"
+        "s_load_dword %7, %17, 0x0\n\t"
+        "s_load_dword %8, %18, 0x0\n\t"
+        "s_load_dword %9, %19, 0x0\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&s"(p.T), "=&s"(p.top_p), "=&s"(p.min_p), "=&s"(p.rep), "=&s"(p.pres), "=&s"(p.freq),
-          "=&s"(p.k), "=&s"(pl), "=&s"(ol)
-        : "s"(pT), "s"(pP), "s"(pM), "s"(pR), "s"(pS), "s"(pF), "s"(pK), "s"(pPL), "s"(pOL)
+          "=&s"(p.k), "=&s"(pl), "=&s"(ol), "=&s"(al)
+        : "s"(pT), "s"(pP), "s"(pM), "s"(pR), "s"(pS), "s"(pF), "s"(pK), "s"(pPL), "s"(pOL), "s"(pAL)
         : "memory");
     p.greedy = is_greedy(p.T);
     p.inv_rep = 1.0f / p.rep;
@@ -318,6 +328,8 @@ __device__ __forceinline__ RowP row_params_scalar(const KArgs& a, int r) {
     p.no = a.output ? min(max(ol, 0), a.owidth) : 0;
     const bool identity = (p.rep == 1.0f && p.pres == 0.0f && p.freq == 0.0f);
     p.has_hist = (p.np > 0 || p.no > 0) && !identity;
+    p.na = a.adj_ids ? min(max(al, 0), a.adjwidth) : 0;
+    p.need_hash = p.has_hist || p.na > 0;
     return p;
 }
 
@@ -342,6 +354,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     //    Buffer loads: a row's loads share one lane offset (the iteration and vector go in the
     //    scalar offset), and loads past the end read zeros, so nothing is clamped.
     const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
+    const bool has_a = a.adj_ids && a.adjwidth > 0;
+    const int32_t* aidrow = has_a ? a.adj_ids + (size_t)r * a.adjstride : nullptr;
+    const float* avrow = has_a ? a.adj_vals + (size_t)r * a.adjstride : nullptr;
     const int32_t* prow = has_p ? a.prompt + (size_t)r * a.pstride : nullptr;
     const int32_t* orow = has_o ? a.output + (size_t)r * a.ostride : nullptr;
     const __amdgpu_buffer_rsrc_t prs = make_rsrc(has_p ? (const void*)prow : (const void*)row,
@@ -350,6 +365,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                                                  has_o ? 4u * (uint32_t)a.owidth : 0u);
     const int hp_raw = __builtin_amdgcn_raw_buffer_load_b32(prs, 4u * (uint32_t)tid, 0u, 0);
     const int ho_raw = __builtin_amdgcn_raw_buffer_load_b32(ors, 4u * (uint32_t)tid, 0u, 0);
+    const __amdgpu_buffer_rsrc_t ais = make_rsrc(has_a ? (const void*)aidrow : (const void*)row,
+                                                 has_a ? 4u * (uint32_t)a.adjwidth : 0u);
+    const __amdgpu_buffer_rsrc_t avs = make_rsrc(has_a ? (const void*)avrow : (const void*)row,
+                                                 has_a ? 4u * (uint32_t)a.adjwidth : 0u);
+    const int ha_id = __builtin_amdgcn_raw_buffer_load_b32(ais, 4u * (uint32_t)tid, 0u, 0);
+    const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
     Slice<T> sl;
     sl.init(row, 0, V);
     const int nbody = sl.nbody;
@@ -372,20 +393,22 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
     if (k == 0) return false;
-    const bool hh = prm.has_hist;
-    // penalties that never raise a logit let history candidates be found by their raw value
-    const bool mono = prm.rep >= 1.0f && prm.pres >= 0.0f && prm.freq >= 0.0f;
-    const bool gather = hh && !mono;
+    const bool hh = prm.has_hist;     // penalties
+    const bool hx = prm.need_hash;    // penalties or logits processors
+    // processors and penalties that never raise a logit let hashed candidates be found by their
+    // raw value (a positive logit bias is only seen once the hash is built)
+    const bool mono = !hh || (prm.rep >= 1.0f && prm.pres >= 0.0f && prm.freq >= 0.0f);
     const int32_t* pr = hh && prm.np > 0 ? prow : nullptr;
     const int32_t* ou = hh && prm.no > 0 ? orow : nullptr;
 
     // 2. LDS state and the history hash
     if (tid == 0) {
         sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.npack = 0u; sm.bc[4] = 0u;
-        sm.pmode = !hh ? 0u : (gather ? 2u : 1u);
+        sm.pmode = hx ? 1u : 0u;
+        sm.adjraise = 0u;
         sm.prep = prm.rep; sm.pinv = prm.inv_rep; sm.ppres = prm.pres; sm.pfreq = prm.freq;
     }
-    if (hh) {
+    if (hx) {
         for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
     }
     sm.pkey[tid] = 0u;   // unpacked slots keep key 0, which ranks below every candidate
@@ -408,6 +431,19 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 if (t >= 0 && t < V) rhash_insert(sm, t, 1u);
             }
         }
+    }
+    if (prm.na > 0) {
+        auto add = [&](int t, float bv) {
+            if (t < 0 || t >= V) return;
+            if (bv == -__builtin_inff()) {
+                rhash_insert(sm, t, kHBan);
+            } else {
+                rhash_insert(sm, t, kHBias, bv);
+                if (bv > 0.0f) sm.adjraise = 1u;
+            }
+        };
+        if (tid < prm.na) add(ha_id, ha_val);
+        for (int i = NT + tid; i < prm.na; i += NT) add(aidrow[i], avrow[i]);
     }
 
     // 3. seed threshold from the first iteration
@@ -444,13 +480,14 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                                                  sm.seedk[4 * lane + 2], sm.seedk[4 * lane + 3], m_seed);
         if (lane == 0) sm.bc[0] = t0;
     }
+    const bool gather = hx && (!mono || sm.adjraise != 0u);
     if (gather) {
+        if (lane == 0) sm.pmode = 2u;  // every wave writes the same value before its stream
         for (int s = tid; s < kRowHash; s += NT) {
             const uint32_t kk = sm.hkey[s];
             if (kk) {
-                const uint32_t v = sm.hval[s];
-                sm.hpen[s] = apply_penalty(Elem<T>::load1(row + (kk - 1u)), (v >> 31) != 0u,
-                                           v & 0x7FFFFFFFu, prm.rep, prm.inv_rep, prm.freq, prm.pres);
+                sm.hpen[s] = apply_hashed(Elem<T>::load1(row + (kk - 1u)), sm.hval[s], sm.hadj[s],
+                                          prm.rep, prm.inv_rep, prm.freq, prm.pres);
             }
         }
     }

@@ -97,13 +97,18 @@ class SampleResult:
 def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p=None,
            repetition_penalty=None, presence_penalty=None, frequency_penalty=None,
            prompt_ids=None, prompt_lens=None, output_ids=None, output_lens=None,
-           uniforms: torch.Tensor | None = None, num_logprobs: int | None = None) -> SampleResult:
+           uniforms: torch.Tensor | None = None, num_logprobs: int | None = None,
+           allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
+           adjust_lens=None) -> SampleResult:
     """Samples one token per row of ``logits`` [B, V] (float32 or bfloat16, on the GPU).
 
     Per-row parameters are scalars or [B] tensors; ``None`` means off (temperature None = every
     row greedy).  Histories are padded int32 [B, W] (ids outside [0, V) are padding).
     ``uniforms`` [B, V] float32 in (0, 1) drive the exponential race and are required whenever
-    ``temperature`` is given.
+    ``temperature`` is given.  Logits processors (before the penalties): ``allowed_mask``
+    int32 [B, ceil(V/32)] bit words (bit set = token allowed, see ``pack_allowed``), and the
+    sparse ``adjust_ids`` int32 / ``adjust_vals`` float32 [B, W]: -inf bans a token, a finite
+    value is added to its logit.
     """
     _check_device(logits, "logits")
     if logits.dim() != 2:
@@ -121,6 +126,25 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     FR = _row_param(frequency_penalty, B, torch.float32, dev, "frequency_penalty")
     pid, pstride, pwidth, plens = _history(prompt_ids, prompt_lens, B, dev, "prompt_ids")
     oid, ostride, owidth, olens = _history(output_ids, output_lens, B, dev, "output_ids")
+    aid, astride, awidth, alens = _history(adjust_ids, adjust_lens, B, dev, "adjust_ids")
+    aval = None
+    if aid is not None:
+        if adjust_vals is None:
+            raise ValueError("adjust_vals is required with adjust_ids")
+        aval = adjust_vals.to(device=dev, dtype=torch.float32)
+        if aval.shape != aid.shape:
+            raise ValueError(f"adjust_vals must have the shape of adjust_ids {tuple(aid.shape)}")
+        if aval.stride() != aid.stride():
+            aid, aval = aid.contiguous(), aval.contiguous()
+            astride = aid.stride(0)
+    AM = None
+    if allowed_mask is not None:
+        _check_device(allowed_mask, "allowed_mask")
+        AM = allowed_mask.to(torch.int32)
+        if AM.dim() != 2 or AM.shape[0] != B or AM.shape[1] < (V + 31) // 32:
+            raise ValueError(f"allowed_mask must be [{B}, >= {(V + 31) // 32}] words")
+        if AM.stride(1) != 1:
+            AM = AM.contiguous()
     U = None
     if uniforms is not None:
         _check_device(uniforms, "uniforms")
@@ -139,7 +163,7 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
         lp_vals = torch.empty((B, L + 1), dtype=torch.float32, device=dev)
         ranks = torch.empty(B, dtype=torch.int32, device=dev)
     L_lib = _lib.lib()
-    nbytes = L_lib.vws_sample_workspace_size(B, V, pwidth + owidth)
+    nbytes = L_lib.vws_sample_workspace_size(B, V, pwidth + owidth + awidth)
     ws = workspace(nbytes, dev)
     a = _lib.SampleArgs()
     a.struct_size = ctypes.sizeof(_lib.SampleArgs)
@@ -149,6 +173,11 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     a.repetition_penalty, a.presence_penalty, a.frequency_penalty = _ptr(R), _ptr(PR), _ptr(FR)
     a.prompt_ids, a.prompt_row_stride, a.prompt_width, a.prompt_lens = _ptr(pid), pstride, pwidth, _ptr(plens)
     a.output_ids, a.output_row_stride, a.output_width, a.output_lens = _ptr(oid), ostride, owidth, _ptr(olens)
+    if AM is not None:
+        a.allowed_mask, a.allowed_row_stride = AM.data_ptr(), AM.stride(0)
+    if aid is not None:
+        a.adjust_ids, a.adjust_vals = aid.data_ptr(), aval.data_ptr()
+        a.adjust_row_stride, a.adjust_width, a.adjust_lens = astride, awidth, _ptr(alens)
     a.uniforms = _ptr(U)
     a.uniforms_row_stride = U.stride(0) if U is not None else 0
     a.sampled, a.row_flags, a.num_kept = sampled.data_ptr(), flags.data_ptr(), nkept.data_ptr()
@@ -159,6 +188,18 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     _lib.check(L_lib.vws_sample(ctypes.byref(a)))
     # keep the argument tensors alive until the work is enqueued (it is, on return)
     return SampleResult(sampled, flags, nkept, lp_ids, lp_vals, ranks)
+
+
+def pack_allowed(allowed: torch.Tensor) -> torch.Tensor:
+    """bool [B, V] (True = allowed) -> int32 [B, ceil(V/32)] bit words, on the same device."""
+    B, V = allowed.shape
+    W = (V + 31) // 32
+    bits = torch.zeros((B, W * 32), dtype=torch.int64, device=allowed.device)
+    bits[:, :V] = allowed.to(torch.int64)
+    weights = torch.bitwise_left_shift(torch.ones(32, dtype=torch.int64, device=allowed.device),
+                                       torch.arange(32, device=allowed.device))
+    words = (bits.view(B, W, 32) * weights).sum(dim=2)
+    return (words - (words >= 2 ** 31).to(torch.int64) * 2 ** 32).to(torch.int32)
 
 
 def argmax(logits: torch.Tensor) -> torch.Tensor:
