@@ -158,3 +158,61 @@ def test_runner_steps_match_oracle(cuda):
         n = len(outputs[r])
         assert b.output_ids[st.slot, :n].tolist() == outputs[r] and st.output_token_ids == outputs[r]
         assert int(b.output_lens[st.slot]) == n
+
+
+def test_runner_logits_processors_match_oracle(cuda):
+    from vllm_webgpu_amd.v1.sample.sampler import processor_lists
+
+    V = 2048
+    model = _FakeModel(V, cuda)
+    runner = ROCmModelRunner(None, cuda, model, max_num_reqs=8, max_prompt_len=16,
+                             max_output_len=16)
+    params = {
+        "bias": _sp(temperature=0.8, top_k=20, seed=31, logit_bias={7: 12.0, 8: -30.0}),
+        "mint": _sp(temperature=0.0, min_tokens=3, stop_token_ids=[1, 2], eos_token_id=3),
+        "bad": _sp(temperature=0.0, bad_words_token_ids=[[5], [1, 9]], repetition_penalty=1.2),
+        "allow": _sp(temperature=1.0, seed=32, allowed_token_ids=[10, 11, 12, 13, 400]),
+    }
+    prompts = {"bias": [4], "mint": [1], "bad": [1], "allow": [10, 11]}
+    mirror = {r: torch.Generator(device=cuda).manual_seed(params[r].seed)
+              for r in params if params[r].seed is not None}
+    outputs = {r: [] for r in params}
+    active = list(params)
+    for step in range(4):
+        so = NS(scheduled_new_reqs=[NS(req_id=r, prompt_token_ids=prompts[r],
+                                       sampling_params=params[r]) for r in active] if step == 0 else [],
+                finished_req_ids=set(), num_scheduled_tokens={r: 1 for r in active})
+        runner.execute_model(so)
+        md = runner.input_batch.make_sampling_metadata(active)
+        mro = runner.sample_tokens(None)
+        B = len(active)
+        u = np.full((B, V), 0.5, np.float32)
+        for i, r in enumerate(active):
+            if r in mirror:
+                row = torch.empty(V, dtype=torch.float32, device=cuda).uniform_(generator=mirror[r])
+                u[i] = row.clamp_(min=2.0 ** -24).cpu().numpy()
+        sps = [params[r] for r in active]
+        prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
+                            [s.top_p for s in sps], [s.min_p for s in sps],
+                            [s.repetition_penalty for s in sps], [s.presence_penalty for s in sps],
+                            [s.frequency_penalty for s in sps])
+        pr = np.full((B, 2), V, np.int32)
+        ou = np.full((B, max(1, step)), V, np.int32)
+        for i, r in enumerate(active):
+            pr[i, :len(prompts[r])] = prompts[r]
+            ou[i, :len(outputs[r])] = outputs[r]
+        ids, vals = processor_lists(md, B, V)
+        allowed = ~md.allowed_token_ids_mask.cpu().numpy()
+        words = np.zeros((B, (V + 31) // 32 * 32), np.uint64)
+        words[:, :V] = allowed
+        bits = (words.reshape(B, -1, 32) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
+        ref = O.sample(model.history[-1], prm, u, prompt_ids=pr, output_ids=ou, allowed=bits,
+                       adjust_ids=ids.numpy(), adjust_vals=vals.numpy())
+        got = [t[0] for t in mro.sampled_token_ids]
+        assert got == ref["token"].tolist(), f"step {step}: {got} vs {ref['token'].tolist()}"
+        tok = dict(zip(active, got))
+        assert tok["bad"] != 5 and tok["allow"] in (10, 11, 12, 13, 400)
+        if step < 3:
+            assert tok["mint"] not in (1, 2, 3)
+        for r, t in zip(active, got):
+            outputs[r].append(t)

@@ -9,7 +9,8 @@ import torch
 from vllm_webgpu_amd.v1.model_runner import InputBatch, ROCmModelRunner, WebGPUModelRunner
 from vllm_webgpu_amd.v1.outputs import LogprobsTensors, ModelRunnerOutput, SamplerOutput
 from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
-from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_uniforms, pad_output_ids
+from vllm_webgpu_amd.v1.sample.sampler import (Sampler, draw_uniforms, pad_output_ids,
+                                                processor_lists)
 
 V = 100
 
@@ -94,18 +95,70 @@ def test_input_batch_append_and_slot_reuse():
         b.add_request("c", [1], sp())              # duplicate id
 
 
-def test_sampler_refuses_cpu_logits_and_unsupported_processors():
+def test_sampler_refuses_cpu_logits_and_unsupported_modes():
     s = Sampler()
     b = InputBatch(1, 2, 2, V, torch.device("cpu"))
     b.add_request("a", [1], sp())
     m = b.make_sampling_metadata(["a"])
     with pytest.raises(ValueError, match="ROCm device"):
         s(torch.zeros(1, V), m)                    # no host fallback
-    m.allowed_token_ids_mask = torch.zeros(1, V, dtype=torch.bool)
-    with pytest.raises(NotImplementedError):
-        s(torch.zeros(1, V), m)
     with pytest.raises(NotImplementedError):
         Sampler(logprobs_mode="processed_logprobs")
+
+
+def _meta(**kw):
+    base = dict(temperature=None, all_greedy=True, all_random=False, top_p=None, top_k=None,
+                generators={}, max_num_logprobs=None, no_penalties=True, prompt_token_ids=None,
+                frequency_penalties=None, presence_penalties=None, repetition_penalties=None,
+                output_token_ids=[[], []])
+    base.update(kw)
+    return SamplingMetadata(**base)
+
+
+def test_processor_lists_bad_words_min_tokens_and_bias():
+    m = _meta(output_token_ids=[[5, 6, 7], [9]],
+              bad_words_token_ids={0: [[3], [6, 7, 11], [5, 12], [1, 2, 3, 4, 5, 13]],
+                                   1: [[9, 14], [8, 15]]},
+              min_tokens={0: (2, {0}), 1: (3, {0, 2})},
+              logit_bias=[None, {4: 1.5, 20: -2.0}])
+    ids, vals = processor_lists(m, 2, V)
+    rows = [{(int(t), float(v)) for t, v in zip(ids[i].tolist(), vals[i].tolist()) if t < V}
+            for i in range(2)]
+    ninf = float("-inf")
+    # row 0: [3] always, [6, 7, 11] matches the output tail, [5, 12] does not, too long skipped;
+    # min_tokens 2 already reached
+    assert rows[0] == {(3, ninf), (11, ninf)}
+    # row 1: [9, 14] matches, [8, 15] does not; min_tokens 3 not reached -> stop ids 0, 2; bias
+    assert rows[1] == {(14, ninf), (0, ninf), (2, ninf), (4, 1.5), (20, -2.0)}
+    assert ids.shape[1] == 5 and (ids[0, 2:] == V).all()          # padded with V
+    assert processor_lists(_meta(), 2, V) is None
+
+
+def test_pack_allowed_bits():
+    from vllm_webgpu_amd.ops import pack_allowed
+    allowed = torch.zeros(2, 70, dtype=torch.bool)
+    allowed[0, [0, 31, 32, 69]] = True
+    allowed[1] = True
+    w = pack_allowed(allowed)
+    assert w.dtype == torch.int32 and w.shape == (2, 3)
+    u = w.to(torch.int64) & 0xFFFFFFFF
+    assert u[0].tolist() == [1 | (1 << 31), 1, 1 << 5]
+    assert u[1].tolist() == [0xFFFFFFFF, 0xFFFFFFFF, (1 << 6) - 1]
+
+
+def test_input_batch_processor_fields():
+    b = InputBatch(2, 4, 4, V, torch.device("cpu"))
+    b.add_request("a", [1], NS(temperature=0.0, logit_bias={3: 2.0}, min_tokens=2,
+                                stop_token_ids=[7], eos_token_id=0,
+                                bad_words_token_ids=[[5]], allowed_token_ids=None))
+    b.add_request("b", [2], NS(temperature=1.0, allowed_token_ids=[1, 2, 3]))
+    m = b.make_sampling_metadata(["a", "b"])
+    assert m.logit_bias == [{3: 2.0}, None]
+    assert m.min_tokens == {0: (2, {0, 7})}
+    assert m.bad_words_token_ids == {0: [[5]]}
+    assert m.allowed_token_ids_mask.shape == (2, V)
+    assert not m.allowed_token_ids_mask[0].any()
+    assert m.allowed_token_ids_mask[1].sum() == V - 3 and not m.allowed_token_ids_mask[1, 1:4].any()
 
 
 def test_runner_without_model_and_grammar():

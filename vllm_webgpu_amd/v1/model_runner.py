@@ -122,6 +122,28 @@ class InputBatch:
         freq = [float(_param(sp, "frequency_penalty", 0.0)) for sp in sps]
         lps = [_param(sp, "logprobs", None) for sp in sps]
         lps = [int(x) for x in lps if x is not None]
+        # logits processors (vLLM-v1 SamplingParams fields)
+        bias = [_param(sp, "logit_bias", None) for sp in sps]
+        bad = {i: [list(w) for w in _param(sp, "bad_words_token_ids", [])]
+               for i, sp in enumerate(sps) if _param(sp, "bad_words_token_ids", None)}
+        mint = {}
+        for i, sp in enumerate(sps):
+            mt = int(_param(sp, "min_tokens", 0))
+            if mt > 0:
+                stop = set(_param(sp, "stop_token_ids", [])) | set(_param(sp, "all_stop_token_ids", []))
+                eos = _param(sp, "eos_token_id", None)
+                if eos is not None:
+                    stop.add(int(eos))
+                mint[i] = (mt, stop)
+        allowed_rows = [_param(sp, "allowed_token_ids", None) for sp in sps]
+        allowed_mask = None
+        if any(a is not None for a in allowed_rows):
+            allowed_mask = torch.zeros((B, self.vocab_size), dtype=torch.bool)
+            for i, ids in enumerate(allowed_rows):
+                if ids is not None:
+                    allowed_mask[i] = True
+                    allowed_mask[i, torch.as_tensor(list(ids), dtype=torch.int64)] = False
+            allowed_mask = allowed_mask.to(dev, non_blocking=True)
 
         def t(x, dtype):
             return torch.tensor(x, dtype=dtype).to(dev, non_blocking=True)
@@ -151,6 +173,10 @@ class InputBatch:
             repetition_penalties=t(rep, torch.float32),
             output_token_ids=[s.output_token_ids for s in states],
             min_p=None if not any(min_p) else t(min_p, torch.float32),
+            allowed_token_ids_mask=allowed_mask,
+            bad_words_token_ids=bad,
+            min_tokens=mint,
+            logit_bias=bias if any(bias) else None,
             output_token_ids_tensor=(None if no_penalties
                                     else self.output_ids[:, :ow].index_select(0, slots)),
             output_token_lens=None if no_penalties else self.output_lens.index_select(0, slots),

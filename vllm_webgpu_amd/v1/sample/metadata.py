@@ -17,6 +17,11 @@ Conventions the kernels rely on:
   id outside ``[0, V)`` is padding.
 * ``generators`` maps a row index to the ``torch.Generator`` of a seeded request; the uniforms of
   that row are drawn from it, the others from torch's default generator.
+* Logits processors (vLLM-v1, applied before the penalties): ``allowed_token_ids_mask`` bool
+  ``[B, V]`` with True for tokens that are *not* allowed (vLLM's convention),
+  ``bad_words_token_ids`` row -> token sequences (the last token of a sequence is banned when the
+  output ends with the rest of it), ``min_tokens`` row -> (minimum output length, stop token
+  ids banned until it is reached), ``logit_bias`` per row (token -> bias) or None.
 """
 from __future__ import annotations
 
@@ -45,3 +50,5 @@ class SamplingMetadata:
     bad_words_token_ids: dict[int, list[list[int]]] = field(default_factory=dict)
     output_token_ids_tensor: torch.Tensor | None = None
     output_token_lens: torch.Tensor | None = None
+    min_tokens: dict[int, tuple[int, set[int]]] = field(default_factory=dict)
+    logit_bias: list[dict[int, float] | None] | None = None

@@ -4,9 +4,11 @@ Reference anchors: the reference samples greedily on the host
 (``vllm_webgpu/v1/model_runner.py:139-159``, ``logits.argmax(axis=-1)``) and otherwise defers to
 vLLM's CPU sampler (``docs/superpowers/specs/2026-06-29-vllm-webgpu-design.md:451``).  This class
 keeps vLLM-v1's ``Sampler.forward(logits, sampling_metadata) -> SamplerOutput`` signature and its
-order of operations -- raw logprobs of the unprocessed logits, penalties, greedy argmax of the
-penalised logits, temperature, min-p, top-k, top-p, exponential race, logprob gather -- but runs
-all of it in a single stream-ordered kernel launch (``vws_sample``) on device-resident logits.
+order of operations -- raw logprobs of the unprocessed logits, logits processors (allowed-token
+mask, bad words, min-tokens, logit bias), penalties, greedy argmax of the processed logits,
+temperature, min-p, top-k, top-p, exponential race, logprob gather -- but runs all of it in a
+single stream-ordered kernel launch (``vws_sample``) on device-resident logits; only the sparse
+processor lists (bad-word matches, min-tokens bans, biases) are built on the host.
 
 Random rows consume caller-side uniforms ``u`` in (0, 1) drawn here with torch's generators
 (the request's own generator for seeded rows), and the race key is ``p / (-ln u)``: an
@@ -50,6 +52,42 @@ def pad_output_ids(output_token_ids: list[list[int]], vocab_size: int,
     return host.to(device, non_blocking=True), lens.to(device, non_blocking=True)
 
 
+def processor_lists(m: SamplingMetadata, B: int, V: int):
+    """Host-side (ids, vals) int32/float32 [B, W] of the sparse logits processors, or None.
+
+    Bad words follow vLLM-v1's ``apply_bad_words``: a sequence bans its last token when the
+    row's output ends with the rest of it (single-token sequences always).  Min-tokens bans the
+    stop tokens while the output is shorter than the minimum.  Logit bias adds its value.
+    Padding ids are V.
+    """
+    rows: list[list[tuple[int, float]]] = [[] for _ in range(B)]
+    for i, words in (m.bad_words_token_ids or {}).items():
+        past = m.output_token_ids[i] if i < len(m.output_token_ids) else []
+        for seq in words:
+            if not seq or len(seq) > len(past) + 1:
+                continue
+            prefix = list(seq[:-1])
+            if not prefix or list(past[-len(prefix):]) == prefix:
+                rows[i].append((int(seq[-1]), float("-inf")))
+    for i, (min_toks, stop_ids) in (m.min_tokens or {}).items():
+        past = m.output_token_ids[i] if i < len(m.output_token_ids) else []
+        if len(past) < min_toks:
+            rows[i].extend((int(t), float("-inf")) for t in stop_ids)
+    for i, bias in enumerate(m.logit_bias or []):
+        if bias:
+            rows[i].extend((int(t), float(b)) for t, b in bias.items())
+    width = max((len(r) for r in rows), default=0)
+    if width == 0:
+        return None
+    ids = torch.full((B, width), V, dtype=torch.int32)
+    vals = torch.zeros((B, width), dtype=torch.float32)
+    for i, r in enumerate(rows):
+        if r:
+            ids[i, :len(r)] = torch.tensor([t for t, _ in r], dtype=torch.int32)
+            vals[i, :len(r)] = torch.tensor([v for _, v in r], dtype=torch.float32)
+    return ids, vals
+
+
 class Sampler:
     """vLLM-v1 ``Sampler`` facade over ``vws_sample``."""
 
@@ -65,9 +103,6 @@ class Sampler:
 
     def forward(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata) -> SamplerOutput:
         m = sampling_metadata
-        if m.allowed_token_ids_mask is not None or m.bad_words_token_ids:
-            raise NotImplementedError(
-                "allowed-token masks and bad-words lists are not applied by the device sampler")
         if logits.dim() != 2:
             raise ValueError(f"logits must be [num_reqs, vocab] (got {tuple(logits.shape)})")
         B, V = logits.shape
@@ -89,9 +124,18 @@ class Sampler:
                              prompt_ids=m.prompt_token_ids, output_ids=out_ids,
                              output_lens=out_lens)
 
+        processors = {}
+        if m.allowed_token_ids_mask is not None:
+            processors["allowed_mask"] = ops.pack_allowed(~m.allowed_token_ids_mask.to(dev, torch.bool))
+        adj = processor_lists(m, B, V)
+        if adj is not None:
+            ids, vals = adj
+            processors.update(adjust_ids=ids.to(dev, non_blocking=True),
+                              adjust_vals=vals.to(dev, non_blocking=True))
+
         res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
                          min_p=m.min_p, uniforms=uniforms, num_logprobs=m.max_num_logprobs,
-                         **penalties)
+                         **penalties, **processors)
         lp = None
         if m.max_num_logprobs is not None:
             lp = LogprobsTensors(res.logprob_ids, res.logprob_vals, res.logprob_ranks)
