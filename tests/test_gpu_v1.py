@@ -216,3 +216,27 @@ def test_runner_logits_processors_match_oracle(cuda):
             assert tok["mint"] not in (1, 2, 3)
         for r, t in zip(active, got):
             outputs[r].append(t)
+
+
+def test_async_output_matches_sync(cuda):
+    V = 1024
+    outs = []
+    for async_output in (False, True):
+        model = _FakeModel(V, cuda)
+        runner = ROCmModelRunner(None, cuda, model, max_num_reqs=4, max_prompt_len=8,
+                                 max_output_len=8)
+        params = {"a": _sp(temperature=0.7, top_k=10, seed=41, repetition_penalty=1.3),
+                  "b": _sp(temperature=0.0, logprobs=3)}
+        steps = []
+        for step in range(3):
+            so = NS(scheduled_new_reqs=[NS(req_id=r, prompt_token_ids=[1, 2], sampling_params=p)
+                                        for r, p in params.items()] if step == 0 else [],
+                    finished_req_ids=set(), num_scheduled_tokens={"a": 1, "b": 1})
+            runner.execute_model(so)
+            res = runner.sample_tokens(None, async_output=async_output)
+            if async_output:
+                assert hasattr(res, "get_output")
+                res = res.get_output()
+            steps.append((res.sampled_token_ids, res.logprobs.logprob_token_ids))
+        outs.append(steps)
+    assert outs[0] == outs[1]

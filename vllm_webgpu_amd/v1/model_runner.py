@@ -194,6 +194,45 @@ class InputBatch:
         self.output_lens.index_add_(0, slots, ok.to(torch.int32))
 
 
+class AsyncModelRunnerOutput:
+    """A step's output whose device-to-host copy is in flight (vLLM-v1's async output)."""
+
+    def __init__(self, batch: InputBatch, req_ids: list[str], sampled: torch.Tensor,
+                 logprobs: Any) -> None:
+        pin = sampled.is_cuda
+        self._batch, self._req_ids = batch, req_ids
+        self._ids = torch.empty(sampled.shape, dtype=sampled.dtype, pin_memory=pin)
+        self._ids.copy_(sampled, non_blocking=pin)
+        self._lp = None
+        if logprobs is not None:
+            self._lp = tuple(torch.empty(t.shape, dtype=t.dtype, pin_memory=pin) for t in logprobs)
+            for h, d in zip(self._lp, logprobs):
+                h.copy_(d, non_blocking=pin)
+        self._event = None
+        if pin:
+            self._event = torch.cuda.Event()
+            self._event.record()
+        self._result: ModelRunnerOutput | None = None
+
+    def get_output(self) -> ModelRunnerOutput:
+        if self._result is None:
+            if self._event is not None:
+                self._event.synchronize()
+            ids = self._ids.tolist()
+            for r, tok in zip(self._req_ids, ids):
+                self._batch.requests[r].output_token_ids.append(tok)
+            lp = None
+            if self._lp is not None:
+                from .outputs import LogprobsTensors
+                lp = LogprobsTensors(*self._lp).tolists()
+            req_ids = self._req_ids
+            self._result = ModelRunnerOutput(
+                req_ids=list(req_ids), req_id_to_index={r: i for i, r in enumerate(req_ids)},
+                sampled_token_ids=[[t] for t in ids], logprobs=lp, prompt_logprobs_dict={},
+                pooler_output=[])
+        return self._result
+
+
 class ROCmModelRunner:
     """Runner for one MI355X: model forward -> cached device logits -> device sampler."""
 
@@ -264,8 +303,16 @@ class ROCmModelRunner:
             logger.exception("execute_model failed: %s", e)
             raise
 
-    def sample_tokens(self, grammar_output: Any) -> ModelRunnerOutput | None:
-        """Samples the cached logits; one device-to-host copy of the sampled ids per step."""
+    def sample_tokens(self, grammar_output: Any, async_output: bool = False):
+        """Samples the cached logits.
+
+        The sampled ids (and logprobs) reach the host through one copy into pinned memory.
+        With ``async_output`` the copy is only enqueued and an ``AsyncModelRunnerOutput`` is
+        returned: its ``get_output()`` waits for the copy, so the host can schedule the next
+        step while the device finishes this one (the device-side history tables are updated on
+        the device either way).  ``get_output()`` must be called before the next step samples:
+        it also appends the ids to the host copies that bad-words matching reads.
+        """
         if self._last_logits is None:
             return None
         if grammar_output is not None and getattr(grammar_output, "grammar_bitmask", None) is not None:
@@ -277,14 +324,8 @@ class ROCmModelRunner:
         out = self.sampler(logits, md)
         sampled = out.sampled_token_ids[:, 0]
         batch.append_sampled(req_ids, sampled)
-        ids = sampled.tolist()
-        for r, tok in zip(req_ids, ids):
-            batch.requests[r].output_token_ids.append(tok)
-        lp = out.logprobs_tensors.tolists() if out.logprobs_tensors is not None else None
-        return ModelRunnerOutput(req_ids=list(req_ids),
-                                 req_id_to_index={r: i for i, r in enumerate(req_ids)},
-                                 sampled_token_ids=[[t] for t in ids], logprobs=lp,
-                                 prompt_logprobs_dict={}, pooler_output=[])
+        pending = AsyncModelRunnerOutput(batch, list(req_ids), sampled, out.logprobs_tensors)
+        return pending if async_output else pending.get_output()
 
     def supported_worker_tasks(self) -> tuple[str, ...]:
         return ("generate",)
