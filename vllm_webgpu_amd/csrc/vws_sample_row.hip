@@ -60,6 +60,7 @@ struct RowSmem {
     uint64_t red[kRowWaves][8];
     uint32_t tauw[kRowWaves];
     uint32_t tau, status, nhash, nkeep;
+    uint32_t ymax, tmaxk;                    // largest packed y key; largest threshold used
     uint32_t adjraise;                       // a positive logit bias was inserted
     uint32_t bc[8];
     // penalty context of the row for the out-of-line fix-up: mode 0 none, 1 penalise, 2 drop
@@ -404,6 +405,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     // 2. LDS state and the history hash
     if (tid == 0) {
         sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.npack = 0u; sm.bc[4] = 0u;
+        sm.ymax = 0u; sm.tmaxk = 0u;
         sm.pmode = hx ? 1u : 0u;
         sm.adjraise = 0u;
         sm.prep = prm.rep; sm.pinv = prm.inv_rep; sm.ppres = prm.pres; sm.pfreq = prm.freq;
@@ -551,10 +553,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) slot(v[j], i0 + j, tid <= 1 && i0 + j < end);
     }
-    // each wave packs its candidates (penalised keys, indices, uniforms) into the row's arrays
-    // as soon as its own stream ends, while other waves are still streaming
-    // The uniform of each lane's first candidate is only loaded here; it is stored just before
-    // the survivors are published, so that its latency overlaps the rank count.
+    // each wave packs its candidates into the row's arrays as soon as its own stream ends, while
+    // other waves are still streaming: the key of y (the processed logit over T; the processed
+    // logit itself for greedy rows), the index and the uniform.  The uniform of each lane's
+    // first candidate is only loaded here; it is stored just before the survivors are
+    // published, so that its latency overlaps the rank count.
+    const float Tt = prm.T;
     float u_first = 0.0f;
     int u_slot = -1;
     if (!cb.ovf) {
@@ -562,10 +566,14 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         uint32_t b = 0;
         if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)cb.cnt);
         const int pbase = __builtin_amdgcn_readlane(b, 0);
+        uint32_t ymx = 0u;
         if (pbase + cb.cnt <= kRowPack) {
             for (int e = lane; e < cb.cnt; e += kWave) {
                 const int32_t ii = sm.cidx[wave][e];
-                sm.pkey[pbase + e] = sm.ckey[wave][e];
+                const uint32_t kx = sm.ckey[wave][e];
+                const uint32_t ky = sampling ? key_of(val_of(kx) / Tt) : kx;
+                ymx = ky > ymx ? ky : ymx;
+                sm.pkey[pbase + e] = ky;
                 sm.pidx[pbase + e] = ii;
                 if (sampling) {
                     const float uv = a.u[(size_t)r * a.ustride + ii];
@@ -574,32 +582,28 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 }
             }
         }
+        ymx = wave_max_u32(ymx);
+        if (lane == 0 && ymx) atomicMax(&sm.ymax, ymx);
     }
     if (lane == 0) {
-        sm.tauw[wave] = cb.tau;
+        atomicMax(&sm.tmaxk, cb.tau);
         if (cb.ovf) atomicOr(&sm.status, 2u);
     }
     __syncthreads();
     const int total = (int)sm.npack;
     if (sm.status != 0u || total > kRowPack) return false;  // tie overflow, too many candidates
 
-    // 5. the k-th largest candidate key.  Candidate t (packed order) goes to thread t, which
-    //    counts the keys above it, sixteen per step with 128-bit LDS reads: the candidate whose
-    //    count brackets k holds the k-th key, the one with none above holds the maximum.  The
-    //    k-th key is exact when it is not below any threshold used; otherwise (a seed above
-    //    the k-th value) the row takes the general path.
-    uint32_t tmax = seed;
-#pragma unroll
-    for (int w = 0; w < kRowWaves; ++w) tmax = tmax > sm.tauw[w] ? tmax : sm.tauw[w];
+    // 5. ranks in y: candidate c's rank is the number of candidate keys above its own, so the
+    //    top k (ties included) are exactly the candidates of rank < k.  Waves split the count
+    //    as (group of 64 candidates, range of keys) pairs, 16 keys per step with 128-bit LDS
+    //    reads, and add their partial ranks into LDS.  Slots past the packed candidates hold
+    //    key 0 and never count.
+    const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
+    const uint32_t mk = sm.ymax;                              // largest y
     const bool mine = tid < total;
     const uint32_t myk = mine ? sm.pkey[tid] : 0u;
-    if (tid == 0) { sm.bc[1] = 0xFFFFFFFFu; sm.bc[2] = 0u; sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
+    if (tid == 0) { sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
     {
-        // The rank of candidate c is the number of candidate keys above its own: rank 0 holds
-        // the maximum, and the k-th largest key is the smallest key of rank < k (ties with it
-        // share its rank).  Waves split the count as (group of 64 candidates, range of keys)
-        // pairs, 16 keys per step with 128-bit LDS reads, and add their partial ranks into
-        // LDS.  Slots past the packed candidates hold key 0 and never count.
         const int ngrp = (total + kWave - 1) / kWave;
         const int nspl = ngrp > 0 ? kRowWaves / ngrp : 0;
         if (wave < ngrp * nspl) {
@@ -621,22 +625,24 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         }
     }
     __syncthreads();
-    if (mine) {
-        const uint32_t rk = sm.crank[tid];
-        if (rk == 0u) sm.bc[2] = myk;                          // the maximum
-        if (rk < (uint32_t)k) atomicMin(&sm.bc[1], myk);       // the k-th largest key
-    }
-    __syncthreads();
-    const uint32_t kth = total >= k ? sm.bc[1] : 0u;
-    const uint32_t mk = sm.bc[2];
-    const bool exact = seed != 0u ? (total >= k && kth >= tmax) : (kth == 0u || kth >= tmax);
-    if (!exact) return false;
+    // Exact when no element left out of the candidates can reach the top k: fewer than k
+    // candidates only without any threshold, and every top-k candidate strictly above the
+    // largest y an element below the thresholds can have (a seed above the k-th value, or a
+    // tie created by the division by T, sends the row to the general path).  NaN keys (0) are
+    // candidates only when no threshold was used.
+    if (tmax != 0u && total < k) return false;
+    const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / Tt : val_of(tmax - 1u))
+                                          : -__builtin_inff();
+    const uint32_t rk = mine ? sm.crank[tid] : 0xFFFFFFFFu;
+    const bool topk = rk < (uint32_t)k;
+    if (topk && myk != 0u && !(val_of(myk) > ylim)) atomicOr(&sm.status, 4u);
 
     if (!sampling) {
-        // greedy: lowest index at the maximum of the penalised logits (0 when every value is NaN)
-        const uint32_t best = wave_min_u32((mine && myk == mk) ? (uint32_t)sm.pidx[tid] : 0x7FFFFFFFu);
+        // greedy: lowest index at the maximum of the processed logits (0 when every value is NaN)
+        const uint32_t best = wave_min_u32(rk == 0u ? (uint32_t)sm.pidx[tid] : 0x7FFFFFFFu);
         if (lane == 0 && best != 0x7FFFFFFFu) atomicMin(&sm.bc[3], best);
         __syncthreads();
+        if (sm.status != 0u) return false;
         if (tid == 0) {
             a.sampled[r] = (mk != 0u) ? (int32_t)sm.bc[3] : 0;
             if (a.flags) a.flags[r] = VWS_FLAG_GREEDY;
@@ -645,23 +651,15 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         return true;
     }
 
-    // 6. survivors of temperature + top-k + min-p: exact masses and race keys, compacted into
-    //    the survivor arrays (any order)
-    const float Tt = prm.T;
-    const float m = mk ? val_of(mk) / Tt : __builtin_nanf("");
+    // 6. survivors of temperature + top-k + min-p: exact masses, compacted into the survivor
+    //    arrays (any order)
+    const float m = mk ? val_of(mk) : __builtin_nanf("");
     if (!(m > -__builtin_inff() && m < __builtin_inff())) return false;  // degenerate row
-    const float kth_y = kth ? val_of(kth) / Tt : -__builtin_inff();
-    // an element below a threshold may still tie with the k-th value after the division by T
-    if (tmax > 0x007FFFFFu && val_of(tmax - 1u) / Tt >= kth_y) return false;
     const float lp_min = (prm.min_p > 0.0f) ? log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)
                                             : -__builtin_inff();
     if (wave * kWave < total) {
-        bool keep = false;
-        float y = 0.0f;
-        if (mine) {
-            y = val_of(myk) / Tt;
-            keep = key_of(y) != 0u && y >= kth_y && (y - m) >= lp_min;
-        }
+        const float y = val_of(myk);
+        const bool keep = topk && (y - m) >= lp_min;
         const uint64_t bal = __ballot(keep);
         uint32_t off = 0;
         if (lane == 0 && bal) off = atomicAdd(&sm.nkeep, (uint32_t)__popcll(bal));
@@ -672,7 +670,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             if (pos < (uint32_t)kRowKeep) {
                 const float e = exp_det(y - m);
                 mw = mass_of(e);
-                sm.sck[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.pidx[tid];
+                sm.sck[pos] = ((uint64_t)myk << 32) | (uint32_t)sm.pidx[tid];
                 sm.sw[pos] = mw;
                 sm.se[pos] = e;
                 sm.spos[pos] = (uint32_t)tid;
@@ -683,6 +681,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
+    if (sm.status != 0u) return false;  // a top-k candidate at or below the largest dropped y
     const int n = (int)sm.nkeep;
     if (n == 0 || n > kRowKeep) return false;
 
