@@ -40,8 +40,15 @@ constexpr int kLoadNT = 2;                   // buffer-load cache policy: non-te
 struct RowSmem {
     uint32_t ckey[kRowWaves][kRowCap];
     int32_t cidx[kRowWaves][kRowCap];
-    alignas(16) uint32_t pkey[kRowPack];     // all candidates of the row, packed in any order
-    int32_t pidx[kRowPack];
+    // all candidates of the row, packed in any order: key(y) and index (k > 64), or one 64-bit
+    // key per candidate (k <= 64)
+    union alignas(16) {
+        struct {
+            uint32_t pkey[kRowPack];
+            int32_t pidx[kRowPack];
+        };
+        uint64_t pk64[kRowPack];
+    };
     float pu[kRowPack];                      // their uniforms (sampled rows)
     uint32_t crank[kRowPack];                // rank of each packed candidate (partial sums)
     uint64_t sC[kRowKeep];                   // survivors' cumulative masses (partial sums)
@@ -55,6 +62,8 @@ struct RowSmem {
     alignas(16) uint64_t sw[kRowKeep];       // exact mass
     float se[kRowKeep];                      // exp(y - max)
     uint32_t spos[kRowKeep];                 // packed position (for the uniform)
+    alignas(16) uint64_t tk[kWave + 1];      // k <= 64: the 65 largest 64-bit keys, descending
+    float tu[kWave];                         // and the uniforms of the first 64
     uint32_t npack;                          // candidates packed so far
     uint32_t seedk[kRowWaves * kSeedPerWave];
     uint64_t red[kRowWaves][8];
@@ -280,8 +289,6 @@ struct RowCand {
     }
 };
 
-// Serves greedy and top-k rows; returns false when the row must take the general path (nothing
-// has been written for it then).
 // Defaults read in place of a missing per-row parameter array, so every parameter is one
 // unconditional scalar load: T, top_p, min_p, repetition, presence, frequency.  The arrays are
 // never written; they are not const so that they live in the global address space, like the
@@ -332,6 +339,153 @@ __device__ __forceinline__ RowP row_params_scalar(const KArgs& a, int r) {
     p.na = a.adj_ids ? min(max(al, 0), a.adjwidth) : 0;
     p.need_hash = p.has_hist || p.na > 0;
     return p;
+}
+
+// floor(a / b) for 0 <= a < 2^20 and 1 <= b <= 1024: (a + 1/2) / b lies at least 1 / (2b) from
+// an integer, far beyond the error of the reciprocal, so the truncation is exact.
+__device__ __forceinline__ int small_div(int a, int b) {
+    return (int)(((float)a + 0.5f) * __builtin_amdgcn_rcpf((float)b));
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+    // the builtin returns int: widen each half as unsigned
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((uint32_t)v, l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Tail of a row with k <= 64, after the candidates are packed as 64-bit keys (key(y) << 32 |
+// index; the index reversed for greedy rows).  The number of keys above a candidate is its
+// position in descending key order, so the 65 largest keys land in tk[] sorted; the rest of
+// the row is finished by wave 0 from registers:
+//   * top-k with ties: the candidates whose y is at least the y of tk[k - 1];
+//   * min-p, then the exact masses; the sum of the masses at and after slot j is the
+//     cumulative mass of that survivor in ascending (y, index) order, a suffix sum;
+//   * top-p removes the survivors whose cumulative mass is at most floor((1 - p) W), the
+//     maximum never; the kept ones are a prefix of the slots;
+//   * the race: the largest e / (-ln u) among the kept survivors, the lowest index on ties.
+// Exact when the k-th key is strictly above the largest y a dropped element can have (ylim).
+// Returns false (uniformly over the workgroup) when the row must take the general path.
+__device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int r, const RowP& prm,
+                                               int k, int total, float ylim, bool sampling,
+                                               float u_first, int u_slot) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool mine = tid < total;
+    const uint64_t myk = mine ? sm.pk64[tid] : 0ull;
+    {
+        // Waves split the count as (group of 64 candidates, range of keys) pairs, 8 keys per
+        // step with 128-bit LDS reads, and add their partial counts into LDS.  Unpacked slots
+        // hold key 0 and never count.
+        const int ngrp = (total + kWave - 1) >> 6;
+        const int nspl = ngrp > 0 ? small_div(kRowWaves, ngrp) : 0;
+        if (wave < ngrp * nspl) {
+            const int sp = small_div(wave, ngrp), g = wave - sp * ngrp;
+            const int c = g * kWave + lane;
+            const uint64_t kc = sm.pk64[c];
+            const int chunk = (small_div(total + nspl - 1, nspl) + 7) & ~7;
+            const int j0 = sp * chunk, j1 = min(j0 + chunk, (total + 7) & ~7);
+            const uint4* p4 = reinterpret_cast<const uint4*>(sm.pk64);
+            uint32_t cnt = 0;
+            for (int j = j0; j < j1; j += 8) {
+                const uint4 a0 = p4[j / 2], a1 = p4[j / 2 + 1], a2 = p4[j / 2 + 2], a3 = p4[j / 2 + 3];
+                const uint64_t v[8] = {((uint64_t)a0.y << 32) | a0.x, ((uint64_t)a0.w << 32) | a0.z,
+                                       ((uint64_t)a1.y << 32) | a1.x, ((uint64_t)a1.w << 32) | a1.z,
+                                       ((uint64_t)a2.y << 32) | a2.x, ((uint64_t)a2.w << 32) | a2.z,
+                                       ((uint64_t)a3.y << 32) | a3.x, ((uint64_t)a3.w << 32) | a3.z};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) cnt += v[i] > kc;
+            }
+            if (c < total && cnt) atomicAdd(&sm.crank[c], cnt);
+        }
+    }
+    if (u_slot >= 0) sm.pu[u_slot] = u_first;
+    __syncthreads();
+    if (mine) {
+        const uint32_t pos = sm.crank[tid];
+        if (pos <= (uint32_t)kWave) sm.tk[pos] = myk;
+        if (sampling && pos < (uint32_t)kWave) sm.tu[pos] = sm.pu[tid];
+        const uint32_t yk = (uint32_t)(myk >> 32);
+        // the k-th key must lie strictly above every dropped element (ties included)
+        if (pos == (uint32_t)(k - 1) && yk != 0u && !(val_of(yk) > ylim)) atomicOr(&sm.status, 4u);
+    }
+    __syncthreads();
+    if (sm.status != 0u) return false;
+    const uint64_t top = total > 0 ? sm.tk[0] : 0ull;
+    if (!sampling) {
+        // greedy: the lowest index at the maximum of the processed logits (0 without candidates)
+        if (tid == 0) {
+            a.sampled[r] = (top >> 32) != 0ull ? (int32_t)(0x7FFFFFFFu - (uint32_t)top) : 0;
+            if (a.flags) a.flags[r] = VWS_FLAG_GREEDY;
+            if (a.nkept) a.nkept[r] = 1;
+        }
+        return true;
+    }
+    const uint32_t y0k = (uint32_t)(top >> 32);
+    const float m = y0k ? val_of(y0k) : __builtin_nanf("");
+    if (!(m > -__builtin_inff() && m < __builtin_inff())) return false;  // degenerate row
+    // fewer candidates than k (no threshold used): every candidate is in the top k
+    const uint32_t ykth = total >= k ? (uint32_t)(sm.tk[k - 1] >> 32) : 0u;
+    if (total > kWave && (uint32_t)(sm.tk[kWave] >> 32) >= ykth) return false;  // > 64 tied members
+    if (wave != 0) return true;
+
+    const bool have = lane < total;
+    const uint64_t key = have ? sm.tk[lane] : 0ull;
+    const float uu = have ? sm.tu[lane] : 0.5f;
+    const uint32_t yk = (uint32_t)(key >> 32);
+    const float y = val_of(yk);
+    const float lp_min = (prm.min_p > 0.0f) ? log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)
+                                            : -__builtin_inff();
+    const bool keep = have && yk >= ykth && (y - m) >= lp_min;
+    const float e = keep ? exp_det(y - m) : 0.0f;
+    const uint64_t w = keep ? mass_of(e) : 0ull;
+    uint64_t C = w, W = w;
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+        const uint64_t t = lane_xor64(W, s);
+        if (!(lane & s)) C += t;
+        W += t;
+    }
+    const float q32 = 1.0f - prm.top_p;
+    const bool topp = q32 > 0.0f;
+    const bool abl = topp && !(q32 < 1.0f);  // top_p <= 0: only the maximum is kept
+    const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
+    const bool removed = keep && topp && (abl ? (C != W) : (C <= thr && C != W));
+    const bool kept = keep && !removed;
+    uint64_t pk = 0ull;
+    if (kept) {
+        const float rkey = e / (0.0f - log_det(uu));
+        if (rkey >= 0.0f) pk = ((uint64_t)f2u(rkey) << 32) | (0x7FFFFFFFu - (uint32_t)key);
+    }
+    const uint64_t best = wave_max_u64(pk);
+    const uint32_t second = wave_max_u32((pk != 0ull && pk != best) ? (uint32_t)(pk >> 32) + 1u : 0u);
+    const int nkept = __popcll(__ballot(kept));
+    const int nrem = __popcll(__ballot(removed));
+    const uint64_t cat = readlane64(C, nkept - 1);              // smallest kept cumulative mass
+    const uint64_t cprev = nrem ? readlane64(C, nkept) : 0ull;  // largest removed one
+    if (lane == 0) {
+        int32_t tok;
+        uint32_t fl = 0;
+        if (best) {
+            tok = (int32_t)(0x7FFFFFFFu - (uint32_t)best);
+            const float bk = u2f((uint32_t)(best >> 32));
+            if (second) {
+                const float sk = u2f(second - 1u);
+                if ((double)sk >= (double)bk * (1.0 - 1e-6)) fl |= VWS_FLAG_RACE_NEAR_TIE;
+            }
+        } else {
+            tok = (int32_t)(uint32_t)top;  // no valid race key: the largest (y, index) kept
+        }
+        if (topp && !abl) {
+            const uint64_t tol = (uint64_t)((double)W * 1e-6);
+            if ((nrem > 0 && thr - cprev <= tol) || (cat > thr && cat - thr <= tol))
+                fl |= VWS_FLAG_TOPP_NEAR_TIE;
+        }
+        a.sampled[r] = tok;
+        if (a.flags) a.flags[r] = fl;
+        if (a.nkept) a.nkept[r] = nkept;
+    }
+    return true;
 }
 
 // Serves greedy and top-k rows; returns false when the row must take the general path (nothing
@@ -413,7 +567,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     if (hx) {
         for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
     }
-    sm.pkey[tid] = 0u;   // unpacked slots keep key 0, which ranks below every candidate
+    sm.pk64[tid] = 0ull;  // unpacked slots keep key 0, which ranks below every candidate
     sm.crank[tid] = 0u;
     if (tid < kRowKeep) sm.sC[tid] = 0ull;
     if (tid == 0) sm.sW = 0ull;
@@ -555,10 +709,13 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     // each wave packs its candidates into the row's arrays as soon as its own stream ends, while
     // other waves are still streaming: the key of y (the processed logit over T; the processed
-    // logit itself for greedy rows), the index and the uniform.  The uniform of each lane's
-    // first candidate is only loaded here; it is stored just before the survivors are
-    // published, so that its latency overlaps the rank count.
+    // logit itself for greedy rows), the index and the uniform.  Rows with k <= 64 pack one
+    // 64-bit key per candidate, (key(y) << 32) | index, with the index reversed for greedy rows
+    // so that the largest key is the lowest index at the maximum.  The uniform of each lane's
+    // first candidate is only loaded here; it is stored once the ranks are counted, so that its
+    // latency overlaps the count.
     const float Tt = prm.T;
+    const bool small = k <= kWave;
     float u_first = 0.0f;
     int u_slot = -1;
     if (!cb.ovf) {
@@ -572,9 +729,13 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 const int32_t ii = sm.cidx[wave][e];
                 const uint32_t kx = sm.ckey[wave][e];
                 const uint32_t ky = sampling ? key_of(val_of(kx) / Tt) : kx;
-                ymx = ky > ymx ? ky : ymx;
-                sm.pkey[pbase + e] = ky;
-                sm.pidx[pbase + e] = ii;
+                if (small) {
+                    sm.pk64[pbase + e] = ((uint64_t)ky << 32) | (uint32_t)(sampling ? ii : 0x7FFFFFFF - ii);
+                } else {
+                    ymx = ky > ymx ? ky : ymx;
+                    sm.pkey[pbase + e] = ky;
+                    sm.pidx[pbase + e] = ii;
+                }
                 if (sampling) {
                     const float uv = a.u[(size_t)r * a.ustride + ii];
                     if (e == lane) { u_first = uv; u_slot = pbase + e; }
@@ -582,8 +743,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                 }
             }
         }
-        ymx = wave_max_u32(ymx);
-        if (lane == 0 && ymx) atomicMax(&sm.ymax, ymx);
+        if (!small) {
+            ymx = wave_max_u32(ymx);
+            if (lane == 0 && ymx) atomicMax(&sm.ymax, ymx);
+        }
     }
     if (lane == 0) {
         atomicMax(&sm.tmaxk, cb.tau);
@@ -592,25 +755,31 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     __syncthreads();
     const int total = (int)sm.npack;
     if (sm.status != 0u || total > kRowPack) return false;  // tie overflow, too many candidates
+    const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
+    // fewer than k candidates can only be exact when no threshold was used
+    if (tmax != 0u && total < k) return false;
+    // the largest y an element below the thresholds can have; -inf when only NaNs were dropped
+    const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / Tt : val_of(tmax - 1u))
+                                          : -__builtin_inff();
+    const bool mine = tid < total;
+    if (small) return row_tail_small(a, sm, r, prm, k, total, ylim, sampling, u_first, u_slot);
 
     // 5. ranks in y: candidate c's rank is the number of candidate keys above its own, so the
     //    top k (ties included) are exactly the candidates of rank < k.  Waves split the count
     //    as (group of 64 candidates, range of keys) pairs, 16 keys per step with 128-bit LDS
     //    reads, and add their partial ranks into LDS.  Slots past the packed candidates hold
     //    key 0 and never count.
-    const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
     const uint32_t mk = sm.ymax;                              // largest y
-    const bool mine = tid < total;
     const uint32_t myk = mine ? sm.pkey[tid] : 0u;
-    if (tid == 0) { sm.bc[3] = 0x7FFFFFFFu; sm.nkeep = 0u; }
+    if (tid == 0) sm.nkeep = 0u;
     {
-        const int ngrp = (total + kWave - 1) / kWave;
-        const int nspl = ngrp > 0 ? kRowWaves / ngrp : 0;
+        const int ngrp = (total + kWave - 1) >> 6;
+        const int nspl = ngrp > 0 ? small_div(kRowWaves, ngrp) : 0;
         if (wave < ngrp * nspl) {
-            const int g = wave % ngrp, sp = wave / ngrp;
+            const int sp = small_div(wave, ngrp), g = wave - sp * ngrp;
             const int c = g * kWave + lane;
             const uint32_t kc = sm.pkey[c];
-            const int chunk = (((total + nspl - 1) / nspl) + 15) & ~15;
+            const int chunk = (small_div(total + nspl - 1, nspl) + 15) & ~15;
             const int j0 = sp * chunk, j1 = min(j0 + chunk, (total + 15) & ~15);
             const uint4* p4 = reinterpret_cast<const uint4*>(sm.pkey);
             uint32_t cnt = 0;
@@ -630,26 +799,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     // largest y an element below the thresholds can have (a seed above the k-th value, or a
     // tie created by the division by T, sends the row to the general path).  NaN keys (0) are
     // candidates only when no threshold was used.
-    if (tmax != 0u && total < k) return false;
-    const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / Tt : val_of(tmax - 1u))
-                                          : -__builtin_inff();
     const uint32_t rk = mine ? sm.crank[tid] : 0xFFFFFFFFu;
     const bool topk = rk < (uint32_t)k;
     if (topk && myk != 0u && !(val_of(myk) > ylim)) atomicOr(&sm.status, 4u);
-
-    if (!sampling) {
-        // greedy: lowest index at the maximum of the processed logits (0 when every value is NaN)
-        const uint32_t best = wave_min_u32(rk == 0u ? (uint32_t)sm.pidx[tid] : 0x7FFFFFFFu);
-        if (lane == 0 && best != 0x7FFFFFFFu) atomicMin(&sm.bc[3], best);
-        __syncthreads();
-        if (sm.status != 0u) return false;
-        if (tid == 0) {
-            a.sampled[r] = (mk != 0u) ? (int32_t)sm.bc[3] : 0;
-            if (a.flags) a.flags[r] = VWS_FLAG_GREEDY;
-            if (a.nkept) a.nkept[r] = 1;
-        }
-        return true;
-    }
 
     // 6. survivors of temperature + top-k + min-p: exact masses, compacted into the survivor
     //    arrays (any order)
