@@ -32,6 +32,7 @@ constexpr int kRowWaves = kGenWaves;         // 16
 constexpr int kRowCap = 512;                 // candidate slots per wave
 constexpr int kRowHash = 2048;               // history hash slots
 constexpr int kRowHashFill = 1536;           // unique history tokens served in LDS
+constexpr int kRowHashBits = 1 << 17;        // presence bits of hashed tokens (token mod 2^17)
 constexpr int kRowKeep = 256;                // survivors finished here
 constexpr int kRowPack = kRowThreads;        // candidates finished here (more: general path)
 constexpr int kSeedPerWave = 16;             // lane maxima each wave contributes to the seed pool
@@ -58,6 +59,7 @@ struct RowSmem {
     uint32_t hval[kRowHash];                 // output count | kHBias | kHBan | kHPrompt
     float hpen[kRowHash];                    // processed value (gather mode)
     float hadj[kRowHash];                    // logit bias (kHBias)
+    alignas(16) uint32_t hbits[kRowHashBits / 32];  // bit (t mod 2^17) set for every hashed token t
     alignas(16) uint64_t sck[kRowKeep];      // survivors: key(y) << 32 | index
     alignas(16) uint64_t sw[kRowKeep];       // exact mass
     float se[kRowKeep];                      // exp(y - max)
@@ -88,6 +90,7 @@ __device__ __forceinline__ uint32_t rhash_slot(int t) {
 
 // inc: 1 counts an output occurrence; otherwise kHPrompt, kHBan or kHBias (with its bias) is set
 __device__ __forceinline__ void rhash_insert(RowSmem& sm, int t, uint32_t inc, float bias = 0.0f) {
+    atomicOr(&sm.hbits[((uint32_t)t >> 5) & (kRowHashBits / 32 - 1)], 1u << (t & 31));
     uint32_t s = rhash_slot(t);
     for (int probe = 0; probe < kRowHash; ++probe) {
         const uint32_t prev = atomicCAS(&sm.hkey[s], 0u, (uint32_t)t + 1u);
@@ -104,6 +107,11 @@ __device__ __forceinline__ void rhash_insert(RowSmem& sm, int t, uint32_t inc, f
         s = (s + 1u) & (kRowHash - 1);
     }
     atomicOr(&sm.status, 1u);
+}
+
+// whether token t may be in the row's hash (exact for vocabularies up to 2^17)
+__device__ __forceinline__ bool rhash_maybe(const RowSmem& sm, int t) {
+    return (sm.hbits[((uint32_t)t >> 5) & (kRowHashBits / 32 - 1)] >> (t & 31)) & 1u;
 }
 
 // slot of token t in the row's hash, -1 when absent
@@ -566,6 +574,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     if (hx) {
         for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
+        for (int s = tid; s < kRowHashBits / 128; s += NT)
+            reinterpret_cast<uint4*>(sm.hbits)[s] = make_uint4(0u, 0u, 0u, 0u);
     }
     sm.pk64[tid] = 0ull;  // unpacked slots keep key 0, which ranks below every candidate
     sm.crank[tid] = 0u;
@@ -719,7 +729,13 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     float u_first = 0.0f;
     int u_slot = -1;
     if (!cb.ovf) {
-        cb.finish();
+        // Mode 2 (something may raise a logit) drops the stream entries of hashed tokens, which
+        // compacts the buffer: done out of line.  In mode 1 the processed value of each hashed
+        // candidate not yet fixed by a compaction replaces its raw value here, found through
+        // the presence bits with one LDS read per candidate.
+        const uint32_t pmode = sm.pmode;
+        const int nfix = pmode == 1u ? cb.nfix : cb.cnt;
+        if (pmode == 2u) cb.finish();
         uint32_t b = 0;
         if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)cb.cnt);
         const int pbase = __builtin_amdgcn_readlane(b, 0);
@@ -727,7 +743,13 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         if (pbase + cb.cnt <= kRowPack) {
             for (int e = lane; e < cb.cnt; e += kWave) {
                 const int32_t ii = sm.cidx[wave][e];
-                const uint32_t kx = sm.ckey[wave][e];
+                uint32_t kx = sm.ckey[wave][e];
+                if (e >= nfix && rhash_maybe(sm, ii)) {
+                    const int hs = rhash_find(sm, ii);
+                    if (hs >= 0)
+                        kx = key_of(apply_hashed(val_of(kx), sm.hval[hs], sm.hadj[hs], sm.prep,
+                                                 sm.pinv, sm.pfreq, sm.ppres));
+                }
                 const uint32_t ky = sampling ? key_of(val_of(kx) / Tt) : kx;
                 if (small) {
                     sm.pk64[pbase + e] = ((uint64_t)ky << 32) | (uint32_t)(sampling ? ii : 0x7FFFFFFF - ii);
