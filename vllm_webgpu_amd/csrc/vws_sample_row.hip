@@ -706,8 +706,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
         load_iter(Bq, it + 3);
     }
-    {   // unaligned head (thread 0) and tail (thread 1), fewer than 2 vectors in total; handled
-        // last, where waiting for their loads holds up nothing
+    if (wave == 0) {
+        // unaligned head (thread 0) and tail (thread 1), fewer than 2 vectors in total; handled
+        // last, and by wave 0 alone, so no other wave waits for its loads
         float v[VEC];
 #pragma unroll
         for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
@@ -741,6 +742,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         const int pbase = __builtin_amdgcn_readlane(b, 0);
         uint32_t ymx = 0u;
         if (pbase + cb.cnt <= kRowPack) {
+            // e = lane first (its uniform stays in flight), then any further candidates
             for (int e = lane; e < cb.cnt; e += kWave) {
                 const int32_t ii = sm.cidx[wave][e];
                 uint32_t kx = sm.ckey[wave][e];
@@ -759,11 +761,17 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
                     sm.pidx[pbase + e] = ii;
                 }
                 if (sampling) {
-                    const float uv = a.u[(size_t)r * a.ustride + ii];
-                    if (e == lane) { u_first = uv; u_slot = pbase + e; }
-                    else sm.pu[pbase + e] = uv;
+                    if (e == lane) {
+                        u_slot = pbase + e;
+                    } else {
+                        sm.pu[pbase + e] = a.u[(size_t)r * a.ustride + ii];
+                    }
                 }
             }
+            // the first candidate's uniform, loaded outside the loop so that nothing waits for
+            // it before it is stored
+            if (sampling && u_slot >= 0)
+                u_first = a.u[(size_t)r * a.ustride + sm.cidx[wave][lane]];
         }
         if (!small) {
             ymx = wave_max_u32(ymx);
