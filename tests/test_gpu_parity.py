@@ -139,3 +139,25 @@ def test_repeat_calls_stable(cuda):
         again = gpu_run(w, cuda)
         assert np.array_equal(again["token"], first["token"])
         assert np.array_equal(again["n_kept"], first["n_kept"])
+
+
+def test_workspace_clean_after_general_path(cuda):
+    """The multi-pass path keeps its history hash in the shared workspace; it must leave zeros
+    behind, since the top-k operation's part counters overlap that region."""
+    import torch
+
+    from tests.cases import _wl
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(21)
+    B, V, H = 8, 20000, 400
+    x = rng.normal(0, 2, (B, V)).astype(np.float32)
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    w = _wl("general_with_history", x, 0.9, k=0, p=0.9, rep=1.2, pres=0.3, freq=0.1, hist=hist, seed=9)
+    assert_same(gpu_run(w, cuda), oracle_run(w), w.name)
+    xt = np.round(rng.normal(size=(12, 30011)) * 8).astype(np.float32) / 8
+    for k in (1, 50):
+        vals, ids = ops.topk(torch.from_numpy(xt).to(cuda), k)
+        rv, ri = O.topk(xt, k)
+        assert np.array_equal(ids.cpu().numpy(), ri)
+        assert np.array_equal(vals.cpu().numpy(), rv)

@@ -834,6 +834,12 @@ logprobs:
             }
         }
     }
+    // the workspace is left as it was found (zeros): other operations that share it, such as
+    // the top-k's part counters, overlap the hash region
+    if (hh) {
+        __syncthreads();
+        for (int i = tid; i < hs; i += NT) { hkey[i] = 0u; hval[i] = 0u; hpen[i] = 0u; hadj[i] = 0u; }
+    }
 }
 
 // Exact top-k ids/values of a row for the topk operation, when its single-pass list
