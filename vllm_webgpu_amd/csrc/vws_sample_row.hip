@@ -375,7 +375,7 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
 // Exact when the k-th key is strictly above the largest y a dropped element can have (ylim).
 // Returns false (uniformly over the workgroup) when the row must take the general path.
 __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int r, const RowP& prm,
-                                               int k, int total, float ylim, bool sampling,
+                                               int k, int total, uint32_t seed, bool sampling,
                                                float u_first, int u_slot) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -407,6 +407,11 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
             if (c < total && cnt) atomicAdd(&sm.crank[c], cnt);
         }
     }
+    // every threshold used (raw keys), and the largest y an element below them can have (-inf
+    // when only NaNs were dropped)
+    const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;
+    const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / prm.T : val_of(tmax - 1u))
+                                          : -__builtin_inff();
     if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
     if (mine) {
@@ -418,7 +423,9 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
         if (pos == (uint32_t)(k - 1) && yk != 0u && !(val_of(yk) > ylim)) atomicOr(&sm.status, 4u);
     }
     __syncthreads();
-    if (sm.status != 0u) return false;
+    // tie or hash overflow, a k-th key not above a dropped element, or fewer than k candidates
+    // with a threshold used
+    if (sm.status != 0u || (tmax != 0u && total < k)) return false;
     const uint64_t top = total > 0 ? sm.tk[0] : 0ull;
     if (!sampling) {
         // greedy: the lowest index at the maximum of the processed logits (0 without candidates)
@@ -784,7 +791,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     __syncthreads();
     const int total = (int)sm.npack;
-    if (sm.status != 0u || total > kRowPack) return false;  // tie overflow, too many candidates
+    if (total > kRowPack) return false;  // too many candidates
+    // the single-wave finish checks the status and the thresholds once its count is running
+    if (small) return row_tail_small(a, sm, r, prm, k, total, seed, sampling, u_first, u_slot);
+    if (sm.status != 0u) return false;  // tie or hash overflow
     const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
     // fewer than k candidates can only be exact when no threshold was used
     if (tmax != 0u && total < k) return false;
@@ -792,7 +802,6 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / Tt : val_of(tmax - 1u))
                                           : -__builtin_inff();
     const bool mine = tid < total;
-    if (small) return row_tail_small(a, sm, r, prm, k, total, ylim, sampling, u_first, u_slot);
 
     // 5. ranks in y: candidate c's rank is the number of candidate keys above its own, so the
     //    top k (ties included) are exactly the candidates of rank < k.  Waves split the count
