@@ -267,6 +267,51 @@ struct RowCand {
         set_tau(__builtin_amdgcn_readfirstlane(
             __hip_atomic_load(&g_row_sh.f.tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)));
     }
+    // Appends all VEC elements of the lanes in hm (raw keys; elements below the threshold and
+    // NaNs included, dropped by filter()); wave-uniform call.
+    template <int VEC>
+    __device__ __forceinline__ void append_vec(const float* v, int i0, uint64_t hm) {
+        if (ovf) return;
+        int n = __popcll(hm) * VEC;
+        if (cnt + n > kRowCap) {
+            const uint64_t rc = row_compact(w, nfix, cnt, k);
+            cnt = __builtin_amdgcn_readfirstlane((uint32_t)rc);
+            nfix = cnt;
+            set_tau(__builtin_amdgcn_readfirstlane((uint32_t)(rc >> 32)));
+            if (cnt + n > kRowCap) { ovf = true; return; }
+        }
+        if ((hm >> lane_id()) & 1ull) {
+            const int pos = cnt + lane_prefix(hm) * VEC;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                g_row_sh.f.ckey[w][pos + j] = key_of(v[j]);
+                g_row_sh.f.cidx[w][pos + j] = i0 + j;
+            }
+        }
+        cnt += n;
+        wave_sync();
+    }
+    // Drops the entries below the threshold (and NaNs) in place, keeping the order.
+    __device__ __forceinline__ void filter() {
+        uint32_t* ck = g_row_sh.f.ckey[w];
+        int32_t* ci = g_row_sh.f.cidx[w];
+        const int lane = lane_id();
+        int out = 0, outfix = 0;
+        for (int base = 0; base < cnt; base += kWave) {
+            const int i = base + lane;
+            uint32_t kk = 0u;
+            int32_t ii = 0;
+            if (i < cnt) { kk = ck[i]; ii = ci[i]; }
+            const bool keep = i < cnt && kk != 0u && kk >= tau;
+            const uint64_t bal = __ballot(keep);
+            if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
+            out += __popcll(bal);
+            outfix += __popcll(__ballot(keep && i < nfix));
+            wave_sync();
+        }
+        cnt = out;
+        nfix = outfix;
+    }
     // Appends (kk, idx) from the lanes where c holds; wave-uniform call.
     __device__ __forceinline__ void append(bool c, uint32_t kk, int32_t idx) {
         uint64_t bal = __ballot(c);
@@ -689,10 +734,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             float mq = buf[q][0];
 #pragma unroll
             for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
-            if (__builtin_expect(__ballot(ok && mq >= cb.tauf) == 0ull, 1)) continue;
-            const int i0 = sl.a + vi * VEC;
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) slot(buf[q][j], i0 + j, ok);
+            const uint64_t hm = __ballot(ok && mq >= cb.tauf);
+            if (__builtin_expect(hm == 0ull, 1)) continue;
+            cb.template append_vec<VEC>(buf[q], sl.a + vi * VEC, hm);
         }
     };
     const bool sampling = !prm.greedy;
@@ -741,6 +785,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         // compacts the buffer: done out of line.  In mode 1 the processed value of each hashed
         // candidate not yet fixed by a compaction replaces its raw value here, found through
         // the presence bits with one LDS read per candidate.
+        cb.filter();
         const uint32_t pmode = sm.pmode;
         const int nfix = pmode == 1u ? cb.nfix : cb.cnt;
         if (pmode == 2u) cb.finish();
