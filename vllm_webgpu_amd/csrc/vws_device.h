@@ -22,10 +22,10 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 // reduction n = rint(d * log2 e), r = d - n * ln2 with a 16-bit head of ln2 (n * head is
 // exact) and an fp32 tail; exp(r) = 1 + r + r^2 Q(r) with Q of degree 4 fitted for this
 // project on [-ln2/2, ln2/2]; exact scaling by 2^n.  Max error 1 ulp (checked on every fp32).
-__device__ __forceinline__ float exp_det(float d) {
-    if (!(d >= -80.0f)) return 0.0f;
-    if (d > 80.0f) d = 80.0f;
-    if (__builtin_fabsf(d) < 0x1p-30f) return 1.0f;
+// Written without branches (special cases are selected at the end) so that it schedules freely
+// in straight-line code.
+__device__ __forceinline__ float exp_det(float d0) {
+    const float d = __builtin_fminf(__builtin_fmaxf(d0, -80.0f), 80.0f);
     const float t = d * 0x1.715476p+0f;
     const float n = __builtin_rintf(t);
     float r = __builtin_fmaf(-n, 0x1.62e4p-1f, d);
@@ -37,21 +37,21 @@ __device__ __forceinline__ float exp_det(float d) {
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
     const int ni = (int)n;
-    return p * u2f((uint32_t)(ni + 127) << 23);
+    const float v = p * u2f((uint32_t)(ni + 127) << 23);
+    const float v1 = __builtin_fabsf(d) < 0x1p-30f ? 1.0f : v;
+    return (d0 >= -80.0f) ? v1 : 0.0f;  // below -80 and NaN: 0
 }
 
 // log(u) for u > 0: u = 2^e m with m in [sqrt(1/2), sqrt(2)], f = m - 1 (exact),
 // log1p(f) = f + f^2 R(f) with R of degree 8 fitted for this project, log u = e ln2 + log1p(f).
 // log(0) = -inf, log(+inf) = +inf, NaN otherwise.  Max error 1 ulp (checked on every fp32).
+// Branch-free like exp_det: the special inputs are selected at the end.
 __device__ __forceinline__ float log_det(float u) {
-    if (!(u > 0.0f)) return (u == 0.0f) ? -__builtin_inff() : __builtin_nanf("");
-    if (u == __builtin_inff()) return u;
-    uint32_t b = f2u(u);
-    int e = 0;
-    if (b < 0x00800000u) { b = f2u(u * 0x1p23f); e = -23; }
-    e += (int)(b >> 23) - 127;
-    uint32_t mb = (b & 0x007FFFFFu) | 0x3F800000u;
-    if (mb > 0x3FB504F3u) { mb -= 0x00800000u; e += 1; }
+    const bool sub = f2u(u) < 0x00800000u;
+    const uint32_t b = f2u(sub ? u * 0x1p23f : u);
+    const bool hi = ((b & 0x007FFFFFu) | 0x3F800000u) > 0x3FB504F3u;
+    const int e = (sub ? -23 : 0) + (int)((b >> 23) & 0xFFu) - 127 + (hi ? 1 : 0);
+    const uint32_t mb = ((b & 0x007FFFFFu) | 0x3F800000u) - (hi ? 0x00800000u : 0u);
     const float f = u2f(mb) - 1.0f;
     const float f2 = f * f;
     float R = __builtin_fmaf(-0x1.4a5298p-4f, f, 0x1.088e82p-3f);
@@ -63,21 +63,22 @@ __device__ __forceinline__ float log_det(float u) {
     R = __builtin_fmaf(R, f, 0x1.555548p-2f);
     R = __builtin_fmaf(R, f, -0x1.fffffep-2f);
     const float L = __builtin_fmaf(f2, R, f);
-    if (e == 0) return L;
     const float ef = (float)e;
-    return __builtin_fmaf(ef, 0x1.62e43p-1f, __builtin_fmaf(ef, -0x1.05c61p-29f, L));
+    const float v = e == 0 ? L : __builtin_fmaf(ef, 0x1.62e43p-1f, __builtin_fmaf(ef, -0x1.05c61p-29f, L));
+    const float vi = u == __builtin_inff() ? u : v;
+    return (u > 0.0f) ? vi : ((u == 0.0f) ? -__builtin_inff() : __builtin_nanf(""));
 }
 
 // floor(e * 2^44) for e in [0, 1]; 0 for e <= 0 or NaN.
 __device__ __forceinline__ uint64_t mass_of(float e) {
-    if (!(e > 0.0f)) return 0;
     const uint32_t b = f2u(e);
-    const int ex = (int)(b >> 23);
+    const int ex = (int)((b >> 23) & 0xFFu);
     const uint64_t mant = ex ? ((b & 0x7FFFFFu) | 0x800000u) : (b & 0x7FFFFFu);
-    const int sh = (ex ? ex : 1) - 106;
-    if (sh >= 0) return mant << sh;
-    if (sh <= -64) return 0;
-    return mant >> (-sh);
+    const int sh = (ex ? ex : 1) - 106;  // <= 21 for e <= 1
+    const uint64_t left = mant << (sh & 63);
+    const uint64_t right = -sh < 64 ? mant >> ((-sh) & 63) : 0ull;
+    const uint64_t m = sh >= 0 ? left : right;
+    return (e > 0.0f) ? m : 0ull;
 }
 
 // Order-preserving key: x < y <=> key(x) < key(y); -0 and +0 share a key; NaN -> 0.

@@ -512,13 +512,23 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
     const bool removed = keep && topp && (abl ? (C != W) : (C <= thr && C != W));
     const bool kept = keep && !removed;
-    uint64_t pk = 0ull;
-    if (kept) {
-        const float rkey = e / (0.0f - log_det(uu));
-        if (rkey >= 0.0f) pk = ((uint64_t)f2u(rkey) << 32) | (0x7FFFFFFFu - (uint32_t)key);
+    // race: key bits + 1 (0 = no valid key) reduced as 32-bit maxima; the lowest index wins
+    // among equal keys, and the best key of the other lanes is the runner-up
+    const float rkey = e / (0.0f - log_det(uu));
+    const uint32_t kb = (kept && rkey >= 0.0f) ? f2u(rkey) + 1u : 0u;
+    const uint32_t kmax = wave_max_u32(kb);
+    const uint64_t at = __ballot(kb == kmax && kmax != 0u);
+    int win = -1;
+    uint32_t widx = 0u;
+    if (at) {
+        win = (int)__builtin_ctzll(at);
+        widx = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, win);
+        if (at & (at - 1ull)) {  // equal keys: the lowest index
+            widx = wave_min_u32(((at >> lane) & 1ull) ? (uint32_t)key : 0xFFFFFFFFu);
+            win = (int)__builtin_ctzll(__ballot(((at >> lane) & 1ull) && (uint32_t)key == widx));
+        }
     }
-    const uint64_t best = wave_max_u64(pk);
-    const uint32_t second = wave_max_u32((pk != 0ull && pk != best) ? (uint32_t)(pk >> 32) + 1u : 0u);
+    const uint32_t second = wave_max_u32(lane != win ? kb : 0u);
     const int nkept = __popcll(__ballot(kept));
     const int nrem = __popcll(__ballot(removed));
     const uint64_t cat = readlane64(C, nkept - 1);              // smallest kept cumulative mass
@@ -526,9 +536,9 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     if (lane == 0) {
         int32_t tok;
         uint32_t fl = 0;
-        if (best) {
-            tok = (int32_t)(0x7FFFFFFFu - (uint32_t)best);
-            const float bk = u2f((uint32_t)(best >> 32));
+        if (kmax) {
+            tok = (int32_t)widx;
+            const float bk = u2f(kmax - 1u);
             if (second) {
                 const float sk = u2f(second - 1u);
                 if ((double)sk >= (double)bk * (1.0 - 1e-6)) fl |= VWS_FLAG_RACE_NEAR_TIE;
