@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 2
+#define VWS_ABI_VERSION 3
 
 /* status codes */
 #define VWS_OK 0
@@ -62,6 +62,12 @@ typedef struct vws_sample_args {
     int32_t dtype;        /* VWS_DTYPE_* */
     const void* logits;   /* [B, V] with row stride below; read only */
     int64_t logits_row_stride; /* elements */
+    /* > 0: the logits are the lm_head output before Gemma's final soft cap, applied here as
+     * cap * tanh(x / cap) (vllm_webgpu/models/gemma4.py:158-163, shaders/gemma/
+     * logit_softcap.wgsl:13-28; tanh(v) = +-1 for |v| >= 20, else (e - 1) / (e + 1) with
+     * e = exp(2v), fp32).  Everything downstream -- processors, penalties, raw logprobs --
+     * sees the capped values.  0 = off. */
+    float logit_softcap;
 
     /* Per-row parameters, device arrays of length B.  NULL selects the default:
      * temperature NULL = every row greedy; top_k NULL/<=0/>=V = off; top_p NULL/>=1 = off;
@@ -188,7 +194,8 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
 int vws_profile_begin(int32_t max_launches);
 int vws_profile_end(double* ms, int32_t* count);
 
-/* Device self-test of the sampler arithmetic: evaluates fn (0 = exp_det, 1 = log_det) at
+/* Device self-test of the sampler arithmetic: evaluates fn (0 = exp_det, 1 = log_det,
+ * 2 = the logit soft cap at cap 1, i.e. its tanh) at
  * every fp32 whose order key lies in [key_lo, key_hi] and accumulates the same 64-bit hash
  * as the CPU oracle's checker into out2[0] and the count into out2[1] (device u64[2],
  * zeroed by this call). */

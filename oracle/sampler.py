@@ -68,7 +68,8 @@ def lib() -> ctypes.CDLL:
             L.vwo_scale_floor.restype = ctypes.c_uint64
             L.vwo_sample_batch.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P, P,
                                            ctypes.c_int, P, P, ctypes.c_int, P, P, ctypes.c_int,
-                                           P, P, P, ctypes.c_int, P, P, P, P]
+                                           P, P, P, ctypes.c_int, P, P, P, P, ctypes.c_float]
+            L.vwo_softcap_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P]
             L.vwo_apply_adjustments_row.argtypes = [P, ctypes.c_int, P, P, P, ctypes.c_int]
             L.vwo_apply_penalties_row.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int,
                                                   ctypes.c_float, ctypes.c_float, ctypes.c_float]
@@ -76,6 +77,7 @@ def lib() -> ctypes.CDLL:
             L.vwo_argmax_row.restype = ctypes.c_int32
             L.vwo_topk_row.argtypes = [P, ctypes.c_int, ctypes.c_int, P, P]
             L.vwo_softmax_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P, P, P]
+            L.vwo_check_softcap.argtypes = [ctypes.c_float, ctypes.c_float, P, P, P, P, P]
             for name in ("vwo_check_exp", "vwo_check_log"):
                 getattr(L, name).argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_uint32,
                                              P, P, P, P]
@@ -127,6 +129,16 @@ def check_exp(lo: float, hi: float, stride: int = 1):
 
 def check_log(lo: float, hi: float, stride: int = 1):
     return _check("vwo_check_log", lo, hi, stride)
+
+
+def check_softcap(lo: float, hi: float):
+    """vwo_softcap at cap 1 on every fp32 of [lo, hi]: max_err (absolute, against tanh in
+    double), hash and count (as check_exp) and max_drop (largest max_{x' <= x} t(x') - t(x))."""
+    me, w, d = ctypes.c_double(), ctypes.c_float(), ctypes.c_double()
+    h, c = ctypes.c_uint64(), ctypes.c_uint64()
+    lib().vwo_check_softcap(ctypes.c_float(lo), ctypes.c_float(hi), ctypes.byref(me),
+                            ctypes.byref(w), ctypes.byref(h), ctypes.byref(c), ctypes.byref(d))
+    return dict(max_err=me.value, worst=w.value, hash=h.value, count=c.value, max_drop=d.value)
 
 
 def _check(name, lo, hi, stride):
@@ -217,7 +229,7 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
            prompt_lens: np.ndarray | None = None, output_lens: np.ndarray | None = None,
            num_logprobs: int | None = None, allowed: np.ndarray | None = None,
            adjust_ids: np.ndarray | None = None, adjust_vals: np.ndarray | None = None,
-           adjust_lens: np.ndarray | None = None) -> dict:
+           adjust_lens: np.ndarray | None = None, softcap: float | None = None) -> dict:
     """Samples every row of fp32 ``logits`` [B, V].
 
     ``params``: PARAMS_DTYPE [B] (see make_params).  ``uniforms``: fp32 [B, V] in (0, 1).
@@ -225,6 +237,7 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
     Logits processors (before the penalties): ``allowed`` uint32 [B, ceil(V/32)] bitmask (bit
     set = allowed, None = all); ``adjust_ids`` int32 / ``adjust_vals`` fp32 [B, Wa]: value
     -inf bans the token, a finite value is added (logit bias).
+    ``softcap`` > 0: the logits first go through Gemma's soft cap (see ``softcap_row``).
     Returns dict(token, flags, n_kept, n_topk, mass_total, threshold, row_max, kth_y,
     [lp_ids, lp_vals, ranks]).
     """
@@ -257,8 +270,16 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
                            _ptr(al), 0 if al is None else al.shape[1],
                            _ptr(ai), _ptr(av), 0 if ai is None else ai.shape[1], _ptr(an),
                            _ptr(prm), _ptr(u), L, _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks),
-                           _ptr(outs))
+                           _ptr(outs), float(softcap or 0.0))
     res = {name: outs[name].copy() for name in ROW_OUT_DTYPE.names}
     if L >= 0:
         res.update(lp_ids=lp_ids, lp_vals=lp_vals, ranks=ranks)
     return res
+
+
+def softcap_row(x: np.ndarray, cap: float) -> np.ndarray:
+    """cap * tanh(x / cap) with the oracle's arithmetic (vwo_softcap), fp32 in and out."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().vwo_softcap_row(_ptr(x), x.size, float(cap), _ptr(out))
+    return out

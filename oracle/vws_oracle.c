@@ -94,6 +94,30 @@ float vwo_log(float u) {
     return fmaf(ef, 0x1.62e43p-1f, fmaf(ef, -0x1.05c61p-29f, L));
 }
 
+/* Gemma's final-logit soft cap, cap * tanh(x / cap), as the reference computes it
+ * (vllm_webgpu/shaders/gemma/logit_softcap.wgsl:13-28): v = x * fl(1 / cap); tanh(v) = +-1 for
+ * |v| >= 20, else (e - 1) / (e + 1) with e = exp(2v), here e = vwo_exp(2v); the result is t * cap
+ * in fp32 (the reference stores it as f16; this library keeps fp32).  NaN stays NaN. */
+float vwo_softcap(float x, float inv_cap, float cap) {
+    if (x != x) return x;
+    const float v = x * inv_cap;
+    float t;
+    if (v >= 20.0f) {
+        t = 1.0f;
+    } else if (v <= -20.0f) {
+        t = -1.0f;
+    } else {
+        const float e = vwo_exp(2.0f * v);
+        t = (e - 1.0f) / (e + 1.0f);
+    }
+    return t * cap;
+}
+
+void vwo_softcap_row(const float* x, int V, float cap, float* out) {
+    const float inv = 1.0f / cap;
+    for (int i = 0; i < V; ++i) out[i] = vwo_softcap(x[i], inv, cap);
+}
+
 /* floor(e * 2^44) for e in [0, 1] (0 for e <= 0 or NaN). */
 uint64_t vwo_mass(float e) {
     if (!(e > 0.0f)) return 0;
@@ -373,19 +397,28 @@ logprobs:
 }
 
 /* Batched driver (rows are independent; OpenMP over rows when built with -fopenmp).
- * prompt/output: padded [B, *_stride] with ids outside [0, V) ignored; lens may be NULL. */
+ * prompt/output: padded [B, *_stride] with ids outside [0, V) ignored; lens may be NULL.
+ * softcap > 0: the logits are first mapped through vwo_softcap (they are the model's output
+ * then: processors, penalties and the raw logprobs all see the capped values). */
 int vwo_sample_batch(const float* logits, int B, int V, const int32_t* prompt, int prompt_stride,
                      const int32_t* prompt_lens, const int32_t* output, int output_stride,
                      const int32_t* output_lens, const uint32_t* allowed, int allowed_stride,
                      const int32_t* adj_ids, const float* adj_vals, int adj_stride,
                      const int32_t* adj_lens, const vwo_params* prm, const float* uniforms,
-                     int L, int32_t* lp_ids, float* lp_vals, int32_t* ranks, vwo_row_out* outs) {
+                     int L, int32_t* lp_ids, float* lp_vals, int32_t* ranks, vwo_row_out* outs,
+                     float softcap) {
 #pragma omp parallel for schedule(dynamic, 1)
     for (int b = 0; b < B; ++b) {
+        float* capped = NULL;
+        if (softcap > 0.0f) {
+            capped = (float*)malloc(sizeof(float) * (size_t)V);
+            vwo_softcap_row(logits + (size_t)b * V, V, softcap, capped);
+        }
         const int np = prompt ? (prompt_lens ? prompt_lens[b] : prompt_stride) : 0;
         const int no = output ? (output_lens ? output_lens[b] : output_stride) : 0;
         const int na = adj_ids ? (adj_lens ? adj_lens[b] : adj_stride) : 0;
-        vwo_sample_row(logits + (size_t)b * V, V, prompt ? prompt + (size_t)b * prompt_stride : NULL, np,
+        vwo_sample_row(capped ? capped : logits + (size_t)b * V, V,
+                       prompt ? prompt + (size_t)b * prompt_stride : NULL, np,
                        output ? output + (size_t)b * output_stride : NULL, no,
                        allowed ? allowed + (size_t)b * allowed_stride : NULL,
                        adj_ids ? adj_ids + (size_t)b * adj_stride : NULL,
@@ -394,6 +427,7 @@ int vwo_sample_batch(const float* logits, int B, int V, const int32_t* prompt, i
                        lp_ids ? lp_ids + (size_t)b * (L + 1) : NULL,
                        lp_vals ? lp_vals + (size_t)b * (L + 1) : NULL, ranks ? ranks + b : NULL,
                        &outs[b]);
+        free(capped);
     }
     return 0;
 }
@@ -454,6 +488,66 @@ void vwo_check_exp(float lo, float hi, uint32_t stride, int64_t* max_ulp, float*
         }
     }
     *max_ulp = mu; *worst = wd; *hash = h; *count = c;
+}
+
+/* vwo_softcap at cap 1 (t(x), the cap's tanh) on every fp32 x whose key lies in [lo, hi]: the
+ * largest absolute error against tanh in double, the same hash as vwo_check_exp (comparable
+ * with the device self-test) and the largest drop max_{x' <= x} t(x') - t(x).  t is not
+ * monotone in fp32: the device sampler's single pass thresholds raw logits and relies on this
+ * drop bound to decide when a capped row is settled.  The drop uses two passes over fixed
+ * chunks (chunk maxima, then each chunk with the running maximum of the chunks before it). */
+void vwo_check_softcap(float lo, float hi, double* max_err, float* worst, uint64_t* hash,
+                       uint64_t* count, double* max_drop) {
+    const uint32_t klo = vwo_key(lo), khi = vwo_key(hi);
+    const int64_t n = (int64_t)khi - klo + 1, nch = 256, per = (n + nch - 1) / nch;
+    float cmax[256];
+    double me = 0.0; float wd = 0.0f; uint64_t h = 0, c = 0;
+#pragma omp parallel
+    {
+        double lme = 0.0; float lwd = 0.0f; uint64_t lh = 0, lc = 0;
+#pragma omp for schedule(dynamic)
+        for (int64_t ch = 0; ch < nch; ++ch) {
+            float m = -2.0f;
+            for (int64_t i = ch * per; i < (ch + 1) * per && i < n; ++i) {
+                const uint32_t key = klo + (uint32_t)i;
+                const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+                const float x = u2f(bits);
+                const float t = vwo_softcap(x, 1.0f, 1.0f);
+                const double err = fabs((double)t - tanh((double)x));
+                if (err > lme) { lme = err; lwd = x; }
+                lh += (uint64_t)f2u(t) * 0x9E3779B97F4A7C15ull ^ (uint64_t)bits;
+                lc++;
+                if (t > m) m = t;
+            }
+            cmax[ch] = m;
+        }
+#pragma omp critical
+        {
+            if (lme > me) { me = lme; wd = lwd; }
+            h += lh; c += lc;
+        }
+    }
+    double drop = 0.0;
+#pragma omp parallel
+    {
+        double ld = 0.0;
+#pragma omp for schedule(dynamic)
+        for (int64_t ch = 0; ch < nch; ++ch) {
+            float run = -2.0f;
+            for (int64_t j = 0; j < ch; ++j) run = cmax[j] > run ? cmax[j] : run;
+            for (int64_t i = ch * per; i < (ch + 1) * per && i < n; ++i) {
+                const uint32_t key = klo + (uint32_t)i;
+                const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+                const float t = vwo_softcap(u2f(bits), 1.0f, 1.0f);
+                if (t > run) run = t;
+                const double d = (double)run - (double)t;
+                if (d > ld) ld = d;
+            }
+        }
+#pragma omp critical
+        if (ld > drop) drop = ld;
+    }
+    *max_err = me; *worst = wd; *hash = h; *count = c; *max_drop = drop;
 }
 
 void vwo_check_log(float lo, float hi, uint32_t stride, int64_t* max_ulp, float* worst,

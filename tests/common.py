@@ -13,15 +13,16 @@ LP_RTOL = 1e-5
 LP_ATOL = 1e-6
 
 
-def oracle_run(w, num_logprobs=None):
+def oracle_run(w, num_logprobs=None, softcap=None):
     B = w.shape[0]
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
     return O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids,
-                    num_logprobs=w.num_logprobs if num_logprobs is None else num_logprobs)
+                    num_logprobs=w.num_logprobs if num_logprobs is None else num_logprobs,
+                    softcap=softcap)
 
 
-def gpu_run(w, device, num_logprobs=None):
+def gpu_run(w, device, num_logprobs=None, softcap=None):
     import torch
 
     from vllm_webgpu_amd import ops
@@ -42,7 +43,7 @@ def gpu_run(w, device, num_logprobs=None):
                      repetition_penalty=torch.from_numpy(w.repetition),
                      presence_penalty=torch.from_numpy(w.presence),
                      frequency_penalty=torch.from_numpy(w.frequency), output_ids=hist,
-                     uniforms=U, num_logprobs=L)
+                     uniforms=U, num_logprobs=L, logit_softcap=softcap)
     torch.cuda.synchronize()
     out = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
                n_kept=res.num_kept.cpu().numpy())

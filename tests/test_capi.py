@@ -127,6 +127,9 @@ def test_valid_args_pass(L):
     (dict(adjust_ids=FAKE, adjust_vals=FAKE, adjust_width=8, adjust_row_stride=4),
      _lib.ERR_INVALID_ARGUMENT, "adjust_row_stride"),
     (dict(allowed_mask=FAKE, allowed_row_stride=31), _lib.ERR_INVALID_ARGUMENT, "allowed_row_stride"),
+    (dict(logit_softcap=-1.0), _lib.ERR_INVALID_ARGUMENT, "logit_softcap"),
+    (dict(logit_softcap=float("nan")), _lib.ERR_INVALID_ARGUMENT, "logit_softcap"),
+    (dict(logit_softcap=float("inf")), _lib.ERR_INVALID_ARGUMENT, "logit_softcap"),
 ])
 def test_invalid_args_rejected(L, over, code, msg):
     assert _status(L, _args(L, **over)) == code

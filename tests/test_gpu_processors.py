@@ -46,7 +46,7 @@ def _adjust(rng, x, width, ban_top=3, pos_bias=False, neg_bias=True):
     return ids, vals
 
 
-def _run(cuda, w, logits_np, ids=None, vals=None, allowed=None, L=None):
+def _run(cuda, w, logits_np, ids=None, vals=None, allowed=None, L=None, softcap=None):
     B, V = w.shape
     if w.dtype == "bf16":
         lg = torch.from_numpy(w.logits.view(np.int16)).to(cuda).view(torch.bfloat16)
@@ -63,13 +63,13 @@ def _run(cuda, w, logits_np, ids=None, vals=None, allowed=None, L=None):
         num_logprobs=L,
         allowed_mask=None if allowed is None else torch.from_numpy(_bits(allowed).view(np.int32)).to(cuda),
         adjust_ids=None if ids is None else torch.from_numpy(ids),
-        adjust_vals=None if vals is None else torch.from_numpy(vals))
+        adjust_vals=None if vals is None else torch.from_numpy(vals), logit_softcap=softcap)
     torch.cuda.synchronize()
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
     ref = O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids, num_logprobs=L,
                    allowed=None if allowed is None else _bits(allowed), adjust_ids=ids,
-                   adjust_vals=vals)
+                   adjust_vals=vals, softcap=softcap)
     tok = res.sampled.cpu().numpy()
     fl = res.flags.cpu().numpy().view(np.uint32)
     bad = np.nonzero(tok != ref["token"])[0]

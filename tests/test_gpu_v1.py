@@ -38,20 +38,21 @@ def _metadata(w, dev, gens, num_logprobs):
         output_token_ids_tensor=hist)
 
 
-@pytest.mark.parametrize("cfg,scale,L", [(2, 0.25, None), (3, 0.05, None), (4, 0.05, None),
-                                         (5, 0.05, 20)])
-def test_sampler_forward_matches_oracle(cuda, cfg, scale, L):
+@pytest.mark.parametrize("cfg,scale,L,cap", [(2, 0.25, None, None), (3, 0.05, None, None),
+                                             (4, 0.05, None, None), (5, 0.05, 20, None),
+                                             (3, 0.05, None, 30.0), (5, 0.05, 20, 30.0)])
+def test_sampler_forward_matches_oracle(cuda, cfg, scale, L, cap):
     w = W.config(cfg, scale=scale)
     B, V = w.shape
     if w.dtype == "bf16":
         logits = torch.from_numpy(w.logits.view(np.int16)).to(cuda).view(torch.bfloat16)
     else:
         logits = torch.from_numpy(w.logits).to(cuda)
-    out = Sampler()(logits, _metadata(w, cuda, _gens(B, cuda, 7000), L))
+    out = Sampler(logit_softcap=cap)(logits, _metadata(w, cuda, _gens(B, cuda, 7000), L))
     u = draw_uniforms(B, V, _gens(B, cuda, 7000), cuda).cpu().numpy()
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
-    ref = O.sample(w.logits_f32(), prm, u, output_ids=w.output_ids, num_logprobs=L)
+    ref = O.sample(w.logits_f32(), prm, u, output_ids=w.output_ids, num_logprobs=L, softcap=cap)
     tok = out.sampled_token_ids.cpu().numpy()
     assert tok.shape == (B, 1) and tok.dtype == np.int32
     bad = np.nonzero(tok[:, 0] != ref["token"])[0]

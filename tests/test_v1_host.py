@@ -104,6 +104,11 @@ def test_sampler_refuses_cpu_logits_and_unsupported_modes():
         s(torch.zeros(1, V), m)                    # no host fallback
     with pytest.raises(NotImplementedError):
         Sampler(logprobs_mode="processed_logprobs")
+    for bad in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(ValueError, match="logit_softcap"):
+            Sampler(logit_softcap=bad)
+    assert Sampler(logit_softcap=30.0).logit_softcap == 30.0
+    assert WebGPUModelRunner(None, device="cpu", logit_softcap=30.0).sampler.logit_softcap == 30.0
 
 
 def _meta(**kw):

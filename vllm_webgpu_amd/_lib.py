@@ -14,7 +14,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2
@@ -56,7 +56,7 @@ class SampleArgs(ctypes.Structure):
 
     _fields_ = [
         ("struct_size", _U32), ("batch", _I32), ("vocab", _I32), ("dtype", _I32),
-        ("logits", _P), ("logits_row_stride", _I64),
+        ("logits", _P), ("logits_row_stride", _I64), ("logit_softcap", ctypes.c_float),
         ("temperature", _P), ("top_k", _P), ("top_p", _P), ("min_p", _P),
         ("repetition_penalty", _P), ("presence_penalty", _P), ("frequency_penalty", _P),
         ("prompt_ids", _P), ("prompt_row_stride", _I64), ("prompt_width", _I32), ("prompt_lens", _P),

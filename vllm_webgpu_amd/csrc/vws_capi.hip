@@ -169,6 +169,8 @@ int validate_sample(const vws_sample_args* a) {
     if ((st = validate_history(a->output_ids, a->output_row_stride, a->output_width, "output"))) return st;
     if ((st = validate_history(a->adjust_ids, a->adjust_row_stride, a->adjust_width, "adjust"))) return st;
     if (a->adjust_ids && !a->adjust_vals) return fail(VWS_ERR_INVALID_ARGUMENT, "adjust_vals is NULL while adjust_ids is set");
+    if (!(a->logit_softcap >= 0.0f) || a->logit_softcap == __builtin_inff())
+        return fail(VWS_ERR_INVALID_ARGUMENT, "logit_softcap must be finite and >= 0 (got %g)", (double)a->logit_softcap);
     if (a->allowed_mask && a->allowed_row_stride < (int64_t)(a->vocab + 31) / 32)
         return fail(VWS_ERR_INVALID_ARGUMENT, "allowed_row_stride < ceil(vocab / 32) words");
     const int hw = sample_history_width(a);
@@ -259,6 +261,8 @@ int vws_sample(const vws_sample_args* a) {
     k.adjstride = a->adjust_row_stride;
     k.adjwidth = a->adjust_ids ? a->adjust_width : 0;
     k.adjlens = a->adjust_lens;
+    k.softcap = a->logit_softcap;
+    k.inv_softcap = a->logit_softcap > 0.0f ? 1.0f / a->logit_softcap : 0.0f;
     k.u = a->uniforms;
     k.ustride = a->uniforms_row_stride;
     k.sampled = a->sampled;
@@ -396,7 +400,7 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
 }
 
 int vws_math_selftest(int32_t fn, uint32_t key_lo, uint32_t key_hi, uint64_t* out2, void* stream) {
-    if (fn != 0 && fn != 1) return fail(VWS_ERR_INVALID_ARGUMENT, "fn must be 0 (exp) or 1 (log)");
+    if (fn < 0 || fn > 2) return fail(VWS_ERR_INVALID_ARGUMENT, "fn must be 0 (exp), 1 (log) or 2 (soft cap)");
     if (!out2) return fail(VWS_ERR_INVALID_ARGUMENT, "out2 is NULL");
     if (key_hi < key_lo) return fail(VWS_ERR_INVALID_ARGUMENT, "key_hi < key_lo");
     hipStream_t s = (hipStream_t)stream;

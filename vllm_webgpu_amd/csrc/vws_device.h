@@ -69,6 +69,36 @@ __device__ __forceinline__ float log_det(float u) {
     return (u > 0.0f) ? vi : ((u == 0.0f) ? -__builtin_inff() : __builtin_nanf(""));
 }
 
+// Gemma's final-logit soft cap, cap * tanh(x / cap), with the reference's formula
+// (vllm_webgpu/shaders/gemma/logit_softcap.wgsl:13-28): v = x * fl(1 / cap); tanh(v) = +-1 for
+// |v| >= 20, else (e - 1) / (e + 1) with e = exp_det(2v); result t * cap in fp32.  NaN stays
+// NaN.  Branch-free; the same operation sequence as the oracle's vwo_softcap.
+__device__ __forceinline__ float softcap_det(float x, float inv_cap, float cap) {
+    const float v = x * inv_cap;
+    const float e = exp_det(2.0f * __builtin_fminf(__builtin_fmaxf(v, -20.0f), 20.0f));
+    const float t0 = (e - 1.0f) / (e + 1.0f);
+    const float t = v >= 20.0f ? 1.0f : (v <= -20.0f ? -1.0f : t0);
+    return x != x ? x : t * cap;
+}
+
+// An upper bound on softcap_det(x') over every x' <= x (NaN excluded).  The fp32 tanh above is
+// not monotone: over every fp32 v in [-20, 20] (it is constant outside), the largest drop
+// max_{v' <= v} t(v') - t(v) is 2^-22.  v = x * (1 / cap) and t * cap round monotonically, so
+// the capped values of x' <= x exceed softcap_det(x) by less than cap * 2^-21; this adds
+// cap * 2^-20.
+__device__ __forceinline__ float softcap_bound(float x, float inv_cap, float cap) {
+    return softcap_det(x, inv_cap, cap) + cap * 0x1p-20f;
+}
+
+// A raw value below x whose capped value lies about twice softcap_bound's margin below x's:
+// x - cap * 2^-19 / (1 - t^2), t = tanh(x / cap) (the cap's slope is 1 - t^2; near saturation
+// the step stops growing at 1024 times its smallest value).  Any value works as a threshold;
+// this one leaves x's capped value clear of the bound of everything below it.
+__device__ __forceinline__ float softcap_lower(float x, float inv_cap, float cap) {
+    const float t = softcap_det(x, inv_cap, cap) * inv_cap;
+    return x - cap * 0x1p-19f / __builtin_fmaxf(1.0f - t * t, 0x1p-10f);
+}
+
 // floor(e * 2^44) for e in [0, 1]; 0 for e <= 0 or NaN.
 __device__ __forceinline__ uint64_t mass_of(float e) {
     const uint32_t b = f2u(e);

@@ -277,7 +277,8 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             const uint32_t kk = __hip_atomic_load(&hkey[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (kk) {
                 const uint32_t v = __hip_atomic_load(&hval[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float raw = Elem<T>::load1(row + (kk - 1u));
+                float raw = Elem<T>::load1(row + (kk - 1u));
+                if (a.softcap > 0.0f) raw = softcap_det(raw, a.inv_softcap, a.softcap);
                 const float bias = u2f(__hip_atomic_load(&hadj[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
                 const float pen = apply_hashed(raw, v, bias, prm.rep, prm.inv_rep, prm.freq, prm.pres);
                 __hip_atomic_store(&hpen[s], f2u(pen), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -316,6 +317,13 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             const int c0 = it * 2 * NT + tid;
             const int i0 = sl.load(c0, v0);
             const int i1 = sl.load(c0 + NT, v1);
+            if (a.softcap > 0.0f) {  // the model's output is the capped logit
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    v0[j] = softcap_det(v0[j], a.inv_softcap, a.softcap);
+                    v1[j] = softcap_det(v1[j], a.inv_softcap, a.softcap);
+                }
+            }
             f(v0, i0);
             f(v1, i1);
         }
@@ -790,7 +798,8 @@ logprobs:
     if (L >= 0) {
         __syncthreads();
         const float m0 = m0key ? val_of(m0key) : 0.0f;
-        const float raw_s = Elem<T>::load1(row + token);
+        float raw_s = Elem<T>::load1(row + token);
+        if (a.softcap > 0.0f) raw_s = softcap_det(raw_s, a.inv_softcap, a.softcap);
         const uint32_t ks = key_of(raw_s);
         double s0 = 0.0;
         const bool have_s0 = !prm.greedy && sm.bc64[4] != 0ull;

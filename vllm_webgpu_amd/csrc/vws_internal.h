@@ -79,6 +79,8 @@ struct KArgs {
     int part_len;           // elements per part (multiple of 64)
     int mode;               // Mode
     int topk_k;             // k for kModeTopK
+    float softcap;          // > 0: Gemma's soft cap applied to every logit first
+    float inv_softcap;      // fl(1 / softcap)
     float* topk_vals;       // [B, k]
     int32_t* topk_ids;      // [B, k]
 };

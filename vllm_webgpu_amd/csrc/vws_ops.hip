@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void selftest_kernel(int fn, uint32_t klo, uin
         const uint32_t key = klo + (uint32_t)i;
         const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
         const float x = u2f(bits);
-        const float y = fn == 0 ? exp_det(x) : log_det(x);
+        const float y = fn == 0 ? exp_det(x) : (fn == 1 ? log_det(x) : softcap_det(x, 1.0f, 1.0f));
         h += ((uint64_t)f2u(y) * 0x9E3779B97F4A7C15ull) ^ (uint64_t)bits;
         c++;
     }

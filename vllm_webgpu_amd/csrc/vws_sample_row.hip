@@ -254,8 +254,10 @@ struct RowCand {
     uint32_t tau;         // threshold key
     float tauf;           // its value form (-inf when every non-NaN value passes)
     bool ovf;             // ties overflowed the buffer
-    __device__ __forceinline__ void init(int w_, int k_) {
+    bool compact_ok;      // a full buffer may be cut to its top k (not with the soft cap)
+    __device__ __forceinline__ void init(int w_, int k_, bool compact_ok_) {
         w = w_; k = k_; cnt = 0; nfix = 0; tau = 0u; tauf = -__builtin_inff(); ovf = false;
+        compact_ok = compact_ok_;
     }
     __device__ __forceinline__ void set_tau(uint32_t t) {
         if (t > tau) {
@@ -274,6 +276,7 @@ struct RowCand {
         if (ovf) return;
         int n = __popcll(hm) * VEC;
         if (cnt + n > kRowCap) {
+            if (!compact_ok) { ovf = true; return; }
             const uint64_t rc = row_compact(w, nfix, cnt, k);
             cnt = __builtin_amdgcn_readfirstlane((uint32_t)rc);
             nfix = cnt;
@@ -318,6 +321,7 @@ struct RowCand {
         if (!bal || ovf) return;
         int n = __popcll(bal);
         if (cnt + n > kRowCap) {
+            if (!compact_ok) { ovf = true; return; }
             const uint64_t rc = row_compact(w, nfix, cnt, k);
             cnt = __builtin_amdgcn_readfirstlane((uint32_t)rc);
             nfix = cnt;
@@ -453,10 +457,11 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
         }
     }
     // every threshold used (raw keys), and the largest y an element below them can have (-inf
-    // when only NaNs were dropped)
+    // when only NaNs were dropped; with the soft cap, a bound on it)
     const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;
-    const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / prm.T : val_of(tmax - 1u))
-                                          : -__builtin_inff();
+    float vlim = val_of(tmax - 1u);
+    if (a.softcap > 0.0f) vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
+    const float ylim = tmax > 0x007FFFFFu ? (sampling ? vlim / prm.T : vlim) : -__builtin_inff();
     if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
     if (mine) {
@@ -709,6 +714,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         if (lane == 0) sm.bc[0] = t0;
     }
     const bool gather = hx && (!mono || sm.adjraise != 0u);
+    // something may raise a logit and the logits are capped: the general path serves the row
+    if (gather && a.softcap > 0.0f) return false;
     if (gather) {
         if (lane == 0) sm.pmode = 2u;  // every wave writes the same value before its stream
         for (int s = tid; s < kRowHash; s += NT) {
@@ -750,7 +757,16 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         }
     };
     const bool sampling = !prm.greedy;
-    cb.init(wave, k);
+    // With the soft cap the buffer keeps raw values throughout (the cap is applied at the pack),
+    // so it is never cut by processed values: a full buffer sends the row to the general path.
+    const bool capped = a.softcap > 0.0f;
+    // The check after the stream bounds the capped value of everything below the threshold by
+    // the capped threshold plus a margin (softcap_bound); a seed at an element's own value
+    // would leave that element, often the k-th, inside the margin.  The seed is lowered below
+    // it by twice the margin in capped units.
+    if (capped && seed > 0x007FFFFFu)
+        seed = key_of(softcap_lower(val_of(seed), a.inv_softcap, a.softcap));
+    cb.init(wave, k, !capped);
     cb.set_tau(seed);
     if (gather) {
         constexpr int per = kRowHash / kRowWaves;
@@ -808,6 +824,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             for (int e = lane; e < cb.cnt; e += kWave) {
                 const int32_t ii = sm.cidx[wave][e];
                 uint32_t kx = sm.ckey[wave][e];
+                if (capped) kx = key_of(softcap_det(val_of(kx), a.inv_softcap, a.softcap));
                 if (e >= nfix && rhash_maybe(sm, ii)) {
                     const int hs = rhash_find(sm, ii);
                     if (hs >= 0)
@@ -853,9 +870,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
     // fewer than k candidates can only be exact when no threshold was used
     if (tmax != 0u && total < k) return false;
-    // the largest y an element below the thresholds can have; -inf when only NaNs were dropped
-    const float ylim = tmax > 0x007FFFFFu ? (sampling ? val_of(tmax - 1u) / Tt : val_of(tmax - 1u))
-                                          : -__builtin_inff();
+    // the largest y an element below the thresholds can have (with the soft cap, a bound on
+    // it); -inf when only NaNs were dropped
+    float vlim = val_of(tmax - 1u);
+    if (capped) vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
+    const float ylim = tmax > 0x007FFFFFu ? (sampling ? vlim / Tt : vlim) : -__builtin_inff();
     const bool mine = tid < total;
 
     // 5. ranks in y: candidate c's rank is the number of candidate keys above its own, so the

@@ -99,7 +99,7 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
            prompt_ids=None, prompt_lens=None, output_ids=None, output_lens=None,
            uniforms: torch.Tensor | None = None, num_logprobs: int | None = None,
            allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
-           adjust_lens=None) -> SampleResult:
+           adjust_lens=None, logit_softcap: float | None = None) -> SampleResult:
     """Samples one token per row of ``logits`` [B, V] (float32 or bfloat16, on the GPU).
 
     Per-row parameters are scalars or [B] tensors; ``None`` means off (temperature None = every
@@ -108,9 +108,13 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     ``temperature`` is given.  Logits processors (before the penalties): ``allowed_mask``
     int32 [B, ceil(V/32)] bit words (bit set = token allowed, see ``pack_allowed``), and the
     sparse ``adjust_ids`` int32 / ``adjust_vals`` float32 [B, W]: -inf bans a token, a finite
-    value is added to its logit.
+    value is added to its logit.  ``logit_softcap`` > 0: ``logits`` are the lm_head output
+    before Gemma's final soft cap, which is applied first (cap * tanh(x / cap)).
     """
     _check_device(logits, "logits")
+    cap = 0.0 if logit_softcap is None else float(logit_softcap)
+    if not (cap >= 0.0) or cap == float("inf"):
+        raise ValueError(f"logit_softcap must be finite and >= 0 (got {logit_softcap})")
     if logits.dim() != 2:
         raise ValueError("logits must be [B, V]")
     if logits.stride(1) != 1:
@@ -169,6 +173,7 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     a.struct_size = ctypes.sizeof(_lib.SampleArgs)
     a.batch, a.vocab, a.dtype = B, V, _dtype_code(logits)
     a.logits, a.logits_row_stride = logits.data_ptr(), logits.stride(0)
+    a.logit_softcap = cap
     a.temperature, a.top_k, a.top_p, a.min_p = _ptr(T), _ptr(K), _ptr(P), _ptr(MP)
     a.repetition_penalty, a.presence_penalty, a.frequency_penalty = _ptr(R), _ptr(PR), _ptr(FR)
     a.prompt_ids, a.prompt_row_stride, a.prompt_width, a.prompt_lens = _ptr(pid), pstride, pwidth, _ptr(plens)
@@ -269,7 +274,8 @@ def apply_penalties(logits: torch.Tensor, repetition_penalty=None, presence_pena
 
 
 def math_selftest(fn: int, key_lo: int, key_hi: int) -> tuple[int, int]:
-    """Device hash of exp_det (fn=0) or log_det (fn=1) over an order-key range; synchronises."""
+    """Device hash of exp_det (fn=0), log_det (fn=1) or the soft cap's tanh (fn=2, cap 1) over
+    an order-key range; synchronises."""
     out = torch.zeros(2, dtype=torch.int64, device="cuda")
     _lib.check(_lib.lib().vws_math_selftest(fn, key_lo, key_hi, out.data_ptr(), _stream_ptr()))
     h, c = out.cpu().tolist()

@@ -91,12 +91,20 @@ def processor_lists(m: SamplingMetadata, B: int, V: int):
 class Sampler:
     """vLLM-v1 ``Sampler`` facade over ``vws_sample``."""
 
-    def __init__(self, logprobs_mode: str = "raw_logprobs") -> None:
+    def __init__(self, logprobs_mode: str = "raw_logprobs",
+                 logit_softcap: float | None = None) -> None:
+        """``logit_softcap``: Gemma's final soft cap, fused into the sampling launch, for models
+        whose forward returns the lm_head output before the cap (reference:
+        ``vllm_webgpu/models/gemma4.py:158-163``).  The capped logits are then the model's
+        output for everything that follows, raw logprobs included."""
         if logprobs_mode != "raw_logprobs":
             raise NotImplementedError(
                 f"logprobs_mode {logprobs_mode!r}: only 'raw_logprobs' (log-softmax of the "
                 "unprocessed logits) is computed by the device sampler")
+        if logit_softcap is not None and not (0.0 < float(logit_softcap) < float("inf")):
+            raise ValueError(f"logit_softcap must be a positive finite number (got {logit_softcap})")
         self.logprobs_mode = logprobs_mode
+        self.logit_softcap = logit_softcap
 
     def __call__(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata) -> SamplerOutput:
         return self.forward(logits, sampling_metadata)
@@ -135,7 +143,7 @@ class Sampler:
 
         res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
                          min_p=m.min_p, uniforms=uniforms, num_logprobs=m.max_num_logprobs,
-                         **penalties, **processors)
+                         logit_softcap=self.logit_softcap, **penalties, **processors)
         lp = None
         if m.max_num_logprobs is not None:
             lp = LogprobsTensors(res.logprob_ids, res.logprob_vals, res.logprob_ranks)
