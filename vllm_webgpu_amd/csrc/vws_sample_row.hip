@@ -424,8 +424,7 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
 // Exact when the k-th key is strictly above the largest y a dropped element can have (ylim).
 // Returns false (uniformly over the workgroup) when the row must take the general path.
 __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int r, const RowP& prm,
-                                               int k, int total, uint32_t seed, bool sampling,
-                                               float u_first, int u_slot) {
+                                               int k, int total, uint32_t seed, bool sampling) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool mine = tid < total;
@@ -462,12 +461,15 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     float vlim = val_of(tmax - 1u);
     if (a.softcap > 0.0f) vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
     const float ylim = tmax > 0x007FFFFFu ? (sampling ? vlim / prm.T : vlim) : -__builtin_inff();
-    if (u_slot >= 0) sm.pu[u_slot] = u_first;
     __syncthreads();
+    // the uniforms of the 64 largest candidates only: loaded now, stored into their slots once
+    // wave 0 is about to race, so that their latency overlaps the slots and the masses
+    const uint32_t mpos = mine ? sm.crank[tid] : 0xFFFFFFFFu;
+    float u_mine = 0.5f;
+    if (sampling && mpos < (uint32_t)kWave) u_mine = a.u[(size_t)r * a.ustride + (uint32_t)myk];
     if (mine) {
-        const uint32_t pos = sm.crank[tid];
+        const uint32_t pos = mpos;
         if (pos <= (uint32_t)kWave) sm.tk[pos] = myk;
-        if (sampling && pos < (uint32_t)kWave) sm.tu[pos] = sm.pu[tid];
         const uint32_t yk = (uint32_t)(myk >> 32);
         // the k-th key must lie strictly above every dropped element (ties included)
         if (pos == (uint32_t)(k - 1) && yk != 0u && !(val_of(yk) > ylim)) atomicOr(&sm.status, 4u);
@@ -492,11 +494,17 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     // fewer candidates than k (no threshold used): every candidate is in the top k
     const uint32_t ykth = total >= k ? (uint32_t)(sm.tk[k - 1] >> 32) : 0u;
     if (total > kWave && (uint32_t)(sm.tk[kWave] >> 32) >= ykth) return false;  // > 64 tied members
-    if (wave != 0) return true;
+    auto store_u = [&]() __attribute__((always_inline)) {
+        if (sampling && mpos < (uint32_t)kWave) sm.tu[mpos] = u_mine;
+    };
+    if (wave != 0) {
+        store_u();
+        __syncthreads();
+        return true;
+    }
 
     const bool have = lane < total;
     const uint64_t key = have ? sm.tk[lane] : 0ull;
-    const float uu = have ? sm.tu[lane] : 0.5f;
     const uint32_t yk = (uint32_t)(key >> 32);
     const float y = val_of(yk);
     const float lp_min = (prm.min_p > 0.0f) ? log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)
@@ -517,6 +525,9 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     const uint64_t thr = (topp && !abl) ? scale_floor(q32, W) : 0ull;
     const bool removed = keep && topp && (abl ? (C != W) : (C <= thr && C != W));
     const bool kept = keep && !removed;
+    store_u();
+    __syncthreads();
+    const float uu = have ? sm.tu[lane] : 0.5f;
     // race: key bits + 1 (0 = no valid key) reduced as 32-bit maxima; the lowest index wins
     // among equal keys, and the best key of the other lanes is the runner-up
     const float rkey = e / (0.0f - log_det(uu));
@@ -583,22 +594,21 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     //    parameters as scalar loads.
     //    Buffer loads: a row's loads share one lane offset (the iteration and vector go in the
     //    scalar offset), and loads past the end read zeros, so nothing is clamped.
+    //    The row addresses are computed without branches (an absent list gets a zero-sized
+    //    buffer, whatever its address), so that the kernel arguments are read in one batch.
     const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
     const bool has_a = a.adj_ids && a.adjwidth > 0;
-    const int32_t* aidrow = has_a ? a.adj_ids + (size_t)r * a.adjstride : nullptr;
-    const float* avrow = has_a ? a.adj_vals + (size_t)r * a.adjstride : nullptr;
-    const int32_t* prow = has_p ? a.prompt + (size_t)r * a.pstride : nullptr;
-    const int32_t* orow = has_o ? a.output + (size_t)r * a.ostride : nullptr;
-    const __amdgpu_buffer_rsrc_t prs = make_rsrc(has_p ? (const void*)prow : (const void*)row,
-                                                 has_p ? 4u * (uint32_t)a.pwidth : 0u);
-    const __amdgpu_buffer_rsrc_t ors = make_rsrc(has_o ? (const void*)orow : (const void*)row,
-                                                 has_o ? 4u * (uint32_t)a.owidth : 0u);
+    const uint64_t ru = (uint64_t)r;
+    const int32_t* aidrow = reinterpret_cast<const int32_t*>((uint64_t)a.adj_ids + 4u * ru * (uint64_t)a.adjstride);
+    const float* avrow = reinterpret_cast<const float*>((uint64_t)a.adj_vals + 4u * ru * (uint64_t)a.adjstride);
+    const int32_t* prow = reinterpret_cast<const int32_t*>((uint64_t)a.prompt + 4u * ru * (uint64_t)a.pstride);
+    const int32_t* orow = reinterpret_cast<const int32_t*>((uint64_t)a.output + 4u * ru * (uint64_t)a.ostride);
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(prow, has_p ? 4u * (uint32_t)a.pwidth : 0u);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(orow, has_o ? 4u * (uint32_t)a.owidth : 0u);
     const int hp_raw = __builtin_amdgcn_raw_buffer_load_b32(prs, 4u * (uint32_t)tid, 0u, 0);
     const int ho_raw = __builtin_amdgcn_raw_buffer_load_b32(ors, 4u * (uint32_t)tid, 0u, 0);
-    const __amdgpu_buffer_rsrc_t ais = make_rsrc(has_a ? (const void*)aidrow : (const void*)row,
-                                                 has_a ? 4u * (uint32_t)a.adjwidth : 0u);
-    const __amdgpu_buffer_rsrc_t avs = make_rsrc(has_a ? (const void*)avrow : (const void*)row,
-                                                 has_a ? 4u * (uint32_t)a.adjwidth : 0u);
+    const __amdgpu_buffer_rsrc_t ais = make_rsrc(aidrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
+    const __amdgpu_buffer_rsrc_t avs = make_rsrc(avrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
     const int ha_id = __builtin_amdgcn_raw_buffer_load_b32(ais, 4u * (uint32_t)tid, 0u, 0);
     const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
     Slice<T> sl;
@@ -797,11 +807,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     }
     // each wave packs its candidates into the row's arrays as soon as its own stream ends, while
     // other waves are still streaming: the key of y (the processed logit over T; the processed
-    // logit itself for greedy rows), the index and the uniform.  Rows with k <= 64 pack one
-    // 64-bit key per candidate, (key(y) << 32) | index, with the index reversed for greedy rows
-    // so that the largest key is the lowest index at the maximum.  The uniform of each lane's
-    // first candidate is only loaded here; it is stored once the ranks are counted, so that its
-    // latency overlaps the count.
+    // logit itself for greedy rows) and the index.  Rows with k <= 64 pack one 64-bit key per
+    // candidate, (key(y) << 32) | index, with the index reversed for greedy rows so that the
+    // largest key is the lowest index at the maximum; their uniforms are loaded for the 64
+    // largest keys only, once ranked.  Larger k load the uniform of every candidate here (that
+    // of each lane's first candidate is stored once the ranks are counted, so that its latency
+    // overlaps the count).
     const float Tt = prm.T;
     const bool small = k <= kWave;
     float u_first = 0.0f;
@@ -811,46 +822,65 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
         // compacts the buffer: done out of line.  In mode 1 the processed value of each hashed
         // candidate not yet fixed by a compaction replaces its raw value here, found through
         // the presence bits with one LDS read per candidate.
-        cb.filter();
         const uint32_t pmode = sm.pmode;
-        const int nfix = pmode == 1u ? cb.nfix : cb.cnt;
-        if (pmode == 2u) cb.finish();
-        uint32_t b = 0;
-        if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)cb.cnt);
-        const int pbase = __builtin_amdgcn_readlane(b, 0);
         uint32_t ymx = 0u;
-        if (pbase + cb.cnt <= kRowPack) {
-            // e = lane first (its uniform stays in flight), then any further candidates
-            for (int e = lane; e < cb.cnt; e += kWave) {
-                const int32_t ii = sm.cidx[wave][e];
-                uint32_t kx = sm.ckey[wave][e];
-                if (capped) kx = key_of(softcap_det(val_of(kx), a.inv_softcap, a.softcap));
-                if (e >= nfix && rhash_maybe(sm, ii)) {
-                    const int hs = rhash_find(sm, ii);
-                    if (hs >= 0)
-                        kx = key_of(apply_hashed(val_of(kx), sm.hval[hs], sm.hadj[hs], sm.prep,
-                                                 sm.pinv, sm.pfreq, sm.ppres));
-                }
-                const uint32_t ky = sampling ? key_of(val_of(kx) / Tt) : kx;
-                if (small) {
-                    sm.pk64[pbase + e] = ((uint64_t)ky << 32) | (uint32_t)(sampling ? ii : 0x7FFFFFFF - ii);
-                } else {
-                    ymx = ky > ymx ? ky : ymx;
-                    sm.pkey[pbase + e] = ky;
-                    sm.pidx[pbase + e] = ii;
-                }
+        // one candidate: its processed value (cap, then the hashed processors and penalties
+        // unless a compaction has applied them) and its packed entry at slot pos
+        auto pack_one = [&](int pos, uint32_t kx, int32_t ii, bool fixed, bool first)
+            __attribute__((always_inline)) {
+            if (capped) kx = key_of(softcap_det(val_of(kx), a.inv_softcap, a.softcap));
+            if (!fixed && rhash_maybe(sm, ii)) {
+                const int hs = rhash_find(sm, ii);
+                if (hs >= 0)
+                    kx = key_of(apply_hashed(val_of(kx), sm.hval[hs], sm.hadj[hs], sm.prep,
+                                             sm.pinv, sm.pfreq, sm.ppres));
+            }
+            const uint32_t ky = sampling ? key_of(val_of(kx) / Tt) : kx;
+            if (small) {
+                sm.pk64[pos] = ((uint64_t)ky << 32) | (uint32_t)(sampling ? ii : 0x7FFFFFFF - ii);
+            } else {
+                ymx = ky > ymx ? ky : ymx;
+                sm.pkey[pos] = ky;
+                sm.pidx[pos] = ii;
                 if (sampling) {
-                    if (e == lane) {
-                        u_slot = pbase + e;
+                    if (first) {
+                        u_slot = pos;  // loaded below, stored once the ranks are counted
                     } else {
-                        sm.pu[pbase + e] = a.u[(size_t)r * a.ustride + ii];
+                        sm.pu[pos] = a.u[(size_t)r * a.ustride + ii];
                     }
                 }
             }
-            // the first candidate's uniform, loaded outside the loop so that nothing waits for
-            // it before it is stored
-            if (sampling && u_slot >= 0)
-                u_first = a.u[(size_t)r * a.ustride + sm.cidx[wave][lane]];
+        };
+        if (pmode != 2u && cb.cnt <= kWave) {
+            // at most one entry per lane: dropped below the threshold and packed from registers
+            const bool have = lane < cb.cnt;
+            const uint32_t kx = have ? sm.ckey[wave][lane] : 0u;
+            const int32_t ii = have ? sm.cidx[wave][lane] : 0;
+            const bool keep = kx != 0u && kx >= cb.tau;
+            const uint64_t bal = __ballot(keep);
+            uint32_t b = 0;
+            if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)__popcll(bal));
+            const int pbase = __builtin_amdgcn_readlane(b, 0);
+            if (keep && pbase + __popcll(bal) <= kRowPack) {
+                pack_one(pbase + lane_prefix(bal), kx, ii, pmode == 0u || lane < cb.nfix, true);
+                if (sampling && !small) u_first = a.u[(size_t)r * a.ustride + ii];
+            }
+        } else {
+            cb.filter();
+            const int nfix = pmode == 1u ? cb.nfix : cb.cnt;
+            if (pmode == 2u) cb.finish();
+            uint32_t b = 0;
+            if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)cb.cnt);
+            const int pbase = __builtin_amdgcn_readlane(b, 0);
+            if (pbase + cb.cnt <= kRowPack) {
+                // e = lane first (its uniform stays in flight), then any further candidates
+                for (int e = lane; e < cb.cnt; e += kWave)
+                    pack_one(pbase + e, sm.ckey[wave][e], sm.cidx[wave][e], e < nfix, e == lane);
+                // the first candidate's uniform, loaded outside the loop so that nothing waits
+                // for it before it is stored
+                if (sampling && !small && u_slot >= 0)
+                    u_first = a.u[(size_t)r * a.ustride + sm.cidx[wave][lane]];
+            }
         }
         if (!small) {
             ymx = wave_max_u32(ymx);
@@ -865,7 +895,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
     const int total = (int)sm.npack;
     if (total > kRowPack) return false;  // too many candidates
     // the single-wave finish checks the status and the thresholds once its count is running
-    if (small) return row_tail_small(a, sm, r, prm, k, total, seed, sampling, u_first, u_slot);
+    if (small) return row_tail_small(a, sm, r, prm, k, total, seed, sampling);
     if (sm.status != 0u) return false;  // tie or hash overflow
     const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
     // fewer than k candidates can only be exact when no threshold was used
@@ -1074,8 +1104,7 @@ __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
 
 template <typename T>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(KArgs a) {
-    const int r = blockIdx.x;
-    if (r >= a.B) return;
+    const int r = blockIdx.x;  // the grid is exactly B workgroups
     if (row_fast<T>(a, g_row_sh.f, r)) return;
     __syncthreads();
     row_general<T>(r, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr());
