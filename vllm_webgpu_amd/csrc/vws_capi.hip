@@ -14,7 +14,7 @@
 namespace vws {
 template <typename T> __global__ void fast_kernel(KArgs);
 template <typename T> __global__ void general_kernel(KArgs);
-template <typename T> __global__ void row_kernel(KArgs);
+template <typename T> __global__ void row_kernel(const void*, int64_t, int, int, KArgs);
 template <typename T> __global__ void argmax_kernel(const T*, int64_t, int, int32_t*);
 template <typename T>
 __global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, float*, float*);
@@ -276,9 +276,9 @@ int vws_sample(const vws_sample_args* a) {
     hipStream_t s = (hipStream_t)a->stream;
     const int ps = prof_start(s, VWS_KERNEL_SAMPLE);
     if (a->dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(row_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
+        hipLaunchKernelGGL(row_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
     else
-        hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k);
+        hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
     prof_stop(s, ps);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();

@@ -577,40 +577,25 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
 // Serves greedy and top-k rows; returns false when the row must take the general path (nothing
 // has been written for it then).
 template <typename T>
-__device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
+__device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, const void* logits,
+                                         int64_t lstride, int V) {
     constexpr int NT = kRowThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int U = 32 / VEC;  // 16-byte loads in flight per lane per iteration
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int V = a.V;
-    const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+    const T* row = reinterpret_cast<const T*>(logits) + (size_t)r * lstride;
     // position of this lane in the workgroup, recomputed where the streaming loop needs it
     auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
 
-    // 1. loads in the order they are consumed, none behind a branch (a load that only some
-    //    paths issue makes the wait for everything before it conservative):
-    //    history ids (clamped to the row width), the first two iterations of logits, then the
-    //    parameters as scalar loads.
+    // 1. loads, none behind a branch (a load that only some paths issue makes the wait for
+    //    everything before it conservative): the first iteration of logits (it needs only the
+    //    preloaded arguments), the history ids and processor lists (zero-sized buffers when
+    //    absent), the second iteration, then the parameters as scalar loads.
     //    Buffer loads: a row's loads share one lane offset (the iteration and vector go in the
     //    scalar offset), and loads past the end read zeros, so nothing is clamped.
     //    The row addresses are computed without branches (an absent list gets a zero-sized
     //    buffer, whatever its address), so that the kernel arguments are read in one batch.
-    const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
-    const bool has_a = a.adj_ids && a.adjwidth > 0;
-    const uint64_t ru = (uint64_t)r;
-    const int32_t* aidrow = reinterpret_cast<const int32_t*>((uint64_t)a.adj_ids + 4u * ru * (uint64_t)a.adjstride);
-    const float* avrow = reinterpret_cast<const float*>((uint64_t)a.adj_vals + 4u * ru * (uint64_t)a.adjstride);
-    const int32_t* prow = reinterpret_cast<const int32_t*>((uint64_t)a.prompt + 4u * ru * (uint64_t)a.pstride);
-    const int32_t* orow = reinterpret_cast<const int32_t*>((uint64_t)a.output + 4u * ru * (uint64_t)a.ostride);
-    const __amdgpu_buffer_rsrc_t prs = make_rsrc(prow, has_p ? 4u * (uint32_t)a.pwidth : 0u);
-    const __amdgpu_buffer_rsrc_t ors = make_rsrc(orow, has_o ? 4u * (uint32_t)a.owidth : 0u);
-    const int hp_raw = __builtin_amdgcn_raw_buffer_load_b32(prs, 4u * (uint32_t)tid, 0u, 0);
-    const int ho_raw = __builtin_amdgcn_raw_buffer_load_b32(ors, 4u * (uint32_t)tid, 0u, 0);
-    const __amdgpu_buffer_rsrc_t ais = make_rsrc(aidrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
-    const __amdgpu_buffer_rsrc_t avs = make_rsrc(avrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
-    const int ha_id = __builtin_amdgcn_raw_buffer_load_b32(ais, 4u * (uint32_t)tid, 0u, 0);
-    const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
     Slice<T> sl;
     sl.init(row, 0, V);
     const int nbody = sl.nbody;
@@ -628,7 +613,25 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r) {
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
+    // the first iteration depends only on the preloaded arguments: issued before anything
+    // waits for the rest of the kernel arguments
     load_iter(A, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
+    const bool has_a = a.adj_ids && a.adjwidth > 0;
+    const uint64_t ru = (uint64_t)r;
+    const int32_t* aidrow = reinterpret_cast<const int32_t*>((uint64_t)a.adj_ids + 4u * ru * (uint64_t)a.adjstride);
+    const float* avrow = reinterpret_cast<const float*>((uint64_t)a.adj_vals + 4u * ru * (uint64_t)a.adjstride);
+    const int32_t* prow = reinterpret_cast<const int32_t*>((uint64_t)a.prompt + 4u * ru * (uint64_t)a.pstride);
+    const int32_t* orow = reinterpret_cast<const int32_t*>((uint64_t)a.output + 4u * ru * (uint64_t)a.ostride);
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(prow, has_p ? 4u * (uint32_t)a.pwidth : 0u);
+    const __amdgpu_buffer_rsrc_t ors = make_rsrc(orow, has_o ? 4u * (uint32_t)a.owidth : 0u);
+    const int hp_raw = __builtin_amdgcn_raw_buffer_load_b32(prs, 4u * (uint32_t)tid, 0u, 0);
+    const int ho_raw = __builtin_amdgcn_raw_buffer_load_b32(ors, 4u * (uint32_t)tid, 0u, 0);
+    const __amdgpu_buffer_rsrc_t ais = make_rsrc(aidrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
+    const __amdgpu_buffer_rsrc_t avs = make_rsrc(avrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
+    const int ha_id = __builtin_amdgcn_raw_buffer_load_b32(ais, 4u * (uint32_t)tid, 0u, 0);
+    const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
     load_iter(Bq, 1);
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
@@ -1103,14 +1106,15 @@ __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(kRowThreads) void row_kernel(KArgs a) {
+__global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
+                                                          int pad, KArgs a) {
     const int r = blockIdx.x;  // the grid is exactly B workgroups
-    if (row_fast<T>(a, g_row_sh.f, r)) return;
+    if (row_fast<T>(a, g_row_sh.f, r, logits, lstride, V)) return;
     __syncthreads();
-    row_general<T>(r, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr());
+    row_general<T>(r, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u);
 }
 
-template __global__ void row_kernel<float>(KArgs);
-template __global__ void row_kernel<uint16_t>(KArgs);
+template __global__ void row_kernel<float>(const void*, int64_t, int, int, KArgs);
+template __global__ void row_kernel<uint16_t>(const void*, int64_t, int, int, KArgs);
 
 }  // namespace vws
