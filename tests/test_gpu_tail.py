@@ -100,3 +100,16 @@ def test_small_k_with_penalties(cuda):
             k=np.array([50, 50, 64, 1, 10, 64, 65, 20], np.int32), p=0.9, mp=0.05,
             rep=1.3, pres=0.4, freq=0.2, hist=hist, seed=8)
     _check(cuda, w)
+
+
+@pytest.mark.parametrize("k", [2, 10, 50, 64, 100])
+def test_seed_above_kth(cuda, k):
+    """Spikes packed into the first iteration (the seed's sample) push the seed above the row's
+    k-th value: fewer than k candidates pass it, and the row must be finished exactly anyway."""
+    rng = np.random.default_rng(200 + k)
+    B, V = 4, 128256
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    for b in range(B):
+        n = max(1, k - 1 - b)  # fewer spikes than k
+        x[b, rng.choice(20000, n, replace=False)] = 40.0 + rng.random(n).astype(np.float32)
+    _check(cuda, _wl(f"seed_high_k{k}", x, 0.9, k=k, p=0.95, seed=9))

@@ -692,9 +692,15 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         for (int i = NT + tid; i < prm.na; i += NT) add(aidrow[i], avrow[i]);
     }
 
-    // 3. seed threshold from the first iteration
+    // 3. seed threshold from the first iteration: the m-th largest lane maximum of the sample.
+    //    The sample holds lambda = (k - 1) * sample / V elements above the row's k-th value on
+    //    average (about Poisson); m = ceil(lambda + 5 sqrt(lambda) + 3) puts the seed above
+    //    the k-th value (the row then takes the general path) with probability at most 1.2e-6
+    //    for any lambda, and keeps
+    //    about m * V / sample candidates (k = 1: the sample's maximum, never above the k-th).
     const int sample = nbody > 0 ? min(NT * U, nbody) * VEC : 0;
-    const int m_seed = sample > 0 ? (int)(((int64_t)3 * k * sample + V - 1) / V) : 0;
+    const float lam = (float)(k - 1) * (float)sample / (float)V;
+    const int m_seed = sample > 0 ? (k > 1 ? (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f) : 1) : 0;
     const bool seeded = sample > 0 && m_seed <= kRowWaves * kSeedPerWave;
     // m <= 64: the pool is every wave's 4 largest lane maxima, and every wave selects the m-th
     // largest of it for itself; otherwise the 16 largest of every wave, selected by wave 0
