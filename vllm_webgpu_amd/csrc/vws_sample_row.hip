@@ -696,8 +696,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     //    The sample holds lambda = (k - 1) * sample / V elements above the row's k-th value on
     //    average (about Poisson); m = ceil(lambda + 5 sqrt(lambda) + 3) puts the seed above
     //    the k-th value (the row then takes the general path) with probability at most 1.2e-6
-    //    for any lambda, and keeps
-    //    about m * V / sample candidates (k = 1: the sample's maximum, never above the k-th).
+    //    for any lambda, and keeps about m * V / sample candidates (k = 1: the sample's
+    //    maximum, never above the k-th).
     const int sample = nbody > 0 ? min(NT * U, nbody) * VEC : 0;
     const float lam = (float)(k - 1) * (float)sample / (float)V;
     const int m_seed = sample > 0 ? (k > 1 ? (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f) : 1) : 0;
