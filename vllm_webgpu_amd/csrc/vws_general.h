@@ -328,6 +328,30 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             f(v1, i1);
         }
     };
+    // the same visit for the race passes, with the chunks' uniforms loaded together with their
+    // logits (a race pass otherwise waits for one uniform load per racing survivor)
+    auto for_rows_u = [&](auto&& f) {
+        for (int it = 0; it < nit; ++it) {
+            float v0[VEC], v1[VEC], u0[VEC], u1[VEC];
+            const int c0 = it * 2 * NT + tid;
+            const int i0 = sl.load(c0, v0);
+            const int i1 = sl.load(c0 + NT, v1);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                u0[j] = (urow && i0 + j < V) ? urow[i0 + j] : 0.5f;
+                u1[j] = (urow && i1 + j < V) ? urow[i1 + j] : 0.5f;
+            }
+            if (a.softcap > 0.0f) {  // the model's output is the capped logit
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    v0[j] = softcap_det(v0[j], a.inv_softcap, a.softcap);
+                    v1[j] = softcap_det(v1[j], a.inv_softcap, a.softcap);
+                }
+            }
+            f(v0, i0, u0);
+            f(v1, i1, u1);
+        }
+    };
 
     const bool sampling = !prm.greedy;
     const int k = prm.k;
@@ -502,7 +526,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             }
         } else if (!topp) {
             // no top-p: every survivor of top-k and min-p races
-            for_rows([&](float* v, int i0) {
+            for_rows_u([&](float* v, int i0, const float* uc) {
                 finalize(v, i0);
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
@@ -510,7 +534,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     if (survivor(v[j], y, d)) {
                         const float e = exp_det(d);
                         if (share_lse) s0_shared += (double)e;
-                        race.add(e, key_of(y), i0 + j, urow[i0 + j]);
+                        race.add(e, key_of(y), i0 + j, uc[j]);
                     } else if (share_lse && v[j] == v[j]) {
                         s0_shared += (double)exp_det(d);
                     }
@@ -548,7 +572,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             if (tid == 0) sm.gcount = 0u;
             __syncthreads();
             uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-            for_rows([&](float* v, int i0) {
+            for_rows_u([&](float* v, int i0, const float* uc) {
                 finalize(v, i0);
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
@@ -556,7 +580,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     if (!survivor(v[j], y, d)) continue;
                     const int b = bucket_of(d);
                     if (b < bstar) {
-                        race.add(exp_det(d), key_of(y), i0 + j, urow[i0 + j]);
+                        race.add(exp_det(d), key_of(y), i0 + j, uc[j]);
                     } else if (b == bstar) {
                         const uint32_t ky = key_of(y);
                         kmin = min(kmin, ky);
@@ -665,7 +689,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                 // tie rule)
                 if (tid == 0) sm.gcount = 0u;
                 __syncthreads();
-                for_rows([&](float* v, int i0) {
+                for_rows_u([&](float* v, int i0, const float* uc) {
                     finalize(v, i0);
 #pragma unroll
                     for (int j = 0; j < VEC; ++j) {
@@ -674,10 +698,10 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                         const uint32_t ky = key_of(y);
                         const int ix = i0 + j;
                         if (ky > khi) {
-                            race.add(exp_det(d), ky, ix, urow[ix]);
+                            race.add(exp_det(d), ky, ix, uc[j]);
                         } else if (ky >= klo) {
                             if (tie_rule) {
-                                if ((uint32_t)ix >= idx_thr) race.add(exp_det(d), ky, ix, urow[ix]);
+                                if ((uint32_t)ix >= idx_thr) race.add(exp_det(d), ky, ix, uc[j]);
                             } else {
                                 const uint32_t pos = atomicAdd(&sm.gcount, 1u);
                                 if (pos < (uint32_t)kGatherCap) sm.u.gather[pos] = ((uint64_t)ky << 32) | (uint32_t)ix;
