@@ -113,3 +113,42 @@ def test_seed_above_kth(cuda, k):
         n = max(1, k - 1 - b)  # fewer spikes than k
         x[b, rng.choice(20000, n, replace=False)] = 40.0 + rng.random(n).astype(np.float32)
     _check(cuda, _wl(f"seed_high_k{k}", x, 0.9, k=k, p=0.95, seed=9))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_unaligned_strided_rows(cuda, dtype):
+    """Rows of a strided view whose starts are not 16-byte aligned (odd offset and stride, odd
+    V): the unaligned head and tail of every row go through the edge loads, on the single-pass
+    path (k <= 64 and k > 64), greedy rows and the multi-pass path (top-k off)."""
+    import torch
+
+    from vllm_webgpu_amd import ops
+    from vllm_webgpu_amd.workloads import _bf16_bits
+
+    rng = np.random.default_rng(31)
+    B, V, pad = 8, 50001, 6
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    x[:, 0] = 30.0 + np.arange(B)        # maxima in the unaligned head ...
+    x[1::2, V - 1] = 60.0                # ... and in the tail of odd rows
+    ks = np.array([50, 1, 64, 65, 0, 200, 5, 0], np.int32)
+    T = np.array([0.8, 0.0, 1.1, 0.7, 0.9, 1.0, 0.0, 1.3], np.float32)
+    w = _wl(f"strided_{dtype}", _bf16_bits(x) if dtype == "bf16" else x, T, k=ks, p=0.9, seed=12,
+            dtype=dtype)
+    ref = oracle_run(w)
+    if dtype == "bf16":
+        wide = np.zeros((B, V + pad), np.uint16)
+        wide[:, 3:3 + V] = w.logits
+        base = torch.from_numpy(wide.view(np.int16)).to(cuda).view(torch.bfloat16)
+    else:
+        wide = np.zeros((B, V + pad), np.float32)
+        wide[:, 3:3 + V] = w.logits
+        base = torch.from_numpy(wide).to(cuda)
+    logits = base[:, 3:3 + V]
+    assert logits.stride(0) == V + pad and logits.data_ptr() % 16 != 0
+    res = ops.sample(logits, temperature=torch.from_numpy(w.temperature),
+                     top_k=torch.from_numpy(w.top_k), top_p=torch.from_numpy(w.top_p),
+                     uniforms=torch.from_numpy(w.uniforms).to(cuda))
+    torch.cuda.synchronize()
+    gpu = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
+               n_kept=res.num_kept.cpu().numpy())
+    assert_same(gpu, ref, w.name)
