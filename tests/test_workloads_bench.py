@@ -41,3 +41,18 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     msg = json.loads(r.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+def test_bench_reads_the_committed_traffic():
+    """roofline.traffic comes from the committed rocprofv3 summary of the headline workload: the
+    summary must name the sampling kernel and give a per-launch figure near the algorithmic
+    bytes (no re-reads)."""
+    import bench
+    from vllm_webgpu_amd import workloads as W
+
+    t = bench.pmc_traffic_bytes(3)
+    assert t is not None
+    w = W.config(3)
+    alg = W.algorithmic_bytes(w, np.full(w.shape[0], 24))
+    assert 0.95 * alg < t < 1.15 * alg
+    assert bench.pmc_traffic_bytes(2) is None
