@@ -46,7 +46,9 @@ def build_args(lib_mod, logits, T, K, P, MP, R, PR, FR, hist, U, out, flags, nke
     a.batch, a.vocab = B, V
     a.dtype = lib_mod.DTYPE_BF16 if logits.dtype == torch.bfloat16 else lib_mod.DTYPE_F32
     a.logits, a.logits_row_stride = logits.data_ptr(), logits.stride(0)
-    a.temperature, a.top_k, a.top_p, a.min_p = T.data_ptr(), K.data_ptr(), P.data_ptr(), MP.data_ptr()
+    all_greedy = bool((T < 1e-5).all())  # greedy batches pass no temperature (and no uniforms)
+    a.temperature = None if all_greedy else T.data_ptr()
+    a.top_k, a.top_p, a.min_p = K.data_ptr(), P.data_ptr(), MP.data_ptr()
     a.repetition_penalty, a.presence_penalty, a.frequency_penalty = R.data_ptr(), PR.data_ptr(), FR.data_ptr()
     if hist is not None:
         a.output_ids, a.output_row_stride, a.output_width = hist.data_ptr(), hist.stride(0), hist.shape[1]
@@ -90,6 +92,43 @@ def cpu_baseline(w, rows: int, iters: int):
                         f"(vLLM-v1 Sampler op sequence on torch CPU tensors), median of {iters} "
                         f"after 3 warm-up, torch threads={cores}"),
                 seconds_per_iter=med)
+
+
+def cpu_reference_ops(w, rows: int, iters: int):
+    """The reference's own host arithmetic, restated in numpy, timed on `rows` rows of the
+    workload: greedy ``logits.argmax(axis=-1)`` over the batch (vllm_webgpu/v1/model_runner.py:145)
+    and the CLI's float64 temperature sampler per row (run_inference.py:386-390: x / T - max, exp,
+    normalise, ``np.random.choice``).  Single-threaded numpy, as the reference runs them."""
+    x = w.logits_f32()[:rows]
+    T = float(w.temperature[0]) if float(w.temperature[0]) > 0 else 1.0
+    rng = np.random.RandomState(0)
+
+    def greedy():
+        return x.argmax(axis=-1)
+
+    def cli_sampler():
+        out = np.empty(x.shape[0], np.int64)
+        for b in range(x.shape[0]):
+            z = x[b].astype(np.float64) / T
+            z = np.exp(z - z.max())
+            out[b] = rng.choice(z.shape[0], p=z / z.sum())
+        return out
+
+    res = []
+    for name, fn, cite in (("numpy greedy argmax", greedy, "vllm_webgpu/v1/model_runner.py:145"),
+                           ("numpy float64 temperature sampler", cli_sampler,
+                            "run_inference.py:386-390")):
+        fn()
+        times = []
+        for _ in range(iters):
+            t0 = time.perf_counter_ns()
+            fn()
+            times.append((time.perf_counter_ns() - t0) * 1e-9)
+        med = float(np.median(times))
+        res.append(dict(value=rows / med, unit="rows/s", cores=1, kind="port", op=name,
+                        sample=f"{rows} rows of {w.name} (V={w.shape[1]}), median of {iters}, "
+                               f"restates {cite}"))
+    return res
 
 
 def pmc_traffic_bytes(config: int):
@@ -187,14 +226,44 @@ def main():
     ref = O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids,
                    num_logprobs=w.num_logprobs)
     mism = int((ref["token"] != gpu_tok).sum())
-    log(f"parity vs oracle: {mism} token mismatches of {B} rows; "
-        f"|S| mean {gpu_kept.mean():.1f}; near-tie rows {int(((gpu_flags & 3) != 0).sum())}")
-    if mism:
-        print(json.dumps({"error": f"parity failure: {mism} token mismatches"}), flush=True)
+    parity = {"rows": int(B), "token_mismatches": mism,
+              "flag_mismatches": int(((ref["flags"] & 0xFF) != (gpu_flags & 0xFF)).sum()),
+              "kept_mismatches": int((ref["n_kept"] != gpu_kept).sum()),
+              "checker": "oracle/vws_oracle.c on the same inputs (set 0)"}
+    near_tie = {"top_p": int(((gpu_flags & 1) != 0).sum()), "race": int(((gpu_flags & 2) != 0).sum())}
+    if w.return_probs:
+        # C1 also returns the temperature-1 probabilities (vws_softmax)
+        probs, rmax, _ = ops.softmax(sets[0][0], torch.ones(B))
+        torch.cuda.synchronize()
+        rp, rrm, _ = O.softmax(w.logits_f32(), 1.0)
+        rel = np.abs(probs.cpu().numpy() - rp) / np.maximum(rp, 1e-30)
+        parity["probs_max_rel_err"] = float(rel[rp > 1e-30].max())
+        parity["row_max_mismatches"] = int((rmax.cpu().numpy() != rrm).sum())
+    log(f"parity vs oracle: {parity}; |S| mean {gpu_kept.mean():.1f}; near-tie rows {near_tie}")
+    if mism or parity["flag_mismatches"] or parity["kept_mismatches"]:
+        print(json.dumps({"error": f"parity failure: {parity}"}), flush=True)
         sys.exit(1)
 
+    # one step: vws_sample over the batch; C1 also returns its softmax probabilities
+    probs_out = None
+    if w.return_probs:
+        probs_out = torch.empty((B, V), dtype=torch.float32, device=dev)
+        pmax = torch.empty(B, dtype=torch.float32, device=dev)
+        plsum = torch.empty(B, dtype=torch.float32, device=dev)
+        ones = torch.ones(B, dtype=torch.float32, device=dev)
+        softmax = L.vws_softmax
+
+        def step(i):
+            lg = sets[i % len(sets)][0]
+            sample(ctypes.byref(argv[i % len(argv)]))
+            softmax(lg.data_ptr(), _lib.DTYPE_F32, B, V, lg.stride(0), ones.data_ptr(),
+                    probs_out.data_ptr(), pmax.data_ptr(), plsum.data_ptr(), stream.cuda_stream)
+    else:
+        def step(i):
+            sample(ctypes.byref(argv[i % len(argv)]))
+
     for i in range(args.warmup):
-        _lib.check(sample(ctypes.byref(argv[i % len(argv)])))
+        step(i)
     torch.cuda.synchronize()
 
     # timed region: exactly `steps` calls, bracketed by synchronisation
@@ -206,7 +275,7 @@ def main():
     t0 = time.perf_counter()
     ev0.record(stream)
     for i in range(args.steps):
-        sample(ctypes.byref(argv[i % len(argv)]))
+        step(i)
     ev1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -221,7 +290,7 @@ def main():
     npair = min(args.steps, 500)
     ops.profile_begin(4 * npair + 8)
     for i in range(npair):
-        sample(ctypes.byref(argv[i % len(argv)]))
+        step(i)
     prof = ops.profile_end()
 
     alg_bytes = W.algorithmic_bytes(w, gpu_kept)
@@ -241,10 +310,15 @@ def main():
         log("calibration copy: 536870912 bytes read + 536870912 bytes written")
 
     cpu = None
+    cpu_ref_ops = None
     if not args.no_cpu_baseline:
         t = time.time()
-        cpu = cpu_baseline(w, args.cpu_rows, args.cpu_iters)
+        cpu = cpu_baseline(w, min(args.cpu_rows, B), args.cpu_iters)
         log(f"cpu baseline {cpu['value']:.1f} rows/s on {cpu['cores']} cores ({time.time() - t:.1f}s)")
+        t = time.time()
+        cpu_ref_ops = cpu_reference_ops(w, min(32, B), 5)
+        log(f"reference numpy ops: {[round(c['value'], 1) for c in cpu_ref_ops]} rows/s "
+            f"({time.time() - t:.1f}s)")
 
     res = {
         "metric": METRIC if args.config == 3 else f"sampled rows/sec + HBM GB/s (% peak), {w.name}",
@@ -270,7 +344,9 @@ def main():
         "hbm_frac_end_to_end": gbps_e2e / PEAK_HBM_GBPS,
         "algorithmic_bytes_per_step": alg_bytes,
         "mean_survivors": float(gpu_kept.mean()),
-        "kernel_us": {"sample": kern_ms * 1e3},
+        "parity": parity,
+        "near_tie_rows": near_tie,
+        "kernel_us": {"sample" if probs_out is None else "sample+softmax": kern_ms * 1e3},
         "kernel_us_event_pairs": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
@@ -279,6 +355,7 @@ def main():
                        else "vws::row_kernel<float>"),
         },
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline_reference_ops": cpu_ref_ops,
     }
     print(json.dumps(res), flush=True)
 

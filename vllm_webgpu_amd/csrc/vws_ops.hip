@@ -153,6 +153,11 @@ __global__ __launch_bounds__(kOpThreads) void penalties_kernel(KArgs a, float* l
         const int t = (int)kk - 1;
         row[t] = apply_penalty(row[t], (v >> 31) != 0u, v & 0x7FFFFFFFu, rep, inv_rep, freq, pres);
     }
+    // The workspace is left as it was found (zeros): the top-k operation keeps its per-row part
+    // counters at the start of the same buffer, and a non-zero counter there would stop its
+    // last-part election from ever firing.
+    __syncthreads();
+    for (int i = threadIdx.x; i < hs; i += kOpThreads) { hkey[i] = 0u; hval[i] = 0u; }
 }
 
 // Hash of f(x) over every fp32 x whose order key lies in [klo, khi]; same accumulation as the
