@@ -153,6 +153,17 @@ int vws_validate_sample_args(const vws_sample_args* args);
  * in oracle/ for the same inputs. */
 int vws_sample(const vws_sample_args* args);
 
+/* vws_sample without a caller workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart
+ * in the reference.  `workspace` and `workspace_bytes` are ignored: the scratch is a static
+ * device array of VWS_NOALLOC_SCRATCH_BYTES per GPU, looked up and cleared on the first call on
+ * each device and held until the process ends.  Batches whose vws_sample_workspace_size exceeds
+ * it are rejected with VWS_ERR_LIMIT.  Every call on one GPU shares that GPU's scratch: calls
+ * that overlap on one GPU (different streams, no ordering between them) race; calls ordered on
+ * one stream do not.  Nothing is allocated, on the host or the device. */
+#define VWS_NOALLOC_SCRATCH_BYTES (16 << 20)
+int vws_sample_noalloc(const vws_sample_args* args);
+
 /* Greedy argmax of each row (lowest index on ties; NaN never selected). */
 int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,
                int64_t row_stride, int32_t* out_ids, void* stream);

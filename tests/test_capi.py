@@ -163,3 +163,15 @@ def test_errors_raise_with_library_text(L):
     assert _status(L, _args(L, dtype=9)) != 0
     with pytest.raises(_lib.VwsError, match="unsupported logits dtype 9"):
         _lib.check(_lib.ERR_UNSUPPORTED_DTYPE)
+
+
+def test_noalloc_checks_before_touching_the_device(L):
+    """vws_sample_noalloc rejects bad arguments and batches beyond its static scratch on the
+    host, before any device call (this test runs without a GPU)."""
+    a = _args(L, output_ids=FAKE, output_width=2048, output_row_stride=2048, batch=4096)
+    assert L.vws_sample_workspace_size(4096, 1000, 2048) > _lib.NOALLOC_SCRATCH_BYTES
+    assert L.vws_sample_noalloc(ctypes.byref(a)) == _lib.ERR_LIMIT
+    assert "static scratch" in _lib.last_error()
+    assert L.vws_sample_noalloc(ctypes.byref(_args(L, **HIST, logits=None))) == _lib.ERR_INVALID_ARGUMENT
+    assert "logits is NULL" in _lib.last_error()
+    assert L.vws_sample_noalloc(ctypes.byref(_args(L, **HIST, struct_size=8))) == _lib.ERR_INVALID_ARGUMENT

@@ -34,10 +34,12 @@ FLAG_GENERAL_PATH = 0x100
 MAX_VOCAB = 1 << 19
 MAX_LOGPROBS = 64
 TOPK_MAX = 256
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 EXPORTED = (
     "vws_abi_version", "vws_last_error", "vws_sample_workspace_size", "vws_workspace_init",
-    "vws_validate_sample_args", "vws_sample", "vws_argmax", "vws_topk_workspace_size",
+    "vws_validate_sample_args", "vws_sample", "vws_sample_noalloc", "vws_argmax",
+    "vws_topk_workspace_size",
     "vws_topk", "vws_softmax", "vws_apply_penalties", "vws_math_selftest",
     "vws_profile_begin", "vws_profile_end",
 )
@@ -96,6 +98,8 @@ def _declare(L):
     L.vws_validate_sample_args.argtypes = [ctypes.POINTER(SampleArgs)]
     L.vws_sample.restype = ctypes.c_int
     L.vws_sample.argtypes = [ctypes.POINTER(SampleArgs)]
+    L.vws_sample_noalloc.restype = ctypes.c_int
+    L.vws_sample_noalloc.argtypes = [ctypes.POINTER(SampleArgs)]
     L.vws_argmax.restype = ctypes.c_int
     L.vws_argmax.argtypes = [_P, _I32, _I32, _I32, _I64, _P, _P]
     L.vws_topk_workspace_size.restype = _SZ

@@ -25,6 +25,11 @@ __global__ void fill_u32_kernel(uint32_t*, size_t, uint32_t);
 
 using namespace vws;
 
+// Static device scratch of vws_sample_noalloc (one copy per GPU, held until the process ends).
+// Host code never uses this name as an address: the per-device address comes from
+// hipGetSymbolAddress (scratch_address below) and only that pointer is handed to kernels.
+static __device__ __align__(256) unsigned char scratch[VWS_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_err;
@@ -97,6 +102,34 @@ void choose_parts(int B, int V, int esize, int* S, int* part_len) {
 }
 
 int esize_of(int dtype) { return dtype == VWS_DTYPE_BF16 ? 2 : 4; }
+
+// Per-device address of `scratch`, looked up once per device with that device current and
+// cleared once by a fill kernel on the caller's stream (the kernels also clear what they use).
+struct ScratchSlot {
+    void* ptr = nullptr;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[64];
+
+int scratch_address(hipStream_t s, void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return fail(VWS_ERR_HIP, "vws_sample_noalloc: no current HIP device (or device index >= 64)");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchSlot& slot = g_scratch[dev];
+    if (!slot.ptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(VWS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        const size_t n = VWS_NOALLOC_SCRATCH_BYTES / 4;
+        hipLaunchKernelGGL(fill_u32_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint32_t*>(p), n, 0u);
+        if (int st = check_launch("vws_sample_noalloc (scratch clear)")) return st;
+        slot.ptr = p;
+    }
+    *out = slot.ptr;
+    return VWS_OK;
+}
 
 // ---- optional per-kernel event timing (vws_profile_begin / vws_profile_end) ----
 struct Profiler {
@@ -282,6 +315,35 @@ int vws_sample(const vws_sample_args* a) {
     prof_stop(s, ps);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();
+}
+
+int vws_sample_noalloc(const vws_sample_args* a) {
+    if (!a) return fail(VWS_ERR_INVALID_ARGUMENT, "args is NULL");
+    if (a->struct_size != sizeof(vws_sample_args))
+        return fail(VWS_ERR_INVALID_ARGUMENT, "struct_size %u != %zu (ABI mismatch)", a->struct_size, sizeof(vws_sample_args));
+    if (a->batch < 1 || a->vocab < 1)
+        return validate_sample(a);  // reports the shape error
+    const int hw = sample_history_width(a);
+    if (hw < 0) return validate_sample(a);
+    const size_t need = ws_layout(a->batch, a->vocab, hw, false).total;
+    if (need > (size_t)VWS_NOALLOC_SCRATCH_BYTES)
+        return fail(VWS_ERR_LIMIT,
+                    "vws_sample_noalloc: this batch needs %zu bytes of scratch (batch %d, history width %d); "
+                    "the static scratch holds %zu (use vws_sample with a caller workspace)",
+                    need, a->batch, hw, (size_t)VWS_NOALLOC_SCRATCH_BYTES);
+    vws_sample_args b = *a;
+    b.workspace = nullptr;
+    b.workspace_bytes = 0;
+    if (need) {
+        // arguments first (host only), so a bad call touches no device state
+        b.workspace = reinterpret_cast<void*>(uintptr_t(256));
+        b.workspace_bytes = VWS_NOALLOC_SCRATCH_BYTES;
+        if (int st = validate_sample(&b)) return st;
+        void* p = nullptr;
+        if (int st = scratch_address((hipStream_t)a->stream, &p)) return st;
+        b.workspace = p;
+    }
+    return vws_sample(&b);
 }
 
 int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
