@@ -241,3 +241,45 @@ def test_async_output_matches_sync(cuda):
             steps.append((res.sampled_token_ids, res.logprobs.logprob_token_ids))
         outs.append(steps)
     assert outs[0] == outs[1]
+
+
+def test_async_next_step_before_get_output(cuda):
+    """execute_model of step N+1 runs before get_output() of step N: the model sees the same
+    inputs and positions, and the steps sample the same tokens, as in the synchronous loop."""
+    V = 1024
+    runs = []
+    for overlap in (False, True):
+        model = _FakeModel(V, cuda)
+        seen = []
+        fwd = model.forward
+
+        def forward(input_ids, positions, so, fwd=fwd, seen=seen):
+            seen.append((input_ids.cpu().tolist(), positions.cpu().tolist()))
+            return fwd(input_ids, positions, so)
+
+        model.forward = forward
+        runner = ROCmModelRunner(None, cuda, model, max_num_reqs=4, max_prompt_len=8,
+                                 max_output_len=8)
+        params = {"a": _sp(temperature=0.7, top_k=10, seed=41, repetition_penalty=1.3),
+                  "b": _sp(temperature=0.0, presence_penalty=0.5, frequency_penalty=0.2)}
+        pending, tokens = [], []
+        for step in range(4):
+            so = NS(scheduled_new_reqs=[NS(req_id=r, prompt_token_ids=[1, 2], sampling_params=p)
+                                        for r, p in params.items()] if step == 0 else [],
+                    finished_req_ids=set(), num_scheduled_tokens={"a": 1, "b": 1})
+            runner.execute_model(so)
+            if overlap and pending:
+                tokens.append(pending.pop().get_output().sampled_token_ids)
+            res = runner.sample_tokens(None, async_output=overlap)
+            if overlap:
+                pending.append(res)
+            else:
+                tokens.append(res.sampled_token_ids)
+        if pending:
+            tokens.append(pending.pop().get_output().sampled_token_ids)
+        runs.append((tokens, seen))
+    assert runs[0] == runs[1]
+    # step 1's inputs are step 0's sampled ids, positions advance by one per step
+    (tok, seen) = runs[0]
+    assert seen[1][0] == [t[0] for t in tok[0]] and seen[1][1] == [2, 2]
+    assert [p for _, p in seen] == [[1, 1], [2, 2], [3, 3], [4, 4]]

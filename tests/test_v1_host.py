@@ -95,6 +95,26 @@ def test_input_batch_append_and_slot_reuse():
         b.add_request("c", [1], sp())              # duplicate id
 
 
+def test_input_batch_decode_inputs_from_device_tables():
+    """The next step's inputs come from the device tables and the sampled-step count, not from
+    the host lists (which lag while a step's output is in flight)."""
+    b = InputBatch(3, 4, 2, V, torch.device("cpu"))
+    b.add_request("a", [5, 6, 7], sp())
+    b.add_request("b", [9], sp())
+    b.add_request("e", [], sp())
+    ids, pos = b.decode_inputs(["a", "b", "e"])
+    assert ids.dtype == torch.int32 and ids.tolist() == [7, 9, 0] and pos.tolist() == [2, 0, -1]
+    b.append_sampled(["b", "a"], torch.tensor([40, 41], dtype=torch.int32))
+    assert b.requests["a"].output_token_ids == [] and b.requests["a"].num_sampled == 1
+    ids, pos = b.decode_inputs(["a", "b"])
+    assert ids.tolist() == [41, 40] and pos.tolist() == [3, 1]
+    b.append_sampled(["a"], torch.tensor([42], dtype=torch.int32))
+    assert b.decode_inputs(["a"])[0].tolist() == [42]
+    b.append_sampled(["a"], torch.tensor([43], dtype=torch.int32))   # past max_output_len
+    with pytest.raises(ValueError):
+        b.decode_inputs(["a"])
+
+
 def test_sampler_refuses_cpu_logits_and_unsupported_modes():
     s = Sampler()
     b = InputBatch(1, 2, 2, V, torch.device("cpu"))

@@ -439,8 +439,8 @@ template <> struct Elem<uint16_t> {  // bfloat16 bit patterns, widened exactly
     }
 };
 
-// Buffer resource over `bytes` bytes at p (raw addressing): loads past the end return zero and
-// never fault, and one 32-bit lane offset plus a scalar offset addresses every load.
+// Buffer resource over `bytes` bytes at p (raw addressing): a load whose vector offset (plus
+// instruction offset) is at or past `bytes` returns zero and never faults.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }

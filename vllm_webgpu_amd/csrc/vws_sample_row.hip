@@ -592,8 +592,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     //    everything before it conservative): the first iteration of logits (it needs only the
     //    preloaded arguments), the history ids and processor lists (zero-sized buffers when
     //    absent), the second iteration, then the parameters as scalar loads.
-    //    Buffer loads: a row's loads share one lane offset (the iteration and vector go in the
-    //    scalar offset), and loads past the end read zeros, so nothing is clamped.
+    //    Buffer loads: loads past the end of the row read zeros (range-checked vector offsets),
+    //    so nothing is clamped.
     //    The row addresses are computed without branches (an absent list gets a zero-sized
     //    buffer, whatever its address), so that the kernel arguments are read in one batch.
     Slice<T> sl;
@@ -602,14 +602,17 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const int nit = (nbody + NT * U - 1) / (NT * U);
     const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + sl.a, 16u * (uint32_t)nbody);
     float A[U][VEC], Bq[U][VEC];
-    // Vectors past the body read zeros; consumers skip them (vi >= nbody).  The loads are
-    // non-temporal (nt): the row is read once, and streaming it with the default policy evicts
-    // the kernel's own code and small operands from L2 and the infinity cache.
+    // Vectors past the body read zeros; consumers skip them (vi >= nbody).  The whole byte
+    // offset is the vector offset (the scalar offset is 0): a raw buffer access is out of range,
+    // returns zeros and fetches nothing when its vector offset plus instruction offset is at or
+    // past the resource's num_records, so the prefetches past the row's end never leave the row.
+    // The loads are non-temporal (nt): the row is read once, and streaming it with the default
+    // policy evicts the kernel's own code and small operands from L2 and the infinity cache.
     auto load_iter = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-                lrs, 16u * (uint32_t)tid_now(), 16u * (uint32_t)((it * U + q) * NT), kLoadNT);
+                lrs, 16u * (uint32_t)(tid_now() + (it * U + q) * NT), 0u, kLoadNT);
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };

@@ -48,10 +48,13 @@ class CachedRequestState:
     generator: torch.Generator | None
     slot: int
     output_token_ids: list[int] = field(default_factory=list)
+    # ids sampled on the device so far; counted when the step samples, so it leads the host
+    # list above while a step's output is still in flight (async output)
+    num_sampled: int = 0
 
     @property
     def num_tokens(self) -> int:
-        return len(self.prompt_token_ids) + len(self.output_token_ids)
+        return len(self.prompt_token_ids) + self.num_sampled
 
 
 class InputBatch:
@@ -154,7 +157,7 @@ class InputBatch:
         # gather only the populated columns: the kernel reads every history column it is given
         pw = max(1, max((len(s.prompt_token_ids) for s in states), default=1))
         ow = max(1, min(self.output_ids.shape[1],
-                        max((len(s.output_token_ids) for s in states), default=1)))
+                        max((s.num_sampled for s in states), default=1)))
         # Rows that are not random draw uniforms too (one [B, V] draw), but the kernel ignores them.
         gens = {i: s.generator for i, s in enumerate(states)
                 if s.generator is not None and not greedy[i]}
@@ -182,10 +185,38 @@ class InputBatch:
             output_token_lens=None if no_penalties else self.output_lens.index_select(0, slots),
         ) if B else None
 
+    def decode_inputs(self, req_ids: list[str]) -> tuple[torch.Tensor, torch.Tensor]:
+        """The next decode step's inputs, int32 [B] on the device: each request's last token
+        (its newest sampled id, read from the device table, else the last prompt id) and its
+        position (number of tokens - 1).  Nothing waits for a step's output to reach the host,
+        so the next step can be scheduled while the previous one's ids are still in flight."""
+        states = [self.requests[r] for r in req_ids]
+        over = [s.req_id for s in states if s.num_sampled > self.output_ids.shape[1]]
+        if over:
+            raise ValueError(f"requests {over} generated more than max_output_len="
+                             f"{self.output_ids.shape[1]} tokens")
+        dev = self.device
+        slots = torch.tensor([s.slot for s in states], dtype=torch.int64, device=dev)
+        ocol = torch.tensor([max(s.num_sampled - 1, 0) for s in states], dtype=torch.int64,
+                            device=dev)
+        pcol = torch.tensor([max(len(s.prompt_token_ids) - 1, 0) for s in states],
+                            dtype=torch.int64, device=dev)
+        has_out = torch.tensor([s.num_sampled > 0 for s in states], device=dev)
+        has_prompt = torch.tensor([len(s.prompt_token_ids) > 0 for s in states], device=dev)
+        last_out = self.output_ids[slots, ocol]
+        last_prompt = self.prompt_ids[slots, pcol]
+        zero = torch.zeros_like(last_out)
+        input_ids = torch.where(has_out, last_out, torch.where(has_prompt, last_prompt, zero))
+        positions = torch.tensor([s.num_tokens - 1 for s in states], dtype=torch.int32, device=dev)
+        return input_ids, positions
+
     def append_sampled(self, req_ids: list[str], sampled: torch.Tensor) -> None:
-        """Appends ``sampled`` (int32 [B] on the device) to the output tables, on the device."""
+        """Appends ``sampled`` (int32 [B] on the device) to the output tables, on the device,
+        and counts the step in each request's ``num_sampled``."""
         if not req_ids:
             return
+        for r in req_ids:
+            self.requests[r].num_sampled += 1
         slots = torch.tensor([self.requests[r].slot for r in req_ids], dtype=torch.int64,
                              device=self.device)
         pos = self.output_lens.index_select(0, slots).long()
@@ -291,12 +322,10 @@ class ROCmModelRunner:
             if not req_ids:
                 self._last_logits, self._last_req_ids = None, []
                 return None
-            reqs = [self.input_batch.requests[r] for r in req_ids]
-            last = [(s.output_token_ids or s.prompt_token_ids)[-1:] for s in reqs]
-            input_ids = torch.tensor([x[0] if x else 0 for x in last], dtype=torch.int32)
-            positions = torch.tensor([s.num_tokens - 1 for s in reqs], dtype=torch.int32)
-            logits = self.model.forward(input_ids.to(self.device), positions.to(self.device),
-                                        scheduler_output)
+            # inputs come from the device tables: correct even while the previous step's
+            # output is still being copied to the host (async output)
+            input_ids, positions = self.input_batch.decode_inputs(req_ids)
+            logits = self.model.forward(input_ids, positions, scheduler_output)
             if logits.shape != (len(req_ids), vocab):
                 raise ValueError(f"model returned logits {tuple(logits.shape)}, expected "
                                  f"({len(req_ids)}, {vocab})")
@@ -313,8 +342,10 @@ class ROCmModelRunner:
         With ``async_output`` the copy is only enqueued and an ``AsyncModelRunnerOutput`` is
         returned: its ``get_output()`` waits for the copy, so the host can schedule the next
         step while the device finishes this one (the device-side history tables are updated on
-        the device either way).  ``get_output()`` must be called before the next step samples:
-        it also appends the ids to the host copies that bad-words matching reads.
+        the device either way).  The next step may be executed before ``get_output()``: its
+        inputs and penalty histories come from the device tables.  Bad-words matching reads the
+        host copies of the generated ids, which ``get_output()`` appends, so a batch that uses
+        bad words must call it before the next step samples.
         """
         if self._last_logits is None:
             return None
