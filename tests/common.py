@@ -65,7 +65,12 @@ def assert_same(gpu, ref, label=""):
     assert not nk.any(), (f"{label}: n_kept mismatch rows {np.nonzero(nk)[0][:8]}: "
                           f"gpu {gpu['n_kept'][nk][:8]} oracle {ref['n_kept'][nk][:8]}")
     if "lp_ids" in ref:
-        assert np.array_equal(gpu["lp_ids"], ref["lp_ids"]), f"{label}: logprob ids differ"
-        assert np.array_equal(gpu["ranks"], ref["ranks"]), f"{label}: ranks differ"
+        bad = np.nonzero((gpu["lp_ids"] != ref["lp_ids"]).any(axis=1))[0]
+        assert bad.size == 0, (f"{label}: logprob ids differ in rows {bad[:8]} (flags "
+                               f"{gpu['flags'][bad[:8]]}): gpu {gpu['lp_ids'][bad[:2]].tolist()} "
+                               f"oracle {ref['lp_ids'][bad[:2]].tolist()}")
+        bad = np.nonzero(gpu["ranks"] != ref["ranks"])[0]
+        assert bad.size == 0, (f"{label}: ranks differ in rows {bad[:8]}: gpu {gpu['ranks'][bad[:8]]} "
+                               f"oracle {ref['ranks'][bad[:8]]}")
         np.testing.assert_allclose(gpu["lp_vals"], ref["lp_vals"], rtol=LP_RTOL, atol=LP_ATOL,
                                    err_msg=f"{label}: logprob values")

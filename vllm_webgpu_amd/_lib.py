@@ -30,6 +30,8 @@ FLAG_RACE_NEAR_TIE = 0x2
 FLAG_DEGENERATE = 0x4
 FLAG_GREEDY = 0x8
 FLAG_GENERAL_PATH = 0x100
+FLAG_STREAM_TOPP = 0x200
+FLAG_TOPP_RECOUNT = 0x400
 
 MAX_VOCAB = 1 << 19
 MAX_LOGPROBS = 64

@@ -306,6 +306,9 @@ int vws_sample(const vws_sample_args* a) {
     k.lp_vals = a->logprob_vals;
     k.lp_ranks = a->logprob_ranks;
     k.mode = kModeSample;
+    // every row would leave the single-pass kernel at once: rows go straight to the top-p
+    // stream or the general path, without the single pass's first loads
+    k.nofast = (a->num_logprobs >= 0 || a->allowed_mask) ? 1 : 0;
     hipStream_t s = (hipStream_t)a->stream;
     const int ps = prof_start(s, VWS_KERNEL_SAMPLE);
     if (a->dtype == VWS_DTYPE_F32)

@@ -846,7 +846,21 @@ logprobs:
             a.lp_vals[(size_t)r * stride] = (raw_s - m0) - logS;
             a.lp_ranks[r] = (int32_t)rk;
         }
-        if (L > 0) {
+        // the buffered top-L candidates overflowed (ties) or their cut holds more than the 128
+        // gathered: the exact selection over the row
+        const bool exact_sel = L > 0 && (sm.bc32[2] != 0u || sm.nsel > 128u);
+        if (exact_sel) {
+            const uint32_t n = general_topk_select<T>(a, sm, r, L);
+            for (uint32_t j = tid; j < n; j += NT) {
+                const uint64_t g = sm.u.gather[j];
+                a.lp_ids[(size_t)r * stride + 1 + j] = (int32_t)(uint32_t)g;
+                a.lp_vals[(size_t)r * stride + 1 + j] = (val_of(~(uint32_t)(g >> 32)) - m0) - logS;
+            }
+            for (int j = (int)n + tid; j < L; j += NT) {
+                a.lp_ids[(size_t)r * stride + 1 + j] = -1;
+                a.lp_vals[(size_t)r * stride + 1 + j] = __builtin_nanf("");
+            }
+        } else if (L > 0) {
             const uint32_t n = min(sm.nsel, 128u);
             for (uint32_t j = tid; j < n; j += NT) {
                 const uint32_t kj = sm.lp_sel_key[j];
@@ -875,15 +889,16 @@ logprobs:
     }
 }
 
-// Exact top-k ids/values of a row for the topk operation, when its single-pass list
-// overflowed (ties): the k-th largest key by a 3-level radix select, the tie group at that key
-// cut by an index radix select (lowest indices first), then the k entries sorted.
+// Exact top-k of a row by raw value (after the soft cap, if any): the k-th largest key by a
+// 3-level radix select, the tie group at that key cut by an index radix select (lowest indices
+// first), then the winners sorted by (value desc, index asc) into sm.u.gather as
+// (~key << 32) | index.  Returns the number of winners, min(k, non-NaN elements).
 template <typename T>
-__device__ __forceinline__ void general_topk_row(const KArgs& a, GenSmem& sm, int r) {
+__device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem& sm, int r, int k) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     const int tid = threadIdx.x;
-    const int V = a.V, k = a.topk_k;
+    const int V = a.V;
     const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
     Slice<T> sl;
     sl.init(row, 0, V);
@@ -894,15 +909,19 @@ __device__ __forceinline__ void general_topk_row(const KArgs& a, GenSmem& sm, in
             const int c0 = it * 2 * NT + tid;
             const int i0 = sl.load(c0, v0);
             const int i1 = sl.load(c0 + NT, v1);
+            if (a.softcap > 0.0f) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    v0[j] = softcap_det(v0[j], a.inv_softcap, a.softcap);
+                    v1[j] = softcap_det(v1[j], a.inv_softcap, a.softcap);
+                }
+            }
             f(v0, i0);
             f(v1, i1);
         }
     };
-    for (int i = tid; i < k; i += NT) {
-        a.topk_vals[(size_t)r * k + i] = __builtin_nanf("");
-        a.topk_ids[(size_t)r * k + i] = -1;
-    }
     uint32_t nvalid = 0;
+    __syncthreads();
     for (int i = tid; i < kBuckets; i += NT) sm.hcnt[i] = 0u;
     __syncthreads();
     for_rows([&](float* v, int i0) {
@@ -914,7 +933,7 @@ __device__ __forceinline__ void general_topk_row(const KArgs& a, GenSmem& sm, in
     });
     const uint32_t nval = (uint32_t)gblock_sum(nvalid, sm);
     const int kk_eff = (uint32_t)k < nval ? k : (int)nval;
-    if (kk_eff == 0) return;
+    if (kk_eff == 0) return 0u;
     uint64_t ab;
     const int b1 = gfind_from_top(sm.hcnt, kBuckets, (uint64_t)kk_eff, &ab, sm);
     uint64_t rem = (uint64_t)kk_eff - ab;
@@ -1005,7 +1024,20 @@ __device__ __forceinline__ void general_topk_row(const KArgs& a, GenSmem& sm, in
             __syncthreads();
         }
     }
-    for (uint32_t j = tid; j < n && j < (uint32_t)k; j += NT) {
+    return n < (uint32_t)k ? n : (uint32_t)k;
+}
+
+// Exact top-k ids/values of a row for the topk operation, when its single-pass list
+// overflowed (ties).
+template <typename T>
+__device__ __forceinline__ void general_topk_row(const KArgs& a, GenSmem& sm, int r) {
+    const int k = a.topk_k;
+    for (int i = threadIdx.x; i < k; i += kGenThreads) {
+        a.topk_vals[(size_t)r * k + i] = __builtin_nanf("");
+        a.topk_ids[(size_t)r * k + i] = -1;
+    }
+    const uint32_t n = general_topk_select<T>(a, sm, r, k);
+    for (uint32_t j = threadIdx.x; j < n; j += kGenThreads) {
         const uint64_t g = sm.u.gather[j];
         a.topk_vals[(size_t)r * k + j] = val_of(~(uint32_t)(g >> 32));
         a.topk_ids[(size_t)r * k + j] = (int32_t)(uint32_t)g;

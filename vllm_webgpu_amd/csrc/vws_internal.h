@@ -78,6 +78,7 @@ struct KArgs {
     int S;                  // parts per row
     int part_len;           // elements per part (multiple of 64)
     int mode;               // Mode
+    int nofast;             // no row can take the single-pass kernel (logprobs, allowed mask)
     int topk_k;             // k for kModeTopK
     float softcap;          // > 0: Gemma's soft cap applied to every logit first
     float inv_softcap;      // fl(1 / softcap)

@@ -53,4 +53,50 @@ __device__ __forceinline__ int fast_k(const KArgs& a, const RowP& p) {
     return 0;
 }
 
+// The race over the kept survivors and the diagnostics of the top-p cut.
+struct RowRace {
+    uint64_t best = 0;     // (key bits << 32) | (0x7FFFFFFF - index), 0 = none
+    uint64_t last = 0;     // max (key(y) << 32 | index) over kept survivors
+    uint64_t cprev = 0;    // largest cumulative mass among removed survivors
+    uint64_t cat = ~0ull;  // smallest cumulative mass among kept survivors
+    uint32_t second = 0;   // key bits + 1 of the best non-winning key, 0 = none
+    uint32_t nkept = 0;
+    uint32_t nrem = 0;     // survivors removed by top-p
+    __device__ __forceinline__ void add_key(float key, int idx) {
+        if (!(key >= 0.0f)) return;  // NaN keys never win
+        const uint64_t pk = ((uint64_t)f2u(key) << 32) | (uint32_t)(0x7FFFFFFF - idx);
+        if (pk > best) {
+            if (best) { const uint32_t o = (uint32_t)(best >> 32) + 1u; second = second > o ? second : o; }
+            best = pk;
+        } else {
+            const uint32_t o = f2u(key) + 1u;
+            second = second > o ? second : o;
+        }
+    }
+    __device__ __forceinline__ void merge(const RowRace& o) {
+        const uint64_t hi = best > o.best ? best : o.best;
+        const uint64_t lo = best > o.best ? o.best : best;
+        const uint32_t l = lo ? (uint32_t)(lo >> 32) + 1u : 0u;
+        second = second > o.second ? second : o.second;
+        second = second > l ? second : l;
+        best = hi;
+        last = last > o.last ? last : o.last;
+        cprev = cprev > o.cprev ? cprev : o.cprev;
+        cat = cat < o.cat ? cat : o.cat;
+        nkept += o.nkept;
+        nrem += o.nrem;
+    }
+    __device__ __forceinline__ void shfl_merge(int off) {
+        RowRace o;
+        o.best = lane_xor64(best, off);
+        o.last = lane_xor64(last, off);
+        o.cprev = lane_xor64(cprev, off);
+        o.cat = lane_xor64(cat, off);
+        o.second = lane_xor(second, off);
+        o.nkept = lane_xor(nkept, off);
+        o.nrem = lane_xor(nrem, off);
+        merge(o);
+    }
+};
+
 }  // namespace vws

@@ -24,6 +24,7 @@
 // seed above the k-th value, degenerate maxima, temperature ties across a threshold) runs the
 // multi-pass path of vws_general.h in the same workgroup, so one launch serves the whole batch.
 #include "vws_general.h"
+#include "vws_topp.h"
 
 namespace vws {
 
@@ -82,6 +83,7 @@ struct RowSmem {
 union RowShared {
     GenSmem g;
     RowSmem f;
+    TopPSmem t;
 };
 
 __device__ __forceinline__ uint32_t rhash_slot(int t) {
@@ -126,54 +128,13 @@ __device__ __forceinline__ int rhash_find(const RowSmem& sm, int t) {
     return -1;
 }
 
-// The race over the kept survivors and the diagnostics of the top-p cut.
-struct RowRace {
-    uint64_t best = 0;     // (key bits << 32) | (0x7FFFFFFF - index), 0 = none
-    uint64_t last = 0;     // max (key(y) << 32 | index) over kept survivors
-    uint64_t cprev = 0;    // largest cumulative mass among removed survivors
-    uint64_t cat = ~0ull;  // smallest cumulative mass among kept survivors
-    uint32_t second = 0;   // key bits + 1 of the best non-winning key, 0 = none
-    uint32_t nkept = 0;
-    uint32_t nrem = 0;     // survivors removed by top-p
-    __device__ __forceinline__ void add_key(float key, int idx) {
-        if (!(key >= 0.0f)) return;  // NaN keys never win
-        const uint64_t pk = ((uint64_t)f2u(key) << 32) | (uint32_t)(0x7FFFFFFF - idx);
-        if (pk > best) {
-            if (best) { const uint32_t o = (uint32_t)(best >> 32) + 1u; second = second > o ? second : o; }
-            best = pk;
-        } else {
-            const uint32_t o = f2u(key) + 1u;
-            second = second > o ? second : o;
-        }
-    }
-    __device__ __forceinline__ void merge(const RowRace& o) {
-        const uint64_t hi = best > o.best ? best : o.best;
-        const uint64_t lo = best > o.best ? o.best : best;
-        const uint32_t l = lo ? (uint32_t)(lo >> 32) + 1u : 0u;
-        second = second > o.second ? second : o.second;
-        second = second > l ? second : l;
-        best = hi;
-        last = last > o.last ? last : o.last;
-        cprev = cprev > o.cprev ? cprev : o.cprev;
-        cat = cat < o.cat ? cat : o.cat;
-        nkept += o.nkept;
-        nrem += o.nrem;
-    }
-    __device__ __forceinline__ void shfl_merge(int off) {
-        RowRace o;
-        o.best = lane_xor64(best, off);
-        o.last = lane_xor64(last, off);
-        o.cprev = lane_xor64(cprev, off);
-        o.cat = lane_xor64(cat, off);
-        o.second = lane_xor(second, off);
-        o.nkept = lane_xor(nkept, off);
-        o.nrem = lane_xor(nrem, off);
-        merge(o);
-    }
-};
-
-// LDS of the row kernel: the single-pass state and the general path's state share it.
+// LDS of the row kernel: the single-pass state, the top-p stream's and the general path's
+// share it.
 __shared__ RowShared g_row_sh;
+
+__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw) {
+    return topp_compact(g_row_sh.t, w, cnt, aw, c, want_raw != 0);
+}
 
 // Applies the logits processors and penalties to wave w's candidates [from, cnt), in place, and
 // returns the new count.  Candidates enter the buffer by their raw value; when nothing can raise
@@ -575,10 +536,11 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
 }
 
 // Serves greedy and top-k rows; returns false when the row must take the general path (nothing
-// has been written for it then).
+// has been written for it then); *topp_row tells whether the single-pass top-p path may serve
+// the row instead.
 template <typename T>
 __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, const void* logits,
-                                         int64_t lstride, int V) {
+                                         int64_t lstride, int V, bool* topp_row) {
     constexpr int NT = kRowThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int U = 32 / VEC;  // 16-byte loads in flight per lane per iteration
@@ -638,7 +600,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     load_iter(Bq, 1);
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
-    if (k == 0) return false;
+    if (k == 0) {
+        *topp_row = topp_eligible(a, prm);
+        return false;
+    }
     const bool hh = prm.has_hist;     // penalties
     const bool hx = prm.need_hash;    // penalties or logits processors
     // processors and penalties that never raise a logit let hashed candidates be found by their
@@ -1118,9 +1083,26 @@ template <typename T>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
                                                           int pad, KArgs a) {
     const int r = blockIdx.x;  // the grid is exactly B workgroups
-    if (row_fast<T>(a, g_row_sh.f, r, logits, lstride, V)) return;
+    bool topp = false;
+    if (a.nofast) {
+        topp = topp_eligible(a, row_params(a, r));
+    } else if (row_fast<T>(a, g_row_sh.f, r, logits, lstride, V, &topp)) {
+        return;
+    }
+    int why = 0;
+    if (topp) {
+        // the single-pass top-p path, inline: it starts after the single-pass function has
+        // returned (no live range crosses that function's stream) and issues its own loads
+        __syncthreads();
+        const RowP prm = row_params(a, r);
+        topp_stream<T>(a, g_row_sh.t, r, prm);
+        why = topp_finish<T>(a, g_row_sh.t, r, prm);
+        if (why == 0) return;
+    }
     __syncthreads();
     row_general<T>(r, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u);
+    // diagnostic: why the single-pass top-p path handed the row over (thread 0 wrote the flags)
+    if (why && threadIdx.x == 0 && a.flags) a.flags[r] |= (uint32_t)why << 16;
 }
 
 template __global__ void row_kernel<float>(const void*, int64_t, int, int, KArgs);

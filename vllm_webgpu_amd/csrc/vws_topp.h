@@ -1,0 +1,972 @@
+// vws_topp.h -- single-pass sampling of rows whose survivors are cut by top-p alone (top-k off,
+// 0 < top_p < 1), and of greedy rows that ask for raw logprobs.
+//
+// One 1024-thread workgroup streams the row once (16-byte non-temporal buffer loads, two
+// iterations in flight, as in the single-pass kernel).  Each wave stores the elements of its
+// share at or above a threshold in an LDS candidate buffer (the threshold is seeded from the
+// first iteration so that the buffers hold a few percent of the row, and raised when a buffer
+// would overflow) and adds every other element into an approximate mass sum: the term 2^z,
+// z = (x - a) c, from the hardware exp2, c = log2(e) / T, a the row's anchor (its seed), plus
+// the sum of |z| 2^z for the error bound.  After the stream:
+//   * the row maximum is the largest candidate; candidates below the highest wave threshold
+//     join the sum exactly; the others get exact masses floor(exp_det(y - max) 2^44) in 2048
+//     buckets of max - y;
+//   * the exact mass of everything below the threshold lies in an interval [S_lo, S_hi] built
+//     from the approximate sum and its error bound.  Top-p's threshold, boundary bucket, cut
+//     inside that bucket and near-tie flags are computed at both ends of the interval; when
+//     they differ, one more pass over the row sums the exact masses below the threshold and
+//     the decision is taken again on the exact value;
+//   * the race runs over the kept candidates (uniforms read at their positions only), and raw
+//     logprobs come from the candidates (top-L, rank) and the sums (log-sum-exp).
+// Rows with penalties, logits processors, an allowed mask or the soft cap, rows whose top-p
+// boundary falls below the threshold, and rows whose buffers overflow (ties) take the
+// multi-pass path instead; nothing is written for them here.
+#pragma once
+
+#include "vws_row.h"
+
+namespace vws {
+
+constexpr int kTpWaves = kGenWaves;       // 16
+constexpr int kTpCapW = 832;              // candidate slots per wave
+constexpr int kTpSlots = kTpCapW + kWave; // and one scratch slot per lane (stores of non-candidates)
+constexpr int kTpSoft = 704;              // a wave holding more after half an iteration compacts
+constexpr int kTpKeep = 512;              // entries a compaction keeps (ties included)
+constexpr float kTpFill = 0.65f;          // share of the slots the seed threshold aims to fill
+constexpr int kTpBuckets = 2048;          // exact-mass buckets of width 1/64 over max - y in [0, 32)
+constexpr int kTpGather = 2048;           // members of the boundary bucket resolved in LDS
+constexpr int kTpRankCap = 256;           // up to this many, without sorting them
+constexpr int kTpLpCap = 256;             // candidates gathered for the top-L logprobs
+constexpr float kLog2e = 0x1.715476p+0f;  // log2(e) rounded to fp32
+
+// Why a row left the single-pass top-p path (recorded in bits 16-23 of its result flags, which
+// are diagnostic like VWS_FLAG_GENERAL_PATH).
+constexpr int VWS_FALLBACK_OVERFLOW = 1;    // a wave's candidate buffer overflowed (ties)
+constexpr int VWS_FALLBACK_SUM = 2;         // the approximate sum is not finite
+constexpr int VWS_FALLBACK_DEGENERATE = 3;  // no finite row maximum
+constexpr int VWS_FALLBACK_MIN_P = 4;       // min-p may keep elements below the candidates
+constexpr int VWS_FALLBACK_BELOW = 5;       // top-p keeps elements below the candidates
+constexpr int VWS_FALLBACK_AMBIGUOUS = 6;   // the exact recount still cuts inconsistently
+constexpr int VWS_FALLBACK_GATHER = 7;      // the boundary bucket holds too many members
+constexpr int VWS_FALLBACK_TOPL = 8;        // the top-L logprobs reach below the candidates
+
+struct TopPSmem {
+    // Each wave's candidates: raw bits during the stream, order keys from the finish on; and
+    // their indices.  Slots kTpCapW.. are per-lane scratch for the stores of non-candidates.
+    uint32_t ck[kTpWaves][kTpSlots];
+    int32_t ci[kTpWaves][kTpSlots];
+    union {
+        uint32_t rhist[kTpWaves][256];    // stream: per-wave radix-select scratch
+        struct {
+            uint64_t hmass[kTpBuckets];   // finish: exact masses of the surviving candidates
+            uint32_t hcnt[kTpBuckets];    // and the number of candidates (every one) per bucket
+        } h;
+    };
+    union {
+        struct {
+            uint64_t key[kTpGather];      // boundary bucket: key(y) << 32 | index
+        } g;
+        struct {
+            uint64_t key[kTpRankCap];     // the same, for up to kTpRankCap members
+            uint64_t w[kTpRankCap];       // and their exact masses
+        } rk;
+        struct {
+            uint32_t key[kTpLpCap];
+            int32_t idx[kTpLpCap];
+        } lp;
+    };
+    // per-wave results of the stream
+    double wS[kTpWaves];                  // sum of the approximate terms below the threshold
+    double wSR[kTpWaves];                 // the same over raw logits (T != 1, log-sum-exp)
+    float wZ[kTpWaves];                   // sum of |z| * term (error bound)
+    uint32_t wTau[kTpWaves];              // final threshold key
+    uint32_t wCnt[kTpWaves];              // buffered entries
+    uint32_t wMax[kTpWaves];              // largest buffered key
+    // finish
+    uint64_t red[kTpWaves][4];            // per-wave records of the finish's reductions
+    double redd[kTpWaves];
+    float anchor;                         // the row's anchor a
+    uint32_t status;                      // bit 0: buffer overflow, bit 1: non-finite sum
+    uint32_t bc[16];
+    uint64_t bc64[16];
+};
+
+// Entries dropped by a compaction, as terms of the approximate sum (per lane), and the new
+// threshold and count (wave-uniform).
+struct TpDrop {
+    double s, sr;
+    float z;
+    uint32_t kth;
+    int cnt;
+};
+
+// Out of line (compaction is rare); defined next to the LDS it works on.
+__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw);
+
+// Whether the single-pass top-p path may serve the row.
+__device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
+    if (a.mode != kModeSample || p.need_hash || a.allowed || a.softcap > 0.0f) return false;
+    if (p.greedy) return a.L >= 0;
+    const bool topk_off = p.k <= 0 || p.k >= a.V;
+    return topk_off && p.top_p > 0.0f && p.top_p < 1.0f;
+}
+
+// Term of the approximate sum, 2^z with z = max((x - aw) c, -256) by the hardware exp2; z is
+// returned for the error bound.  NaN and -inf give z = -256 and a zero term.
+__device__ __forceinline__ float tp_term(float x, float aw, float c, float& z) {
+    z = __builtin_fmaxf((x - aw) * c, -256.0f);
+    return __builtin_amdgcn_exp2f(z);
+}
+
+// Bucket of d = y - max <= 0: floor(-d * 64), the last bucket from -d >= 32 on (zero masses).
+__device__ __forceinline__ int tp_bucket(float d) {
+    const float dd = -d;
+    return dd < 32.0f ? (int)(dd * 64.0f) : kTpBuckets - 1;
+}
+
+__device__ __forceinline__ uint32_t tp_u(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t tp_u64(uint64_t v) {
+    return ((uint64_t)tp_u((uint32_t)(v >> 32)) << 32) | tp_u((uint32_t)v);
+}
+__device__ __forceinline__ float tp_uf(float v) { return u2f(tp_u(f2u(v))); }
+
+// Per-wave candidate buffer of the top-p stream: every element of the wave's share at or above
+// tau (raw bits and index); the rest joins the approximate sum (also the entries a compaction
+// drops).
+struct TpBuf {
+    int w, cnt;
+    uint32_t tau;
+    float tauf;
+    bool ovf;
+    __device__ __forceinline__ void init(int w_) {
+        w = w_; cnt = 0; tau = 0u; tauf = -__builtin_inff(); ovf = false;
+    }
+    __device__ __forceinline__ void set_tau(uint32_t t) {
+        if (t > tau) {
+            tau = t;
+            tauf = (tau > 0x007FFFFFu) ? val_of(tau) : -__builtin_inff();
+        }
+    }
+    // Stores the elements c[j] of one vector of every lane (v, first index i0), with one
+    // capacity check for the whole vector and no branch per element: a lane stores every
+    // element, the non-candidates into its own scratch slot.  Wave-uniform call.  A full
+    // buffer marks the row for the multi-pass path (the stream compacts every half iteration,
+    // from kTpSoft entries on, so this takes more than kTpCapW - kTpSoft candidates in half an
+    // iteration of one wave).
+    template <int VEC>
+    __device__ __forceinline__ void append_vec(TopPSmem& sm, const float* v, const bool* c, int i0) {
+        uint64_t bal[VEC];
+        int tot = 0;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            bal[j] = __ballot(c[j]);
+            tot += __popcll(bal[j]);
+        }
+        if (ovf || cnt + tot > kTpCapW) {
+            if (!ovf && lane_id() == 0) atomicOr(&sm.status, 1u);
+            ovf = true;
+            return;
+        }
+        const int scratch = kTpCapW + lane_id();
+        int base = cnt;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const int pos = c[j] ? base + lane_prefix(bal[j]) : scratch;
+            sm.ck[w][pos] = f2u(v[j]);
+            sm.ci[w][pos] = i0 + j;
+            base += __popcll(bal[j]);
+        }
+        cnt = base;
+    }
+};
+
+// Keeps the kTpKeep largest values (ties included) of wave w's buffer and raises its threshold
+// to the smallest kept value; the dropped entries are returned as terms of the approximate sum.
+__device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, float aw, float c,
+                                               bool want_raw) {
+    TpDrop d{0.0, 0.0, 0.0f, 0u, 0};
+    const int lane = lane_id();
+    uint32_t* ck = sm.ck[w];
+    int32_t* ci = sm.ci[w];
+    for (int i = lane; i < cnt; i += kWave) ck[i] = key_of(u2f(ck[i]));  // raw bits -> keys
+    wave_sync();
+    const uint32_t kth = wave_kth_largest(ck, cnt, kTpKeep, sm.rhist[w]);
+    int out = 0;
+    for (int base = 0; base < cnt; base += kWave) {
+        const int i = base + lane;
+        bool keep = false;
+        uint32_t kk = 0u;
+        int32_t ii = 0;
+        if (i < cnt) {
+            kk = ck[i];
+            ii = ci[i];
+            keep = kk >= kth;
+            if (!keep) {
+                const float x = val_of(kk);
+                float z;
+                const float t = tp_term(x, aw, c, z);
+                d.s += (double)t;
+                d.z = __builtin_fmaf(__builtin_fabsf(z), t, d.z);
+                if (want_raw) {
+                    float z2;
+                    d.sr += (double)tp_term(x, aw, kLog2e, z2);
+                }
+            }
+        }
+        const uint64_t bal = __ballot(keep);
+        if (keep) {
+            const int pos = out + lane_prefix(bal);
+            ck[pos] = f2u(val_of(kk));  // back to raw bits
+            ci[pos] = ii;
+        }
+        out += __popcll(bal);
+        wave_sync();
+    }
+    d.kth = kth;
+    d.cnt = out;
+    return d;
+}
+
+// The stream over row r.  Publishes each wave's results into sm; topp_finish completes the row.
+template <typename T>
+__device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r, const RowP& prm) {
+    constexpr int NT = kGenThreads;
+    constexpr int VEC = Elem<T>::kVec;
+    constexpr int U = 32 / VEC;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int V = a.V;
+    const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+    Slice<T> sl;
+    sl.init(row, 0, V);
+    const int nbody = sl.nbody;
+    const int nit = (nbody + NT * U - 1) / (NT * U);
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + sl.a, 16u * (uint32_t)nbody);
+    auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
+    // every byte offset in the vector offset: loads past the row's end return zeros
+    auto load_iter = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+                lrs, 16u * (uint32_t)(tid_now() + (it * U + q) * NT), 0u, 2 /* nt */);
+            Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
+        }
+    };
+    float A[U][VEC], Bq[U][VEC];
+    load_iter(A, 0);
+    load_iter(Bq, 1);
+
+    // seed: a threshold from the lane maxima over the first iteration.  A lane's maximum over its
+    // E elements reaches tau with probability 1 - (1 - phi)^E when a fraction phi of the
+    // elements does, so a wave's m-th largest lane maximum, m = 64 (1 - (1 - phi)^E), admits
+    // about phi of the row; phi aims at kTpFill of the buffers' capacity.  Every wave uses the
+    // median of the 16 waves' estimates (the row keeps every element at or above the highest
+    // threshold any wave used, so one common threshold wastes no slots).
+    float lmax = -__builtin_inff();
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+        const bool ok = q * NT + tid < nbody;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) lmax = ok ? __builtin_fmaxf(lmax, A[q][j]) : lmax;
+    }
+    const float share = (float)V / (float)kTpWaves;
+    const float phi = __builtin_fminf(1.0f, kTpFill * (float)kTpCapW / share);
+    const bool seeded = phi < 1.0f && nbody > 0;
+    uint32_t tw = 0u;
+    if (seeded) {
+        // elements per lane in the first iteration (fewer when the row is shorter than it)
+        const float e = __builtin_fminf((float)(U * VEC), __builtin_fmaxf(1.0f, (float)nbody * VEC / NT));
+        const float pl = 1.0f - __builtin_amdgcn_exp2f(e * __builtin_amdgcn_logf(1.0f - phi));
+        const int msel = min(64, max(1, (int)__builtin_ceilf(64.0f * pl)));
+        tw = wave_mth_largest64(key_of(lmax), msel);
+    }
+    if (tid == 0) sm.status = 0u;
+    if (lane == 0) sm.bc[wave] = tw;  // bc is free until the finish's first barrier
+    __syncthreads();
+    uint32_t tau0 = 0u;
+    if (seeded) tau0 = wave_mth_largest64(lane < kTpWaves ? sm.bc[lane] : 0u, kTpWaves / 2);
+    if (tau0 <= 0x007FFFFFu || tau0 >= 0xFF800000u) tau0 = 0u;  // -inf, or +inf (degenerate row)
+    const float aw = tau0 ? val_of(tau0) : 0.0f;
+    const bool greedy = prm.greedy;
+    const float c = greedy ? kLog2e : kLog2e / prm.T;
+    const bool want_raw = a.L >= 0 && !greedy && prm.T != 1.0f;
+
+    TpBuf cb;
+    cb.init(wave);
+    cb.set_tau(tau0);
+    double acc = 0.0, accr = 0.0;
+    float accz = 0.0f;
+    // one vector of VEC elements starting at element i0 (okv: in the row): candidates into the
+    // buffer, every other element into the sums (a zero term for NaN and -inf)
+    auto consume = [&](const float* v, int i0, bool okv, bool any_lane) __attribute__((always_inline)) {
+        bool cj[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) cj[j] = okv && v[j] >= cb.tauf;
+        if (any_lane) cb.append_vec<VEC>(sm, v, cj, i0);
+        float s = 0.0f, z = 0.0f, sr = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const bool inc = okv && !cj[j];
+            float zj;
+            const float t = tp_term(v[j], aw, c, zj);
+            const float tt = inc ? t : 0.0f;
+            s += tt;
+            z = __builtin_fmaf(__builtin_fabsf(zj), tt, z);
+            if (want_raw) {
+                float z2;
+                const float tr = tp_term(v[j], aw, kLog2e, z2);
+                sr += inc ? tr : 0.0f;
+            }
+        }
+        acc += (double)s;
+        accz += z;
+        if (want_raw) accr += (double)sr;
+    };
+    // keeps the buffer's fill at most kTpSoft every half iteration: the dropped entries join the sum
+    auto shrink = [&]() __attribute__((always_inline)) {
+        if (cb.cnt > kTpSoft && !cb.ovf) {
+            const TpDrop d = topp_compact_entry(wave, cb.cnt, aw, c, want_raw ? 1 : 0);
+            acc += d.s;
+            accr += d.sr;
+            accz += d.z;
+            cb.cnt = __builtin_amdgcn_readfirstlane(d.cnt);
+            cb.set_tau(__builtin_amdgcn_readfirstlane(d.kth));
+        }
+    };
+    auto examine = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
+        const int t = tid_now();
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if (q == U / 2) shrink();
+            const int vi = (it * U + q) * NT + t;
+            const bool okv = vi < nbody;
+            float mq = buf[q][0];
+#pragma unroll
+            for (int j = 1; j < VEC; ++j) mq = __builtin_fmaxf(mq, buf[q][j]);
+            consume(buf[q], sl.a + vi * VEC, okv, __ballot(okv && mq >= cb.tauf) != 0ull);
+        }
+    };
+    for (int it = 0; it < nit && !cb.ovf; it += 2) {
+        examine(A, it);
+        load_iter(A, it + 2);
+        shrink();
+        if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
+        load_iter(Bq, it + 3);
+        shrink();
+    }
+    if (wave == 0 && !cb.ovf) {
+        // unaligned head (thread 0) and tail (thread 1), element by element
+        float v[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
+        int i0 = 0;
+        if (tid <= 1) i0 = sl.load_edge(tid, v);
+        const int end = tid == 0 ? sl.a : V;
+        bool anyl = false;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            if (!(tid <= 1 && i0 + j < end)) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
+            anyl = anyl || v[j] >= cb.tauf;
+        }
+        consume(v, i0, true, __ballot(anyl) != 0ull);
+    }
+
+    // publish the wave's results
+    double s = acc, sr = accr;
+    float z = accz;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        s += __shfl_xor(s, o, kWave);
+        sr += __shfl_xor(sr, o, kWave);
+        z += __shfl_xor(z, o, kWave);
+    }
+    uint32_t kmax = 0u;
+    for (int i = lane; i < cb.cnt; i += kWave) {
+        const uint32_t kk = key_of(u2f(sm.ck[wave][i]));
+        kmax = kk > kmax ? kk : kmax;
+    }
+    kmax = wave_max_u32(kmax);
+    if (lane == 0) {
+        sm.wS[wave] = s;
+        sm.wSR[wave] = sr;
+        sm.wZ[wave] = z;
+        sm.wTau[wave] = cb.tau;
+        sm.wCnt[wave] = (uint32_t)cb.cnt;
+        sm.wMax[wave] = kmax;
+        if (wave == 0) sm.anchor = aw;
+        const bool finite = (s == s) && s < 1e300 && (z == z) && z < 3e38f && (sr == sr) && sr < 1e300;
+        if (!finite) atomicOr(&sm.status, 2u);
+    }
+}
+
+// Block scan of v: *excl = sum over the threads below this one (ascending order), returns the
+// total.  Two barriers; `slot` picks the LDS column (consecutive scans may share it).
+__device__ __forceinline__ uint64_t tp_scan(uint64_t v, TopPSmem& sm, int slot, uint64_t* excl) {
+    const int lane = lane_id(), w = threadIdx.x >> 6;
+    uint64_t s = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint64_t t = __shfl_up(s, o, kWave);
+        if (lane >= o) s += t;
+    }
+    __syncthreads();
+    if (lane == kWave - 1) sm.red[w][slot] = s;
+    __syncthreads();
+    uint64_t below = 0ull, total = 0ull;
+#pragma unroll
+    for (int i = 0; i < kTpWaves; ++i) {
+        const uint64_t x = sm.red[i][slot];
+        below += i < w ? x : 0ull;
+        total += x;
+    }
+    *excl = below + (s - v);
+    return tp_u64(total);
+}
+
+// Sum of the per-wave records sm.red[*][slot] (after a barrier), as a scalar.
+__device__ __forceinline__ uint64_t tp_sum16(const TopPSmem& sm, int slot) {
+    uint64_t t = 0ull;
+#pragma unroll
+    for (int i = 0; i < kTpWaves; ++i) t += sm.red[i][slot];
+    return tp_u64(t);
+}
+
+// Sum over the wave of a double (butterfly).
+__device__ __forceinline__ double tp_wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Exact sum of the masses of the survivors below the candidates (every element whose key is
+// below tauk), and their number: one more pass over the row, for rows the interval left
+// ambiguous.  Results are scalars; every thread calls it.
+template <typename T>
+__device__ __forceinline__ void topp_exact_below(const KArgs& a, TopPSmem& sm, int r, float Tt,
+                                                 float m, float lp_min, uint32_t tauk,
+                                                 uint64_t* mass, uint64_t* count) {
+    constexpr int NT = kGenThreads;
+    constexpr int VEC = Elem<T>::kVec;
+    const int tid = threadIdx.x;
+    const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+    Slice<T> sl;
+    sl.init(row, 0, a.V);
+    const int nch = sl.nchunks();
+    uint64_t w = 0ull, n = 0ull;
+    for (int c0 = tid; c0 < nch; c0 += NT) {
+        float v[VEC];
+        sl.load(c0, v);  // NaN outside the row
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const uint32_t kx = key_of(v[j]);
+            const float y = v[j] / Tt;
+            const float d = y - m;
+            const bool s = kx != 0u && kx < tauk && key_of(y) != 0u && d >= lp_min;
+            w += s ? mass_of(exp_det(d)) : 0ull;
+            n += s ? 1ull : 0ull;
+        }
+    }
+    w = wave_sum_u64(w);
+    n = wave_sum_u64(n);
+    __syncthreads();
+    if (lane_id() == 0) {
+        sm.red[tid >> 6][0] = w;
+        sm.red[tid >> 6][1] = n;
+    }
+    __syncthreads();
+    *mass = tp_sum16(sm, 0);
+    *count = tp_sum16(sm, 1);
+}
+
+// Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
+// take the multi-pass path (VWS_FALLBACK_*).  Every return decision is uniform over the
+// workgroup: values that decide are read from LDS after a barrier, or are scalars.
+template <typename T>
+__device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, const RowP& prm) {
+    constexpr int NT = kGenThreads;
+    constexpr int VEC = Elem<T>::kVec;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int L = a.L;
+    const bool greedy = prm.greedy;
+    const float Tt = tp_uf(greedy ? 1.0f : prm.T);
+    __syncthreads();  // every wave's stream results are published
+    if (sm.status != 0u) return (sm.status & 1u) ? VWS_FALLBACK_OVERFLOW : VWS_FALLBACK_SUM;
+    uint32_t tauk = 0u, maxk = 0u;
+#pragma unroll
+    for (int w = 0; w < kTpWaves; ++w) {
+        tauk = sm.wTau[w] > tauk ? sm.wTau[w] : tauk;
+        maxk = sm.wMax[w] > maxk ? sm.wMax[w] : maxk;
+    }
+    tauk = tp_u(tauk);
+    maxk = tp_u(maxk);
+    // a finite row maximum (always a candidate: no threshold exceeds a wave's own maximum)
+    if (maxk <= 0x007FFFFFu || maxk >= 0xFF800000u) return VWS_FALLBACK_DEGENERATE;
+    const float xmax = val_of(maxk);
+    const float m = greedy ? xmax : xmax / Tt;  // max y (the division is monotone)
+    if (!(m > -__builtin_inff() && m < __builtin_inff())) return VWS_FALLBACK_DEGENERATE;
+    const float lp_min = (!greedy && prm.min_p > 0.0f)
+                             ? tp_uf(log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)) : -__builtin_inff();
+    const float aw = tp_uf(sm.anchor);
+    for (int i = tid; i < kTpBuckets; i += NT) {
+        sm.h.hmass[i] = 0ull;
+        sm.h.hcnt[i] = 0u;
+    }
+    if (tid == 0) sm.bc[7] = 0u;  // top-L members gathered
+    __syncthreads();
+
+    // exact masses of the buffered entries (now turned into order keys): candidates into the
+    // buckets, the others into Sx
+    const int cnt = (int)tp_u(sm.wCnt[wave]);
+    {
+        uint64_t wc = 0ull, sx = 0ull;
+        uint32_t nxs = 0u;
+        float s0b = 0.0f;
+        for (int i = lane; i < cnt; i += kWave) {
+            const float x = u2f(sm.ck[wave][i]);
+            const uint32_t kk = key_of(x);
+            sm.ck[wave][i] = kk;
+            const float y = greedy ? x : x / Tt;
+            const float d = y - m;
+            const bool surv = !greedy && key_of(y) != 0u && d >= lp_min;
+            const uint64_t w = surv ? mass_of(exp_det(d)) : 0ull;
+            if (L >= 0) s0b += exp_det(x - xmax);
+            if (kk >= tauk) {
+                const int b = tp_bucket(d);
+                atomicAdd(&sm.h.hcnt[b], 1u);
+                if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
+                wc += w;
+            } else {
+                sx += w;
+                nxs += surv ? 1u : 0u;
+            }
+        }
+        wc = wave_sum_u64(wc);
+        sx = wave_sum_u64(sx);
+        const uint64_t nn = wave_sum_u64(nxs);
+        const double sb = tp_wave_sum_f64((double)s0b);
+        if (lane == 0) {
+            sm.red[wave][0] = wc;
+            sm.red[wave][1] = sx;
+            sm.red[wave][2] = nn;
+            sm.redd[wave] = sb;
+        }
+    }
+    __syncthreads();
+    const uint64_t Wc = tp_sum16(sm, 0);
+    const uint64_t Sx = tp_sum16(sm, 1);
+    const uint64_t NXS = tp_sum16(sm, 2);
+    double S0b = 0.0;
+#pragma unroll
+    for (int w = 0; w < kTpWaves; ++w) S0b += sm.redd[w];
+
+    int32_t token = 0;
+    uint32_t flags = VWS_FLAG_STREAM_TOPP;
+    int32_t nkept = 1;
+    if (greedy) {
+        // the lowest index at the maximum
+        uint64_t best = 0ull;
+        for (int i = lane; i < cnt; i += kWave) {
+            if (sm.ck[wave][i] == maxk) {
+                const uint64_t pk = ((uint64_t)maxk << 32) | (uint32_t)(0x7FFFFFFF - sm.ci[wave][i]);
+                best = pk > best ? pk : best;
+            }
+        }
+        best = wave_max_u64(best);
+        __syncthreads();
+        if (lane == 0) sm.red[wave][3] = best;
+        __syncthreads();
+        best = 0ull;
+#pragma unroll
+        for (int w = 0; w < kTpWaves; ++w) best = sm.red[w][3] > best ? sm.red[w][3] : best;
+        token = (int32_t)(0x7FFFFFFFu - tp_u((uint32_t)best));
+        flags |= VWS_FLAG_GREEDY;
+    } else {
+        // ---- wave 0: the interval of the exact mass below the candidates (the anchor's
+        // scale, then the error bound of the terms), and whether survivors lie below them
+        const float q32 = 1.0f - prm.top_p;  // in (0, 1)
+        if (wave == 0) {
+            const double tt = (double)Tt, md = (double)m;
+            const double ln2 = 0.6931471805599453;
+            const double ad = (double)aw;
+            const double mw = 0x1p44 * exp(ad / tt - md);
+            // relative error of a term against its exact mass: exp_det (1 ulp), the hardware
+            // exp2 (assumed 4 ulp), the vector partial sum (VEC - 1 roundings), the rounding of
+            // d = fl(y - max) and, for T != 1, of y = fl(x / T) (|d|, |y| <= |z| ln2 +
+            // |a/T - m|, |a/T|), and the argument (x - a) * c (three roundings of |z|, plus c's
+            // own)
+            const double k0 = 0x1p-23 + 0x1p-21 + (double)(VEC - 1) * 0x1p-24 +
+                              fabs(ad / tt - md) * 0x1p-24 +
+                              (Tt != 1.0f ? fabs(ad / tt) * 0x1p-24 : 0.0) + 0x1p-40;
+            const double k1 = ((Tt != 1.0f ? 2.0 : 1.0) + 4.0) * ln2 * 0x1p-24;
+            const double ws = lane < kTpWaves ? sm.wS[lane] : 0.0;
+            const double wz = lane < kTpWaves ? (double)sm.wZ[lane] : 0.0;
+            const double sap = tp_wave_sum_f64(mw * ws);
+            const double err0 = tp_wave_sum_f64(mw * (k0 * ws + k1 * wz * (1.0 + 0x1p-8)));
+            if (lane == 0) {
+                int why = 0;
+                // every element of the row outside the buffers may be a term (the floor of each
+                // exact mass loses less than one unit)
+                const double nterms = (double)a.V;
+                const double err = err0 * 1.01 + 2.0;
+                uint64_t nlo = 0ull, nhi = 0ull;
+                if (!(sap < 1e30 && err < 1e30)) why = VWS_FALLBACK_SUM;
+                if (lp_min > -__builtin_inff()) {
+                    // min-p: the sum is exact (zero) only when no element below the candidates
+                    // survives it (the largest of them is the float just below the threshold)
+                    if (tauk > 0x00800000u && val_of(tauk - 1u) / Tt - m >= lp_min) why = VWS_FALLBACK_MIN_P;
+                    sm.bc[9] = 0u;
+                } else {
+                    const double lo = floor(sap - err) - nterms;
+                    nlo = lo > 0.0 ? (uint64_t)lo : 0ull;
+                    nhi = (uint64_t)ceil(sap + err);
+                    sm.bc[9] = tauk > 0x007FFFFFu ? 1u : 0u;  // elements below the candidates survive
+                }
+                sm.bc[8] = (uint32_t)why;
+                sm.bc64[0] = nlo + Sx;
+                sm.bc64[1] = nhi + Sx;
+            }
+        }
+        __syncthreads();
+        if (const int why = (int)tp_u(sm.bc[8])) return why;
+        // survivors below every candidate: the stream's terms (all survive without min-p) and
+        // the buffered ones below the threshold
+        bool any_below_nc = tp_u(sm.bc[9]) != 0u || NXS > 0ull;
+        uint64_t S[2] = {tp_u64(sm.bc64[0]), tp_u64(sm.bc64[1])};
+
+        // decides top-p for S[0] and S[1]; when they differ, once more on the exact value
+        int bstar = -1, gathered = -1;
+        uint32_t ng = 0u, cpos = 0u, tflags = 0u;
+        bool ranked = false;
+        uint64_t thr0 = 0ull, W0 = 0ull, cat0 = 0ull;
+        for (int attempt = 0;; ++attempt) {
+            uint64_t thr[2], W[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                W[e] = S[e] + Wc;
+                thr[e] = scale_floor(q32, W[e]);
+            }
+            bool decided = false;
+            if (S[0] > thr[0] && S[1] > thr[1]) return VWS_FALLBACK_BELOW;  // boundary below the candidates
+            if (S[0] <= thr[0] && S[1] <= thr[1]) {
+                // ---- boundary bucket: the last b (from the top) with S + suffix(b) > thr
+                if (tid == 0) {
+                    sm.bc[0] = 0xFFFFFFFFu;
+                    sm.bc[1] = 0xFFFFFFFFu;
+                }
+                {
+                    const int b0 = 2 * tid, b1 = 2 * tid + 1;
+                    const uint64_t m0 = sm.h.hmass[b0], m1 = sm.h.hmass[b1];
+                    uint64_t below_me;                                        // buckets < b0
+                    const uint64_t tot = tp_scan(m0 + m1, sm, 0, &below_me);  // (barriers)
+                    const uint64_t suf0 = tot - below_me;                     // buckets >= b0
+                    const uint64_t suf1 = suf0 - m0;                          // buckets >= b1
+                    const uint64_t suf2 = suf1 - m1;                          // buckets > b1
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        if (S[e] + suf1 > thr[e] && S[e] + suf2 <= thr[e]) { sm.bc[e] = (uint32_t)b1; sm.bc64[2 + e] = suf2; }
+                        if (S[e] + suf0 > thr[e] && S[e] + suf1 <= thr[e]) { sm.bc[e] = (uint32_t)b0; sm.bc64[2 + e] = suf1; }
+                    }
+                }
+                __syncthreads();
+                const int b0s = (int)tp_u(sm.bc[0]);
+                if (b0s >= kTpBuckets - 1) return VWS_FALLBACK_GATHER;  // not found, or the zero-mass bucket
+                if (b0s == (int)tp_u(sm.bc[1])) {
+                    bstar = b0s;
+                    const uint64_t below = tp_u64(sm.bc64[2]);  // mass of the candidates in buckets > bstar
+                    // ---- the boundary bucket's members
+                    if (gathered != bstar) {
+                        gathered = bstar;
+                        if (tid == 0) sm.bc[4] = 0u;
+                        __syncthreads();
+                        for (int i = lane; i < cnt; i += kWave) {
+                            const uint32_t kk = sm.ck[wave][i];
+                            if (kk < tauk) continue;
+                            const float y = val_of(kk) / Tt;
+                            const float d = y - m;
+                            if (!(key_of(y) != 0u && d >= lp_min) || tp_bucket(d) != bstar) continue;
+                            const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
+                            if (pos < (uint32_t)kTpGather)
+                                sm.g.key[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.ci[wave][i];
+                        }
+                        __syncthreads();
+                        ng = tp_u(sm.bc[4]);
+                        if (ng == 0u || ng > (uint32_t)kTpGather) return VWS_FALLBACK_GATHER;
+                        ranked = ng <= (uint32_t)kTpRankCap;
+                        if (ranked) {
+                            // members in any order, with their exact masses
+                            if (tid < (int)ng)
+                                sm.rk.w[tid] = mass_of(exp_det(val_of((uint32_t)(sm.rk.key[tid] >> 32)) - m));
+                        } else {
+                            uint32_t P = 1u;
+                            while (P < ng) P <<= 1;
+                            for (uint32_t i = ng + tid; i < P; i += NT) sm.g.key[i] = ~0ull;
+                            __syncthreads();
+                            for (uint32_t size = 2; size <= P; size <<= 1) {
+                                for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                                    for (uint32_t t = tid; t < P / 2; t += NT) {
+                                        const uint32_t i = 2 * t - (t & (stride - 1));
+                                        const uint32_t j = i + stride;
+                                        const bool up = (i & size) == 0;
+                                        const uint64_t x = sm.g.key[i], z = sm.g.key[j];
+                                        if ((x > z) == up) { sm.g.key[i] = z; sm.g.key[j] = x; }
+                                    }
+                                    __syncthreads();
+                                }
+                            }
+                        }
+                        __syncthreads();
+                    }
+                    // ---- the cut: the first member (ascending) whose cumulative mass exceeds
+                    // thr, at both ends of the interval
+                    if (tid == 0) {
+                        sm.bc[5] = 0xFFFFFFFFu;
+                        sm.bc[6] = 0xFFFFFFFFu;
+                    }
+                    __syncthreads();
+                    if (ranked) {
+                        // a member's cumulative mass counts the members at or below it
+                        if (tid < (int)ng) {
+                            const uint64_t gj = sm.rk.key[tid];
+                            const uint64_t wj = sm.rk.w[tid];
+                            uint64_t cj = 0ull;
+                            uint32_t rankj = 0u;
+                            for (uint32_t i = 0; i < ng; ++i) {
+                                const bool le = sm.rk.key[i] <= gj;
+                                cj += le ? sm.rk.w[i] : 0ull;
+                                rankj += le ? 1u : 0u;
+                            }
+#pragma unroll
+                            for (int e = 0; e < 2; ++e) {
+                                const uint64_t base = S[e] + below;
+                                if (base + cj > thr[e] && base + cj - wj <= thr[e]) {
+                                    sm.bc[5 + e] = rankj - 1u;
+                                    sm.bc64[4 + 2 * e] = base + cj - wj;
+                                    sm.bc64[5 + 2 * e] = base + cj;
+                                }
+                            }
+                        }
+                    } else {
+                        const uint32_t j0 = 2 * tid, j1 = 2 * tid + 1;
+                        const uint64_t w0 = j0 < ng ? mass_of(exp_det(val_of((uint32_t)(sm.g.key[j0] >> 32)) - m)) : 0ull;
+                        const uint64_t w1 = j1 < ng ? mass_of(exp_det(val_of((uint32_t)(sm.g.key[j1] >> 32)) - m)) : 0ull;
+                        uint64_t pre;
+                        tp_scan(w0 + w1, sm, 1, &pre);
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const uint64_t base = S[e] + below;
+                            if (j0 < ng && base + pre + w0 > thr[e] && base + pre <= thr[e]) {
+                                sm.bc[5 + e] = j0;
+                                sm.bc64[4 + 2 * e] = base + pre;
+                                sm.bc64[5 + 2 * e] = base + pre + w0;
+                            }
+                            if (j1 < ng && base + pre + w0 + w1 > thr[e] && base + pre + w0 <= thr[e]) {
+                                sm.bc[5 + e] = j1;
+                                sm.bc64[4 + 2 * e] = base + pre + w0;
+                                sm.bc64[5 + 2 * e] = base + pre + w0 + w1;
+                            }
+                        }
+                    }
+                    __syncthreads();
+                    cpos = tp_u(sm.bc[5]);
+                    if (cpos < ng && cpos == tp_u(sm.bc[6])) {
+                        // the two terms of the near-tie test (tol = 1e-6 W) must agree too
+                        uint32_t t1[2], t2[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const uint64_t cprev = tp_u64(sm.bc64[4 + 2 * e]);
+                            const uint64_t cat = tp_u64(sm.bc64[5 + 2 * e]);
+                            const uint64_t tol = (uint64_t)((double)W[e] * 1e-6);
+                            t1[e] = (thr[e] - cprev <= tol) ? 1u : 0u;
+                            t2[e] = (cat > thr[e] && cat - thr[e] <= tol) ? 2u : 0u;
+                            if (e == 0) { thr0 = thr[0]; W0 = W[0]; cat0 = cat; }
+                        }
+                        if (t1[0] == t1[1] && t2[0] == t2[1]) {
+                            tflags = t1[0] | t2[0];
+                            decided = true;
+                        }
+                    }
+                }
+            }
+            if (decided) break;
+            if (attempt) return VWS_FALLBACK_AMBIGUOUS;
+            // ambiguous: the exact mass below the candidates, then the decision once more
+            uint64_t exact, nbelow;
+            topp_exact_below<T>(a, sm, r, Tt, m, lp_min, tauk, &exact, &nbelow);
+            S[0] = S[1] = exact;
+            any_below_nc = nbelow > 0ull;
+            flags |= VWS_FLAG_TOPP_RECOUNT;
+        }
+        (void)thr0;
+        (void)W0;
+        (void)cat0;
+
+        // ---- race over the kept survivors: candidates above the boundary bucket, and the
+        // boundary bucket's members from the cut on
+        RowRace rs;
+        uint32_t below_cands = 0u;  // surviving candidates in buckets below the boundary
+        for (int i = lane; i < cnt; i += kWave) {
+            const uint32_t kk = sm.ck[wave][i];
+            if (kk < tauk) continue;
+            const float y = val_of(kk) / Tt;
+            const float d = y - m;
+            if (!(key_of(y) != 0u && d >= lp_min)) continue;
+            const int b = tp_bucket(d);
+            if (b > bstar) { below_cands++; continue; }
+            if (b == bstar) continue;
+            const int32_t idx = sm.ci[wave][i];
+            const uint64_t lk = ((uint64_t)key_of(y) << 32) | (uint32_t)idx;
+            rs.nkept++;
+            rs.last = rs.last > lk ? rs.last : lk;
+            rs.add_key(exp_det(d) / (0.0f - log_det(a.u[(size_t)r * a.ustride + idx])), idx);
+        }
+        for (uint32_t j = (uint32_t)tid; j < ng; j += NT) {
+            const uint64_t g = sm.g.key[j];
+            if (ranked) {
+                // kept: at or after the cut in ascending order
+                uint32_t rankj = 0u;
+                for (uint32_t i = 0; i < ng; ++i) rankj += sm.rk.key[i] <= g ? 1u : 0u;
+                if (rankj - 1u < cpos) continue;
+            } else if (j < cpos) {
+                continue;
+            }
+            const int32_t idx = (int32_t)(uint32_t)g;
+            rs.nkept++;
+            rs.last = rs.last > g ? rs.last : g;
+            rs.add_key(exp_det(val_of((uint32_t)(g >> 32)) - m) /
+                           (0.0f - log_det(a.u[(size_t)r * a.ustride + idx])), idx);
+        }
+        rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
+        rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);
+        const uint32_t nbw = (uint32_t)wave_sum_u64(below_cands);
+        __syncthreads();  // the per-wave records' last readers are done
+        if (lane == 0) {
+            sm.red[wave][0] = rs.best;
+            sm.red[wave][1] = rs.last;
+            sm.red[wave][2] = ((uint64_t)rs.second << 32) | rs.nkept;
+            sm.red[wave][3] = nbw;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            RowRace all;
+            uint64_t nbelow = 0ull;
+            for (int w = 0; w < kTpWaves; ++w) {
+                RowRace o;
+                o.best = sm.red[w][0];
+                o.last = sm.red[w][1];
+                o.second = (uint32_t)(sm.red[w][2] >> 32);
+                o.nkept = (uint32_t)sm.red[w][2];
+                all.merge(o);
+                nbelow += sm.red[w][3];
+            }
+            // the first near-tie term counts when a survivor was removed: below the candidates,
+            // among them, or in the boundary bucket
+            const bool any_removed = any_below_nc || nbelow > 0ull || cpos > 0u;
+            uint32_t f = 0u;
+            if ((any_removed && (tflags & 1u)) || (tflags & 2u)) f |= VWS_FLAG_TOPP_NEAR_TIE;
+            int32_t tok;
+            if (all.best) {
+                tok = (int32_t)(0x7FFFFFFF - (uint32_t)(all.best & 0xFFFFFFFFu));
+                const float bk = u2f((uint32_t)(all.best >> 32));
+                if (all.second) {
+                    const float sk = u2f(all.second - 1u);
+                    if ((double)sk >= (double)bk * (1.0 - 1e-6)) f |= VWS_FLAG_RACE_NEAR_TIE;
+                }
+            } else {
+                tok = (int32_t)(uint32_t)(all.last & 0xFFFFFFFFu);
+            }
+            sm.bc[12] = (uint32_t)tok;
+            sm.bc[13] = f;
+            sm.bc[14] = all.nkept;
+        }
+        __syncthreads();
+        token = (int32_t)tp_u(sm.bc[12]);
+        flags |= tp_u(sm.bc[13]);
+        nkept = (int32_t)tp_u(sm.bc[14]);
+    }
+
+    // ---- raw logprobs: every element at or above the sampled one is a candidate
+    float logS = 0.0f, xs = 0.0f;
+    uint32_t rank = 0u;
+    if (L >= 0) {
+        const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+        xs = tp_uf(Elem<T>::load1(row + token));
+        const uint32_t ks = key_of(xs);
+        uint32_t rk = 0u;
+        for (int i = lane; i < cnt; i += kWave) rk += sm.ck[wave][i] >= ks ? 1u : 0u;
+        rk = (uint32_t)wave_sum_u64(rk);
+        uint32_t ncand = 0u;
+        {
+            // the L largest raw values lie in the buckets from the top that hold L candidates
+            const int b0 = 2 * tid, b1 = 2 * tid + 1;
+            const uint32_t c0 = sm.h.hcnt[b0], c1 = sm.h.hcnt[b1];
+            uint64_t pre;                                                 // candidates in buckets < b0
+            ncand = (uint32_t)tp_scan(c0 + c1, sm, 2, &pre);
+            if (L > 0) {
+                if (pre < (uint64_t)L && pre + c0 >= (uint64_t)L) sm.bc[15] = (uint32_t)b0;
+                if (pre + c0 < (uint64_t)L && pre + c0 + c1 >= (uint64_t)L) sm.bc[15] = (uint32_t)b1;
+            }
+            if (lane == 0) sm.red[wave][3] = rk;
+            if (wave == 0) {
+                // log-sum-exp of the raw logits: the buffered part plus the stream's terms
+                const double sw = lane < kTpWaves ? ((greedy || Tt == 1.0f) ? sm.wS[lane] : sm.wSR[lane]) : 0.0;
+                const double s0 = S0b + tp_wave_sum_f64(sw) * exp((double)aw - (double)xmax);
+                if (lane == 0) sm.bc64[8] = (uint64_t)__double_as_longlong(s0);
+            }
+        }
+        __syncthreads();
+        rank = (uint32_t)tp_sum16(sm, 3);
+        logS = (float)log(__longlong_as_double((long long)tp_u64(sm.bc64[8])));
+        if (L > 0) {
+            if (ncand < (uint32_t)L) return VWS_FALLBACK_TOPL;  // the top-L reaches below the candidates
+            const int bl = (int)tp_u(sm.bc[15]);
+            for (int i = lane; i < cnt; i += kWave) {
+                const uint32_t kk = sm.ck[wave][i];
+                if (kk < tauk) continue;
+                const float d = (greedy ? val_of(kk) : val_of(kk) / Tt) - m;
+                if (tp_bucket(d) > bl) continue;
+                const uint32_t pos = atomicAdd(&sm.bc[7], 1u);
+                if (pos < (uint32_t)kTpLpCap) {
+                    sm.lp.key[pos] = kk;
+                    sm.lp.idx[pos] = sm.ci[wave][i];
+                }
+            }
+            __syncthreads();
+            if (tp_u(sm.bc[7]) > (uint32_t)kTpLpCap) return VWS_FALLBACK_TOPL;
+        }
+    }
+
+    // ---- outputs (nothing was written before this point)
+    if (tid == 0) {
+        a.sampled[r] = token;
+        if (a.flags) a.flags[r] = flags;
+        if (a.nkept) a.nkept[r] = nkept;
+    }
+    if (L >= 0) {
+        const int stride = L + 1;
+        if (tid == 0) {
+            a.lp_ids[(size_t)r * stride] = token;
+            a.lp_vals[(size_t)r * stride] = (xs - xmax) - logS;
+            a.lp_ranks[r] = (int32_t)rank;
+        }
+        if (L > 0) {
+            const uint32_t n = tp_u(sm.bc[7]);
+            for (uint32_t j = tid; j < n; j += NT) {
+                const uint32_t kj = sm.lp.key[j];
+                const int32_t ij = sm.lp.idx[j];
+                int pos = 0;
+                for (uint32_t i = 0; i < n; ++i) {
+                    const uint32_t ki = sm.lp.key[i];
+                    pos += (ki > kj || (ki == kj && sm.lp.idx[i] < ij)) ? 1 : 0;
+                }
+                if (pos < L) {
+                    a.lp_ids[(size_t)r * stride + 1 + pos] = ij;
+                    a.lp_vals[(size_t)r * stride + 1 + pos] = (val_of(kj) - xmax) - logS;
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+}  // namespace vws
