@@ -52,11 +52,13 @@ extern "C" {
 #define VWS_FLAG_GREEDY 0x8u         /* temperature < 1e-5 (or NaN): argmax of penalised x */
 #define VWS_FLAG_GENERAL_PATH 0x100u /* served by the multi-pass kernel (diagnostic only) */
 #define VWS_FLAG_STREAM_TOPP 0x200u  /* served by the single-pass top-p path (diagnostic only) */
-#define VWS_FLAG_TOPP_RECOUNT 0x400u /* ... after an exact recount of its tail (diagnostic only) */
+#define VWS_FLAG_TOPP_RECOUNT 0x400u /* ... after an exact pass over its tail (diagnostic only) */
+#define VWS_FLAG_TOPP_WIDE 0x800u    /* ... with its nucleus reaching below the candidates: one
+                                        more pass races them (diagnostic only) */
 /* Bits 16-23 (diagnostic only): why a row left the single-pass top-p path for the multi-pass
- * kernel (1 candidate overflow, 2 non-finite sum, 3 no finite maximum, 4 min-p below the
- * candidates, 5 top-p boundary below the candidates, 6 ambiguous after the recount, 7 boundary
- * bucket too large, 8 top-L below the candidates). */
+ * kernel (1 candidate overflow, 2 non-finite sum, 3 no finite maximum, 6 ambiguous after the
+ * exact pass, 7 boundary bucket too large, 8 top-L below the candidates; 4 and 5 are no longer
+ * used). */
 
 #define VWS_MAX_VOCAB (1 << 19)       /* masses are floor(e * 2^44) summed in 64 bits */
 #define VWS_MAX_LOGPROBS 64

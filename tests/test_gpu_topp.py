@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
 
 STREAM = 0x200
 GENERAL = 0x100
+WIDE = 0x800
 
 
 def _wl(x, T, p, k=0, mp=0.0, L=None, seed=0, dtype="f32"):
@@ -38,7 +39,8 @@ def _check(w, cuda, label, min_stream=None):
     stream = int(((got["flags"] & STREAM) != 0).sum())
     general = int(((got["flags"] & GENERAL) != 0).sum())
     why = np.bincount((got["flags"] >> 16) & 0xFF, minlength=9)[1:]
-    print(f"{label}: {w.shape} stream rows {stream}, multi-pass rows {general}, "
+    wide = int(((got["flags"] & WIDE) != 0).sum())
+    print(f"{label}: {w.shape} stream rows {stream} (wide {wide}), multi-pass rows {general}, "
           f"fallback reasons {why.tolist()}", flush=True)
     assert_same(got, ref, label)
     if min_stream is not None:
@@ -160,3 +162,21 @@ def test_strided_unaligned_rows(cuda):
     ref = O.sample(x, prm, u)
     assert np.array_equal(res.sampled.cpu().numpy(), ref["token"])
     assert np.array_equal(res.num_kept.cpu().numpy(), ref["n_kept"])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("L", [None, 3])
+def test_wide_rows(cuda, dtype, L):
+    """Nuclei far larger than the candidate buffers (flat rows, high temperature, p near 1): one
+    exact pass over the logits and uniforms decides them; every fourth row also has a min-p
+    that keeps survivors below the candidates, and with logprobs the sampled token is mostly
+    not a candidate (its rank takes a pass of its own)."""
+    rng = np.random.default_rng(60 + (L or 0) + (5 if dtype == "bf16" else 0))
+    B, V = 16, 120000
+    x = rng.normal(0, 1.5, (B, V)).astype(np.float32)
+    T = rng.uniform(0.9, 1.6, B).astype(np.float32)
+    p = rng.uniform(0.9, 0.999, B).astype(np.float32)
+    w = _wl(x, T, p, seed=60, dtype=dtype, L=L)
+    w.min_p[::4] = np.float32(0.001)
+    got = _check(w, cuda, f"wide {dtype} L={L}")
+    assert int(((got["flags"] & WIDE) != 0).sum()) >= B - 2

@@ -32,6 +32,7 @@ FLAG_GREEDY = 0x8
 FLAG_GENERAL_PATH = 0x100
 FLAG_STREAM_TOPP = 0x200
 FLAG_TOPP_RECOUNT = 0x400
+FLAG_TOPP_WIDE = 0x800
 
 MAX_VOCAB = 1 << 19
 MAX_LOGPROBS = 64

@@ -188,6 +188,9 @@ __device__ __forceinline__ int gfind_from_top(const C* bins, int nb, uint64_t ta
 
 // ---- the row ------------------------------------------------------------------------------
 
+template <typename T>
+__device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem& sm, int r, int k);
+
 struct RaceAcc {
     uint64_t best = 0;     // (key bits << 32) | (0x7FFFFFFF - index), 0 = none
     uint32_t second = 0;   // key bits + 1 of the best non-winning key, 0 = none

@@ -136,6 +136,31 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
     return topp_compact(g_row_sh.t, w, cnt, aw, c, want_raw != 0);
 }
 
+template <typename T>
+__device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
+                                             float lp_min, uint32_t key, int bstar) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the kernarg segment exists only in the device pass
+    // every argument is uniform: into scalar registers (the buffer descriptors need them there)
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
+    using KArgsConst = const KArgs __attribute__((address_space(4)));
+    const KArgs a = *(KArgsConst*)(((uint64_t)hi << 32) | lo);
+    kind = __builtin_amdgcn_readfirstlane(kind);
+    r = __builtin_amdgcn_readfirstlane(r);
+    bstar = __builtin_amdgcn_readfirstlane(bstar);
+    key = tp_u(key);
+    Tt = tp_uf(Tt);
+    m = tp_uf(m);
+    lp_min = tp_uf(lp_min);
+    TopPSmem& sm = g_row_sh.t;
+    if (kind == kTpPassExact) topp_exact_pass<T>(a, sm, r, Tt, m, lp_min, key);
+    else if (kind == kTpPassWideRace) topp_wide_race<T>(a, sm, r, Tt, m, lp_min, key, bstar);
+    else topp_rank_pass<T>(a, sm, r, key);
+#else
+    (void)kind; (void)r; (void)kernarg; (void)Tt; (void)m; (void)lp_min; (void)key; (void)bstar;
+#endif
+}
+
 // Applies the logits processors and penalties to wave w's candidates [from, cnt), in place, and
 // returns the new count.  Candidates enter the buffer by their raw value; when nothing can raise
 // a logit (mode 1: bans, non-positive biases, penalties with r >= 1, f >= 0, p >= 0) the raw
@@ -1096,7 +1121,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
         __syncthreads();
         const RowP prm = row_params(a, r);
         topp_stream<T>(a, g_row_sh.t, r, prm);
-        why = topp_finish<T>(a, g_row_sh.t, r, prm);
+        why = topp_finish<T>(a, g_row_sh.t, r, prm, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u);
         if (why == 0) return;
     }
     __syncthreads();

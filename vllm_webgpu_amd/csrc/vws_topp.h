@@ -14,13 +14,18 @@
 //   * the exact mass of everything below the threshold lies in an interval [S_lo, S_hi] built
 //     from the approximate sum and its error bound.  Top-p's threshold, boundary bucket, cut
 //     inside that bucket and near-tie flags are computed at both ends of the interval; when
-//     they differ, one more pass over the row sums the exact masses below the threshold and
-//     the decision is taken again on the exact value;
+//     they differ, or when the boundary lies below the candidates (or min-p keeps elements
+//     below them), one more pass over the row adds the exact masses of everything below the
+//     candidates into the buckets and the decision is taken again on exact values;
+//   * when the boundary bucket then reaches the values below the candidates (a wide row), a
+//     further pass over the logits and the uniforms races the survivors it keeps there and
+//     gathers the boundary bucket's members there;
 //   * the race runs over the kept candidates (uniforms read at their positions only), and raw
-//     logprobs come from the candidates (top-L, rank) and the sums (log-sum-exp).
-// Rows with penalties, logits processors, an allowed mask or the soft cap, rows whose top-p
-// boundary falls below the threshold, and rows whose buffers overflow (ties) take the
-// multi-pass path instead; nothing is written for them here.
+//     logprobs come from the candidates (top-L, rank) and the sums (log-sum-exp); a sampled
+//     token below the candidates is ranked by one more pass.
+// Rows with penalties, logits processors, an allowed mask or the soft cap, rows whose buffers
+// overflow (ties) and the rare rows listed under VWS_FALLBACK_* take the multi-pass path
+// instead; nothing is written for them here.
 #pragma once
 
 #include "vws_row.h"
@@ -44,8 +49,6 @@ constexpr float kLog2e = 0x1.715476p+0f;  // log2(e) rounded to fp32
 constexpr int VWS_FALLBACK_OVERFLOW = 1;    // a wave's candidate buffer overflowed (ties)
 constexpr int VWS_FALLBACK_SUM = 2;         // the approximate sum is not finite
 constexpr int VWS_FALLBACK_DEGENERATE = 3;  // no finite row maximum
-constexpr int VWS_FALLBACK_MIN_P = 4;       // min-p may keep elements below the candidates
-constexpr int VWS_FALLBACK_BELOW = 5;       // top-p keeps elements below the candidates
 constexpr int VWS_FALLBACK_AMBIGUOUS = 6;   // the exact recount still cuts inconsistently
 constexpr int VWS_FALLBACK_GATHER = 7;      // the boundary bucket holds too many members
 constexpr int VWS_FALLBACK_TOPL = 8;        // the top-L logprobs reach below the candidates
@@ -119,8 +122,9 @@ __device__ __forceinline__ float tp_term(float x, float aw, float c, float& z) {
 }
 
 // Bucket of d = y - max <= 0: floor(-d * 64), the last bucket from -d >= 32 on (zero masses).
+// (d > 0 cannot occur; it would land in bucket 0.)
 __device__ __forceinline__ int tp_bucket(float d) {
-    const float dd = -d;
+    const float dd = __builtin_fmaxf(-d, 0.0f);
     return dd < 32.0f ? (int)(dd * 64.0f) : kTpBuckets - 1;
 }
 
@@ -438,51 +442,238 @@ __device__ __forceinline__ double tp_wave_sum_f64(double v) {
     return v;
 }
 
-// Exact sum of the masses of the survivors below the candidates (every element whose key is
-// below tauk), and their number: one more pass over the row, for rows the interval left
-// ambiguous.  Results are scalars; every thread calls it.
-template <typename T>
-__device__ __forceinline__ void topp_exact_below(const KArgs& a, TopPSmem& sm, int r, float Tt,
-                                                 float m, float lp_min, uint32_t tauk,
-                                                 uint64_t* mass, uint64_t* count) {
+// One more pass over row r in the finish (every thread calls it): the aligned body as 16-byte
+// buffer loads, UP vectors per thread per step with the next step's loads in flight, then the
+// unaligned head and tail (threads 0 and 1).  f(v, u, i0, ok) gets the VEC elements of one
+// vector from element i0 on (ok: the vector lies in the row; head and tail are NaN-padded)
+// and, with WITH_U, their uniforms (dword-aligned 16-byte loads; zeros past the row's end).
+template <typename T, bool WITH_U, typename F>
+__device__ __forceinline__ void tp_row_pass(const KArgs& a, int r, F&& f) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
+    constexpr int UW = WITH_U ? VEC / 4 : 0;          // uniform loads per vector
+    constexpr int UP = (WITH_U && VEC == 8) ? 2 : 4;  // vectors per thread per step
     const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int V = a.V;
     const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+    const float* urow = WITH_U ? a.u + (size_t)r * a.ustride : nullptr;
     Slice<T> sl;
-    sl.init(row, 0, a.V);
-    const int nch = sl.nchunks();
-    uint64_t w = 0ull, n = 0ull;
-    for (int c0 = tid; c0 < nch; c0 += NT) {
-        float v[VEC];
-        sl.load(c0, v);  // NaN outside the row
+    sl.init(row, 0, V);
+    const int nbody = sl.nbody;
+    const int nit = (nbody + NT * UP - 1) / (NT * UP);
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + sl.a, 16u * (uint32_t)nbody);
+    const __amdgpu_buffer_rsrc_t urs = make_rsrc(WITH_U ? (const void*)urow : (const void*)row,
+                                                 WITH_U ? 4u * (uint32_t)V : 0u);
+    auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
+    using W4 = decltype(__builtin_amdgcn_raw_buffer_load_b128(lrs, 0u, 0u, 0));
+    auto load = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], int it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < UP; ++q) {
+            const uint32_t vi = (uint32_t)(tid_now() + (it * UP + q) * NT);
+            lw[q] = __builtin_amdgcn_raw_buffer_load_b128(lrs, 16u * vi, 0u, 2 /* nt */);
+#pragma unroll
+            for (int g = 0; g < UW; ++g)
+                uw[q][g] = __builtin_amdgcn_raw_buffer_load_b128(
+                    urs, 4u * ((uint32_t)sl.a + vi * (uint32_t)VEC + 4u * (uint32_t)g), 0u, 2);
+        }
+    };
+    auto consume = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], int it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < UP; ++q) {
+            const int vi = (it * UP + q) * NT + tid_now();
+            float v[VEC], u[VEC];
+            Elem<T>::from_words((uint32_t)lw[q][0], (uint32_t)lw[q][1], (uint32_t)lw[q][2],
+                                (uint32_t)lw[q][3], v);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) u[j] = WITH_U ? u2f((uint32_t)uw[q][j / 4][j % 4]) : 0.0f;
+            f(v, u, sl.a + vi * VEC, vi < nbody);
+        }
+    };
+    W4 la[UP], lb[UP];
+    W4 ua[UP][UW > 0 ? UW : 1], ub[UP][UW > 0 ? UW : 1];
+    load(la, ua, 0);
+    load(lb, ub, 1);
+    for (int it = 0; it < nit; it += 2) {
+        consume(la, ua, it);
+        load(la, ua, it + 2);
+        if (it + 1 < nit) consume(lb, ub, it + 1);
+        load(lb, ub, it + 3);
+    }
+    if (wave == 0) {
+        float v[VEC], u[VEC];
+        int i0 = 0, end = 0;
+        if (tid <= 1) {
+            i0 = sl.load_edge(tid, v);
+            end = tid == 0 ? sl.a : V;
+        } else {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
+        }
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) u[j] = (WITH_U && i0 + j < end) ? urow[i0 + j] : 0.0f;
+        f(v, u, i0, tid <= 1);
+    }
+}
+
+// Exact masses of the survivors below the candidates (elements whose key is below tauk), each
+// added into its bucket of sm.h.hmass, which then holds every survivor of the row; thread 0
+// leaves their total mass and number in sm.bc64[10] and sm.bc64[11].  One pass over the row,
+// for rows whose decision the interval leaves open or puts below the candidates, and for min-p
+// rows with survivors below the candidates.
+template <typename T>
+__device__ __forceinline__ void topp_exact_pass(const KArgs& a, TopPSmem& sm, int r, float Tt,
+                                                float m, float lp_min, uint32_t tauk) {
+    constexpr int VEC = Elem<T>::kVec;
+    const int tid = threadIdx.x;
+    uint64_t sw = 0ull, n = 0ull;
+    tp_row_pass<T, false>(a, r, [&](const float* v, const float*, int, bool ok) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const uint32_t kx = key_of(v[j]);
             const float y = v[j] / Tt;
             const float d = y - m;
-            const bool s = kx != 0u && kx < tauk && key_of(y) != 0u && d >= lp_min;
-            w += s ? mass_of(exp_det(d)) : 0ull;
+            const bool s = ok && kx != 0u && kx < tauk && key_of(y) != 0u && d >= lp_min;
+            const uint64_t w = s ? mass_of(exp_det(d)) : 0ull;
+            if (w) atomicAdd((unsigned long long*)&sm.h.hmass[tp_bucket(d)], (unsigned long long)w);
+            sw += w;
             n += s ? 1ull : 0ull;
         }
-    }
-    w = wave_sum_u64(w);
+    });
+    sw = wave_sum_u64(sw);
     n = wave_sum_u64(n);
     __syncthreads();
     if (lane_id() == 0) {
-        sm.red[tid >> 6][0] = w;
+        sm.red[tid >> 6][0] = sw;
         sm.red[tid >> 6][1] = n;
     }
     __syncthreads();
-    *mass = tp_sum16(sm, 0);
-    *count = tp_sum16(sm, 1);
+    const uint64_t tw = tp_sum16(sm, 0), tn = tp_sum16(sm, 1);
+    if (tid == 0) {
+        sm.bc64[10] = tw;
+        sm.bc64[11] = tn;
+    }
 }
+
+// Smallest key k in [key(-inf), tauk) with P(k), for a predicate that holds from some key on;
+// tauk when none does.  Uniform bisection (scalar).
+template <typename P>
+__device__ __forceinline__ uint32_t tp_first_key(uint32_t tauk, P&& pred) {
+    uint32_t lo = 0x007FFFFFu, hi = tauk > lo ? tauk : lo;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (pred(mid)) hi = mid;
+        else lo = mid + 1u;
+    }
+    return lo;
+}
+
+// Wide rows (the boundary bucket bstar reaches the values below the candidates), once bstar is
+// known: the race over the survivors below the candidates that top-p keeps (buckets above
+// bstar), and bstar's members below the candidates appended to the gather list (key(y) << 32 |
+// index, counter sm.bc[4]).  The bucket of a value never rises as the value grows (x / T, y - m
+// and the bucket all round monotonically), and neither does min-p's test fail, so kept, boundary
+// and removed survivors are key ranges, found by bisection; the pass compares keys, and only
+// kept elements compute their race key (from the uniforms streamed with the logits).  Thread 0
+// leaves the race's best (RowRace::best), second (RowRace::second), the kept and the removed
+// counts in sm.bc64[10..13].
+template <typename T>
+__device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int r, float Tt,
+                                               float m, float lp_min, uint32_t tauk, int bstar) {
+    constexpr int VEC = Elem<T>::kVec;
+    const int tid = threadIdx.x, lane = tid & 63;
+    auto bucket_of_key = [&](uint32_t k) __attribute__((always_inline)) { return tp_bucket(val_of(k) / Tt - m); };
+    const uint32_t ksv = lp_min > -__builtin_inff()
+        ? tp_first_key(tauk, [&](uint32_t k) __attribute__((always_inline)) { return val_of(k) / Tt - m >= lp_min; })
+        : 0x007FFFFFu;
+    uint32_t kkeep = tp_first_key(tauk, [&](uint32_t k) __attribute__((always_inline)) { return bucket_of_key(k) < bstar; });
+    uint32_t kmem = tp_first_key(tauk, [&](uint32_t k) __attribute__((always_inline)) { return bucket_of_key(k) <= bstar; });
+    kkeep = tp_u(kkeep > ksv ? kkeep : ksv);
+    kmem = tp_u(kmem > ksv ? kmem : ksv);
+    RowRace rs;
+    uint32_t nrem = 0u;
+    tp_row_pass<T, true>(a, r, [&](const float* v, const float* u, int i0, bool ok) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const uint32_t kx = ok ? key_of(v[j]) : 0u;
+            if (kx >= tauk) continue;
+            if (kx >= kkeep) {
+                const float d = v[j] / Tt - m;
+                rs.nkept++;
+                rs.add_key(exp_det(d) / (0.0f - log_det(u[j])), i0 + j);
+            } else if (kx >= kmem) {
+                const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
+                if (pos < (uint32_t)kTpGather)
+                    sm.g.key[pos] = ((uint64_t)key_of(v[j] / Tt) << 32) | (uint32_t)(i0 + j);
+            } else {
+                nrem += kx >= ksv ? 1u : 0u;
+            }
+        }
+    });
+    rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
+    rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);
+    const uint64_t nr = wave_sum_u64(nrem);
+    __syncthreads();
+    if (lane == 0) {
+        sm.red[tid >> 6][0] = rs.best;
+        sm.red[tid >> 6][1] = ((uint64_t)rs.second << 32) | rs.nkept;
+        sm.red[tid >> 6][2] = nr;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        RowRace all;
+        uint64_t nremt = 0ull;
+        for (int w = 0; w < kTpWaves; ++w) {
+            RowRace o;
+            o.best = sm.red[w][0];
+            o.second = (uint32_t)(sm.red[w][1] >> 32);
+            o.nkept = (uint32_t)sm.red[w][1];
+            all.merge(o);
+            nremt += sm.red[w][2];
+        }
+        sm.bc64[10] = all.best;
+        sm.bc64[11] = all.second;
+        sm.bc64[12] = all.nkept;
+        sm.bc64[13] = nremt;
+    }
+}
+
+// Number of elements of row r whose raw value is at or above the one with key ks (> 0): the
+// rank of a sampled token that is not a candidate.  Scalar result; every thread calls it.
+template <typename T>
+__device__ __forceinline__ uint32_t topp_rank_pass(const KArgs& a, TopPSmem& sm, int r, uint32_t ks) {
+    constexpr int VEC = Elem<T>::kVec;
+    const int tid = threadIdx.x;
+    uint64_t n = 0ull;
+    tp_row_pass<T, false>(a, r, [&](const float* v, const float*, int, bool ok) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) n += (ok && key_of(v[j]) >= ks) ? 1ull : 0ull;
+    });
+    n = wave_sum_u64(n);
+    __syncthreads();
+    if (lane_id() == 0) sm.red[tid >> 6][0] = n;
+    __syncthreads();
+    const uint64_t t = tp_sum16(sm, 0);
+    if (tid == 0) sm.bc64[10] = t;
+    return (uint32_t)t;
+}
+
+// The finish's further passes over the row (the rarer cases) run out of line, so that their
+// registers stay out of the stream and the finish; defined next to the LDS they use.  Every
+// thread calls it; its scalar results are in sm.bc64[10..13] after a barrier.
+constexpr int kTpPassExact = 0;     // topp_exact_pass
+constexpr int kTpPassWideRace = 1;  // topp_wide_race (bstar)
+constexpr int kTpPassRank = 2;      // topp_rank_pass (key)
+template <typename T>
+__device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
+                                             float lp_min, uint32_t key, int bstar);
 
 // Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
 // take the multi-pass path (VWS_FALLBACK_*).  Every return decision is uniform over the
 // workgroup: values that decide are read from LDS after a barrier, or are scalars.
 template <typename T>
-__device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, const RowP& prm) {
+__device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
+                                           uint64_t kernarg) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -508,6 +699,10 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     const float lp_min = (!greedy && prm.min_p > 0.0f)
                              ? tp_uf(log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)) : -__builtin_inff();
     const float aw = tp_uf(sm.anchor);
+    auto pass = [&](int kind, uint32_t key, int bs) __attribute__((always_inline)) {
+        topp_pass_entry<T>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        __syncthreads();
+    };
     for (int i = tid; i < kTpBuckets; i += NT) {
         sm.h.hmass[i] = 0ull;
         sm.h.hcnt[i] = 0u;
@@ -553,7 +748,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         }
     }
     __syncthreads();
-    const uint64_t Wc = tp_sum16(sm, 0);
+    uint64_t Wc = tp_sum16(sm, 0);  // candidates' mass (wide rows: every survivor's)
     const uint64_t Sx = tp_sum16(sm, 1);
     const uint64_t NXS = tp_sum16(sm, 2);
     double S0b = 0.0;
@@ -611,10 +806,12 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 const double err = err0 * 1.01 + 2.0;
                 uint64_t nlo = 0ull, nhi = 0ull;
                 if (!(sap < 1e30 && err < 1e30)) why = VWS_FALLBACK_SUM;
+                sm.bc[10] = 0u;
                 if (lp_min > -__builtin_inff()) {
                     // min-p: the sum is exact (zero) only when no element below the candidates
-                    // survives it (the largest of them is the float just below the threshold)
-                    if (tauk > 0x00800000u && val_of(tauk - 1u) / Tt - m >= lp_min) why = VWS_FALLBACK_MIN_P;
+                    // survives it (the largest of them is the float just below the threshold);
+                    // otherwise the wide pass sums the survivors below the candidates exactly
+                    if (tauk > 0x00800000u && val_of(tauk - 1u) / Tt - m >= lp_min) sm.bc[10] = 1u;
                     sm.bc[9] = 0u;
                 } else {
                     const double lo = floor(sap - err) - nterms;
@@ -634,12 +831,29 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         bool any_below_nc = tp_u(sm.bc[9]) != 0u || NXS > 0ull;
         uint64_t S[2] = {tp_u64(sm.bc64[0]), tp_u64(sm.bc64[1])};
 
-        // decides top-p for S[0] and S[1]; when they differ, once more on the exact value
+        // decides top-p for S[0] and S[1]; when they differ, or when the boundary lies below
+        // the candidates, the exact pass puts every survivor's exact mass into the buckets (S is
+        // 0 from then on) and the decision is taken once more.  A boundary bucket at or below
+        // the largest value under the candidates makes the row wide: one more pass races the
+        // kept survivors below the candidates and gathers the boundary bucket's members there.
         int bstar = -1, gathered = -1;
         uint32_t ng = 0u, cpos = 0u, tflags = 0u;
         bool ranked = false;
-        uint64_t thr0 = 0ull, W0 = 0ull, cat0 = 0ull;
-        for (int attempt = 0;; ++attempt) {
+        bool exact = false, wide = false, go_exact = tp_u(sm.bc[10]) != 0u;
+        int bnc = kTpBuckets;       // bucket of the largest value below the candidates
+        uint64_t wide_kept = 0ull;  // survivors below the candidates kept (wide rows)
+        uint64_t wbest = 0ull;      // and their race (RowRace fields)
+        uint32_t wsec = 0u;
+        for (;;) {
+            if (go_exact && !exact) {
+                pass(kTpPassExact, tauk, 0);
+                Wc += tp_u64(sm.bc64[10]);
+                any_below_nc = tp_u64(sm.bc64[11]) > 0ull;
+                S[0] = S[1] = 0ull;
+                exact = true;
+                if (tauk > 0x007FFFFFu) bnc = tp_bucket(val_of(tauk - 1u) / Tt - m);
+                flags |= VWS_FLAG_TOPP_RECOUNT;
+            }
             uint64_t thr[2], W[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -647,7 +861,10 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 thr[e] = scale_floor(q32, W[e]);
             }
             bool decided = false;
-            if (S[0] > thr[0] && S[1] > thr[1]) return VWS_FALLBACK_BELOW;  // boundary below the candidates
+            if (S[0] > thr[0] && S[1] > thr[1]) {  // the boundary lies below the candidates
+                go_exact = true;
+                continue;
+            }
             if (S[0] <= thr[0] && S[1] <= thr[1]) {
                 // ---- boundary bucket: the last b (from the top) with S + suffix(b) > thr
                 if (tid == 0) {
@@ -677,6 +894,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                     // ---- the boundary bucket's members
                     if (gathered != bstar) {
                         gathered = bstar;
+                        wide = exact && bstar >= bnc;
+                        __syncthreads();
                         if (tid == 0) sm.bc[4] = 0u;
                         __syncthreads();
                         for (int i = lane; i < cnt; i += kWave) {
@@ -688,6 +907,14 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                             const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
                             if (pos < (uint32_t)kTpGather)
                                 sm.g.key[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.ci[wave][i];
+                        }
+                        if (wide) {
+                            pass(kTpPassWideRace, tauk, bstar);
+                            wbest = tp_u64(sm.bc64[10]);
+                            wsec = (uint32_t)tp_u64(sm.bc64[11]);
+                            wide_kept = tp_u64(sm.bc64[12]);
+                            any_below_nc = tp_u64(sm.bc64[13]) > 0ull;
+                            flags |= VWS_FLAG_TOPP_WIDE;
                         }
                         __syncthreads();
                         ng = tp_u(sm.bc[4]);
@@ -779,7 +1006,6 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                             const uint64_t tol = (uint64_t)((double)W[e] * 1e-6);
                             t1[e] = (thr[e] - cprev <= tol) ? 1u : 0u;
                             t2[e] = (cat > thr[e] && cat - thr[e] <= tol) ? 2u : 0u;
-                            if (e == 0) { thr0 = thr[0]; W0 = W[0]; cat0 = cat; }
                         }
                         if (t1[0] == t1[1] && t2[0] == t2[1]) {
                             tflags = t1[0] | t2[0];
@@ -789,17 +1015,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 }
             }
             if (decided) break;
-            if (attempt) return VWS_FALLBACK_AMBIGUOUS;
-            // ambiguous: the exact mass below the candidates, then the decision once more
-            uint64_t exact, nbelow;
-            topp_exact_below<T>(a, sm, r, Tt, m, lp_min, tauk, &exact, &nbelow);
-            S[0] = S[1] = exact;
-            any_below_nc = nbelow > 0ull;
-            flags |= VWS_FLAG_TOPP_RECOUNT;
+            if (exact) return VWS_FALLBACK_AMBIGUOUS;
+            go_exact = true;  // ambiguous: once more on the exact masses
         }
-        (void)thr0;
-        (void)W0;
-        (void)cat0;
 
         // ---- race over the kept survivors: candidates above the boundary bucket, and the
         // boundary bucket's members from the cut on
@@ -849,6 +1067,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         __syncthreads();
         if (tid == 0) {
             RowRace all;
+            all.best = wbest;  // the race below the candidates (wide rows), counted once
+            all.second = wsec;
             uint64_t nbelow = 0ull;
             for (int w = 0; w < kTpWaves; ++w) {
                 RowRace o;
@@ -877,7 +1097,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             }
             sm.bc[12] = (uint32_t)tok;
             sm.bc[13] = f;
-            sm.bc[14] = all.nkept;
+            sm.bc[14] = all.nkept + (uint32_t)wide_kept;
         }
         __syncthreads();
         token = (int32_t)tp_u(sm.bc[12]);
@@ -892,9 +1112,16 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
         xs = tp_uf(Elem<T>::load1(row + token));
         const uint32_t ks = key_of(xs);
+        // a sampled token below the candidates (wide rows) is ranked by a pass over the row
+        const bool rank_pass = ks < tauk;
         uint32_t rk = 0u;
-        for (int i = lane; i < cnt; i += kWave) rk += sm.ck[wave][i] >= ks ? 1u : 0u;
-        rk = (uint32_t)wave_sum_u64(rk);
+        if (rank_pass) {
+            pass(kTpPassRank, ks, 0);
+            rk = wave == 0 ? (uint32_t)tp_u64(sm.bc64[10]) : 0u;  // the per-wave records below add up
+        } else {
+            for (int i = lane; i < cnt; i += kWave) rk += sm.ck[wave][i] >= ks ? 1u : 0u;
+            rk = (uint32_t)wave_sum_u64(rk);
+        }
         uint32_t ncand = 0u;
         {
             // the L largest raw values lie in the buckets from the top that hold L candidates
