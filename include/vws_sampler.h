@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 3
+#define VWS_ABI_VERSION 4
 
 /* status codes */
 #define VWS_OK 0
@@ -44,6 +44,7 @@ extern "C" {
 /* logits element types */
 #define VWS_DTYPE_F32 0
 #define VWS_DTYPE_BF16 1
+#define VWS_DTYPE_F16 2  /* IEEE binary16 (the reference's f16 logits), widened exactly */
 
 /* per-row result flags (vws_sample_args.row_flags) */
 #define VWS_FLAG_TOPP_NEAR_TIE 0x1u  /* top-p cumulative mass within 1e-6 of the threshold */
@@ -76,6 +77,9 @@ typedef struct vws_sample_args {
      * e = exp(2v), fp32).  Everything downstream -- processors, penalties, raw logprobs --
      * sees the capped values.  0 = off. */
     float logit_softcap;
+    /* Non-zero: each capped value is rounded to f16 (nearest, ties to even) and widened back,
+     * as the reference's shader stores it into an f16 buffer (logit_softcap.wgsl:28). */
+    int32_t logit_softcap_f16;
 
     /* Per-row parameters, device arrays of length B.  NULL selects the default:
      * temperature NULL = every row greedy; top_k NULL/<=0/>=V = off; top_p NULL/>=1 = off;
@@ -214,7 +218,7 @@ int vws_profile_begin(int32_t max_launches);
 int vws_profile_end(double* ms, int32_t* count);
 
 /* Device self-test of the sampler arithmetic: evaluates fn (0 = exp_det, 1 = log_det,
- * 2 = the logit soft cap at cap 1, i.e. its tanh) at
+ * 2 = the logit soft cap at cap 1, i.e. its tanh, 3 = fp32 -> f16 -> fp32 rounding) at
  * every fp32 whose order key lies in [key_lo, key_hi] and accumulates the same 64-bit hash
  * as the CPU oracle's checker into out2[0] and the count into out2[1] (device u64[2],
  * zeroed by this call). */

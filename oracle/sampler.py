@@ -68,8 +68,12 @@ def lib() -> ctypes.CDLL:
             L.vwo_scale_floor.restype = ctypes.c_uint64
             L.vwo_sample_batch.argtypes = [P, ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P, P,
                                            ctypes.c_int, P, P, ctypes.c_int, P, P, ctypes.c_int,
-                                           P, P, P, ctypes.c_int, P, P, P, P, ctypes.c_float]
-            L.vwo_softcap_row.argtypes = [P, ctypes.c_int, ctypes.c_float, P]
+                                           P, P, P, ctypes.c_int, P, P, P, P, ctypes.c_float,
+                                           ctypes.c_int]
+            L.vwo_softcap_row.argtypes = [P, ctypes.c_int, ctypes.c_float, ctypes.c_int, P]
+            L.vwo_check_round_f16.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_uint32, P, P]
+            L.vwo_round_f16.argtypes = [ctypes.c_float]
+            L.vwo_round_f16.restype = ctypes.c_float
             L.vwo_apply_adjustments_row.argtypes = [P, ctypes.c_int, P, P, P, ctypes.c_int]
             L.vwo_apply_penalties_row.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, ctypes.c_int,
                                                   ctypes.c_float, ctypes.c_float, ctypes.c_float]
@@ -139,6 +143,13 @@ def check_softcap(lo: float, hi: float):
     lib().vwo_check_softcap(ctypes.c_float(lo), ctypes.c_float(hi), ctypes.byref(me),
                             ctypes.byref(w), ctypes.byref(h), ctypes.byref(c), ctypes.byref(d))
     return dict(max_err=me.value, worst=w.value, hash=h.value, count=c.value, max_drop=d.value)
+
+
+def check_round_f16(lo: float, hi: float, stride: int = 1):
+    """vwo_round_f16 on every fp32 of [lo, hi]: hash and count (as check_exp)."""
+    h, c = ctypes.c_uint64(), ctypes.c_uint64()
+    lib().vwo_check_round_f16(lo, hi, stride, ctypes.byref(h), ctypes.byref(c))
+    return dict(hash=h.value, count=c.value)
 
 
 def _check(name, lo, hi, stride):
@@ -229,7 +240,8 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
            prompt_lens: np.ndarray | None = None, output_lens: np.ndarray | None = None,
            num_logprobs: int | None = None, allowed: np.ndarray | None = None,
            adjust_ids: np.ndarray | None = None, adjust_vals: np.ndarray | None = None,
-           adjust_lens: np.ndarray | None = None, softcap: float | None = None) -> dict:
+           adjust_lens: np.ndarray | None = None, softcap: float | None = None,
+           softcap_f16: bool = False) -> dict:
     """Samples every row of fp32 ``logits`` [B, V].
 
     ``params``: PARAMS_DTYPE [B] (see make_params).  ``uniforms``: fp32 [B, V] in (0, 1).
@@ -237,7 +249,8 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
     Logits processors (before the penalties): ``allowed`` uint32 [B, ceil(V/32)] bitmask (bit
     set = allowed, None = all); ``adjust_ids`` int32 / ``adjust_vals`` fp32 [B, Wa]: value
     -inf bans the token, a finite value is added (logit bias).
-    ``softcap`` > 0: the logits first go through Gemma's soft cap (see ``softcap_row``).
+    ``softcap`` > 0: the logits first go through Gemma's soft cap (see ``softcap_row``), each
+    result rounded to f16 when ``softcap_f16``.
     Returns dict(token, flags, n_kept, n_topk, mass_total, threshold, row_max, kth_y,
     [lp_ids, lp_vals, ranks]).
     """
@@ -270,16 +283,22 @@ def sample(logits: np.ndarray, params: np.ndarray, uniforms: np.ndarray | None =
                            _ptr(al), 0 if al is None else al.shape[1],
                            _ptr(ai), _ptr(av), 0 if ai is None else ai.shape[1], _ptr(an),
                            _ptr(prm), _ptr(u), L, _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks),
-                           _ptr(outs), float(softcap or 0.0))
+                           _ptr(outs), float(softcap or 0.0), 1 if softcap_f16 else 0)
     res = {name: outs[name].copy() for name in ROW_OUT_DTYPE.names}
     if L >= 0:
         res.update(lp_ids=lp_ids, lp_vals=lp_vals, ranks=ranks)
     return res
 
 
-def softcap_row(x: np.ndarray, cap: float) -> np.ndarray:
-    """cap * tanh(x / cap) with the oracle's arithmetic (vwo_softcap), fp32 in and out."""
+def softcap_row(x: np.ndarray, cap: float, round_f16: bool = False) -> np.ndarray:
+    """cap * tanh(x / cap) with the oracle's arithmetic (vwo_softcap), fp32 in and out; each
+    result rounded to f16 and widened back when ``round_f16``."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(x)
-    lib().vwo_softcap_row(_ptr(x), x.size, float(cap), _ptr(out))
+    lib().vwo_softcap_row(_ptr(x), x.size, float(cap), 1 if round_f16 else 0, _ptr(out))
     return out
+
+
+def round_f16(x: float) -> float:
+    """vwo_round_f16: fp32 -> binary16 (nearest, ties to even) -> fp32."""
+    return lib().vwo_round_f16(float(x))

@@ -113,9 +113,35 @@ float vwo_softcap(float x, float inv_cap, float cap) {
     return t * cap;
 }
 
-void vwo_softcap_row(const float* x, int V, float cap, float* out) {
+/* fp32 -> binary16 (round to nearest, ties to even; overflow to +-inf, underflow through the
+ * subnormals to +-0) -> fp32: the value an f16 store keeps, widened back exactly.  The
+ * reference's soft-cap shader writes its fp32 result t * cap into an f16 buffer
+ * (vllm_webgpu/shaders/gemma/logit_softcap.wgsl:28). */
+float vwo_round_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    const int neg = (x >> 31) != 0u;
+    if (ax > 0x7F800000u) return f;                      /* NaN */
+    if (ax >= 0x477FF000u) return neg ? -INFINITY : INFINITY;  /* >= 65520: rounds to inf */
+    if (ax <= 0x33000000u) return neg ? -0.0f : 0.0f;    /* <= 2^-25: ties to 0 (even) */
+    const int e = (int)(ax >> 23) - 127;                 /* -25 <= e <= 15 */
+    const int shift = e < -14 ? 13 + (-14 - e) : 13;     /* mantissa bits an f16 drops */
+    uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    m >>= shift;
+    if (rem > half || (rem == half && (m & 1u))) m += 1u;
+    const float r = ldexpf((float)m, e - 23 + shift);   /* exact: m <= 2^11 */
+    return neg ? -r : r;
+}
+
+/* The soft cap of a row; round_f16: each result as an f16 store keeps it. */
+void vwo_softcap_row(const float* x, int V, float cap, int round_f16, float* out) {
     const float inv = 1.0f / cap;
-    for (int i = 0; i < V; ++i) out[i] = vwo_softcap(x[i], inv, cap);
+    for (int i = 0; i < V; ++i) {
+        const float c = vwo_softcap(x[i], inv, cap);
+        out[i] = round_f16 ? vwo_round_f16(c) : c;
+    }
 }
 
 /* floor(e * 2^44) for e in [0, 1] (0 for e <= 0 or NaN). */
@@ -399,20 +425,21 @@ logprobs:
 /* Batched driver (rows are independent; OpenMP over rows when built with -fopenmp).
  * prompt/output: padded [B, *_stride] with ids outside [0, V) ignored; lens may be NULL.
  * softcap > 0: the logits are first mapped through vwo_softcap (they are the model's output
- * then: processors, penalties and the raw logprobs all see the capped values). */
+ * then: processors, penalties and the raw logprobs all see the capped values); softcap_f16:
+ * each capped value rounded as an f16 store (vwo_round_f16). */
 int vwo_sample_batch(const float* logits, int B, int V, const int32_t* prompt, int prompt_stride,
                      const int32_t* prompt_lens, const int32_t* output, int output_stride,
                      const int32_t* output_lens, const uint32_t* allowed, int allowed_stride,
                      const int32_t* adj_ids, const float* adj_vals, int adj_stride,
                      const int32_t* adj_lens, const vwo_params* prm, const float* uniforms,
                      int L, int32_t* lp_ids, float* lp_vals, int32_t* ranks, vwo_row_out* outs,
-                     float softcap) {
+                     float softcap, int softcap_f16) {
 #pragma omp parallel for schedule(dynamic, 1)
     for (int b = 0; b < B; ++b) {
         float* capped = NULL;
         if (softcap > 0.0f) {
             capped = (float*)malloc(sizeof(float) * (size_t)V);
-            vwo_softcap_row(logits + (size_t)b * V, V, softcap, capped);
+            vwo_softcap_row(logits + (size_t)b * V, V, softcap, softcap_f16, capped);
         }
         const int np = prompt ? (prompt_lens ? prompt_lens[b] : prompt_stride) : 0;
         const int no = output ? (output_lens ? output_lens[b] : output_stride) : 0;
@@ -488,6 +515,29 @@ void vwo_check_exp(float lo, float hi, uint32_t stride, int64_t* max_ulp, float*
         }
     }
     *max_ulp = mu; *worst = wd; *hash = h; *count = c;
+}
+
+/* vwo_round_f16 on every fp32 of [lo, hi] (bit stride): the same hash as vwo_check_exp, to
+ * compare with the device's fp32 -> f16 -> fp32 conversion. */
+void vwo_check_round_f16(float lo, float hi, uint32_t stride, uint64_t* hash, uint64_t* count) {
+    uint64_t h = 0, c = 0;
+    const uint32_t klo = vwo_key(lo), khi = vwo_key(hi);
+#pragma omp parallel
+    {
+        uint64_t lh = 0, lc = 0;
+#pragma omp for schedule(static)
+        for (int64_t kk = klo; kk <= (int64_t)khi; kk += stride) {
+            const uint32_t key = (uint32_t)kk;
+            const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+            lh += (uint64_t)f2u(vwo_round_f16(u2f(bits))) * 0x9E3779B97F4A7C15ull ^ (uint64_t)bits;
+            lc++;
+        }
+#pragma omp critical
+        {
+            h += lh; c += lc;
+        }
+    }
+    *hash = h; *count = c;
 }
 
 /* vwo_softcap at cap 1 (t(x), the cap's tanh) on every fp32 x whose key lies in [lo, hi]: the

@@ -13,23 +13,23 @@ LP_RTOL = 1e-5
 LP_ATOL = 1e-6
 
 
-def oracle_run(w, num_logprobs=None, softcap=None):
+def oracle_run(w, num_logprobs=None, softcap=None, softcap_f16=False):
     B = w.shape[0]
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
     return O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids,
                     num_logprobs=w.num_logprobs if num_logprobs is None else num_logprobs,
-                    softcap=softcap)
+                    softcap=softcap, softcap_f16=softcap_f16)
 
 
-def gpu_run(w, device, num_logprobs=None, softcap=None):
+def gpu_run(w, device, num_logprobs=None, softcap=None, softcap_f16=False):
     import torch
 
     from vllm_webgpu_amd import ops
 
     if w.dtype == "bf16":
         logits = torch.from_numpy(w.logits.view(np.int16)).to(device).view(torch.bfloat16)
-    else:
+    else:  # float32 or float16, sampled as they are
         logits = torch.from_numpy(w.logits).to(device)
     greedy_all = bool(np.all(~(w.temperature >= np.float32(1e-5))))
     T = torch.from_numpy(w.temperature)
@@ -43,7 +43,8 @@ def gpu_run(w, device, num_logprobs=None, softcap=None):
                      repetition_penalty=torch.from_numpy(w.repetition),
                      presence_penalty=torch.from_numpy(w.presence),
                      frequency_penalty=torch.from_numpy(w.frequency), output_ids=hist,
-                     uniforms=U, num_logprobs=L, logit_softcap=softcap)
+                     uniforms=U, num_logprobs=L, logit_softcap=softcap,
+                     logit_softcap_f16=softcap_f16)
     torch.cuda.synchronize()
     out = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
                n_kept=res.num_kept.cpu().numpy())

@@ -87,3 +87,60 @@ def test_sampler_caps_first():
     for key in ("token", "flags", "n_kept", "lp_ids", "lp_vals", "ranks"):
         assert np.array_equal(a[key], b[key]), key
     assert a["token"][0] < 50            # greedy over 50 tied maxima at +cap: lowest index
+
+
+def test_round_f16_matches_numpy():
+    """vwo_round_f16 against numpy's float32 -> float16 cast (round to nearest even) on random
+    values of every magnitude, the f16 boundaries (max, overflow midpoint, subnormals, the
+    smallest subnormal's half) and the specials."""
+    rng = np.random.default_rng(4)
+    bits = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    special = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 65536.0, -65520.0,
+                        2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0000001, 2.0 ** -26, 3 * 2.0 ** -25,
+                        2.0 ** -14, 2.0 ** -14 * (1 - 2 ** -11), 6.1e-5, 1e-8, 30.0, 29.99,
+                        np.inf, -np.inf], np.float32)
+    ties = (np.arange(1, 4000, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -10)
+    scaled = (rng.standard_normal(50000) * 30).astype(np.float32)
+    for v in (x, special, ties, scaled):
+        with np.errstate(over="ignore"):
+            want = v.astype(np.float16).astype(np.float32)
+        got = np.array([O.round_f16(float(t)) for t in v], np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+            v[got.view(np.uint32) != want.view(np.uint32)][:5]
+    assert np.isnan(O.round_f16(float("nan")))
+
+
+def test_reference_known_answer_f16_store():
+    """The reference's test compares f16 results; with the f16 store the cap's output is an f16
+    value itself."""
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        x = (rng.standard_normal(64) * 50.0).astype(np.float16).astype(np.float32)
+        expected = (np.tanh(x / 30.0) * 30.0).astype(np.float16).astype(np.float32)
+        got = O.softcap_row(x, 30.0, round_f16=True)
+        assert np.array_equal(got, got.astype(np.float16).astype(np.float32))
+        np.testing.assert_allclose(got, expected, rtol=1e-2, atol=1e-2)
+
+
+def test_sampler_caps_first_f16_store():
+    """sample(x, softcap=c, softcap_f16=True) == sample(f16(softcap_row(x, c))), including
+    greedy rows whose maxima tie only after the f16 rounding (lowest index wins)."""
+    rng = np.random.default_rng(6)
+    B, V = 5, 4000
+    x = (rng.standard_normal((B, V)) * 40).astype(np.float32)
+    x[0, [100, 2000, 3000]] = [70.0, 70.01, 70.02]   # distinct in fp32, one f16 value once capped
+    x[3, [5, 6]] = [60.0, 60.001]
+    prm = O.make_params(B, np.array([0.0, 0.8, 1.0, 0.0, 0.6], np.float32),
+                        np.array([0, 20, 0, 0, 100], np.int32), 0.9, 0.0, 1.0, 0.0, 0.0)
+    u = rng.uniform(1e-7, 1.0, (B, V)).astype(np.float32)
+    capped = np.stack([O.softcap_row(r, 30.0, round_f16=True) for r in x])
+    assert capped[0, 100] == capped[0, 2000] == capped[0, 3000]
+    assert O.softcap_row(x[0, [100, 2000]], 30.0)[0] != O.softcap_row(x[0, [100, 2000]], 30.0)[1]
+    a = O.sample(x, prm, u, num_logprobs=3, softcap=30.0, softcap_f16=True)
+    b = O.sample(capped, prm, u, num_logprobs=3)
+    for key in ("token", "flags", "n_kept", "lp_ids", "lp_vals", "ranks"):
+        assert np.array_equal(a[key], b[key]), key
+    if capped[0].max() == capped[0, 100]:
+        assert a["token"][0] == np.flatnonzero(capped[0] == capped[0].max())[0]

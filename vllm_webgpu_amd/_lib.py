@@ -14,7 +14,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2
@@ -24,6 +24,7 @@ ERR_LIMIT = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
 
 FLAG_TOPP_NEAR_TIE = 0x1
 FLAG_RACE_NEAR_TIE = 0x2
@@ -62,6 +63,7 @@ class SampleArgs(ctypes.Structure):
     _fields_ = [
         ("struct_size", _U32), ("batch", _I32), ("vocab", _I32), ("dtype", _I32),
         ("logits", _P), ("logits_row_stride", _I64), ("logit_softcap", ctypes.c_float),
+        ("logit_softcap_f16", _I32),
         ("temperature", _P), ("top_k", _P), ("top_p", _P), ("min_p", _P),
         ("repetition_penalty", _P), ("presence_penalty", _P), ("frequency_penalty", _P),
         ("prompt_ids", _P), ("prompt_row_stride", _I64), ("prompt_width", _I32), ("prompt_lens", _P),

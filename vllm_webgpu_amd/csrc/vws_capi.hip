@@ -101,7 +101,7 @@ void choose_parts(int B, int V, int esize, int* S, int* part_len) {
     *part_len = len;
 }
 
-int esize_of(int dtype) { return dtype == VWS_DTYPE_BF16 ? 2 : 4; }
+int esize_of(int dtype) { return dtype == VWS_DTYPE_F32 ? 4 : 2; }
 
 // Per-device address of `scratch`, looked up once per device with that device current and
 // cleared once by a fill kernel on the caller's stream (the kernels also clear what they use).
@@ -162,7 +162,7 @@ int validate_rows(const void* logits, int32_t dtype, int32_t B, int32_t V, int64
     if (B < 1) return fail(VWS_ERR_INVALID_ARGUMENT, "batch must be >= 1 (got %d)", B);
     if (V < 1 || V > VWS_MAX_VOCAB)
         return fail(VWS_ERR_LIMIT, "vocab must be in [1, %d] (got %d)", VWS_MAX_VOCAB, V);
-    if (dtype != VWS_DTYPE_F32 && dtype != VWS_DTYPE_BF16)
+    if (dtype != VWS_DTYPE_F32 && dtype != VWS_DTYPE_BF16 && dtype != VWS_DTYPE_F16)
         return fail(VWS_ERR_UNSUPPORTED_DTYPE, "unsupported logits dtype %d", dtype);
     if (stride < V) return fail(VWS_ERR_INVALID_ARGUMENT, "logits_row_stride %lld < vocab %d", (long long)stride, V);
     return VWS_OK;
@@ -296,6 +296,7 @@ int vws_sample(const vws_sample_args* a) {
     k.adjlens = a->adjust_lens;
     k.softcap = a->logit_softcap;
     k.inv_softcap = a->logit_softcap > 0.0f ? 1.0f / a->logit_softcap : 0.0f;
+    k.softcap_f16 = (a->logit_softcap > 0.0f && a->logit_softcap_f16) ? 1 : 0;
     k.u = a->uniforms;
     k.ustride = a->uniforms_row_stride;
     k.sampled = a->sampled;
@@ -313,8 +314,10 @@ int vws_sample(const vws_sample_args* a) {
     const int ps = prof_start(s, VWS_KERNEL_SAMPLE);
     if (a->dtype == VWS_DTYPE_F32)
         hipLaunchKernelGGL(row_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
-    else
+    else if (a->dtype == VWS_DTYPE_BF16)
         hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
+    else
+        hipLaunchKernelGGL(row_kernel<_Float16>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
     prof_stop(s, ps);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();
@@ -359,9 +362,12 @@ int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, 
     if (dtype == VWS_DTYPE_F32)
         hipLaunchKernelGGL(argmax_kernel<float>, dim3(batch), dim3(1024), 0, s,
                            static_cast<const float*>(logits), row_stride, vocab, out_ids);
-    else
+    else if (dtype == VWS_DTYPE_BF16)
         hipLaunchKernelGGL(argmax_kernel<uint16_t>, dim3(batch), dim3(1024), 0, s,
                            static_cast<const uint16_t*>(logits), row_stride, vocab, out_ids);
+    else
+        hipLaunchKernelGGL(argmax_kernel<_Float16>, dim3(batch), dim3(1024), 0, s,
+                           static_cast<const _Float16*>(logits), row_stride, vocab, out_ids);
     prof_stop(s, ps);
     if ((st = check_launch("vws_argmax"))) return st;
     return ok();
@@ -394,16 +400,20 @@ int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, in
     const int ps = prof_start(s, VWS_KERNEL_TOPK);
     if (dtype == VWS_DTYPE_F32)
         hipLaunchKernelGGL(fast_kernel<float>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
-    else
+    else if (dtype == VWS_DTYPE_BF16)
         hipLaunchKernelGGL(fast_kernel<uint16_t>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
+    else
+        hipLaunchKernelGGL(fast_kernel<_Float16>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
     prof_stop(s, ps);
     if ((st = check_launch("vws_topk"))) return st;
     // rows whose single-pass candidate lists overflowed (ties) are finished exactly here
     const int pg = prof_start(s, VWS_KERNEL_TOPK);
     if (dtype == VWS_DTYPE_F32)
         hipLaunchKernelGGL(general_kernel<float>, dim3(batch), dim3(kGenThreads), 0, s, ka);
-    else
+    else if (dtype == VWS_DTYPE_BF16)
         hipLaunchKernelGGL(general_kernel<uint16_t>, dim3(batch), dim3(kGenThreads), 0, s, ka);
+    else
+        hipLaunchKernelGGL(general_kernel<_Float16>, dim3(batch), dim3(kGenThreads), 0, s, ka);
     prof_stop(s, pg);
     if ((st = check_launch("vws_topk (general kernel)"))) return st;
     return ok();
@@ -420,9 +430,13 @@ int vws_softmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,
         hipLaunchKernelGGL(softmax_kernel<float>, dim3(batch), dim3(1024), 0, s,
                            static_cast<const float*>(logits), row_stride, vocab, temperature, probs,
                            row_max, log_sum);
-    else
+    else if (dtype == VWS_DTYPE_BF16)
         hipLaunchKernelGGL(softmax_kernel<uint16_t>, dim3(batch), dim3(1024), 0, s,
                            static_cast<const uint16_t*>(logits), row_stride, vocab, temperature,
+                           probs, row_max, log_sum);
+    else
+        hipLaunchKernelGGL(softmax_kernel<_Float16>, dim3(batch), dim3(1024), 0, s,
+                           static_cast<const _Float16*>(logits), row_stride, vocab, temperature,
                            probs, row_max, log_sum);
     prof_stop(s, ps);
     if ((st = check_launch("vws_softmax"))) return st;
@@ -465,7 +479,7 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
 }
 
 int vws_math_selftest(int32_t fn, uint32_t key_lo, uint32_t key_hi, uint64_t* out2, void* stream) {
-    if (fn < 0 || fn > 2) return fail(VWS_ERR_INVALID_ARGUMENT, "fn must be 0 (exp), 1 (log) or 2 (soft cap)");
+    if (fn < 0 || fn > 3) return fail(VWS_ERR_INVALID_ARGUMENT, "fn must be 0 (exp), 1 (log), 2 (soft cap) or 3 (f16 rounding)");
     if (!out2) return fail(VWS_ERR_INVALID_ARGUMENT, "out2 is NULL");
     if (key_hi < key_lo) return fail(VWS_ERR_INVALID_ARGUMENT, "key_hi < key_lo");
     hipStream_t s = (hipStream_t)stream;

@@ -81,6 +81,16 @@ __device__ __forceinline__ float softcap_det(float x, float inv_cap, float cap) 
     return x != x ? x : t * cap;
 }
 
+// fp32 -> f16 (nearest, ties to even; overflow to +-inf) -> fp32: what an f16 store keeps.
+__device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)v; }
+
+// The model's capped logit: softcap_det, rounded as an f16 store when the model stores the
+// cap's output in f16 (vllm_webgpu/shaders/gemma/logit_softcap.wgsl:28).
+__device__ __forceinline__ float softcap_out(float x, float inv_cap, float cap, bool f16) {
+    const float c = softcap_det(x, inv_cap, cap);
+    return f16 ? round_f16(c) : c;
+}
+
 // An upper bound on softcap_det(x') over every x' <= x (NaN excluded).  The fp32 tanh above is
 // not monotone: over every fp32 v in [-20, 20] (it is constant outside), the largest drop
 // max_{v' <= v} t(v') - t(v) is 2^-22.  v = x * (1 / cap) and t * cap round monotonically, so
@@ -435,6 +445,26 @@ template <> struct Elem<uint16_t> {  // bfloat16 bit patterns, widened exactly
         for (int i = 0; i < 4; ++i) {
             out[2 * i] = u2f(w[i] << 16);
             out[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+        }
+    }
+};
+
+template <> struct Elem<_Float16> {  // IEEE binary16, widened exactly
+    static constexpr int kVec = 8;
+    __device__ __forceinline__ static float lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+    __device__ __forceinline__ static float hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+    __device__ __forceinline__ static float load1(const _Float16* p) { return (float)*p; }
+    __device__ __forceinline__ static void load_vec(const _Float16* p, float* out) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        from_words(v.x, v.y, v.z, v.w, out);
+    }
+    __device__ __forceinline__ static void from_words(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                      float* out) {
+        const uint32_t w[4] = {w0, w1, w2, w3};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[2 * i] = lo(w[i]);
+            out[2 * i + 1] = hi(w[i]);
         }
     }
 };

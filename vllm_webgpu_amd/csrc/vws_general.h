@@ -281,7 +281,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             if (kk) {
                 const uint32_t v = __hip_atomic_load(&hval[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 float raw = Elem<T>::load1(row + (kk - 1u));
-                if (a.softcap > 0.0f) raw = softcap_det(raw, a.inv_softcap, a.softcap);
+                if (a.softcap > 0.0f) raw = softcap_out(raw, a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 const float bias = u2f(__hip_atomic_load(&hadj[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
                 const float pen = apply_hashed(raw, v, bias, prm.rep, prm.inv_rep, prm.freq, prm.pres);
                 __hip_atomic_store(&hpen[s], f2u(pen), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -323,8 +323,8 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             if (a.softcap > 0.0f) {  // the model's output is the capped logit
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
-                    v0[j] = softcap_det(v0[j], a.inv_softcap, a.softcap);
-                    v1[j] = softcap_det(v1[j], a.inv_softcap, a.softcap);
+                    v0[j] = softcap_out(v0[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
+                    v1[j] = softcap_out(v1[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 }
             }
             f(v0, i0);
@@ -347,8 +347,8 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             if (a.softcap > 0.0f) {  // the model's output is the capped logit
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
-                    v0[j] = softcap_det(v0[j], a.inv_softcap, a.softcap);
-                    v1[j] = softcap_det(v1[j], a.inv_softcap, a.softcap);
+                    v0[j] = softcap_out(v0[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
+                    v1[j] = softcap_out(v1[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 }
             }
             f(v0, i0, u0);
@@ -826,7 +826,7 @@ logprobs:
         __syncthreads();
         const float m0 = m0key ? val_of(m0key) : 0.0f;
         float raw_s = Elem<T>::load1(row + token);
-        if (a.softcap > 0.0f) raw_s = softcap_det(raw_s, a.inv_softcap, a.softcap);
+        if (a.softcap > 0.0f) raw_s = softcap_out(raw_s, a.inv_softcap, a.softcap, a.softcap_f16 != 0);
         const uint32_t ks = key_of(raw_s);
         double s0 = 0.0;
         const bool have_s0 = !prm.greedy && sm.bc64[4] != 0ull;
@@ -915,8 +915,8 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
             if (a.softcap > 0.0f) {
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
-                    v0[j] = softcap_det(v0[j], a.inv_softcap, a.softcap);
-                    v1[j] = softcap_det(v1[j], a.inv_softcap, a.softcap);
+                    v0[j] = softcap_out(v0[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
+                    v1[j] = softcap_out(v1[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 }
             }
             f(v0, i0);

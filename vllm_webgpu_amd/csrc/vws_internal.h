@@ -82,6 +82,7 @@ struct KArgs {
     int topk_k;             // k for kModeTopK
     float softcap;          // > 0: Gemma's soft cap applied to every logit first
     float inv_softcap;      // fl(1 / softcap)
+    int softcap_f16;        // capped values rounded as an f16 store
     float* topk_vals;       // [B, k]
     int32_t* topk_ids;      // [B, k]
 };

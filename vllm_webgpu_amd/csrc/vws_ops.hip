@@ -171,7 +171,8 @@ __global__ __launch_bounds__(256) void selftest_kernel(int fn, uint32_t klo, uin
         const uint32_t key = klo + (uint32_t)i;
         const uint32_t bits = (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
         const float x = u2f(bits);
-        const float y = fn == 0 ? exp_det(x) : (fn == 1 ? log_det(x) : softcap_det(x, 1.0f, 1.0f));
+        const float y = fn == 0 ? exp_det(x)
+                      : (fn == 1 ? log_det(x) : (fn == 2 ? softcap_det(x, 1.0f, 1.0f) : round_f16(x)));
         h += ((uint64_t)f2u(y) * 0x9E3779B97F4A7C15ull) ^ (uint64_t)bits;
         c++;
     }
@@ -195,5 +196,7 @@ template __global__ void argmax_kernel<float>(const float*, int64_t, int, int32_
 template __global__ void argmax_kernel<uint16_t>(const uint16_t*, int64_t, int, int32_t*);
 template __global__ void softmax_kernel<float>(const float*, int64_t, int, const float*, float*, float*, float*);
 template __global__ void softmax_kernel<uint16_t>(const uint16_t*, int64_t, int, const float*, float*, float*, float*);
+template __global__ void argmax_kernel<_Float16>(const _Float16*, int64_t, int, int32_t*);
+template __global__ void softmax_kernel<_Float16>(const _Float16*, int64_t, int, const float*, float*, float*, float*);
 
 }  // namespace vws

@@ -792,5 +792,6 @@ __global__ __launch_bounds__(kFastThreads) void fast_kernel(KArgs a) {
 
 template __global__ void fast_kernel<float>(KArgs);
 template __global__ void fast_kernel<uint16_t>(KArgs);
+template __global__ void fast_kernel<_Float16>(KArgs);
 
 }  // namespace vws

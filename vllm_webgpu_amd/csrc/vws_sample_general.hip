@@ -20,5 +20,6 @@ __global__ __launch_bounds__(kGenThreads) void general_kernel(KArgs a) {
 
 template __global__ void general_kernel<float>(KArgs);
 template __global__ void general_kernel<uint16_t>(KArgs);
+template __global__ void general_kernel<_Float16>(KArgs);
 
 }  // namespace vws

@@ -415,6 +415,10 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool mine = tid < total;
     const uint64_t myk = mine ? sm.pk64[tid] : 0ull;
+    // every candidate's uniform is loaded now, so that the latency overlaps the rank count; the
+    // 64 largest candidates store theirs once ranked
+    float u_mine = 0.5f;
+    if (sampling && mine) u_mine = a.u[(size_t)r * a.ustride + (uint32_t)myk];
     {
         // Waves split the count as (group of 64 candidates, range of keys) pairs, 8 keys per
         // step with 128-bit LDS reads, and add their partial counts into LDS.  Unpacked slots
@@ -445,14 +449,15 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     // when only NaNs were dropped; with the soft cap, a bound on it)
     const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;
     float vlim = val_of(tmax - 1u);
-    if (a.softcap > 0.0f) vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
+    if (a.softcap > 0.0f) {
+        vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
+        if (a.softcap_f16) vlim = round_f16(vlim);  // the rounding is monotone: still a bound
+    }
     const float ylim = tmax > 0x007FFFFFu ? (sampling ? vlim / prm.T : vlim) : -__builtin_inff();
     __syncthreads();
-    // the uniforms of the 64 largest candidates only: loaded now, stored into their slots once
-    // wave 0 is about to race, so that their latency overlaps the slots and the masses
+    // the uniforms of the 64 largest candidates are stored into their slots once wave 0 is
+    // about to race
     const uint32_t mpos = mine ? sm.crank[tid] : 0xFFFFFFFFu;
-    float u_mine = 0.5f;
-    if (sampling && mpos < (uint32_t)kWave) u_mine = a.u[(size_t)r * a.ustride + (uint32_t)myk];
     if (mine) {
         const uint32_t pos = mpos;
         if (pos <= (uint32_t)kWave) sm.tk[pos] = myk;
@@ -830,7 +835,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         // unless a compaction has applied them) and its packed entry at slot pos
         auto pack_one = [&](int pos, uint32_t kx, int32_t ii, bool fixed, bool first)
             __attribute__((always_inline)) {
-            if (capped) kx = key_of(softcap_det(val_of(kx), a.inv_softcap, a.softcap));
+            if (capped) kx = key_of(softcap_out(val_of(kx), a.inv_softcap, a.softcap, a.softcap_f16 != 0));
             if (!fixed && rhash_maybe(sm, ii)) {
                 const int hs = rhash_find(sm, ii);
                 if (hs >= 0)
@@ -905,7 +910,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // the largest y an element below the thresholds can have (with the soft cap, a bound on
     // it); -inf when only NaNs were dropped
     float vlim = val_of(tmax - 1u);
-    if (capped) vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
+    if (capped) {
+        vlim = softcap_bound(vlim, a.inv_softcap, a.softcap);
+        if (a.softcap_f16) vlim = round_f16(vlim);  // the rounding is monotone: still a bound
+    }
     const float ylim = tmax > 0x007FFFFFu ? (sampling ? vlim / Tt : vlim) : -__builtin_inff();
     const bool mine = tid < total;
 
@@ -1132,5 +1140,6 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
 
 template __global__ void row_kernel<float>(const void*, int64_t, int, int, KArgs);
 template __global__ void row_kernel<uint16_t>(const void*, int64_t, int, int, KArgs);
+template __global__ void row_kernel<_Float16>(const void*, int64_t, int, int, KArgs);
 
 }  // namespace vws

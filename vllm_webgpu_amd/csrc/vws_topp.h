@@ -62,7 +62,7 @@ struct TopPSmem {
         uint32_t rhist[kTpWaves][256];    // stream: per-wave radix-select scratch
         struct {
             uint64_t hmass[kTpBuckets];   // finish: exact masses of the surviving candidates
-            uint32_t hcnt[kTpBuckets];    // and the number of candidates (every one) per bucket
+            uint32_t hcnt[kTpBuckets];    // and the number of candidates per bucket (top-L logprobs)
         } h;
     };
     union {
@@ -728,7 +728,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (L >= 0) s0b += exp_det(x - xmax);
             if (kk >= tauk) {
                 const int b = tp_bucket(d);
-                atomicAdd(&sm.h.hcnt[b], 1u);
+                if (L > 0) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
                 if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
                 wc += w;
             } else {
@@ -1023,20 +1023,38 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         // boundary bucket's members from the cut on
         RowRace rs;
         uint32_t below_cands = 0u;  // surviving candidates in buckets below the boundary
-        for (int i = lane; i < cnt; i += kWave) {
-            const uint32_t kk = sm.ck[wave][i];
-            if (kk < tauk) continue;
-            const float y = val_of(kk) / Tt;
-            const float d = y - m;
-            if (!(key_of(y) != 0u && d >= lp_min)) continue;
-            const int b = tp_bucket(d);
-            if (b > bstar) { below_cands++; continue; }
-            if (b == bstar) continue;
-            const int32_t idx = sm.ci[wave][i];
-            const uint64_t lk = ((uint64_t)key_of(y) << 32) | (uint32_t)idx;
-            rs.nkept++;
-            rs.last = rs.last > lk ? rs.last : lk;
-            rs.add_key(exp_det(d) / (0.0f - log_det(a.u[(size_t)r * a.ustride + idx])), idx);
+        const float* urow = a.u + (size_t)r * a.ustride;
+        // four entries per lane at a time, their uniforms loaded together: a lane waits for one
+        // memory latency per four entries, not per kept entry
+        for (int i0 = lane; i0 < cnt; i0 += 4 * kWave) {
+            float dq[4], uq[4];
+            uint32_t yq[4];
+            int32_t iq[4];
+            bool kq[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = i0 + q * kWave;
+                const uint32_t kk = i < cnt ? sm.ck[wave][i] : 0u;
+                const float y = val_of(kk) / Tt;
+                const float d = y - m;
+                const bool sv = kk != 0u && kk >= tauk && key_of(y) != 0u && d >= lp_min;
+                const int b = tp_bucket(d);
+                below_cands += (sv && b > bstar) ? 1u : 0u;
+                kq[q] = sv && b < bstar;
+                dq[q] = d;
+                yq[q] = key_of(y);
+                iq[q] = i < cnt ? sm.ci[wave][i] : 0;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) uq[q] = kq[q] ? urow[iq[q]] : 0.5f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (!kq[q]) continue;
+                const uint64_t lk = ((uint64_t)yq[q] << 32) | (uint32_t)iq[q];
+                rs.nkept++;
+                rs.last = rs.last > lk ? rs.last : lk;
+                rs.add_key(exp_det(dq[q]) / (0.0f - log_det(uq[q])), iq[q]);
+            }
         }
         for (uint32_t j = (uint32_t)tid; j < ng; j += NT) {
             const uint64_t g = sm.g.key[j];

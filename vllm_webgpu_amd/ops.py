@@ -36,7 +36,9 @@ def _dtype_code(t: torch.Tensor) -> int:
         return _lib.DTYPE_F32
     if t.dtype == torch.bfloat16:
         return _lib.DTYPE_BF16
-    raise TypeError(f"logits dtype {t.dtype} is not supported (float32 or bfloat16)")
+    if t.dtype == torch.float16:
+        return _lib.DTYPE_F16
+    raise TypeError(f"logits dtype {t.dtype} is not supported (float32, bfloat16 or float16)")
 
 
 def _check_device(t: torch.Tensor, name: str) -> None:
@@ -99,8 +101,10 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
            prompt_ids=None, prompt_lens=None, output_ids=None, output_lens=None,
            uniforms: torch.Tensor | None = None, num_logprobs: int | None = None,
            allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
-           adjust_lens=None, logit_softcap: float | None = None) -> SampleResult:
-    """Samples one token per row of ``logits`` [B, V] (float32 or bfloat16, on the GPU).
+           adjust_lens=None, logit_softcap: float | None = None,
+           logit_softcap_f16: bool = False) -> SampleResult:
+    """Samples one token per row of ``logits`` [B, V] (float32, bfloat16 or float16, on the
+    GPU; each widened exactly to fp32).
 
     Per-row parameters are scalars or [B] tensors; ``None`` means off (temperature None = every
     row greedy).  Histories are padded int32 [B, W] (ids outside [0, V) are padding).
@@ -109,7 +113,9 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     int32 [B, ceil(V/32)] bit words (bit set = token allowed, see ``pack_allowed``), and the
     sparse ``adjust_ids`` int32 / ``adjust_vals`` float32 [B, W]: -inf bans a token, a finite
     value is added to its logit.  ``logit_softcap`` > 0: ``logits`` are the lm_head output
-    before Gemma's final soft cap, which is applied first (cap * tanh(x / cap)).
+    before Gemma's final soft cap, which is applied first (cap * tanh(x / cap)); with
+    ``logit_softcap_f16`` each capped value is rounded to float16 (the reference's shader
+    stores the cap's output in an f16 buffer).
     """
     _check_device(logits, "logits")
     cap = 0.0 if logit_softcap is None else float(logit_softcap)
@@ -174,6 +180,7 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     a.batch, a.vocab, a.dtype = B, V, _dtype_code(logits)
     a.logits, a.logits_row_stride = logits.data_ptr(), logits.stride(0)
     a.logit_softcap = cap
+    a.logit_softcap_f16 = 1 if logit_softcap_f16 else 0
     a.temperature, a.top_k, a.top_p, a.min_p = _ptr(T), _ptr(K), _ptr(P), _ptr(MP)
     a.repetition_penalty, a.presence_penalty, a.frequency_penalty = _ptr(R), _ptr(PR), _ptr(FR)
     a.prompt_ids, a.prompt_row_stride, a.prompt_width, a.prompt_lens = _ptr(pid), pstride, pwidth, _ptr(plens)

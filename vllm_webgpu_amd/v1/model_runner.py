@@ -270,13 +270,15 @@ class ROCmModelRunner:
     def __init__(self, vllm_config: Any, device: torch.device | str | None = None,
                  model: Any = None, max_num_reqs: int = 1024, max_prompt_len: int = 8192,
                  max_output_len: int = 8192, vocab_size: int | None = None,
-                 logit_softcap: float | None = None) -> None:
+                 logit_softcap: float | None = None, logit_softcap_f16: bool = False) -> None:
         """``logit_softcap``: set when ``model`` returns logits before Gemma's final soft cap;
-        the sampler then applies the cap inside its launch."""
+        the sampler then applies the cap inside its launch (``logit_softcap_f16``: rounding
+        each capped value to float16, as the reference stores it).  The model's logits may be
+        float32, bfloat16 or float16 (sampled without a cast)."""
         self.vllm_config = vllm_config
         self.device = torch.device(device if device is not None else "cuda")
         self.model = model
-        self.sampler = Sampler(logit_softcap=logit_softcap)
+        self.sampler = Sampler(logit_softcap=logit_softcap, logit_softcap_f16=logit_softcap_f16)
         self._last_logits: torch.Tensor | None = None
         self._last_req_ids: list[str] = []
         self._max = (max_num_reqs, max_prompt_len, max_output_len)

@@ -92,11 +92,13 @@ class Sampler:
     """vLLM-v1 ``Sampler`` facade over ``vws_sample``."""
 
     def __init__(self, logprobs_mode: str = "raw_logprobs",
-                 logit_softcap: float | None = None) -> None:
+                 logit_softcap: float | None = None, logit_softcap_f16: bool = False) -> None:
         """``logit_softcap``: Gemma's final soft cap, fused into the sampling launch, for models
         whose forward returns the lm_head output before the cap (reference:
         ``vllm_webgpu/models/gemma4.py:158-163``).  The capped logits are then the model's
-        output for everything that follows, raw logprobs included."""
+        output for everything that follows, raw logprobs included.  ``logit_softcap_f16``:
+        each capped value is rounded to float16, as the reference's shader stores it
+        (``shaders/gemma/logit_softcap.wgsl:28``).  Logits may be float32, bfloat16 or float16."""
         if logprobs_mode != "raw_logprobs":
             raise NotImplementedError(
                 f"logprobs_mode {logprobs_mode!r}: only 'raw_logprobs' (log-softmax of the "
@@ -105,6 +107,7 @@ class Sampler:
             raise ValueError(f"logit_softcap must be a positive finite number (got {logit_softcap})")
         self.logprobs_mode = logprobs_mode
         self.logit_softcap = logit_softcap
+        self.logit_softcap_f16 = bool(logit_softcap_f16)
 
     def __call__(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata) -> SamplerOutput:
         return self.forward(logits, sampling_metadata)
@@ -143,7 +146,8 @@ class Sampler:
 
         res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
                          min_p=m.min_p, uniforms=uniforms, num_logprobs=m.max_num_logprobs,
-                         logit_softcap=self.logit_softcap, **penalties, **processors)
+                         logit_softcap=self.logit_softcap,
+                         logit_softcap_f16=self.logit_softcap_f16, **penalties, **processors)
         lp = None
         if m.max_num_logprobs is not None:
             lp = LogprobsTensors(res.logprob_ids, res.logprob_vals, res.logprob_ranks)

@@ -22,8 +22,8 @@ SEED_BASE = 20261201
 @dataclass
 class Workload:
     name: str
-    logits: np.ndarray                 # [B, V] float32, or uint16 bf16 bit patterns
-    dtype: str                         # "f32" | "bf16"
+    logits: np.ndarray                 # [B, V] float32, uint16 bf16 bit patterns, or float16
+    dtype: str                         # "f32" | "bf16" | "f16"
     temperature: np.ndarray            # [B] f32
     top_k: np.ndarray                  # [B] i32 (0 = off)
     top_p: np.ndarray                  # [B] f32 (1 = off)
@@ -44,6 +44,8 @@ class Workload:
     def logits_f32(self) -> np.ndarray:
         if self.dtype == "bf16":
             return (self.logits.astype(np.uint32) << 16).view(np.float32)
+        if self.dtype == "f16":
+            return self.logits.astype(np.float32)  # exact
         return self.logits
 
 
