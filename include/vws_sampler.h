@@ -122,9 +122,16 @@ typedef struct vws_sample_args {
     const int32_t* adjust_lens;
 
     /* Uniforms in (0, 1), fp32 [B, V] (row stride in elements); read only at surviving
-     * tokens.  Required when temperature is non-NULL. */
+     * tokens.  Required when temperature is non-NULL, unless rng_seeds is given. */
     const float* uniforms;
     int64_t uniforms_row_stride;
+    /* Generated uniforms instead (when uniforms is NULL): device u64 [B] keys and offsets
+     * (rng_offsets NULL = 0).  Token t of row r draws word t % 4 of Philox-4x32-10 (Salmon et
+     * al., SC 2011) at counter (t / 4, offset lo, offset hi, 0) with key (seed lo, seed hi),
+     * as (2 floor(w / 2^9) + 1) 2^-24, evaluated only at the tokens that race.  No [B, V]
+     * buffer is read or needs to be written. */
+    const uint64_t* rng_seeds;
+    const uint64_t* rng_offsets;
 
     /* Outputs */
     int32_t* sampled;    /* [B] token ids */

@@ -71,6 +71,10 @@ def lib() -> ctypes.CDLL:
                                            P, P, P, ctypes.c_int, P, P, P, P, ctypes.c_float,
                                            ctypes.c_int]
             L.vwo_softcap_row.argtypes = [P, ctypes.c_int, ctypes.c_float, ctypes.c_int, P]
+            L.vwo_philox4x32_10.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32]
+            L.vwo_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]
+            L.vwo_philox_uniform.restype = ctypes.c_float
+            L.vwo_philox_uniforms.argtypes = [P, P, ctypes.c_int, ctypes.c_int, P]
             L.vwo_check_round_f16.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_uint32, P, P]
             L.vwo_round_f16.argtypes = [ctypes.c_float]
             L.vwo_round_f16.restype = ctypes.c_float
@@ -143,6 +147,23 @@ def check_softcap(lo: float, hi: float):
     lib().vwo_check_softcap(ctypes.c_float(lo), ctypes.c_float(hi), ctypes.byref(me),
                             ctypes.byref(w), ctypes.byref(h), ctypes.byref(c), ctypes.byref(d))
     return dict(max_err=me.value, worst=w.value, hash=h.value, count=c.value, max_drop=d.value)
+
+
+def philox4x32_10(counter, key) -> list[int]:
+    """Philox-4x32-10 of a 4-word counter under a 2-word key: the 4 output words."""
+    c = np.ascontiguousarray(np.asarray(counter, np.uint32))
+    assert c.shape == (4,)
+    lib().vwo_philox4x32_10(_ptr(c), int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF)
+    return [int(v) for v in c]
+
+
+def philox_uniforms(seeds: np.ndarray, V: int, offsets: np.ndarray | None = None) -> np.ndarray:
+    """The uniforms [B, V] the device generates from per-row 64-bit seeds (and offsets)."""
+    sd = np.ascontiguousarray(np.asarray(seeds).astype(np.uint64))
+    off = None if offsets is None else np.ascontiguousarray(np.asarray(offsets).astype(np.uint64))
+    out = np.empty((sd.shape[0], V), np.float32)
+    lib().vwo_philox_uniforms(_ptr(sd), _ptr(off), sd.shape[0], V, _ptr(out))
+    return out
 
 
 def check_round_f16(lo: float, hi: float, stride: int = 1):

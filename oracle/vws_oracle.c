@@ -113,6 +113,42 @@ float vwo_softcap(float x, float inv_cap, float cap) {
     return t * cap;
 }
 
+/* Philox-4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as easy as 1, 2, 3",
+ * SC 2011): ten rounds, each multiplying counter words 0 and 2 by the round constants (32 x 32
+ * -> 64 bits) and mixing the halves with the other words and the key; the key advances by
+ * the Weyl constants after each round.  c: the counter (in), the four output words (out). */
+void vwo_philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+    for (int i = 0; i < 10; ++i) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c[0] = n0; c[1] = n1; c[2] = n2; c[3] = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+/* The sampler's generated uniform of token t for a row with 64-bit key `seed` and 64-bit
+ * `offset`: word t % 4 of Philox-4x32-10 at counter (t / 4, offset lo, offset hi, 0) with key
+ * (seed lo, seed hi), mapped to (2 floor(w / 2^9) + 1) 2^-24, an odd multiple of 2^-24 in
+ * (0, 1) (exact in fp32, never 0 or 1). */
+float vwo_philox_uniform(uint64_t seed, uint64_t offset, uint32_t t) {
+    uint32_t c[4] = {t >> 2, (uint32_t)offset, (uint32_t)(offset >> 32), 0u};
+    vwo_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    return (float)(2u * (c[t & 3u] >> 9) + 1u) * 0x1p-24f;
+}
+
+/* Every row's uniforms [B, V] from per-row seeds and offsets (offsets may be NULL: 0). */
+void vwo_philox_uniforms(const uint64_t* seeds, const uint64_t* offsets, int B, int V, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < V; ++t)
+            out[(size_t)b * V + t] = vwo_philox_uniform(seeds[b], offsets ? offsets[b] : 0u, (uint32_t)t);
+}
+
 /* fp32 -> binary16 (round to nearest, ties to even; overflow to +-inf, underflow through the
  * subnormals to +-0) -> fp32: the value an f16 store keeps, widened back exactly.  The
  * reference's soft-cap shader writes its fp32 result t * cap into an f16 buffer

@@ -123,7 +123,7 @@ def test_sampler_forward_f16_logits_without_cast(cuda, cap):
     import torch
 
     from tests.test_gpu_v1 import _gens, _metadata
-    from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_uniforms
+    from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_seeds
 
     w = _f16(W.config(3, 0.05))
     B, V = w.shape
@@ -131,7 +131,7 @@ def test_sampler_forward_f16_logits_without_cast(cuda, cap):
     assert logits.dtype == torch.float16
     out = Sampler(logit_softcap=cap, logit_softcap_f16=cap is not None)(
         logits, _metadata(w, cuda, _gens(B, cuda, 7100), 3))
-    u = draw_uniforms(B, V, _gens(B, cuda, 7100), cuda).cpu().numpy()
+    u = O.philox_uniforms(draw_seeds(B, _gens(B, cuda, 7100), cuda).cpu().numpy(), V)
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
     ref = O.sample(w.logits_f32(), prm, u, output_ids=w.output_ids, num_logprobs=3, softcap=cap,

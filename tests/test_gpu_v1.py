@@ -1,8 +1,9 @@
 """GPU parity of the vLLM-v1 front end: ``Sampler.forward`` and the model runner's
 ``execute_model`` / ``sample_tokens`` loop against the CPU oracle on the same inputs.
 
-Every random row is seeded, so the uniforms the sampler draws can be redrawn here from
-generators with the same seeds and handed to the oracle; tokens must then agree bit for bit and
+Every random row is seeded, so the per-row keys the sampler draws (the race's uniforms are
+generated from them in the kernel) can be redrawn here from generators with the same seeds, and
+the oracle's copy of the generator turns them into the same uniforms; tokens must then agree bit for bit and
 raw logprobs within rtol 1e-5."""
 from types import SimpleNamespace as NS
 
@@ -14,7 +15,7 @@ from oracle import sampler as O
 from vllm_webgpu_amd import workloads as W
 from vllm_webgpu_amd.v1.model_runner import ROCmModelRunner
 from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
-from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_uniforms
+from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +50,7 @@ def test_sampler_forward_matches_oracle(cuda, cfg, scale, L, cap):
     else:
         logits = torch.from_numpy(w.logits).to(cuda)
     out = Sampler(logit_softcap=cap)(logits, _metadata(w, cuda, _gens(B, cuda, 7000), L))
-    u = draw_uniforms(B, V, _gens(B, cuda, 7000), cuda).cpu().numpy()
+    u = O.philox_uniforms(draw_seeds(B, _gens(B, cuda, 7000), cuda).cpu().numpy(), V)
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
     ref = O.sample(w.logits_f32(), prm, u, output_ids=w.output_ids, num_logprobs=L, softcap=cap)
@@ -125,8 +126,9 @@ def test_runner_steps_match_oracle(cuda):
         u = np.full((B, V), 0.5, np.float32)
         for i, r in enumerate(active):
             if r in mirror:
-                row = torch.empty(V, dtype=torch.float32, device=cuda).uniform_(generator=mirror[r])
-                u[i] = row.clamp_(min=2.0 ** -24).cpu().numpy()
+                sd = torch.randint(-2 ** 63, 2 ** 63 - 1, (1,), dtype=torch.int64, device=cuda,
+                                   generator=mirror[r])
+                u[i] = O.philox_uniforms(sd.cpu().numpy(), V)[0]
         sps = [params[r] for r in active]
         prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
                             [s.top_p for s in sps], [s.min_p for s in sps],
@@ -190,8 +192,9 @@ def test_runner_logits_processors_match_oracle(cuda):
         u = np.full((B, V), 0.5, np.float32)
         for i, r in enumerate(active):
             if r in mirror:
-                row = torch.empty(V, dtype=torch.float32, device=cuda).uniform_(generator=mirror[r])
-                u[i] = row.clamp_(min=2.0 ** -24).cpu().numpy()
+                sd = torch.randint(-2 ** 63, 2 ** 63 - 1, (1,), dtype=torch.int64, device=cuda,
+                                   generator=mirror[r])
+                u[i] = O.philox_uniforms(sd.cpu().numpy(), V)[0]
         sps = [params[r] for r in active]
         prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
                             [s.top_p for s in sps], [s.min_p for s in sps],

@@ -9,7 +9,7 @@ import torch
 from vllm_webgpu_amd.v1.model_runner import InputBatch, ROCmModelRunner, WebGPUModelRunner
 from vllm_webgpu_amd.v1.outputs import LogprobsTensors, ModelRunnerOutput, SamplerOutput
 from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
-from vllm_webgpu_amd.v1.sample.sampler import (Sampler, draw_uniforms, pad_output_ids,
+from vllm_webgpu_amd.v1.sample.sampler import (Sampler, draw_seeds, pad_output_ids,
                                                 processor_lists)
 
 V = 100
@@ -30,15 +30,15 @@ def test_pad_output_ids_ragged():
     assert ids.shape == (2, 1) and ids.eq(V).all() and lens.tolist() == [0, 0]
 
 
-def test_draw_uniforms_open_interval_and_seeded_rows():
+def test_draw_seeds_seeded_rows_reproducible():
     g1 = torch.Generator().manual_seed(5)
-    u = draw_uniforms(3, 5000, {1: g1}, torch.device("cpu"))
-    assert u.dtype == torch.float32 and u.shape == (3, 5000)
-    assert float(u.min()) > 0.0 and float(u.max()) < 1.0
+    s1 = draw_seeds(3, {1: g1}, torch.device("cpu"))
+    assert s1.dtype == torch.int64 and s1.shape == (3,)
     g2 = torch.Generator().manual_seed(5)
-    u2 = draw_uniforms(3, 5000, {1: g2}, torch.device("cpu"))
-    assert torch.equal(u[1], u2[1])          # seeded row reproducible
-    assert not torch.equal(u[0], u2[0])      # unseeded rows are fresh draws
+    s2 = draw_seeds(3, {1: g2}, torch.device("cpu"))
+    assert s1[1] == s2[1]                     # seeded row reproducible
+    assert s1[0] != s2[0] or s1[2] != s2[2]   # unseeded rows are fresh draws
+    assert draw_seeds(3, {1: g2}, torch.device("cpu"))[1] != s1[1]  # next step: a new key
 
 
 def test_input_batch_metadata_fields():

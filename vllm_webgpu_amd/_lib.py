@@ -71,7 +71,7 @@ class SampleArgs(ctypes.Structure):
         ("allowed_mask", _P), ("allowed_row_stride", _I64),
         ("adjust_ids", _P), ("adjust_vals", _P), ("adjust_row_stride", _I64), ("adjust_width", _I32),
         ("adjust_lens", _P),
-        ("uniforms", _P), ("uniforms_row_stride", _I64),
+        ("uniforms", _P), ("uniforms_row_stride", _I64), ("rng_seeds", _P), ("rng_offsets", _P),
         ("sampled", _P), ("row_flags", _P), ("num_kept", _P),
         ("num_logprobs", _I32), ("logprob_ids", _P), ("logprob_vals", _P), ("logprob_ranks", _P),
         ("workspace", _P), ("workspace_bytes", _SZ), ("stream", _P),

@@ -190,8 +190,10 @@ int validate_sample(const vws_sample_args* a) {
     if (st) return st;
     if (!a->sampled) return fail(VWS_ERR_INVALID_ARGUMENT, "sampled is NULL");
     if (a->temperature) {
-        if (!a->uniforms) return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms are required when temperature is given");
-        if (a->uniforms_row_stride < a->vocab) return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms_row_stride < vocab");
+        if (!a->uniforms && !a->rng_seeds)
+            return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms or rng_seeds are required when temperature is given");
+        if (a->uniforms && a->uniforms_row_stride < a->vocab)
+            return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms_row_stride < vocab");
     }
     if (a->num_logprobs < -1 || a->num_logprobs > VWS_MAX_LOGPROBS)
         return fail(VWS_ERR_LIMIT, "num_logprobs must be in [-1, %d] (got %d)", VWS_MAX_LOGPROBS, a->num_logprobs);
@@ -299,6 +301,8 @@ int vws_sample(const vws_sample_args* a) {
     k.softcap_f16 = (a->logit_softcap > 0.0f && a->logit_softcap_f16) ? 1 : 0;
     k.u = a->uniforms;
     k.ustride = a->uniforms_row_stride;
+    k.rng_seed = a->uniforms ? nullptr : a->rng_seeds;
+    k.rng_offset = a->uniforms ? nullptr : a->rng_offsets;
     k.sampled = a->sampled;
     k.flags = a->row_flags;
     k.nkept = a->num_kept;

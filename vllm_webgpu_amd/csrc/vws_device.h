@@ -121,6 +121,36 @@ __device__ __forceinline__ uint64_t mass_of(float e) {
     return (e > 0.0f) ? m : 0ull;
 }
 
+// Philox-4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as easy as 1, 2, 3",
+// SC 2011): ten rounds, each multiplying counter words 0 and 2 by the round constants (32 x 32
+// -> 64 bits) and mixing the halves with the other words and the key; the key advances by the
+// Weyl constants after each round.  c: the counter (in), the four output words (out).
+__device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+        const uint32_t lo0 = c[0] * 0xD2511F53u, hi0 = __umulhi(c[0], 0xD2511F53u);
+        const uint32_t lo1 = c[2] * 0xCD9E8D57u, hi1 = __umulhi(c[2], 0xCD9E8D57u);
+        const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+        c[0] = n0;
+        c[1] = lo1;
+        c[2] = n2;
+        c[3] = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+// The race's generated uniform of token t for a row with 64-bit key `seed` and `offset`: word
+// t % 4 of Philox-4x32-10 at counter (t / 4, offset lo, offset hi, 0) with key (seed lo, seed
+// hi), as (2 floor(w / 2^9) + 1) 2^-24, an odd multiple of 2^-24 in (0, 1).
+__device__ __forceinline__ float philox_uniform(uint64_t seed, uint64_t offset, uint32_t t) {
+    uint32_t c[4] = {t >> 2, (uint32_t)offset, (uint32_t)(offset >> 32), 0u};
+    philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    const uint32_t j = t & 3u;
+    const uint32_t w = j == 0u ? c[0] : (j == 1u ? c[1] : (j == 2u ? c[2] : c[3]));
+    return (float)(2u * (w >> 9) + 1u) * 0x1p-24f;
+}
+
 // Order-preserving key: x < y <=> key(x) < key(y); -0 and +0 share a key; NaN -> 0.
 __device__ __forceinline__ uint32_t key_of(float x) {
     uint32_t b = f2u(x);

@@ -519,7 +519,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             if (tid == 0) {
                 const int idx = argmax_hi;
                 const float y = val_of(maxkey) / Tt;
-                race.add(1.0f, key_of(y), idx, urow[idx]);
+                race.add(1.0f, key_of(y), idx, row_uniform(a, r, idx));
             }
             if (share_lse) {
                 for_rows([&](float* v, int i0) {
@@ -537,7 +537,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     if (survivor(v[j], y, d)) {
                         const float e = exp_det(d);
                         if (share_lse) s0_shared += (double)e;
-                        race.add(e, key_of(y), i0 + j, uc[j]);
+                        race.add(e, key_of(y), i0 + j, urow ? uc[j] : row_uniform(a, r, i0 + j));
                     } else if (share_lse && v[j] == v[j]) {
                         s0_shared += (double)exp_det(d);
                     }
@@ -583,7 +583,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     if (!survivor(v[j], y, d)) continue;
                     const int b = bucket_of(d);
                     if (b < bstar) {
-                        race.add(exp_det(d), key_of(y), i0 + j, uc[j]);
+                        race.add(exp_det(d), key_of(y), i0 + j, urow ? uc[j] : row_uniform(a, r, i0 + j));
                     } else if (b == bstar) {
                         const uint32_t ky = key_of(y);
                         kmin = min(kmin, ky);
@@ -701,10 +701,10 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                         const uint32_t ky = key_of(y);
                         const int ix = i0 + j;
                         if (ky > khi) {
-                            race.add(exp_det(d), ky, ix, uc[j]);
+                            race.add(exp_det(d), ky, ix, urow ? uc[j] : row_uniform(a, r, ix));
                         } else if (ky >= klo) {
                             if (tie_rule) {
-                                if ((uint32_t)ix >= idx_thr) race.add(exp_det(d), ky, ix, uc[j]);
+                                if ((uint32_t)ix >= idx_thr) race.add(exp_det(d), ky, ix, urow ? uc[j] : row_uniform(a, r, ix));
                             } else {
                                 const uint32_t pos = atomicAdd(&sm.gcount, 1u);
                                 if (pos < (uint32_t)kGatherCap) sm.u.gather[pos] = ((uint64_t)ky << 32) | (uint32_t)ix;
@@ -759,7 +759,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     if (removed) { nrem_in++; cprev = cprev > C ? cprev : C; }
                     else {
                         cat = cat < C ? cat : C;
-                        race.add(exp_det(val_of(ky) - m), ky, ix, urow[ix]);
+                        race.add(exp_det(val_of(ky) - m), ky, ix, row_uniform(a, r, ix));
                     }
                 }
                 const uint64_t nrem_b = gblock_sum(nrem_in, sm);

@@ -61,6 +61,8 @@ struct KArgs {
     const int32_t* adjlens;
     const float* u;
     int64_t ustride;
+    const uint64_t* rng_seed;   // [B] keys of the generated uniforms (when u is NULL)
+    const uint64_t* rng_offset; // [B] their counter offsets, or NULL (0)
     int32_t* sampled;
     uint32_t* flags;
     int32_t* nkept;

@@ -44,6 +44,13 @@ __device__ __forceinline__ RowP row_params(const KArgs& a, int r) {
     return p;
 }
 
+// The race's uniform of token t in row r: the caller's [B, V] uniforms, or the generated one
+// (philox_uniform of the row's key and offset) when the caller passes keys instead.
+__device__ __forceinline__ float row_uniform(const KArgs& a, int r, int t) {
+    if (a.u) return a.u[(size_t)r * a.ustride + t];
+    return philox_uniform(a.rng_seed[r], a.rng_offset ? a.rng_offset[r] : 0ull, (uint32_t)t);
+}
+
 // k served by the single-pass kernel for this row, or 0 when the row needs the general kernel.
 __device__ __forceinline__ int fast_k(const KArgs& a, const RowP& p) {
     if (a.mode == kModeTopK) return a.topk_k;

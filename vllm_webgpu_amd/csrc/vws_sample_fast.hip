@@ -629,7 +629,7 @@ __device__ __forceinline__ void fast_finish_row(const KArgs& a, FastSmem& sm, in
 #pragma unroll
     for (int s = 0; s < NU; ++s) {
         const int j = s * NT + tid;
-        ureg[s] = j < N ? a.u[(size_t)r * a.ustride + mi[j]] : 0.5f;
+        ureg[s] = j < N ? row_uniform(a, r, mi[j]) : 0.5f;
     }
 
     const float Tt = prm.T;

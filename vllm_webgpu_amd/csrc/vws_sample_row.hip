@@ -418,7 +418,7 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     // every candidate's uniform is loaded now, so that the latency overlaps the rank count; the
     // 64 largest candidates store theirs once ranked
     float u_mine = 0.5f;
-    if (sampling && mine) u_mine = a.u[(size_t)r * a.ustride + (uint32_t)myk];
+    if (sampling && mine) u_mine = row_uniform(a, r, (int)(uint32_t)myk);
     {
         // Waves split the count as (group of 64 candidates, range of keys) pairs, 8 keys per
         // step with 128-bit LDS reads, and add their partial counts into LDS.  Unpacked slots
@@ -853,7 +853,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
                     if (first) {
                         u_slot = pos;  // loaded below, stored once the ranks are counted
                     } else {
-                        sm.pu[pos] = a.u[(size_t)r * a.ustride + ii];
+                        sm.pu[pos] = row_uniform(a, r, ii);
                     }
                 }
             }
@@ -870,7 +870,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             const int pbase = __builtin_amdgcn_readlane(b, 0);
             if (keep && pbase + __popcll(bal) <= kRowPack) {
                 pack_one(pbase + lane_prefix(bal), kx, ii, pmode == 0u || lane < cb.nfix, true);
-                if (sampling && !small) u_first = a.u[(size_t)r * a.ustride + ii];
+                if (sampling && !small) u_first = row_uniform(a, r, ii);
             }
         } else {
             cb.filter();
@@ -886,7 +886,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
                 // the first candidate's uniform, loaded outside the loop so that nothing waits
                 // for it before it is stored
                 if (sampling && !small && u_slot >= 0)
-                    u_first = a.u[(size_t)r * a.ustride + sm.cidx[wave][lane]];
+                    u_first = row_uniform(a, r, sm.cidx[wave][lane]);
             }
         }
         if (!small) {

@@ -592,7 +592,8 @@ __device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int
     kmem = tp_u(kmem > ksv ? kmem : ksv);
     RowRace rs;
     uint32_t nrem = 0u;
-    tp_row_pass<T, true>(a, r, [&](const float* v, const float* u, int i0, bool ok) __attribute__((always_inline)) {
+    // gen: the uniforms are generated (at the kept elements only) instead of streamed
+    auto body = [&](const float* v, const float* u, int i0, bool ok, bool gen) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const uint32_t kx = ok ? key_of(v[j]) : 0u;
@@ -600,7 +601,8 @@ __device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int
             if (kx >= kkeep) {
                 const float d = v[j] / Tt - m;
                 rs.nkept++;
-                rs.add_key(exp_det(d) / (0.0f - log_det(u[j])), i0 + j);
+                const float uu = gen ? row_uniform(a, r, i0 + j) : u[j];
+                rs.add_key(exp_det(d) / (0.0f - log_det(uu)), i0 + j);
             } else if (kx >= kmem) {
                 const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
                 if (pos < (uint32_t)kTpGather)
@@ -609,7 +611,14 @@ __device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int
                 nrem += kx >= ksv ? 1u : 0u;
             }
         }
-    });
+    };
+    if (a.u) {
+        tp_row_pass<T, true>(a, r, [&](const float* v, const float* u, int i0, bool ok)
+                                       __attribute__((always_inline)) { body(v, u, i0, ok, false); });
+    } else {
+        tp_row_pass<T, false>(a, r, [&](const float* v, const float* u, int i0, bool ok)
+                                        __attribute__((always_inline)) { body(v, u, i0, ok, true); });
+    }
     rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
     rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);
     const uint64_t nr = wave_sum_u64(nrem);
@@ -1023,7 +1032,6 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         // boundary bucket's members from the cut on
         RowRace rs;
         uint32_t below_cands = 0u;  // surviving candidates in buckets below the boundary
-        const float* urow = a.u + (size_t)r * a.ustride;
         // four entries per lane at a time, their uniforms loaded together: a lane waits for one
         // memory latency per four entries, not per kept entry
         for (int i0 = lane; i0 < cnt; i0 += 4 * kWave) {
@@ -1046,7 +1054,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 iq[q] = i < cnt ? sm.ci[wave][i] : 0;
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) uq[q] = kq[q] ? urow[iq[q]] : 0.5f;
+            for (int q = 0; q < 4; ++q) uq[q] = kq[q] ? row_uniform(a, r, iq[q]) : 0.5f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 if (!kq[q]) continue;
@@ -1070,7 +1078,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             rs.nkept++;
             rs.last = rs.last > g ? rs.last : g;
             rs.add_key(exp_det(val_of((uint32_t)(g >> 32)) - m) /
-                           (0.0f - log_det(a.u[(size_t)r * a.ustride + idx])), idx);
+                           (0.0f - log_det(row_uniform(a, r, idx))), idx);
         }
         rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
         rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);

@@ -102,14 +102,17 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
            uniforms: torch.Tensor | None = None, num_logprobs: int | None = None,
            allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
            adjust_lens=None, logit_softcap: float | None = None,
-           logit_softcap_f16: bool = False) -> SampleResult:
+           logit_softcap_f16: bool = False, rng_seeds: torch.Tensor | None = None,
+           rng_offsets: torch.Tensor | None = None) -> SampleResult:
     """Samples one token per row of ``logits`` [B, V] (float32, bfloat16 or float16, on the
     GPU; each widened exactly to fp32).
 
     Per-row parameters are scalars or [B] tensors; ``None`` means off (temperature None = every
     row greedy).  Histories are padded int32 [B, W] (ids outside [0, V) are padding).
-    ``uniforms`` [B, V] float32 in (0, 1) drive the exponential race and are required whenever
-    ``temperature`` is given.  Logits processors (before the penalties): ``allowed_mask``
+    ``uniforms`` [B, V] float32 in (0, 1) drive the exponential race; instead, ``rng_seeds``
+    [B] int64 (and optionally ``rng_offsets`` [B] int64) let the kernel generate them
+    (Philox-4x32-10 keyed per row, evaluated only where a token races).  One of the two is
+    required whenever ``temperature`` is given.  Logits processors (before the penalties): ``allowed_mask``
     int32 [B, ceil(V/32)] bit words (bit set = token allowed, see ``pack_allowed``), and the
     sparse ``adjust_ids`` int32 / ``adjust_vals`` float32 [B, W]: -inf bans a token, a finite
     value is added to its logit.  ``logit_softcap`` > 0: ``logits`` are the lm_head output
@@ -163,6 +166,12 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
             U = U.contiguous()
         if U.shape != (B, V):
             raise ValueError(f"uniforms must be [{B}, {V}]")
+    SEED = OFF = None
+    if rng_seeds is not None and U is None:
+        SEED = _row_param(rng_seeds, B, torch.int64, dev, "rng_seeds")
+        OFF = _row_param(rng_offsets, B, torch.int64, dev, "rng_offsets")
+    if T is not None and U is None and SEED is None:
+        raise ValueError("uniforms or rng_seeds are required when temperature is given")
     sampled = torch.empty(B, dtype=torch.int32, device=dev)
     flags = torch.empty(B, dtype=torch.int32, device=dev)
     nkept = torch.empty(B, dtype=torch.int32, device=dev)
@@ -192,6 +201,7 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
         a.adjust_row_stride, a.adjust_width, a.adjust_lens = astride, awidth, _ptr(alens)
     a.uniforms = _ptr(U)
     a.uniforms_row_stride = U.stride(0) if U is not None else 0
+    a.rng_seeds, a.rng_offsets = _ptr(SEED), _ptr(OFF)
     a.sampled, a.row_flags, a.num_kept = sampled.data_ptr(), flags.data_ptr(), nkept.data_ptr()
     a.num_logprobs = L
     a.logprob_ids, a.logprob_vals, a.logprob_ranks = _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks)

@@ -10,9 +10,11 @@ temperature, min-p, top-k, top-p, exponential race, logprob gather -- but runs a
 single stream-ordered kernel launch (``vws_sample``) on device-resident logits; only the sparse
 processor lists (bad-word matches, min-tokens bans, biases) are built on the host.
 
-Random rows consume caller-side uniforms ``u`` in (0, 1) drawn here with torch's generators
-(the request's own generator for seeded rows), and the race key is ``p / (-ln u)``: an
-exponential race, as vLLM's ``random_sample`` (``probs / q.exponential_()``).
+Random rows race with the key ``p / (-ln u)``: an exponential race, as vLLM's
+``random_sample`` (``probs / q.exponential_()``).  The uniforms ``u`` are generated inside the
+launch (Philox-4x32-10, only where a token races) from one 64-bit key per row and step, drawn
+here with torch's generators -- the request's own generator for seeded rows -- so no ``[B, V]``
+tensor is drawn or read.
 
 There is no host fallback: without the HIP library, or for logits that are not on a ROCm device,
 ``forward`` raises.
@@ -25,16 +27,19 @@ from ... import ops
 from ..outputs import LogprobsTensors, SamplerOutput
 from .metadata import SamplingMetadata
 
-_U_MIN = 2.0 ** -24   # smallest uniform handed to the race: -ln(u) stays finite and positive
+_SEED_LO, _SEED_HI = -2 ** 63, 2 ** 63 - 1
 
 
-def draw_uniforms(B: int, V: int, generators: dict[int, torch.Generator],
-                  device: torch.device) -> torch.Tensor:
-    """float32 ``[B, V]`` uniforms in (0, 1); row ``i`` comes from ``generators[i]`` if present."""
-    u = torch.rand((B, V), dtype=torch.float32, device=device)
+def draw_seeds(B: int, generators: dict[int, torch.Generator],
+               device: torch.device) -> torch.Tensor:
+    """int64 ``[B]`` keys of the race's generated uniforms, one fresh draw per row and step: row
+    ``i`` draws from ``generators[i]`` if present (a seeded request samples the same tokens
+    again), the others from torch's default generator."""
+    seeds = torch.randint(_SEED_LO, _SEED_HI, (B,), dtype=torch.int64, device=device)
     for i, g in generators.items():
-        u[i].uniform_(generator=g)
-    return u.clamp_(min=_U_MIN)
+        seeds[i] = torch.randint(_SEED_LO, _SEED_HI, (1,), dtype=torch.int64, device=device,
+                                 generator=g)[0]
+    return seeds
 
 
 def pad_output_ids(output_token_ids: list[list[int]], vocab_size: int,
@@ -120,9 +125,9 @@ class Sampler:
         dev = logits.device
 
         temperature = None if m.all_greedy else m.temperature
-        uniforms = None
+        seeds = None
         if temperature is not None:
-            uniforms = draw_uniforms(B, V, m.generators, dev)
+            seeds = draw_seeds(B, m.generators, dev)
 
         penalties = {}
         if not m.no_penalties:
@@ -145,7 +150,7 @@ class Sampler:
                               adjust_vals=vals.to(dev, non_blocking=True))
 
         res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
-                         min_p=m.min_p, uniforms=uniforms, num_logprobs=m.max_num_logprobs,
+                         min_p=m.min_p, rng_seeds=seeds, num_logprobs=m.max_num_logprobs,
                          logit_softcap=self.logit_softcap,
                          logit_softcap_f16=self.logit_softcap_f16, **penalties, **processors)
         lp = None
