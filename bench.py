@@ -63,6 +63,63 @@ def build_args(lib_mod, logits, T, K, P, MP, R, PR, FR, hist, U, out, flags, nke
     return a
 
 
+def v1_forward_timing(w, logits, T, K, P, MP, R, PR, FR, hist, dev, steps: int, warmup: int):
+    """Sampler.forward (vLLM-v1 signature) on device-resident metadata: wall time per call
+    (host work included, synchronised at both ends) and stream time per call (hipEvents)."""
+    import torch
+
+    from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
+    from vllm_webgpu_amd.v1.sample.sampler import Sampler
+
+    greedy = ~(w.temperature >= np.float32(1e-5))
+    m = SamplingMetadata(
+        temperature=None if greedy.all() else T, all_greedy=bool(greedy.all()),
+        all_random=not greedy.any(), top_p=P, top_k=K, generators={},
+        max_num_logprobs=w.num_logprobs, no_penalties=hist is None, prompt_token_ids=None,
+        frequency_penalties=FR, presence_penalties=PR, repetition_penalties=R,
+        output_token_ids=[], min_p=MP, output_token_ids_tensor=hist)
+    sampler = Sampler()
+    for _ in range(warmup):
+        sampler(logits, m)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        sampler(logits, m)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e6
+    return {"wall_us": wall, "gpu_us": e0.elapsed_time(e1) / steps * 1e3, "steps": steps,
+            "uniforms": "generated in the kernel (Philox-4x32-10, one key per row and step)"}
+
+
+def generated_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
+                        stream, B, steps: int, warmup: int) -> float:
+    """The sampling kernel alone with generated uniforms (keys instead of a [B, V] tensor)."""
+    import torch
+
+    dev = out.device
+    seeds = torch.arange(1, B + 1, dtype=torch.int64, device=dev) * 0x9E3779B97F4A7C15 // 7
+    argv = []
+    for lg, _, h in sets:
+        a = build_args(lib_mod, lg, T, K, P, MP, R, PR, FR, h, None, out, flags, nkept, ws, lp)
+        a.rng_seeds = seeds.data_ptr()
+        a.stream = stream.cuda_stream
+        argv.append(a)
+    for i in range(warmup):
+        lib_mod.check(L.vws_sample(ctypes.byref(argv[i % len(argv)])))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        L.vws_sample(ctypes.byref(argv[i % len(argv)]))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps * 1e3
+
+
 def cpu_baseline(w, rows: int, iters: int):
     """torch CPU restatement of vLLM's sampler on `rows` rows of the workload, all host cores."""
     import torch
@@ -300,6 +357,16 @@ def main():
         f"e2e {gbps_e2e:.0f} GB/s ({gbps_e2e / PEAK_HBM_GBPS:.1%})  kernel {gbps_kern:.0f} GB/s "
         f"({gbps_kern / PEAK_HBM_GBPS:.1%})")
 
+    # the same step through the vLLM-v1 front end (Sampler.forward on a SamplingMetadata), with
+    # the uniforms generated in the kernel from one key per row (no [B, V] tensor), and the
+    # kernel alone in that mode
+    v1 = v1_forward_timing(w, sets[0][0], T, K, P, MP, R, PR, FR, sets[0][2], dev,
+                           min(args.steps, 300), min(args.warmup, 30))
+    gen_us = generated_kernel_us(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
+                                 stream, B, min(args.steps, 300), min(args.warmup, 30))
+    log(f"v1 Sampler.forward: {v1['wall_us']:.1f} us/step wall, {v1['gpu_us']:.1f} us/step on the "
+        f"stream; kernel with generated uniforms {gen_us:.2f} us")
+
     if args.calibrate_copy:
         a = torch.empty(1 << 27, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
@@ -347,6 +414,9 @@ def main():
         "parity": parity,
         "near_tie_rows": near_tie,
         "kernel_us": {"sample" if probs_out is None else "sample+softmax": kern_ms * 1e3},
+        "kernel_us_generated_uniforms": gen_us,
+        "v1_sampler_forward": {**v1, "kernel_us": kern_ms * 1e3,
+                               "wall_vs_kernel": v1["wall_us"] / (kern_ms * 1e3)},
         "kernel_us_event_pairs": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",

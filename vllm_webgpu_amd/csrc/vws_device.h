@@ -128,15 +128,35 @@ __device__ __forceinline__ uint64_t mass_of(float e) {
 __device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
 #pragma unroll
     for (int i = 0; i < 10; ++i) {
-        const uint32_t lo0 = c[0] * 0xD2511F53u, hi0 = __umulhi(c[0], 0xD2511F53u);
-        const uint32_t lo1 = c[2] * 0xCD9E8D57u, hi1 = __umulhi(c[2], 0xCD9E8D57u);
-        const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+        const uint64_t p0 = (uint64_t)c[0] * 0xD2511F53u;  // one 32 x 32 -> 64 multiply each
+        const uint64_t p1 = (uint64_t)c[2] * 0xCD9E8D57u;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
         c[0] = n0;
-        c[1] = lo1;
+        c[1] = (uint32_t)p1;
         c[2] = n2;
-        c[3] = lo0;
+        c[3] = (uint32_t)p0;
         k0 += 0x9E3779B9u;
         k1 += 0xBB67AE85u;
+    }
+}
+
+// A Philox word as the race's uniform: (2 floor(w / 2^9) + 1) 2^-24, an odd multiple of
+// 2^-24 in (0, 1), exact in fp32.
+__device__ __forceinline__ float philox_word_uniform(uint32_t w) {
+    return (float)(2u * (w >> 9) + 1u) * 0x1p-24f;
+}
+
+// The generated uniforms of the N consecutive tokens t0 .. t0 + N - 1, t0 a multiple of 4 and
+// N of 4: one Philox block per 4 tokens (philox_uniform of each).
+template <int N>
+__device__ __forceinline__ void philox_uniforms_aligned(uint64_t seed, uint64_t offset, uint32_t t0,
+                                                        float (&u)[N]) {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) {
+        uint32_t c[4] = {(t0 >> 2) + (uint32_t)q, (uint32_t)offset, (uint32_t)(offset >> 32), 0u};
+        philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) u[4 * q + j] = philox_word_uniform(c[j]);
     }
 }
 
@@ -148,7 +168,7 @@ __device__ __forceinline__ float philox_uniform(uint64_t seed, uint64_t offset, 
     philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
     const uint32_t j = t & 3u;
     const uint32_t w = j == 0u ? c[0] : (j == 1u ? c[1] : (j == 2u ? c[2] : c[3]));
-    return (float)(2u * (w >> 9) + 1u) * 0x1p-24f;
+    return philox_word_uniform(w);
 }
 
 // Order-preserving key: x < y <=> key(x) < key(y); -0 and +0 share a key; NaN -> 0.

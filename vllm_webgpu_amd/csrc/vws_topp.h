@@ -593,7 +593,20 @@ __device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int
     RowRace rs;
     uint32_t nrem = 0u;
     // gen: the uniforms are generated (at the kept elements only) instead of streamed
+    const uint64_t gseed = a.u ? 0ull : a.rng_seed[r];
+    const uint64_t goff = (a.u || !a.rng_offset) ? 0ull : a.rng_offset[r];
     auto body = [&](const float* v, const float* u, int i0, bool ok, bool gen) __attribute__((always_inline)) {
+        // generated uniforms: one Philox block per 4 tokens when the vector starts on a block
+        // (the body's vectors all do when the row's aligned start does), else token by token
+        float ug[VEC];
+        const bool blocks = gen && (i0 & 3) == 0;
+        bool anykept = false;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+            const uint32_t kx = ok ? key_of(v[j]) : 0u;
+            anykept = anykept || (kx < tauk && kx >= kkeep);
+        }
+        if (blocks && anykept) philox_uniforms_aligned<VEC>(gseed, goff, (uint32_t)i0, ug);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const uint32_t kx = ok ? key_of(v[j]) : 0u;
@@ -601,7 +614,7 @@ __device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int
             if (kx >= kkeep) {
                 const float d = v[j] / Tt - m;
                 rs.nkept++;
-                const float uu = gen ? row_uniform(a, r, i0 + j) : u[j];
+                const float uu = !gen ? u[j] : (blocks ? ug[j] : row_uniform(a, r, i0 + j));
                 rs.add_key(exp_det(d) / (0.0f - log_det(uu)), i0 + j);
             } else if (kx >= kmem) {
                 const uint32_t pos = atomicAdd(&sm.bc[4], 1u);

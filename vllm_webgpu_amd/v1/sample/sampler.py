@@ -65,6 +65,8 @@ def processor_lists(m: SamplingMetadata, B: int, V: int):
     stop tokens while the output is shorter than the minimum.  Logit bias adds its value.
     Padding ids are V.
     """
+    if not m.bad_words_token_ids and not m.min_tokens and not (m.logit_bias and any(m.logit_bias)):
+        return None  # the common case, without a pass over the rows
     rows: list[list[tuple[int, float]]] = [[] for _ in range(B)]
     for i, words in (m.bad_words_token_ids or {}).items():
         past = m.output_token_ids[i] if i < len(m.output_token_ids) else []
