@@ -188,18 +188,23 @@ def cpu_reference_ops(w, rows: int, iters: int):
     return res
 
 
+PROFILE_SUMMARIES = {1: "sample_c1_b1_v32000.md", 2: "sample_c2_b64_v32000.md",
+                     3: "sample_c3_b256_v128256.md", 4: "sample_c4_b512_v262144_bf16.md",
+                     5: "sample_c5_b1024_v151936.md"}
+
+
 def pmc_traffic_bytes(config: int):
     """HBM bytes per row_kernel launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (copy-calibrated); None when no summary covers this workload."""
-    if config != 3:
+    name = PROFILE_SUMMARIES.get(config)
+    if name is None:
         return None
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "sample_c3_b256_v128256.md")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         text = open(path).read()
     except OSError:
         return None
-    m = re.search(r"^\| `void vws::row_kernel<float>\([^`]*` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
+    m = re.search(r"^\| `void vws::row_kernel<[a-z ]+>\([^`]*` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
                   text, re.M)
     return None if m is None else float(m.group(1)) * 1e6
 
@@ -214,6 +219,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--cpu-iters", type=int, default=30)
+    ap.add_argument("--skip-v1", action="store_true",
+                    help="skip the v1 Sampler.forward and generated-uniform timings (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 512 MiB device copy (for PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -360,12 +367,14 @@ def main():
     # the same step through the vLLM-v1 front end (Sampler.forward on a SamplingMetadata), with
     # the uniforms generated in the kernel from one key per row (no [B, V] tensor), and the
     # kernel alone in that mode
-    v1 = v1_forward_timing(w, sets[0][0], T, K, P, MP, R, PR, FR, sets[0][2], dev,
-                           min(args.steps, 300), min(args.warmup, 30))
-    gen_us = generated_kernel_us(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
-                                 stream, B, min(args.steps, 300), min(args.warmup, 30))
-    log(f"v1 Sampler.forward: {v1['wall_us']:.1f} us/step wall, {v1['gpu_us']:.1f} us/step on the "
-        f"stream; kernel with generated uniforms {gen_us:.2f} us")
+    v1 = gen_us = None
+    if not args.skip_v1:
+        v1 = v1_forward_timing(w, sets[0][0], T, K, P, MP, R, PR, FR, sets[0][2], dev,
+                               min(args.steps, 300), min(args.warmup, 30))
+        gen_us = generated_kernel_us(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws,
+                                     lp, stream, B, min(args.steps, 300), min(args.warmup, 30))
+        log(f"v1 Sampler.forward: {v1['wall_us']:.1f} us/step wall, {v1['gpu_us']:.1f} us/step on "
+            f"the stream; kernel with generated uniforms {gen_us:.2f} us")
 
     if args.calibrate_copy:
         a = torch.empty(1 << 27, dtype=torch.float32, device=dev)
@@ -415,8 +424,8 @@ def main():
         "near_tie_rows": near_tie,
         "kernel_us": {"sample" if probs_out is None else "sample+softmax": kern_ms * 1e3},
         "kernel_us_generated_uniforms": gen_us,
-        "v1_sampler_forward": {**v1, "kernel_us": kern_ms * 1e3,
-                               "wall_vs_kernel": v1["wall_us"] / (kern_ms * 1e3)},
+        "v1_sampler_forward": None if v1 is None else {
+            **v1, "kernel_us": kern_ms * 1e3, "wall_vs_kernel": v1["wall_us"] / (kern_ms * 1e3)},
         "kernel_us_event_pairs": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",

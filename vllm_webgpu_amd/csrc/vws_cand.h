@@ -58,7 +58,7 @@ struct CandBuf {
             uint32_t kk = 0;
             int32_t ii = 0;
             if (i < cnt) { kk = ck[i]; ii = ci[i]; keep = kk >= kth; }
-            const uint64_t bal = __ballot(keep);
+            const uint64_t bal = wave_ballot(keep);
             if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
             out += __popcll(bal);
             wave_sync();
@@ -73,13 +73,13 @@ struct CandBuf {
     // Appends (kk, idx) from the lanes where c holds; wave-uniform call.  Callers pass
     // c = (value >= tauf) already (NaN values never pass).
     __device__ __forceinline__ void append(bool c, uint32_t kk, int32_t idx) {
-        uint64_t bal = __ballot(c);
+        uint64_t bal = wave_ballot(c);
         if (!bal || ovf) return;
         int n = __popcll(bal);
         if (cnt + n > cap) {
             compact();
             c = c && kk >= tau;
-            bal = __ballot(c);
+            bal = wave_ballot(c);
             n = __popcll(bal);
             if (cnt + n > cap) { ovf = true; return; }
         }
@@ -114,7 +114,7 @@ __device__ __forceinline__ uint32_t wave_kth_largest_multi(const uint32_t* base,
         const uint32_t s = c0 + c1 + c2 + c3;
         const uint32_t incl = wave_incl_scan(s);
         const uint32_t excl = incl - s;
-        const uint64_t hit = __ballot(excl < rem && rem <= incl);
+        const uint64_t hit = wave_ballot(excl < rem && rem <= incl);
         const int L = __ffsll((unsigned long long)hit) - 1;
         uint32_t bin = 0, r = rem - excl;
         if (r <= c0) bin = 255 - 4 * lane;

@@ -18,6 +18,11 @@ constexpr float kSamplingEps = 1e-5f;
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
+// Wave ballot of a condition.  HIP's __ballot takes an int, which makes the compiler materialise
+// the condition in a register and compare it again; the builtin on a bool uses the compare's
+// lane mask directly.
+__device__ __forceinline__ uint64_t wave_ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
 // exp(d) for d in [-80, 80] (clamped above), 0 below -80 and for NaN.  Cody-Waite
 // reduction n = rint(d * log2 e), r = d - n * ln2 with a 16-bit head of ln2 (n * head is
 // exact) and an fp32 tail; exp(r) = 1 + r + r^2 Q(r) with Q of degree 4 fitted for this
@@ -346,7 +351,7 @@ __device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t* keys, int n
         const uint32_t s = c0 + c1 + c2 + c3;
         const uint32_t incl = wave_incl_scan(s);
         const uint32_t excl = incl - s;
-        const uint64_t hit = __ballot(excl < rem && rem <= incl);
+        const uint64_t hit = wave_ballot(excl < rem && rem <= incl);
         const int L = __ffsll((unsigned long long)hit) - 1;
         uint32_t bin = 0, r = rem - excl;
         if (r <= c0) bin = 255 - 4 * lane;
@@ -370,7 +375,7 @@ __device__ __forceinline__ uint32_t wave_top4(uint32_t v) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t mk = wave_max_u32(v);
-        const uint64_t at = __ballot(v == mk);  // never empty: mk is some lane's key
+        const uint64_t at = wave_ballot(v == mk);  // never empty: mk is some lane's key
         if (lane == (int)__builtin_ctzll(at)) v = 0u;
         if (lane == i) mine = mk;
     }
@@ -384,7 +389,7 @@ __device__ __forceinline__ uint32_t wave_mth_largest64(uint32_t v, int m) {
 #pragma unroll
     for (int b = 31; b >= 0; --b) {
         const uint32_t cand = ans | (1u << b);
-        if (__popcll(__ballot(v >= cand)) >= m) ans = cand;
+        if (__popcll(wave_ballot(v >= cand)) >= m) ans = cand;
     }
     return ans;
 }

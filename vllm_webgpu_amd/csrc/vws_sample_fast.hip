@@ -356,10 +356,10 @@ __device__ __forceinline__ void fast_stream_part(const KArgs& a, FastSmem& sm, i
     // candidate test of one element (wave-uniform call)
     auto slot = [&](float v, int idx, bool valid) __attribute__((always_inline)) {
         bool c = valid && v >= cb.tauf;
-        if (__ballot(c) == 0ull) return;
+        if (wave_ballot(c) == 0ull) return;
         if (hh) {
             const bool hit = c && fbit(sm, idx, lo);
-            if (__ballot(hit) != 0ull) {
+            if (wave_ballot(hit) != 0ull) {
                 if (gather) {
                     c = c && !hit;
                 } else if (hit) {
@@ -399,7 +399,7 @@ __device__ __forceinline__ void fast_stream_part(const KArgs& a, FastSmem& sm, i
             for (int q = 0; q < U; ++q)
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) any |= (buf[q][j] >= cb.tauf);
-            if (__ballot(any) != 0ull) {
+            if (wave_ballot(any) != 0ull) {
 #pragma unroll
                 for (int q = 0; q < U; ++q) {
                     const int i0 = body_index(sl, (it * U + q) * NT + tid);
@@ -479,7 +479,7 @@ __device__ __forceinline__ void fast_stream_part(const KArgs& a, FastSmem& sm, i
         for (int base = 0; base < cb.cnt; base += 64) {
             const int i = base + lane;
             const bool keep = i < cb.cnt && cb.ck[i] >= kth;
-            const uint64_t bal = __ballot(keep);
+            const uint64_t bal = wave_ballot(keep);
             uint32_t off = 0;
             if (lane == 0 && bal) off = atomicAdd(&sm.outcnt, (uint32_t)__popcll(bal));
             off = __shfl(off, 0, 64);
@@ -674,7 +674,7 @@ __device__ __forceinline__ void fast_finish_row(const KArgs& a, FastSmem& sm, in
             y = val_of(mk[j]) / Tt;
             keep = key_of(y) != 0u && y >= kth_y && (y - m) >= lp_min;
         }
-        const uint64_t bal = __ballot(keep);
+        const uint64_t bal = wave_ballot(keep);
         uint32_t off = 0;
         if (lane == 0 && bal) off = atomicAdd(&sm.nkeep, (uint32_t)__popcll(bal));
         off = __shfl(off, 0, 64);

@@ -195,7 +195,7 @@ __device__ __noinline__ int row_fixup(int w, int from, int cnt) {
                 }
             }
         }
-        const uint64_t bal = __ballot(keep);
+        const uint64_t bal = wave_ballot(keep);
         if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
         out += __popcll(bal);
         wave_sync();
@@ -222,7 +222,7 @@ __device__ __noinline__ uint64_t row_compact(int w, int nfix, int cnt, int k) {
         uint32_t kk = 0;
         int32_t ii = 0;
         if (i < cnt) { kk = ck[i]; ii = ci[i]; keep = kk >= kth; }
-        const uint64_t bal = __ballot(keep);
+        const uint64_t bal = wave_ballot(keep);
         if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
         out += __popcll(bal);
         wave_sync();
@@ -292,10 +292,10 @@ struct RowCand {
             int32_t ii = 0;
             if (i < cnt) { kk = ck[i]; ii = ci[i]; }
             const bool keep = i < cnt && kk != 0u && kk >= tau;
-            const uint64_t bal = __ballot(keep);
+            const uint64_t bal = wave_ballot(keep);
             if (keep) { const int pos = out + lane_prefix(bal); ck[pos] = kk; ci[pos] = ii; }
             out += __popcll(bal);
-            outfix += __popcll(__ballot(keep && i < nfix));
+            outfix += __popcll(wave_ballot(keep && i < nfix));
             wave_sync();
         }
         cnt = out;
@@ -303,7 +303,7 @@ struct RowCand {
     }
     // Appends (kk, idx) from the lanes where c holds; wave-uniform call.
     __device__ __forceinline__ void append(bool c, uint32_t kk, int32_t idx) {
-        uint64_t bal = __ballot(c);
+        uint64_t bal = wave_ballot(c);
         if (!bal || ovf) return;
         int n = __popcll(bal);
         if (cnt + n > kRowCap) {
@@ -313,7 +313,7 @@ struct RowCand {
             nfix = cnt;
             set_tau(__builtin_amdgcn_readfirstlane((uint32_t)(rc >> 32)));
             c = c && kk >= tau;
-            bal = __ballot(c);
+            bal = wave_ballot(c);
             n = __popcll(bal);
             if (cnt + n > kRowCap) { ovf = true; return; }
         }
@@ -524,7 +524,7 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     const float rkey = e / (0.0f - log_det(uu));
     const uint32_t kb = (kept && rkey >= 0.0f) ? f2u(rkey) + 1u : 0u;
     const uint32_t kmax = wave_max_u32(kb);
-    const uint64_t at = __ballot(kb == kmax && kmax != 0u);
+    const uint64_t at = wave_ballot(kb == kmax && kmax != 0u);
     int win = -1;
     uint32_t widx = 0u;
     if (at) {
@@ -532,12 +532,12 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
         widx = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, win);
         if (at & (at - 1ull)) {  // equal keys: the lowest index
             widx = wave_min_u32(((at >> lane) & 1ull) ? (uint32_t)key : 0xFFFFFFFFu);
-            win = (int)__builtin_ctzll(__ballot(((at >> lane) & 1ull) && (uint32_t)key == widx));
+            win = (int)__builtin_ctzll(wave_ballot(((at >> lane) & 1ull) && (uint32_t)key == widx));
         }
     }
     const uint32_t second = wave_max_u32(lane != win ? kb : 0u);
-    const int nkept = __popcll(__ballot(kept));
-    const int nrem = __popcll(__ballot(removed));
+    const int nkept = __popcll(wave_ballot(kept));
+    const int nrem = __popcll(wave_ballot(removed));
     const uint64_t cat = readlane64(C, nkept - 1);              // smallest kept cumulative mass
     const uint64_t cprev = nrem ? readlane64(C, nkept) : 0ull;  // largest removed one
     if (lane == 0) {
@@ -753,7 +753,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     RowCand cb;
     auto slot = [&](float v, int idx, bool valid) __attribute__((always_inline)) {
         const bool c = valid && v >= cb.tauf;
-        if (__ballot(c) == 0ull) return;
+        if (wave_ballot(c) == 0ull) return;
         cb.append(c, key_of(v), idx);  // raw value; penalties are applied by RowCand::finish
     };
     // One vector (VEC elements per lane) at a time: the lane maximum against the threshold
@@ -768,7 +768,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             float mq = buf[q][0];
 #pragma unroll
             for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
-            const uint64_t hm = __ballot(ok && mq >= cb.tauf);
+            const uint64_t hm = wave_ballot(ok && mq >= cb.tauf);
             if (__builtin_expect(hm == 0ull, 1)) continue;
             cb.template append_vec<VEC>(buf[q], sl.a + vi * VEC, hm);
         }
@@ -864,7 +864,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             const uint32_t kx = have ? sm.ckey[wave][lane] : 0u;
             const int32_t ii = have ? sm.cidx[wave][lane] : 0;
             const bool keep = kx != 0u && kx >= cb.tau;
-            const uint64_t bal = __ballot(keep);
+            const uint64_t bal = wave_ballot(keep);
             uint32_t b = 0;
             if (lane == 0) b = atomicAdd(&sm.npack, (uint32_t)__popcll(bal));
             const int pbase = __builtin_amdgcn_readlane(b, 0);
@@ -965,7 +965,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     if (wave * kWave < total) {
         const float y = val_of(myk);
         const bool keep = topk && (y - m) >= lp_min;
-        const uint64_t bal = __ballot(keep);
+        const uint64_t bal = wave_ballot(keep);
         uint32_t off = 0;
         if (lane == 0 && bal) off = atomicAdd(&sm.nkeep, (uint32_t)__popcll(bal));
         off = __builtin_amdgcn_readlane(off, 0);

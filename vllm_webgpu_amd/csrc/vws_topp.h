@@ -34,7 +34,7 @@ namespace vws {
 
 constexpr int kTpWaves = kGenWaves;       // 16
 constexpr int kTpCapW = 832;              // candidate slots per wave
-constexpr int kTpSlots = kTpCapW + kWave; // and one scratch slot per lane (stores of non-candidates)
+constexpr int kTpSlots = kTpCapW;         // slots per wave
 constexpr int kTpSoft = 704;              // a wave holding more after half an iteration compacts
 constexpr int kTpKeep = 512;              // entries a compaction keeps (ties included)
 constexpr float kTpFill = 0.65f;          // share of the slots the seed threshold aims to fill
@@ -55,7 +55,7 @@ constexpr int VWS_FALLBACK_TOPL = 8;        // the top-L logprobs reach below th
 
 struct TopPSmem {
     // Each wave's candidates: raw bits during the stream, order keys from the finish on; and
-    // their indices.  Slots kTpCapW.. are per-lane scratch for the stores of non-candidates.
+    // their indices.
     uint32_t ck[kTpWaves][kTpSlots];
     int32_t ci[kTpWaves][kTpSlots];
     union {
@@ -128,6 +128,15 @@ __device__ __forceinline__ int tp_bucket(float d) {
     return dd < 32.0f ? (int)(dd * 64.0f) : kTpBuckets - 1;
 }
 
+// A buffered entry's index word from the finish on: the element index (bits 0-18; V <= 2^19),
+// the entry's bucket (bits 19-29), a survivor bit and a bit for entries below the row's final
+// threshold, so that later phases need no division or bucket of their own.
+constexpr uint32_t kTpIdxMask = (1u << 19) - 1u;
+constexpr uint32_t kTpSurv = 1u << 30;
+constexpr uint32_t kTpBelow = 1u << 31;
+__device__ __forceinline__ int tp_code_bucket(uint32_t c) { return (int)((c >> 19) & 0x7FFu); }
+__device__ __forceinline__ bool tp_code_cand(uint32_t c) { return (c & (kTpBelow | kTpSurv)) == kTpSurv; }
+
 __device__ __forceinline__ uint32_t tp_u(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ uint64_t tp_u64(uint64_t v) {
     return ((uint64_t)tp_u((uint32_t)(v >> 32)) << 32) | tp_u((uint32_t)v);
@@ -151,33 +160,31 @@ struct TpBuf {
             tauf = (tau > 0x007FFFFFu) ? val_of(tau) : -__builtin_inff();
         }
     }
-    // Stores the elements c[j] of one vector of every lane (v, first index i0), with one
-    // capacity check for the whole vector and no branch per element: a lane stores every
-    // element, the non-candidates into its own scratch slot.  Wave-uniform call.  A full
-    // buffer marks the row for the multi-pass path (the stream compacts every half iteration,
-    // from kTpSoft entries on, so this takes more than kTpCapW - kTpSoft candidates in half an
-    // iteration of one wave).
+    // Stores the candidates of one vector of every lane (elements v[j] >= tauf of a vector in
+    // the row, okv; first index i0; bal[j] the wave's ballot of element j's test), with one
+    // capacity check for the whole vector; each candidate lane writes its own slot (exec-masked
+    // stores, placed by mbcnt).  Wave-uniform call.  A full buffer marks the row for the
+    // multi-pass path (the stream compacts every half iteration, from kTpSoft entries on, so
+    // this takes more than kTpCapW - kTpSoft candidates in half an iteration of one wave).
     template <int VEC>
-    __device__ __forceinline__ void append_vec(TopPSmem& sm, const float* v, const bool* c, int i0) {
-        uint64_t bal[VEC];
+    __device__ __forceinline__ void append_vec(TopPSmem& sm, const float* v, const uint64_t* bal,
+                                               bool okv, int i0) {
         int tot = 0;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            bal[j] = __ballot(c[j]);
-            tot += __popcll(bal[j]);
-        }
+        for (int j = 0; j < VEC; ++j) tot += __popcll(bal[j]);
         if (ovf || cnt + tot > kTpCapW) {
             if (!ovf && lane_id() == 0) atomicOr(&sm.status, 1u);
             ovf = true;
             return;
         }
-        const int scratch = kTpCapW + lane_id();
         int base = cnt;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            const int pos = c[j] ? base + lane_prefix(bal[j]) : scratch;
-            sm.ck[w][pos] = f2u(v[j]);
-            sm.ci[w][pos] = i0 + j;
+            if (okv && v[j] >= tauf) {  // the lanes of bal[j]
+                const int pos = base + lane_prefix(bal[j]);
+                sm.ck[w][pos] = f2u(v[j]);
+                sm.ci[w][pos] = i0 + j;
+            }
             base += __popcll(bal[j]);
         }
         cnt = base;
@@ -217,7 +224,7 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
                 }
             }
         }
-        const uint64_t bal = __ballot(keep);
+        const uint64_t bal = wave_ballot(keep);
         if (keep) {
             const int pos = out + lane_prefix(bal);
             ck[pos] = f2u(val_of(kk));  // back to raw bits
@@ -301,16 +308,24 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     double acc = 0.0, accr = 0.0;
     float accz = 0.0f;
     // one vector of VEC elements starting at element i0 (okv: in the row): candidates into the
-    // buffer, every other element into the sums (a zero term for NaN and -inf)
-    auto consume = [&](const float* v, int i0, bool okv, bool any_lane) __attribute__((always_inline)) {
-        bool cj[VEC];
+    // buffer, every other element into the sums (a zero term for NaN and -inf).  The ballots of
+    // the element tests decide whether any lane appends (no separate vector test: a wave almost
+    // always has a candidate somewhere in a vector position).
+    auto consume = [&](const float* v, int i0, bool okv) __attribute__((always_inline)) {
+        uint64_t bal[VEC];
+        uint64_t any = 0ull;
+        // ballots of single compares (the compiler takes their lane masks as they are)
+        const uint64_t okm = wave_ballot(okv);
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) cj[j] = okv && v[j] >= cb.tauf;
-        if (any_lane) cb.append_vec<VEC>(sm, v, cj, i0);
+        for (int j = 0; j < VEC; ++j) {
+            bal[j] = wave_ballot(v[j] >= cb.tauf) & okm;
+            any |= bal[j];
+        }
+        if (any) cb.append_vec<VEC>(sm, v, bal, okv, i0);
         float s = 0.0f, z = 0.0f, sr = 0.0f;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            const bool inc = okv && !cj[j];
+            const bool inc = okv && !(v[j] >= cb.tauf);
             float zj;
             const float t = tp_term(v[j], aw, c, zj);
             const float tt = inc ? t : 0.0f;
@@ -343,11 +358,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         for (int q = 0; q < U; ++q) {
             if (q == U / 2) shrink();
             const int vi = (it * U + q) * NT + t;
-            const bool okv = vi < nbody;
-            float mq = buf[q][0];
-#pragma unroll
-            for (int j = 1; j < VEC; ++j) mq = __builtin_fmaxf(mq, buf[q][j]);
-            consume(buf[q], sl.a + vi * VEC, okv, __ballot(okv && mq >= cb.tauf) != 0ull);
+            consume(buf[q], sl.a + vi * VEC, vi < nbody);
         }
     };
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
@@ -366,13 +377,10 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         int i0 = 0;
         if (tid <= 1) i0 = sl.load_edge(tid, v);
         const int end = tid == 0 ? sl.a : V;
-        bool anyl = false;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) {
+        for (int j = 0; j < VEC; ++j)
             if (!(tid <= 1 && i0 + j < end)) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
-            anyl = anyl || v[j] >= cb.tauf;
-        }
-        consume(v, i0, true, __ballot(anyl) != 0ull);
+        consume(v, i0, true);
     }
 
     // publish the wave's results
@@ -742,14 +750,18 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         for (int i = lane; i < cnt; i += kWave) {
             const float x = u2f(sm.ck[wave][i]);
             const uint32_t kk = key_of(x);
-            sm.ck[wave][i] = kk;
             const float y = greedy ? x : x / Tt;
             const float d = y - m;
             const bool surv = !greedy && key_of(y) != 0u && d >= lp_min;
-            const uint64_t w = surv ? mass_of(exp_det(d)) : 0ull;
-            if (L >= 0) s0b += exp_det(x - xmax);
+            const float e = exp_det(d);
+            const uint64_t w = surv ? mass_of(e) : 0ull;
+            // raw logprobs' normaliser: x - max x is d itself for greedy rows and T = 1
+            if (L >= 0) s0b += (greedy || Tt == 1.0f) ? e : exp_det(x - xmax);
+            const int b = tp_bucket(d);
+            sm.ck[wave][i] = kk;
+            sm.ci[wave][i] = (int32_t)(((uint32_t)sm.ci[wave][i] & kTpIdxMask) | ((uint32_t)b << 19) |
+                                       (surv ? kTpSurv : 0u) | (kk < tauk ? kTpBelow : 0u));
             if (kk >= tauk) {
-                const int b = tp_bucket(d);
                 if (L > 0) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
                 if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
                 wc += w;
@@ -785,7 +797,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         uint64_t best = 0ull;
         for (int i = lane; i < cnt; i += kWave) {
             if (sm.ck[wave][i] == maxk) {
-                const uint64_t pk = ((uint64_t)maxk << 32) | (uint32_t)(0x7FFFFFFF - sm.ci[wave][i]);
+                const uint64_t pk = ((uint64_t)maxk << 32) |
+                                    (0x7FFFFFFFu - ((uint32_t)sm.ci[wave][i] & kTpIdxMask));
                 best = pk > best ? pk : best;
             }
         }
@@ -921,14 +934,12 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                         if (tid == 0) sm.bc[4] = 0u;
                         __syncthreads();
                         for (int i = lane; i < cnt; i += kWave) {
-                            const uint32_t kk = sm.ck[wave][i];
-                            if (kk < tauk) continue;
-                            const float y = val_of(kk) / Tt;
-                            const float d = y - m;
-                            if (!(key_of(y) != 0u && d >= lp_min) || tp_bucket(d) != bstar) continue;
+                            const uint32_t c = (uint32_t)sm.ci[wave][i];
+                            if (!tp_code_cand(c) || tp_code_bucket(c) != bstar) continue;
+                            const float y = val_of(sm.ck[wave][i]) / Tt;
                             const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
                             if (pos < (uint32_t)kTpGather)
-                                sm.g.key[pos] = ((uint64_t)key_of(y) << 32) | (uint32_t)sm.ci[wave][i];
+                                sm.g.key[pos] = ((uint64_t)key_of(y) << 32) | (c & kTpIdxMask);
                         }
                         if (wide) {
                             pass(kTpPassWideRace, tauk, bstar);
@@ -1055,19 +1066,22 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int i = i0 + q * kWave;
-                const uint32_t kk = i < cnt ? sm.ck[wave][i] : 0u;
-                const float y = val_of(kk) / Tt;
-                const float d = y - m;
-                const bool sv = kk != 0u && kk >= tauk && key_of(y) != 0u && d >= lp_min;
-                const int b = tp_bucket(d);
+                const uint32_t c = i < cnt ? (uint32_t)sm.ci[wave][i] : kTpBelow;
+                const bool sv = tp_code_cand(c);
+                const int b = tp_code_bucket(c);
                 below_cands += (sv && b > bstar) ? 1u : 0u;
                 kq[q] = sv && b < bstar;
-                dq[q] = d;
-                yq[q] = key_of(y);
-                iq[q] = i < cnt ? sm.ci[wave][i] : 0;
+                iq[q] = (int32_t)(c & kTpIdxMask);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) uq[q] = kq[q] ? row_uniform(a, r, iq[q]) : 0.5f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (!kq[q]) continue;
+                const float y = val_of(sm.ck[wave][i0 + q * kWave]) / Tt;
+                dq[q] = y - m;
+                yq[q] = key_of(y);
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 if (!kq[q]) continue;
@@ -1187,14 +1201,12 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (ncand < (uint32_t)L) return VWS_FALLBACK_TOPL;  // the top-L reaches below the candidates
             const int bl = (int)tp_u(sm.bc[15]);
             for (int i = lane; i < cnt; i += kWave) {
-                const uint32_t kk = sm.ck[wave][i];
-                if (kk < tauk) continue;
-                const float d = (greedy ? val_of(kk) : val_of(kk) / Tt) - m;
-                if (tp_bucket(d) > bl) continue;
+                const uint32_t c = (uint32_t)sm.ci[wave][i];
+                if ((c & kTpBelow) || tp_code_bucket(c) > bl) continue;
                 const uint32_t pos = atomicAdd(&sm.bc[7], 1u);
                 if (pos < (uint32_t)kTpLpCap) {
-                    sm.lp.key[pos] = kk;
-                    sm.lp.idx[pos] = sm.ci[wave][i];
+                    sm.lp.key[pos] = sm.ck[wave][i];
+                    sm.lp.idx[pos] = (int32_t)(c & kTpIdxMask);
                 }
             }
             __syncthreads();
