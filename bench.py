@@ -95,6 +95,28 @@ def v1_forward_timing(w, logits, T, K, P, MP, R, PR, FR, hist, dev, steps: int, 
             "uniforms": "generated in the kernel (Philox-4x32-10, one key per row and step)"}
 
 
+def history_free_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
+                           stream, steps: int, warmup: int) -> float:
+    """The sampling kernel on the same logits and uniforms with no history (penalties off)."""
+    import torch
+
+    argv = []
+    for lg, u, _ in sets:
+        a = build_args(lib_mod, lg, T, K, P, MP, R, PR, FR, None, u, out, flags, nkept, ws, lp)
+        a.stream = stream.cuda_stream
+        argv.append(a)
+    for i in range(warmup):
+        lib_mod.check(L.vws_sample(ctypes.byref(argv[i % len(argv)])))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        L.vws_sample(ctypes.byref(argv[i % len(argv)]))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps * 1e3
+
+
 def generated_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
                         stream, B, steps: int, warmup: int) -> float:
     """The sampling kernel alone with generated uniforms (keys instead of a [B, V] tensor)."""
@@ -367,6 +389,14 @@ def main():
     # the same step through the vLLM-v1 front end (Sampler.forward on a SamplingMetadata), with
     # the uniforms generated in the kernel from one key per row (no [B, V] tensor), and the
     # kernel alone in that mode
+    # the same launch without the history (the penalty step skipped): what re-hashing the
+    # padded histories every step costs inside the launch
+    nohist_us = None
+    if H0 is not None and not args.skip_v1:
+        nohist_us = history_free_kernel_us(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags,
+                                           nkept, ws, lp, stream, min(args.steps, 300),
+                                           min(args.warmup, 30))
+        log(f"the same launch without the history: {nohist_us:.2f} us")
     v1 = gen_us = None
     if not args.skip_v1:
         v1 = v1_forward_timing(w, sets[0][0], T, K, P, MP, R, PR, FR, sets[0][2], dev,
@@ -424,6 +454,7 @@ def main():
         "near_tie_rows": near_tie,
         "kernel_us": {"sample" if probs_out is None else "sample+softmax": kern_ms * 1e3},
         "kernel_us_generated_uniforms": gen_us,
+        "kernel_us_without_history": nohist_us,
         "v1_sampler_forward": None if v1 is None else {
             **v1, "kernel_us": kern_ms * 1e3, "wall_vs_kernel": v1["wall_us"] / (kern_ms * 1e3)},
         "kernel_us_event_pairs": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
