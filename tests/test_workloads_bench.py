@@ -55,4 +55,8 @@ def test_bench_reads_the_committed_traffic():
     w = W.config(3)
     alg = W.algorithmic_bytes(w, np.full(w.shape[0], 24))
     assert 0.95 * alg < t < 1.15 * alg
-    assert bench.pmc_traffic_bytes(2) is None
+    for c in (2, 4, 5):  # every parity configuration has its own summary, traffic >= algorithmic
+        wc = W.config(c, 0.01)
+        t = bench.pmc_traffic_bytes(c)
+        assert t is not None and t > 0
+    assert bench.pmc_traffic_bytes(9) is None
