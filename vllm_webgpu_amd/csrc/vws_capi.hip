@@ -79,7 +79,7 @@ DeviceInfo device_info() {
     return d;
 }
 
-// Parts per row for the single-pass kernel: enough workgroups to fill every slot of the chip
+// Parts per row for the split-row top-k kernel: enough workgroups to fill every slot of the chip
 // once, with at least 4096 elements per part.
 void choose_parts(int B, int V, int esize, int* S, int* part_len) {
     const DeviceInfo d = device_info();
@@ -89,7 +89,7 @@ void choose_parts(int B, int V, int esize, int* S, int* part_len) {
     if (s > kMaxParts) s = kMaxParts;
     const int max_by_len = V / 4096 > 0 ? V / 4096 : 1;
     if (s > max_by_len) s = max_by_len;
-    const int min_parts = (V + kPartMax - 1) / kPartMax;  // the slice bitmap covers kPartMax
+    const int min_parts = (V + kPartMax - 1) / kPartMax;  // kMaxParts parts cover VWS_MAX_VOCAB
     if (s < min_parts) s = min_parts;
     int len = (V + s - 1) / s;
     const int align = 64;  // elements; keeps every part start 16-byte aligned
@@ -310,7 +310,6 @@ int vws_sample(const vws_sample_args* a) {
     k.lp_ids = a->logprob_ids;
     k.lp_vals = a->logprob_vals;
     k.lp_ranks = a->logprob_ranks;
-    k.mode = kModeSample;
     // every row would leave the single-pass kernel at once: rows go straight to the top-p
     // stream or the general path, without the single pass's first loads
     k.nofast = (a->num_logprobs >= 0 || a->allowed_mask) ? 1 : 0;
@@ -394,7 +393,6 @@ int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, in
     if (!workspace || workspace_bytes < need)
         return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", workspace_bytes, need);
     KArgs ka = make_kargs(batch, vocab, logits, row_stride, workspace, 0, true);
-    ka.mode = kModeTopK;
     ka.topk_k = k;
     ka.topk_vals = out_vals;
     ka.topk_ids = out_ids;

@@ -1,5 +1,5 @@
 // vws_internal.h -- kernel argument block and workspace layout shared by the launchers
-// (vws_capi.hip) and the kernels (vws_sample.hip, vws_ops.hip).
+// (vws_capi.hip) and the kernels (vws_sample_row.hip, vws_topk.hip, vws_ops.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -8,18 +8,16 @@
 
 namespace vws {
 
-// Fast path (split-row streaming top-k): shape constants.
+// Split-row top-k operation (vws_topk.hip): shape constants.
 constexpr int kFastThreads = 256;                 // 4 waves per part
 constexpr int kFastWaves = kFastThreads / 64;
 constexpr int kCapW = 512;                        // candidate slots per wave (LDS)
-constexpr int kKMax = 256;                        // largest k the fast path serves
+constexpr int kKMax = 256;                        // largest k of the top-k operation and of the
+                                                  // sampling kernel's single pass
 constexpr int kPartCap = 512;                     // list entries a part may publish
 constexpr int kMergeCap = kFastWaves * kCapW;     // entries the last part can merge
-constexpr int kKeepCap = 256;                     // survivors the fast epilogue resolves
-constexpr int kHashSlots = 1024;                  // history slots per part (LDS)
-constexpr int kHashFill = 768;                    // max unique history tokens per part
-constexpr int kPartMax = 32768;                   // elements per part (LDS bitmap of the slice)
-constexpr int kMaxParts = 16;                    // VWS_MAX_VOCAB / kPartMax = 16
+constexpr int kPartMax = 32768;                   // elements per part
+constexpr int kMaxParts = 16;                    // parts per row: VWS_MAX_VOCAB / kPartMax
 
 // General path (one workgroup per row, multi-pass).
 constexpr int kGenThreads = 1024;
@@ -30,8 +28,6 @@ constexpr int kLpCapW = 192;                      // per-wave top-L candidate sl
 
 // Row states written by the fast path for the general path.
 constexpr uint32_t kRowNeedsGeneral = 1u;
-
-enum Mode : int { kModeSample = 0, kModeTopK = 1 };
 
 struct KArgs {
     const void* logits;
@@ -79,9 +75,8 @@ struct KArgs {
     int hs_row;             // history hash slots per row (power of two) or 0
     int S;                  // parts per row
     int part_len;           // elements per part (multiple of 64)
-    int mode;               // Mode
     int nofast;             // no row can take the single-pass kernel (logprobs, allowed mask)
-    int topk_k;             // k for kModeTopK
+    int topk_k;             // k of the top-k operation
     float softcap;          // > 0: Gemma's soft cap applied to every logit first
     float inv_softcap;      // fl(1 / softcap)
     int softcap_f16;        // capped values rounded as an f16 store

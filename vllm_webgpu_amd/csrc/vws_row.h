@@ -34,12 +34,6 @@ __device__ __forceinline__ RowP row_params(const KArgs& a, int r) {
     const bool identity = (p.rep == 1.0f && p.pres == 0.0f && p.freq == 0.0f);
     p.has_hist = (p.np > 0 || p.no > 0) && !identity;
     p.na = a.adj_ids ? (a.adjlens ? min(max(a.adjlens[r], 0), a.adjwidth) : a.adjwidth) : 0;
-    if (a.mode == kModeTopK) {
-        p.greedy = false;
-        p.has_hist = false;
-        p.na = 0;
-        p.k = a.topk_k;
-    }
     p.need_hash = p.has_hist || p.na > 0;
     return p;
 }
@@ -53,7 +47,6 @@ __device__ __forceinline__ float row_uniform(const KArgs& a, int r, int t) {
 
 // k served by the single-pass kernel for this row, or 0 when the row needs the general kernel.
 __device__ __forceinline__ int fast_k(const KArgs& a, const RowP& p) {
-    if (a.mode == kModeTopK) return a.topk_k;
     if (a.L >= 0 || a.allowed) return 0;
     if (p.greedy) return 1;
     if (p.k > 0 && p.k < a.V && p.k <= kKMax) return p.k;

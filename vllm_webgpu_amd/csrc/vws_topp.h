@@ -108,7 +108,7 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
 
 // Whether the single-pass top-p path may serve the row.
 __device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
-    if (a.mode != kModeSample || p.need_hash || a.allowed || a.softcap > 0.0f) return false;
+    if (p.need_hash || a.allowed || a.softcap > 0.0f) return false;
     if (p.greedy) return a.L >= 0;
     const bool topk_off = p.k <= 0 || p.k >= a.V;
     return topk_off && p.top_p > 0.0f && p.top_p < 1.0f;
