@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 4
+#define VWS_ABI_VERSION 5
 
 /* status codes */
 #define VWS_OK 0
@@ -58,8 +58,8 @@ extern "C" {
                                         more pass races them (diagnostic only) */
 /* Bits 16-23 (diagnostic only): why a row left the single-pass top-p path for the multi-pass
  * kernel (1 candidate overflow, 2 non-finite sum, 3 no finite maximum, 6 ambiguous after the
- * exact pass, 7 boundary bucket too large, 8 top-L below the candidates; 4 and 5 are no longer
- * used). */
+ * exact pass, 7 boundary bucket too large, 8 top-L below the candidates, 9 a pass shared with
+ * other workgroups not completed in time; 4 and 5 are no longer used). */
 
 #define VWS_MAX_VOCAB (1 << 19)       /* masses are floor(e * 2^44) summed in 64 bits */
 #define VWS_MAX_LOGPROBS 64
@@ -154,9 +154,13 @@ int32_t vws_abi_version(void);
 const char* vws_last_error(void);
 
 /* Bytes of workspace vws_sample needs for this shape and history width
- * (prompt_width + output_width + adjust_width): the history hash of rows served by the
- * multi-pass path, B x (power of two >= 2 x history_width, at least 64) x 16 bytes.  0 without
- * a history, in which case `workspace` may be NULL. */
+ * (prompt_width + output_width + adjust_width): a fixed region (about 530 KiB, first) through
+ * which the workgroups of one launch share the extra passes over a row's logits that some
+ * top-p rows need, and through which a batch larger than the device's resident workgroups
+ * gets its rows handed out; then the history hash of rows served by the multi-pass path,
+ * B x (power of two >= 2 x history_width, at least 64) x 16 bytes.  Every operation's
+ * workspace starts with that same region (the others leave it alone), so one buffer can serve
+ * them all in stream order. */
 size_t vws_sample_workspace_size(int32_t batch, int32_t vocab, int32_t history_width);
 
 /* Clears a workspace on `stream` (a fill kernel, safe under graph capture).  Required once

@@ -60,12 +60,16 @@ def test_abi_constants_match_header(L):
 
 
 def test_workspace_sizes(L):
+    # a fixed region first (rows' shared passes, the row queue), the same for every batch
+    c0 = L.vws_sample_workspace_size(256, 128256, 0)
+    assert c0 > 500_000 and c0 % 256 == 0
+    assert L.vws_sample_workspace_size(1, 100, 0) == c0
+    assert L.vws_sample_workspace_size(4096, 262144, 0) == c0
+    # then the history hash: 256 rows x 1024 slots (power of two >= 2 x 512) x 4 words
     a = L.vws_sample_workspace_size(256, 128256, 512)
-    # history hash only: 256 rows x 1024 slots (power of two >= 2 x 512) x 4 words
-    assert a == 256 * 1024 * 16
-    assert L.vws_sample_workspace_size(256, 128256, 0) == 0       # no history: no workspace
-    assert L.vws_sample_workspace_size(512, 128256, 512) == 2 * a
-    assert L.vws_sample_workspace_size(4, 100, 1) == 4 * 64 * 16  # at least 64 slots
+    assert a == c0 + 256 * 1024 * 16
+    assert L.vws_sample_workspace_size(512, 128256, 512) == c0 + 2 * 256 * 1024 * 16
+    assert L.vws_sample_workspace_size(4, 100, 1) == c0 + 4 * 64 * 16  # at least 64 slots
     assert L.vws_sample_workspace_size(0, 100, 0) == 0
     assert L.vws_sample_workspace_size(4, 100, -1) == 0
     t = L.vws_topk_workspace_size(8, 1000, 50)
@@ -151,8 +155,11 @@ def test_processor_lists_grow_the_required_workspace(L):
     assert _status(L, _args(L, allowed_mask=FAKE, allowed_row_stride=32)) == _lib.OK
 
 
-def test_no_history_needs_no_workspace(L):
-    assert _status(L, _args(L, workspace=None, workspace_bytes=0)) == _lib.OK
+def test_sampling_always_needs_the_shared_region(L):
+    assert _status(L, _args(L, workspace=None, workspace_bytes=0)) == _lib.ERR_WORKSPACE_TOO_SMALL
+    c0 = L.vws_sample_workspace_size(4, 1000, 0)
+    assert _status(L, _args(L, workspace_bytes=c0 - 256)) == _lib.ERR_WORKSPACE_TOO_SMALL
+    assert _status(L, _args(L, workspace_bytes=c0)) == _lib.OK
 
 
 def test_greedy_batches_need_no_uniforms(L):

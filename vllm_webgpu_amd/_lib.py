@@ -14,7 +14,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2

@@ -58,6 +58,7 @@ int check_launch(const char* what) {
 struct DeviceInfo {
     int cus = 0;
     int fast_blocks_per_cu = 0;
+    int row_blocks_per_cu = 0;  // sampling workgroups resident per CU at once
 };
 
 DeviceInfo device_info() {
@@ -74,6 +75,9 @@ DeviceInfo device_info() {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fast_kernel<float>, kFastThreads, 0) != hipSuccess || n <= 0) n = 4;
         d.fast_blocks_per_cu = n;
+        int nr = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nr, row_kernel<float>, kGenThreads, 0) != hipSuccess || nr <= 0) nr = 1;
+        d.row_blocks_per_cu = nr;
         (void)hipGetLastError();
     }
     return d;
@@ -237,6 +241,7 @@ KArgs make_kargs(int B, int V, const void* logits, int64_t stride, void* ws, int
     }
     k.hist_hash = w.hs_row ? reinterpret_cast<uint32_t*>(base + w.hash) : nullptr;
     k.hs_row = w.hs_row;
+    if (!parts && ws) k.coop = reinterpret_cast<CoopState*>(base + w.coop);
     return k;
 }
 
@@ -313,14 +318,23 @@ int vws_sample(const vws_sample_args* a) {
     // every row would leave the single-pass kernel at once: rows go straight to the top-p
     // stream or the general path, without the single pass's first loads
     k.nofast = (a->num_logprobs >= 0 || a->allowed_mask) ? 1 : 0;
+    // more rows than workgroups resident at once: the kernel counts its workgroups, so that one
+    // whose row is done waits for other rows' passes only once no workgroup is left to start
+    const int grid = a->batch;
+    if (k.coop) {
+        const DeviceInfo d = device_info();
+        if (a->batch > kCoopMaxGrid) k.coop = nullptr;
+        else if (a->batch > d.cus * d.row_blocks_per_cu) k.coop_count = 1;
+    }
+    const int cf = (k.coop ? 1 : 0) | (k.coop_count ? 2 : 0);
     hipStream_t s = (hipStream_t)a->stream;
     const int ps = prof_start(s, VWS_KERNEL_SAMPLE);
     if (a->dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(row_kernel<float>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
+        hipLaunchKernelGGL(row_kernel<float>, dim3(grid), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, cf, k);
     else if (a->dtype == VWS_DTYPE_BF16)
-        hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
+        hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(grid), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, cf, k);
     else
-        hipLaunchKernelGGL(row_kernel<_Float16>, dim3(a->batch), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, 0, k);
+        hipLaunchKernelGGL(row_kernel<_Float16>, dim3(grid), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, cf, k);
     prof_stop(s, ps);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();

@@ -524,6 +524,36 @@ template <> struct Elem<_Float16> {  // IEEE binary16, widened exactly
     }
 };
 
+// Data shared between the workgroups of one launch (which may run on different XCDs, whose L2
+// caches are not coherent with each other): every access is an agent-scope atomic, which the
+// memory model makes coherent across XCDs without whole-cache writeback or invalidation.  A
+// workgroup publishes with stores_complete() (its own accesses have all completed) and a
+// barrier before the single atomic that signals them; the reader issues its loads only after
+// it has seen that signal.
+__device__ __forceinline__ uint32_t ag_load32(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ag_load64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ag_store32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ag_store64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ag_add32(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ag_add64(uint64_t* p, uint64_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stores_complete() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Buffer resource over `bytes` bytes at p (raw addressing): a load whose vector offset (plus
 // instruction offset) is at or past `bytes` returns zero and never faults.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {

@@ -29,6 +29,53 @@ constexpr int kLpCapW = 192;                      // per-wave top-L candidate sl
 // Row states written by the fast path for the general path.
 constexpr uint32_t kRowNeedsGeneral = 1u;
 
+// Cooperative passes (vws_topp.h).  A top-p row whose decision needs a further pass over its
+// logits hands the pass out in chunks of kCoopChunkVecs 16-byte vectors through a slot here;
+// workgroups whose own row is done take chunks and add their results into the slot.  The
+// region sits at the start of every workspace; each launch leaves it ready for the next one.
+constexpr int kCoopSlots = 16;
+constexpr int kCoopMaxChunks = 64;
+constexpr int kCoopBuckets = 2048;                // the top-p path's exact-mass buckets
+constexpr int kCoopGather = 2048;                 // boundary-bucket members a slot gathers
+constexpr int kCoopChunkVecs = 2 * kGenThreads;   // vectors per chunk (a multiple of this)
+constexpr uint32_t kCoopIdle = 0xFFFFFF00u;       // claim counter of a slot with nothing posted
+
+struct CoopSlot {
+    uint64_t claim;    // generation << 32 | next chunk to hand out
+    uint64_t posted;   // generation << 32 | chunks of the pass
+    uint64_t sw, n, nrem;                  // totals added by the workgroups that helped
+    uint32_t done;     // chunks finished by workgroups other than the owner
+    uint32_t owner;    // row + 1 while a row holds the slot, 0 when free
+    uint32_t ngather;  // boundary-bucket members appended to gkey
+    int32_t kind, r, bstar;                // the pass (read once the chunk is claimed)
+    uint32_t key, ksv, kkeep, kmem;
+    float Tt, m, lp_min;
+    int32_t cvecs;     // vectors per chunk
+    uint32_t pad[2];
+    uint64_t race[kCoopMaxChunks][2];      // wide race per chunk: best, second << 32 | kept
+    uint64_t hmass[kCoopBuckets];          // exact pass: bucket masses
+    uint64_t gkey[kCoopGather];            // wide race: boundary-bucket members
+};
+
+// wgs: workgroups started (bits 0-19) and finished (bits 20-39), counted only when the grid is
+// larger than the device holds at once (coop_count); rows holding a slot (bits 40-51); top-p
+// rows in progress, which may still open a pass (bits 52-63).
+constexpr uint64_t kCoopStarted = 1ull;
+constexpr uint64_t kCoopFinished = 1ull << 20;
+constexpr uint64_t kCoopActive = 1ull << 40;
+constexpr uint64_t kCoopPending = 1ull << 52;
+constexpr int kCoopMaxGrid = (1 << 20) - 1;
+inline __host__ __device__ uint32_t coop_started(uint64_t w) { return (uint32_t)(w & 0xFFFFFu); }
+inline __host__ __device__ uint32_t coop_finished(uint64_t w) { return (uint32_t)((w >> 20) & 0xFFFFFu); }
+inline __host__ __device__ uint32_t coop_active(uint64_t w) { return (uint32_t)((w >> 40) & 0xFFFu); }
+inline __host__ __device__ uint32_t coop_pending(uint64_t w) { return (uint32_t)(w >> 52); }
+
+struct CoopState {
+    uint64_t wgs;
+    uint32_t pad[62];
+    CoopSlot slot[kCoopSlots];
+};
+
 struct KArgs {
     const void* logits;
     int64_t lstride;
@@ -82,11 +129,13 @@ struct KArgs {
     int softcap_f16;        // capped values rounded as an f16 store
     float* topk_vals;       // [B, k]
     int32_t* topk_ids;      // [B, k]
+    CoopState* coop;        // cooperative passes (sampling workspace), or null
+    int coop_count;         // B exceeds the workgroups resident at once: count them in coop->wgs
 };
 
 // Workspace layout (bytes, 256-aligned sections).
 struct WsLayout {
-    size_t counter, state, meta, list, hash, total;
+    size_t counter, state, meta, list, coop, hash, total;
     int hs_row;
 };
 
@@ -99,20 +148,23 @@ inline int hash_slots_for(int history_width) {
     return s;
 }
 
-// Workspace sections.  Sampling and the penalty op keep only the history hash of the multi-pass
-// path (B x hs_row x 4 words); the split top-k op also needs its per-row
-// counters, row states and part lists (parts = true).
+// Workspace sections.  Every layout starts with the cooperative-pass region at offset 0, so that
+// one workspace can serve every operation in turn (the region keeps its state between sampling
+// calls; the other operations leave it alone).  Then: sampling and the penalty op, the history
+// hash of the multi-pass path (B x hs_row x 4 words); the split top-k op (parts = true), its
+// per-row counters, row states and part lists.
 inline WsLayout ws_layout(int B, int V, int history_width, bool parts) {
     (void)V;
     WsLayout w{};
     size_t off = 0;
+    w.coop = off;    off = align256(off + sizeof(CoopState));
     if (parts) {
         w.counter = off; off = align256(off + sizeof(uint32_t) * (size_t)B);
         w.state = off;   off = align256(off + sizeof(uint32_t) * (size_t)B);
         w.meta = off;    off = align256(off + sizeof(uint32_t) * 4 * (size_t)B * kMaxParts);
         w.list = off;    off = align256(off + sizeof(uint2) * (size_t)B * kMaxParts * kPartCap);
     }
-    w.hs_row = hash_slots_for(history_width);
+    w.hs_row = parts ? 0 : hash_slots_for(history_width);
     w.hash = off;    off = align256(off + sizeof(uint32_t) * 4 * (size_t)B * (size_t)w.hs_row);
     w.total = off;
     return w;

@@ -136,28 +136,437 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
     return topp_compact(g_row_sh.t, w, cnt, aw, c, want_raw != 0);
 }
 
-template <typename T>
-__device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
-                                             float lp_min, uint32_t key, int bstar) {
+// lane l's value of v, in every lane (wave-uniform l)
+__device__ __forceinline__ uint64_t lane_bcast64(uint64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 #if defined(__HIP_DEVICE_COMPILE__)  // the kernarg segment exists only in the device pass
-    // every argument is uniform: into scalar registers (the buffer descriptors need them there)
+// The launch arguments of an out-of-line function, read from the kernel's kernarg segment (the
+// kernel hands over its address; a callee has no register of its own for it) into scalar
+// registers.
+__device__ __forceinline__ KArgs kargs_at(uint64_t kernarg) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
     using KArgsConst = const KArgs __attribute__((address_space(4)));
-    const KArgs a = *(KArgsConst*)(((uint64_t)hi << 32) | lo);
+    return *(KArgsConst*)(((uint64_t)hi << 32) | lo);
+}
+#endif
+
+template <typename T>
+__device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KArgs a = kargs_at(kernarg);
+    r = __builtin_amdgcn_readfirstlane(r);
+    v0 = __builtin_amdgcn_readfirstlane(v0);
+    v1 = __builtin_amdgcn_readfirstlane(v1);
+    edges = __builtin_amdgcn_readfirstlane(edges);
+    TopPSmem& sm = g_row_sh.t;
+    TpPassDesc d;
+    d.kind = (int)tp_u((uint32_t)sm.pd.kind);
+    d.key = tp_u(sm.pd.key);
+    d.bstar = (int)tp_u((uint32_t)sm.pd.bstar);
+    d.Tt = tp_uf(sm.pd.Tt);
+    d.m = tp_uf(sm.pd.m);
+    d.lp_min = tp_uf(sm.pd.lp_min);
+    d.ksv = tp_u(sm.pd.ksv);
+    d.kkeep = tp_u(sm.pd.kkeep);
+    d.kmem = tp_u(sm.pd.kmem);
+    TpPassAcc acc;
+    tp_pass_range<T>(a, sm, r, d, v0, v1, edges != 0, acc);
+    tp_pass_reduce(sm, d.kind, acc);
+#else
+    (void)r; (void)kernarg; (void)v0; (void)v1; (void)edges;
+#endif
+}
+
+template <typename T>
+__device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
+                                             float lp_min, uint32_t key, int bstar) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int NT = kGenThreads;
+    // every argument is uniform: into scalar registers (the buffer descriptors need them there)
+    const KArgs a = kargs_at(kernarg);
     kind = __builtin_amdgcn_readfirstlane(kind);
     r = __builtin_amdgcn_readfirstlane(r);
     bstar = __builtin_amdgcn_readfirstlane(bstar);
-    key = tp_u(key);
-    Tt = tp_uf(Tt);
-    m = tp_uf(m);
-    lp_min = tp_uf(lp_min);
+    const int tid = threadIdx.x, lane = tid & 63;
     TopPSmem& sm = g_row_sh.t;
-    if (kind == kTpPassExact) topp_exact_pass<T>(a, sm, r, Tt, m, lp_min, key);
-    else if (kind == kTpPassWideRace) topp_wide_race<T>(a, sm, r, Tt, m, lp_min, key, bstar);
-    else topp_rank_pass<T>(a, sm, r, key);
+    TpPassDesc d;
+    d.kind = kind;
+    d.key = tp_u(key);
+    d.bstar = bstar;
+    d.Tt = tp_uf(Tt);
+    d.m = tp_uf(m);
+    d.lp_min = tp_uf(lp_min);
+    d.ksv = d.kkeep = d.kmem = 0u;
+    if (kind == kTpPassWideRace) {
+        tp_wide_keys(d, &sm.cp[8]);
+        __syncthreads();
+        const uint32_t ksv = tp_u(sm.cp[8]);
+        const uint32_t kkeep = tp_u(sm.cp[9]), kmem = tp_u(sm.cp[10]);
+        d.ksv = ksv;
+        d.kkeep = kkeep > ksv ? kkeep : ksv;
+        d.kmem = kmem > ksv ? kmem : ksv;
+    }
+    Slice<T> sl;
+    sl.init(reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride, 0, a.V);
+    const int nbody = __builtin_amdgcn_readfirstlane(sl.nbody);
+    // chunks of kCoopChunkVecs vectors (a multiple of it for rows of more than
+    // kCoopMaxChunks chunks)
+    const int cmul = (nbody + kCoopMaxChunks * kCoopChunkVecs - 1) / (kCoopMaxChunks * kCoopChunkVecs);
+    const int cvecs = (cmul > 0 ? cmul : 1) * kCoopChunkVecs;
+    const int nch = (nbody + cvecs - 1) / cvecs;
+    CoopState* st = a.coop;
+    const bool coop = st != nullptr && nch >= kCoopMinChunks && nch <= kCoopMaxChunks;
+    if (tid == 0) {
+        sm.pd = d;  // what topp_range_entry runs
+        sm.cp[4] = kCoopNone;
+    }
+    if (coop && tid < kWave) {
+        // wave 0: a free slot for the row
+        const uint32_t own = lane < kCoopSlots ? ag_load32(&st->slot[lane].owner) : 1u;
+        uint64_t fr = wave_ballot(own == 0u);
+        if (lane == 0) {
+            while (fr) {
+                const int s = __builtin_ctzll(fr);
+                fr &= fr - 1ull;
+                uint32_t expect = 0u;
+                if (__hip_atomic_compare_exchange_strong(&st->slot[s].owner, &expect, (uint32_t)r + 1u,
+                                                         __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)) {
+                    sm.cp[4] = (uint32_t)s;
+                    break;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t slot = tp_u(sm.cp[4]);
+    if (slot == kCoopNone) {
+        topp_range_entry<T>(r, kernarg, 0, nbody, 1);
+        return;
+    }
+    CoopSlot& S = st->slot[slot];
+    // describe the pass and clear the totals it adds to, then open its chunks
+    if (kind == kTpPassExact)
+        for (int b = tid; b < kCoopBuckets; b += NT) ag_store64(&S.hmass[b], 0ull);
+    if (kind == kTpPassWideRace && tid < kCoopMaxChunks) {
+        ag_store64(&S.race[tid][0], 0ull);
+        ag_store64(&S.race[tid][1], 0ull);
+    }
+    if (tid == 0) {
+        ag_store64(&S.sw, 0ull);
+        ag_store64(&S.n, 0ull);
+        ag_store64(&S.nrem, 0ull);
+        ag_store32(&S.ngather, 0u);
+        ag_store32(&S.done, 0u);
+        ag_store32(reinterpret_cast<uint32_t*>(&S.kind), (uint32_t)kind);
+        ag_store32(reinterpret_cast<uint32_t*>(&S.r), (uint32_t)r);
+        ag_store32(reinterpret_cast<uint32_t*>(&S.bstar), (uint32_t)bstar);
+        ag_store32(&S.key, d.key);
+        ag_store32(&S.ksv, d.ksv);
+        ag_store32(&S.kkeep, d.kkeep);
+        ag_store32(&S.kmem, d.kmem);
+        ag_store32(reinterpret_cast<uint32_t*>(&S.Tt), f2u(d.Tt));
+        ag_store32(reinterpret_cast<uint32_t*>(&S.m), f2u(d.m));
+        ag_store32(reinterpret_cast<uint32_t*>(&S.lp_min), f2u(d.lp_min));
+        ag_store32(reinterpret_cast<uint32_t*>(&S.cvecs), (uint32_t)cvecs);
+    }
+    stores_complete();
+    __syncthreads();
+    uint32_t gen = 0u;
+    if (tid == 0) {
+        gen = (uint32_t)(ag_load64(&S.claim) >> 40) + 1u;
+        if (!sm.coop_hold) {
+            ag_add64(&st->wgs, kCoopActive);  // the row holds a slot until it is done
+            sm.coop_hold = 1u;
+        }
+        ag_store64(&S.claim, coop_claim_word(gen, (uint32_t)nch));
+        sm.cp[5] = coop_chunk_of(ag_add64(&S.claim, 1ull));
+    }
+    __syncthreads();
+    // the chunks the row claims itself, one at a time; thread 0 keeps the totals
+    RowRace tr;
+    uint64_t t0 = 0ull, t1 = 0ull, t3 = 0ull;
+    uint32_t own = 0u;
+    uint32_t c = tp_u(sm.cp[5]);
+    for (int k = 0; c != kCoopNone; ++k) {
+        const int v0 = (int)c * cvecs;
+        const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
+        topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        __syncthreads();
+        if (tid == 0) {
+            ++own;
+            if (kind == kTpPassWideRace) {
+                RowRace o;
+                o.best = sm.bc64[10];
+                o.second = (uint32_t)sm.bc64[11];
+                o.nkept = (uint32_t)sm.bc64[12];
+                tr.merge(o);
+                t3 += sm.bc64[13];
+            } else {
+                t0 += sm.bc64[10];
+                t1 += sm.bc64[11];
+            }
+            // the next chunk, claimed once this one has run (helpers take the others meanwhile)
+            sm.cp[6 + (k & 1)] = coop_chunk_of(ag_add64(&S.claim, 1ull));
+        }
+        __syncthreads();
+        c = tp_u(sm.cp[6 + (k & 1)]);
+    }
+    // the chunks other workgroups claimed: every one is running, so the wait ends
+    if (tid == 0) {
+        const uint32_t others = (uint32_t)nch - own;
+        uint32_t done = ag_load32(&S.done);
+        for (int poll = 0; done < others && poll < kCoopWaitPolls; ++poll) {
+            __builtin_amdgcn_s_sleep(1);
+            done = ag_load32(&S.done);
+        }
+        sm.cp[4] = done >= others ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!tp_u(sm.cp[4])) {
+        // the slot stays held: a late chunk may still add into it
+        if (tid == 0) sm.coop_fail = 1u;
+        return;
+    }
+    // their totals
+    RowRace hr;
+    if (kind == kTpPassWideRace && tid < nch) {
+        hr.best = ag_load64(&S.race[tid][0]);
+        const uint64_t x = ag_load64(&S.race[tid][1]);
+        hr.second = (uint32_t)(x >> 32);
+        hr.nkept = (uint32_t)x;
+    }
+    if (kind == kTpPassWideRace && tid < kWave) {
+        hr.shfl_merge(32); hr.shfl_merge(16); hr.shfl_merge(8);
+        hr.shfl_merge(4); hr.shfl_merge(2); hr.shfl_merge(1);
+    }
+    if (kind == kTpPassExact) {
+        for (int b = tid; b < kCoopBuckets; b += NT) {
+            const uint64_t v = ag_load64(&S.hmass[b]);
+            if (v) sm.h.hmass[b] += v;
+        }
+    }
+    uint32_t base = 0u, ngh = 0u;
+    if (kind == kTpPassWideRace) {
+        // the boundary members the others gathered, after the row's own
+        ngh = ag_load32(&S.ngather);
+        base = tp_u(sm.bc[4]);
+        const uint32_t nld = ngh < (uint32_t)kCoopGather ? ngh : (uint32_t)kCoopGather;
+        for (uint32_t i = (uint32_t)tid; i < nld; i += NT)
+            if (base + i < (uint32_t)kTpGather) sm.g.key[base + i] = ag_load64(&S.gkey[i]);
+    }
+    // the totals sw, n, nrem, one per lane of wave 0, in one round trip (thread 0 uses them)
+    uint64_t hsw = 0ull, hn = 0ull, hrem = 0ull;
+    if (tid < kWave) {
+        const uint64_t v = tid < 3 ? ag_load64(&S.sw + tid) : 0ull;
+        hsw = lane_bcast64(v, 0);
+        hn = lane_bcast64(v, 1);
+        hrem = lane_bcast64(v, 2);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (kind == kTpPassExact) {
+            sm.bc64[10] = t0 + hsw;
+            sm.bc64[11] = t1 + hn;
+        } else if (kind == kTpPassWideRace) {
+            tr.merge(hr);
+            sm.bc64[10] = tr.best;
+            sm.bc64[11] = tr.second;
+            sm.bc64[12] = tr.nkept;
+            sm.bc64[13] = t3 + hrem;
+            sm.bc[4] = base + ngh;
+        } else {
+            sm.bc64[10] = t0 + hn;
+        }
+        // free the slot: nothing open, no owner
+        ag_store64(&S.claim, coop_claim_word(gen, 0u));
+        ag_store32(&S.owner, 0u);
+    }
 #else
     (void)kind; (void)r; (void)kernarg; (void)Tt; (void)m; (void)lp_min; (void)key; (void)bstar;
+#endif
+}
+
+// A workgroup without a row (or between two rows) runs chunks of the passes other rows opened,
+// adding its totals into their slots.  spin: poll again while rows hold slots (no row of the
+// launch is left to start, so no row waits for this workgroup's CU); otherwise return once no
+// chunk is open.
+template <typename T>
+__device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int NT = kGenThreads;
+    const KArgs a = kargs_at(kernarg);
+    spin = __builtin_amdgcn_readfirstlane(spin);
+    CoopState* st = a.coop;
+    TopPSmem& sm = g_row_sh.t;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // the slot whose description sm.pd holds, its generation, and a chunk claimed there
+    uint32_t got = kCoopNone, gen = 0u, c = kCoopNone;
+    for (int poll = 0; poll < kCoopHelpPolls; ++poll) {
+        if (c == kCoopNone) {
+            // wave 0: the slots with chunks open, a claim on one of them, its description
+            if (tid < kWave) {
+                const uint64_t cl = lane < kCoopSlots ? ag_load64(&st->slot[lane].claim) : 0ull;
+                uint64_t open = wave_ballot(lane < kCoopSlots && coop_chunk_of(cl) != kCoopNone);
+                uint32_t g = kCoopNone, cc = kCoopNone, gn = 0u;
+                if (lane == 0) {
+                    while (open) {
+                        const int s = __builtin_ctzll(open);
+                        open &= open - 1ull;
+                        // acquire: the pass description is read after the claim
+                        const uint64_t x = __hip_atomic_fetch_add(&st->slot[s].claim, 1ull, __ATOMIC_ACQUIRE,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+                        cc = coop_chunk_of(x);
+                        if (cc != kCoopNone) {
+                            g = (uint32_t)s;
+                            gn = (uint32_t)(x >> 40);
+                            break;
+                        }
+                    }
+                }
+                g = (uint32_t)__builtin_amdgcn_readfirstlane((int)g);
+                uint32_t stop = 0u;
+                if (g != kCoopNone) {
+                    // the description's words (kind, r, bstar, key, ksv, kkeep, kmem, Tt, m,
+                    // lp_min, cvecs), one per lane, in one round trip
+                    const uint32_t* dw = reinterpret_cast<const uint32_t*>(&st->slot[g].kind);
+                    const uint32_t w = lane < 11 ? ag_load32(dw + lane) : 0u;
+                    if (lane < 11) sm.cp[8 + lane] = w;
+                    if (lane == 0) {
+                        sm.cp[2] = cc;
+                        sm.cp[1] = gn;
+                    }
+                } else if (lane == 0) {
+                    stop = (!spin || coop_pending(ag_load64(&st->wgs)) == 0u) ? 1u : 0u;
+                }
+                if (lane == 0) {
+                    sm.cp[0] = g;
+                    sm.cp[3] = stop;
+                }
+            }
+            __syncthreads();
+            got = tp_u(sm.cp[0]);
+            if (got == kCoopNone) {
+                const bool stop = tp_u(sm.cp[3]) != 0u;
+                __syncthreads();  // every wave has read the broadcast before wave 0 writes it again
+                if (stop) break;
+                __builtin_amdgcn_s_sleep(8);
+                continue;
+            }
+            c = tp_u(sm.cp[2]);
+            gen = tp_u(sm.cp[1]);
+            if (tid == 0) {
+                // the description as topp_range_entry reads it
+                sm.pd.kind = (int)sm.cp[8];
+                sm.pd.bstar = (int)sm.cp[10];
+                sm.pd.key = sm.cp[11];
+                sm.pd.ksv = sm.cp[12];
+                sm.pd.kkeep = sm.cp[13];
+                sm.pd.kmem = sm.cp[14];
+                sm.pd.Tt = u2f(sm.cp[15]);
+                sm.pd.m = u2f(sm.cp[16]);
+                sm.pd.lp_min = u2f(sm.cp[17]);
+            }
+        }
+        const int r = (int)tp_u(sm.cp[9]);
+        const int kind = (int)tp_u(sm.cp[8]);
+        const int cvecs = (int)tp_u(sm.cp[18]);
+        CoopSlot& S = st->slot[got];
+        // an owner only ever describes a row of this launch and a pass it knows
+        if (r < 0 || r >= a.B || kind < kTpPassExact || kind > kTpPassRank || c >= (uint32_t)kCoopMaxChunks ||
+            cvecs <= 0) {
+            __syncthreads();
+            c = kCoopNone;
+            continue;
+        }
+        // the chunk's totals start from zero here
+        if (kind == kTpPassExact)
+            for (int b = tid; b < kTpBuckets; b += NT) sm.h.hmass[b] = 0ull;
+        if (tid == 0) sm.bc[4] = 0u;
+        __syncthreads();
+        Slice<T> sl;
+        sl.init(reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride, 0, a.V);
+        const int nbody = __builtin_amdgcn_readfirstlane(sl.nbody);
+        const int v0 = (int)c * cvecs;
+        const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
+        topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        __syncthreads();
+        // the next chunk, claimed while this one's totals go out (before this one counts as
+        // done, so the pass cannot have been replaced meanwhile)
+        uint64_t nx = 0ull;
+        if (tid == 0)
+            nx = __hip_atomic_fetch_add(&S.claim, 1ull, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        // added into the slot
+        if (kind == kTpPassExact) {
+            for (int b = tid; b < kTpBuckets; b += NT) {
+                const uint64_t v = sm.h.hmass[b];
+                if (v) ag_add64(&S.hmass[b], v);
+            }
+            if (tid == 0) {
+                ag_add64(&S.sw, sm.bc64[10]);
+                ag_add64(&S.n, sm.bc64[11]);
+            }
+        } else if (kind == kTpPassWideRace) {
+            const uint32_t ng = sm.bc[4];
+            if (tid == 0) {
+                ag_store64(&S.race[c][0], sm.bc64[10]);
+                ag_store64(&S.race[c][1], (sm.bc64[11] << 32) | (uint32_t)sm.bc64[12]);
+                ag_add64(&S.nrem, sm.bc64[13]);
+                sm.cp[4] = ng ? ag_add32(&S.ngather, ng) : 0u;
+            }
+            __syncthreads();
+            const uint32_t base = tp_u(sm.cp[4]);
+            const uint32_t nst = ng < (uint32_t)kTpGather ? ng : (uint32_t)kTpGather;
+            for (uint32_t i = (uint32_t)tid; i < nst; i += NT)
+                if (base + i < (uint32_t)kCoopGather) ag_store64(&S.gkey[base + i], sm.g.key[i]);
+        } else if (tid == 0) {
+            ag_add64(&S.n, sm.bc64[10]);
+        }
+        stores_complete();
+        __syncthreads();
+        if (tid == 0) {
+            ag_add32(&S.done, 1u);
+            // the claimed next chunk: of this pass (same generation) it runs with the same
+            // description; of a later pass the description is read again (a claimed chunk always
+            // runs); none: look again
+            const uint32_t cn = coop_chunk_of(nx);
+            const bool same = ((uint32_t)(nx >> 40) & 0xFFFFFFu) == (gen & 0xFFFFFFu);
+            sm.cp[5] = cn;
+            sm.cp[6] = (cn != kCoopNone && !same) ? 1u : 0u;
+            sm.cp[7] = (uint32_t)(nx >> 40);
+        }
+        __syncthreads();
+        c = tp_u(sm.cp[5]);
+        if (c != kCoopNone && tp_u(sm.cp[6])) {
+            // a later pass in the same slot: its description
+            if (tid < kWave) {
+                const uint32_t* dw = reinterpret_cast<const uint32_t*>(&S.kind);
+                const uint32_t w = lane < 11 ? ag_load32(dw + lane) : 0u;
+                if (lane < 11) sm.cp[8 + lane] = w;
+            }
+            __syncthreads();
+            gen = tp_u(sm.cp[7]);
+            if (tid == 0) {
+                sm.pd.kind = (int)sm.cp[8];
+                sm.pd.bstar = (int)sm.cp[10];
+                sm.pd.key = sm.cp[11];
+                sm.pd.ksv = sm.cp[12];
+                sm.pd.kkeep = sm.cp[13];
+                sm.pd.kmem = sm.cp[14];
+                sm.pd.Tt = u2f(sm.cp[15]);
+                sm.pd.m = u2f(sm.cp[16]);
+                sm.pd.lp_min = u2f(sm.cp[17]);
+            }
+        }
+        __syncthreads();
+    }
+#else
+    (void)kernarg; (void)spin;
 #endif
 }
 
@@ -1099,11 +1508,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
 // register of its own for it); the launch arguments are read from there into scalar registers.
 template <typename T>
 __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
-#if defined(__HIP_DEVICE_COMPILE__)  // the kernarg segment exists only in the device pass
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)kernarg);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(kernarg >> 32));
-    using KArgsConst = const KArgs __attribute__((address_space(4)));
-    const KArgs a = *(KArgsConst*)(((uint64_t)hi << 32) | lo);
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KArgs a = kargs_at(kernarg);
     const RowP prm = row_params(a, r);
     general_row<T>(a, g_row_sh.g, r, prm);
 #else
@@ -1112,30 +1518,155 @@ __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
 #endif
 }
 
+// One row: the single pass, the single-pass top-p path or the multi-pass path.  Returns whether
+// the row took one of the longer paths (top-p or multi-pass), whose workgroup then looks for
+// chunks of other rows' passes.
 template <typename T>
-__global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
-                                                          int pad, KArgs a) {
-    const int r = blockIdx.x;  // the grid is exactly B workgroups
+__device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logits, int64_t lstride,
+                                        int V, uint64_t kernarg) {
     bool topp = false;
     if (a.nofast) {
         topp = topp_eligible(a, row_params(a, r));
     } else if (row_fast<T>(a, g_row_sh.f, r, logits, lstride, V, &topp)) {
-        return;
+        return false;
     }
     int why = 0;
     if (topp) {
         // the single-pass top-p path, inline: it starts after the single-pass function has
         // returned (no live range crosses that function's stream) and issues its own loads
         __syncthreads();
+        // a top-p row in progress may open a cooperative pass
+        if (threadIdx.x == 0 && a.coop) ag_add64(&a.coop->wgs, kCoopPending);
         const RowP prm = row_params(a, r);
         topp_stream<T>(a, g_row_sh.t, r, prm);
-        why = topp_finish<T>(a, g_row_sh.t, r, prm, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u);
-        if (why == 0) return;
+        why = topp_finish<T>(a, g_row_sh.t, r, prm, kernarg);
+        // done with it: no longer pending, and no longer holding slots (thread 0 set the mark)
+        if (threadIdx.x == 0 && a.coop)
+            ag_add64(&a.coop->wgs, 0ull - kCoopPending - (g_row_sh.t.coop_hold ? kCoopActive : 0ull));
+        if (why == 0) return true;
     }
     __syncthreads();
-    row_general<T>(r, (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u);
+    row_general<T>(r, kernarg);
     // diagnostic: why the single-pass top-p path handed the row over (thread 0 wrote the flags)
     if (why && threadIdx.x == 0 && a.flags) a.flags[r] |= (uint32_t)why << 16;
+    return true;
+}
+
+// After the workgroup's row: look for chunks of the passes other rows opened.  Every row has a
+// workgroup: those of the longer paths poll while top-p rows are in progress (the device runs
+// nothing else of the launch meanwhile).  More rows than the device holds at once: every
+// workgroup counts itself finished; once every workgroup has started it polls while top-p rows
+// are in progress, before that it only runs chunks already open (so that it keeps no row from
+// starting).  Out of line: nothing but the kernarg address stays live across the row.
+template <typename T>
+__device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KArgs a = kargs_at(kernarg);
+    long_row = __builtin_amdgcn_readfirstlane(long_row);
+    if (!a.coop) return;
+    if (!a.coop_count) {
+        if (long_row) {
+            __syncthreads();
+            coop_help_entry<T>(kernarg, 1);
+        }
+        return;
+    }
+    TopPSmem& sm = g_row_sh.t;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint64_t x = ag_add64(&a.coop->wgs, kCoopFinished);
+        const bool all_started = coop_started(x) == gridDim.x;
+        // the last workgroup to finish: every one has started and finished, no row is pending
+        if (coop_finished(x) + 1u == gridDim.x) ag_store64(&a.coop->wgs, 0ull);
+        sm.cp[6] = (all_started && coop_pending(x) != 0u) ? 2u : (coop_active(x) != 0u ? 1u : 0u);
+    }
+    __syncthreads();
+    const uint32_t how = tp_u(sm.cp[6]);
+    if (how) {
+        __syncthreads();
+        coop_help_entry<T>(kernarg, how == 2u ? 1 : 0);
+    }
+#else
+    (void)kernarg;
+    (void)long_row;
+#endif
+}
+
+// The row workgroup b serves when the launch counts its workgroups (more rows than the device
+// holds at once): the sampled rows whose survivors top-p alone cuts (top-k off, 0 < top_p < 1:
+// the longer paths) first, then the others, each group in index order, so that long rows do
+// not start last.  Every thread calls it; two passes over the rows' top-k, top-p and
+// temperature.
+__device__ __noinline__ int row_order_entry(uint64_t kernarg, int b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int NT = kGenThreads;
+    const KArgs a = kargs_at(kernarg);
+    b = __builtin_amdgcn_readfirstlane(b);
+    TopPSmem& sm = g_row_sh.t;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int B = a.B;
+    auto is_long = [&](int i) __attribute__((always_inline)) {
+        const int k = a.top_k ? a.top_k[i] : 0;
+        const float p = a.top_p ? a.top_p[i] : 1.0f;
+        const float t = a.temperature ? a.temperature[i] : 0.0f;
+        return !is_greedy(t) && (k <= 0 || k >= a.V) && p > 0.0f && p < 1.0f;
+    };
+    // pass 1: the number of long rows
+    uint32_t nl = 0u;
+    for (int base = 0; base < B; base += NT) {
+        const int i = base + tid;
+        nl += (uint32_t)__popcll(wave_ballot(i < B && is_long(i)));
+    }
+    if (lane == 0) sm.cp[8 + wave] = nl;
+    if (tid == 0) sm.cp[0] = (uint32_t)b;  // fallback: the identity
+    __syncthreads();
+    uint32_t F = 0u;
+#pragma unroll
+    for (int w = 0; w < kGenWaves; ++w) F += sm.cp[8 + w];
+    F = tp_u(F);
+    __syncthreads();
+    // pass 2: the b-th row of the order (ranks among the long rows, or among the others)
+    uint32_t before = 0u;  // long rows before this chunk
+    for (int base = 0; base < B; base += NT) {
+        const int i = base + tid;
+        const bool l = i < B && is_long(i);
+        const uint64_t bal = wave_ballot(l);
+        if (lane == 0) sm.cp[8 + wave] = (uint32_t)__popcll(bal);
+        __syncthreads();
+        uint32_t below = before;  // long rows before this thread's row
+        for (int w = 0; w < wave; ++w) below += sm.cp[8 + w];
+        below += (uint32_t)lane_prefix(bal);
+        if (i < B) {
+            if (l && below == (uint32_t)b) sm.cp[0] = (uint32_t)i;
+            if (!l && (uint32_t)i - below == (uint32_t)b - F && (uint32_t)b >= F) sm.cp[0] = (uint32_t)i;
+        }
+        uint32_t chunk = 0u;
+#pragma unroll
+        for (int w = 0; w < kGenWaves; ++w) chunk += sm.cp[8 + w];
+        before += chunk;
+        __syncthreads();
+    }
+    return (int)tp_u(sm.cp[0]);
+#else
+    (void)kernarg;
+    return b;
+#endif
+}
+
+// One workgroup per row (the grid is exactly B workgroups).  `coop` (preloaded with the row's
+// address, stride and V, so that testing it costs no argument read): bit 0, the cooperative
+// region is present; bit 1, the workgroups are counted (KArgs::coop_count).
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
+                                                          int coop, KArgs a) {
+    const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u;
+    int r = blockIdx.x;
+    if (coop & 2) {
+        if (threadIdx.x == 0) ag_add64(&a.coop->wgs, kCoopStarted);
+        r = __builtin_amdgcn_readfirstlane(row_order_entry(kernarg, r));
+    }
+    const bool long_row = row_one<T>(a, r, logits, lstride, V, kernarg);
+    if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T>(kernarg, long_row ? 1 : 0);
 }
 
 template __global__ void row_kernel<float>(const void*, int64_t, int, int, KArgs);

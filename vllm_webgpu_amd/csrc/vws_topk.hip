@@ -35,25 +35,9 @@ struct FastSmem {
     uint32_t bcast[8];
 };
 
-// Cross-workgroup hand-off of the part lists.  Stores and loads are agent-scope atomics, which
-// the memory model makes coherent across XCD L2s without whole-cache writeback/invalidate; the
-// arrival counter is incremented only after every store of the workgroup has completed
-// (s_waitcnt), so the last arriver, which reads with agent-scope atomic loads after seeing the
-// final count, observes all lists.
-__device__ __forceinline__ void publish_u32(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t fetch_u32(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t fetch_u64(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void stores_complete() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
+// Cross-workgroup hand-off of the part lists: agent-scope atomic stores and loads (ag_*); the
+// arrival counter is incremented only after every store of the workgroup has completed, so the
+// last arriver, which reads after seeing the final count, observes all lists.
 
 template <typename T>
 __device__ __forceinline__ int body_index(const Slice<T>& sl, int vi) {
@@ -281,22 +265,21 @@ __device__ __forceinline__ void fast_stream_part(const KArgs& a, FastSmem& sm, i
                 const uint32_t pos = off + (uint32_t)lane_prefix(bal);
                 if (pos < (uint32_t)kPartCap) {
                     const uint64_t e = ((uint64_t)(uint32_t)cb.ci[i] << 32) | cb.ck[i];
-                    __hip_atomic_store(reinterpret_cast<uint64_t*>(out + pos), e, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                    ag_store64(reinterpret_cast<uint64_t*>(out + pos), e);
                 }
             }
         }
         __syncthreads();
         if (tid == 0) {
             const uint32_t n = sm.outcnt;
-            publish_u32(&a.part_meta[pm + 0], n);
-            publish_u32(&a.part_meta[pm + 1], excl);
-            publish_u32(&a.part_meta[pm + 2], (n > (uint32_t)kPartCap) ? 1u : 0u);
+            ag_store32(&a.part_meta[pm + 0], n);
+            ag_store32(&a.part_meta[pm + 1], excl);
+            ag_store32(&a.part_meta[pm + 2], (n > (uint32_t)kPartCap) ? 1u : 0u);
         }
     } else if (tid == 0) {
-        publish_u32(&a.part_meta[pm + 0], 0u);
-        publish_u32(&a.part_meta[pm + 1], 0u);
-        publish_u32(&a.part_meta[pm + 2], 1u);
+        ag_store32(&a.part_meta[pm + 0], 0u);
+        ag_store32(&a.part_meta[pm + 1], 0u);
+        ag_store32(&a.part_meta[pm + 2], 1u);
     }
 }
 
@@ -319,7 +302,7 @@ __device__ __forceinline__ void fast_topk_merge(const KArgs& a, FastSmem& sm, in
 #pragma unroll
     for (int s = 0; s < NSPEC; ++s) {
         const int e = s * NT + tid, pp = e / kSpec, i = e % kSpec;
-        spec[s] = pp < S ? fetch_u64(reinterpret_cast<const uint64_t*>(
+        spec[s] = pp < S ? ag_load64(reinterpret_cast<const uint64_t*>(
                                a.part_list + ((size_t)r * kMaxParts + pp) * kPartCap + i))
                          : 0ull;
     }
@@ -327,8 +310,8 @@ __device__ __forceinline__ void fast_topk_merge(const KArgs& a, FastSmem& sm, in
     __syncthreads();
     if (tid < S) {
         const size_t pm = ((size_t)r * kMaxParts + tid) * 4;
-        sm.pcnt[tid] = fetch_u32(&a.part_meta[pm + 0]);
-        if (fetch_u32(&a.part_meta[pm + 2])) atomicOr(&sm.status, 4u);
+        sm.pcnt[tid] = ag_load32(&a.part_meta[pm + 0]);
+        if (ag_load32(&a.part_meta[pm + 2])) atomicOr(&sm.status, 4u);
     }
     __syncthreads();
     if (tid == 0) {
@@ -354,7 +337,7 @@ __device__ __forceinline__ void fast_topk_merge(const KArgs& a, FastSmem& sm, in
         if (n <= kSpec) continue;
         const uint2* src = a.part_list + ((size_t)r * kMaxParts + pp) * kPartCap;
         for (int i = kSpec + tid; i < n; i += NT) {
-            const uint64_t e = fetch_u64(reinterpret_cast<const uint64_t*>(src + i));
+            const uint64_t e = ag_load64(reinterpret_cast<const uint64_t*>(src + i));
             const int o = (int)sm.poff[pp] + i;
             mk[o] = (uint32_t)e;
             mi[o] = (int32_t)(uint32_t)(e >> 32);
@@ -403,13 +386,12 @@ __global__ __launch_bounds__(kFastThreads) void fast_kernel(KArgs a) {
     stores_complete();
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&a.row_counter[r], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = ag_add32(&a.row_counter[r], 1u);
         sm.last = (prev == (uint32_t)(a.S - 1)) ? 1u : 0u;
     }
     __syncthreads();
     if (!sm.last) return;
-    if (threadIdx.x == 0) publish_u32(&a.row_counter[r], 0u);
+    if (threadIdx.x == 0) ag_store32(&a.row_counter[r], 0u);
     fast_topk_merge(a, sm, r, k);
 }
 

@@ -52,6 +52,28 @@ constexpr int VWS_FALLBACK_DEGENERATE = 3;  // no finite row maximum
 constexpr int VWS_FALLBACK_AMBIGUOUS = 6;   // the exact recount still cuts inconsistently
 constexpr int VWS_FALLBACK_GATHER = 7;      // the boundary bucket holds too many members
 constexpr int VWS_FALLBACK_TOPL = 8;        // the top-L logprobs reach below the candidates
+constexpr int VWS_FALLBACK_COOP = 9;        // a cooperative pass was not completed in time
+
+// The finish's further passes over the row (the rarer cases; tp_pass_range).
+constexpr int kTpPassExact = 0;     // exact masses below the candidates
+constexpr int kTpPassWideRace = 1;  // the race and the boundary members below the candidates
+constexpr int kTpPassRank = 2;      // the rank of a sampled token below the candidates
+
+// One further pass over a row, as every workgroup that works on it sees it.
+struct TpPassDesc {
+    int kind;                   // kTpPass*
+    uint32_t key;               // the row's threshold key tauk (rank pass: the sampled token's key)
+    int bstar;                  // wide race: the boundary bucket
+    float Tt, m, lp_min;        // temperature, max y, min-p's bound on y - max (or -inf)
+    uint32_t ksv, kkeep, kmem;  // wide race: key thresholds (tp_wide_keys)
+};
+
+// A workgroup's results over its share of a pass (per thread until tp_pass_reduce).
+struct TpPassAcc {
+    uint64_t sw = 0, n = 0;  // exact: survivors' mass and number; rank: elements at or above the key
+    RowRace rs;              // wide race: the kept survivors' race
+    uint32_t nrem = 0;       // wide race: survivors top-p removes
+};
 
 struct TopPSmem {
     // Each wave's candidates: raw bits during the stream, order keys from the finish on; and
@@ -92,6 +114,12 @@ struct TopPSmem {
     uint32_t status;                      // bit 0: buffer overflow, bit 1: non-finite sum
     uint32_t bc[16];
     uint64_t bc64[16];
+    // cooperative passes: the pass being run, broadcasts, and whether the row holds a count in
+    // CoopState::wgs (released when the row is done)
+    TpPassDesc pd;
+    uint32_t cp[19];
+    uint32_t coop_hold;
+    uint32_t coop_fail;                   // a cooperative pass of the row was not completed
 };
 
 // Entries dropped by a compaction, as terms of the approximate sum (per lane), and the new
@@ -450,17 +478,20 @@ __device__ __forceinline__ double tp_wave_sum_f64(double v) {
     return v;
 }
 
-// One more pass over row r in the finish (every thread calls it): the aligned body as 16-byte
-// buffer loads, UP vectors per thread per step with the next step's loads in flight, then the
-// unaligned head and tail (threads 0 and 1).  f(v, u, i0, ok) gets the VEC elements of one
-// vector from element i0 on (ok: the vector lies in the row; head and tail are NaN-padded)
-// and, with WITH_U, their uniforms (dword-aligned 16-byte loads; zeros past the row's end).
+// ---- further passes over the row ------------------------------------------------------
+
+// The aligned body vectors [v0, v1) of row r, and its unaligned head and tail when `edges`
+// (every thread calls it): 16-byte buffer loads over just that range (loads past its end read
+// zeros and fetch nothing), one vector per thread per step with the next step's load in flight
+// (a range is a chunk of a few steps: the second load overlaps the first step's work).  f(v, u, i0, ok) gets the VEC elements of one vector from element i0 on (ok: the
+// vector lies in the range; head and tail are NaN-padded) and, with WITH_U, their uniforms
+// (dword-aligned 16-byte loads).
 template <typename T, bool WITH_U, typename F>
-__device__ __forceinline__ void tp_row_pass(const KArgs& a, int r, F&& f) {
+__device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int v1, bool edges, F&& f) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
-    constexpr int UW = WITH_U ? VEC / 4 : 0;          // uniform loads per vector
-    constexpr int UP = (WITH_U && VEC == 8) ? 2 : 4;  // vectors per thread per step
+    constexpr int UW = WITH_U ? VEC / 4 : 0;  // uniform loads per vector
+    constexpr int UP = 1;                     // vectors per thread per step
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int V = a.V;
@@ -468,34 +499,39 @@ __device__ __forceinline__ void tp_row_pass(const KArgs& a, int r, F&& f) {
     const float* urow = WITH_U ? a.u + (size_t)r * a.ustride : nullptr;
     Slice<T> sl;
     sl.init(row, 0, V);
-    const int nbody = sl.nbody;
-    const int nit = (nbody + NT * UP - 1) / (NT * UP);
-    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + sl.a, 16u * (uint32_t)nbody);
-    const __amdgpu_buffer_rsrc_t urs = make_rsrc(WITH_U ? (const void*)urow : (const void*)row,
-                                                 WITH_U ? 4u * (uint32_t)V : 0u);
+    const int nv = v1 - v0;
+    const int nit = (nv + NT * UP - 1) / (NT * UP);
+    const int e0 = sl.a + v0 * VEC;  // first element of the range
+    const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + e0, 16u * (uint32_t)nv);
+    const __amdgpu_buffer_rsrc_t urs = make_rsrc(WITH_U ? (const void*)(urow + e0) : (const void*)row,
+                                                 WITH_U ? 4u * (uint32_t)(nv * VEC) : 0u);
     auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
     using W4 = decltype(__builtin_amdgcn_raw_buffer_load_b128(lrs, 0u, 0u, 0));
+    // vectors (it * UP + q) * NT + tid lie past the range for every thread once
+    // (it * UP + q) * NT >= nv: such loads and their work are skipped (a uniform test)
     auto load = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < UP; ++q) {
+            if ((it * UP + q) * NT >= nv) break;
             const uint32_t vi = (uint32_t)(tid_now() + (it * UP + q) * NT);
             lw[q] = __builtin_amdgcn_raw_buffer_load_b128(lrs, 16u * vi, 0u, 2 /* nt */);
 #pragma unroll
             for (int g = 0; g < UW; ++g)
                 uw[q][g] = __builtin_amdgcn_raw_buffer_load_b128(
-                    urs, 4u * ((uint32_t)sl.a + vi * (uint32_t)VEC + 4u * (uint32_t)g), 0u, 2);
+                    urs, 4u * (vi * (uint32_t)VEC + 4u * (uint32_t)g), 0u, 2);
         }
     };
     auto consume = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < UP; ++q) {
+            if ((it * UP + q) * NT >= nv) break;
             const int vi = (it * UP + q) * NT + tid_now();
             float v[VEC], u[VEC];
             Elem<T>::from_words((uint32_t)lw[q][0], (uint32_t)lw[q][1], (uint32_t)lw[q][2],
                                 (uint32_t)lw[q][3], v);
 #pragma unroll
             for (int j = 0; j < VEC; ++j) u[j] = WITH_U ? u2f((uint32_t)uw[q][j / 4][j % 4]) : 0.0f;
-            f(v, u, sl.a + vi * VEC, vi < nbody);
+            f(v, u, e0 + vi * VEC, vi < nv);
         }
     };
     W4 la[UP], lb[UP];
@@ -508,7 +544,7 @@ __device__ __forceinline__ void tp_row_pass(const KArgs& a, int r, F&& f) {
         if (it + 1 < nit) consume(lb, ub, it + 1);
         load(lb, ub, it + 3);
     }
-    if (wave == 0) {
+    if (edges && wave == 0) {
         float v[VEC], u[VEC];
         int i0 = 0, end = 0;
         if (tid <= 1) {
@@ -521,45 +557,6 @@ __device__ __forceinline__ void tp_row_pass(const KArgs& a, int r, F&& f) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) u[j] = (WITH_U && i0 + j < end) ? urow[i0 + j] : 0.0f;
         f(v, u, i0, tid <= 1);
-    }
-}
-
-// Exact masses of the survivors below the candidates (elements whose key is below tauk), each
-// added into its bucket of sm.h.hmass, which then holds every survivor of the row; thread 0
-// leaves their total mass and number in sm.bc64[10] and sm.bc64[11].  One pass over the row,
-// for rows whose decision the interval leaves open or puts below the candidates, and for min-p
-// rows with survivors below the candidates.
-template <typename T>
-__device__ __forceinline__ void topp_exact_pass(const KArgs& a, TopPSmem& sm, int r, float Tt,
-                                                float m, float lp_min, uint32_t tauk) {
-    constexpr int VEC = Elem<T>::kVec;
-    const int tid = threadIdx.x;
-    uint64_t sw = 0ull, n = 0ull;
-    tp_row_pass<T, false>(a, r, [&](const float* v, const float*, int, bool ok) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            const uint32_t kx = key_of(v[j]);
-            const float y = v[j] / Tt;
-            const float d = y - m;
-            const bool s = ok && kx != 0u && kx < tauk && key_of(y) != 0u && d >= lp_min;
-            const uint64_t w = s ? mass_of(exp_det(d)) : 0ull;
-            if (w) atomicAdd((unsigned long long*)&sm.h.hmass[tp_bucket(d)], (unsigned long long)w);
-            sw += w;
-            n += s ? 1ull : 0ull;
-        }
-    });
-    sw = wave_sum_u64(sw);
-    n = wave_sum_u64(n);
-    __syncthreads();
-    if (lane_id() == 0) {
-        sm.red[tid >> 6][0] = sw;
-        sm.red[tid >> 6][1] = n;
-    }
-    __syncthreads();
-    const uint64_t tw = tp_sum16(sm, 0), tn = tp_sum16(sm, 1);
-    if (tid == 0) {
-        sm.bc64[10] = tw;
-        sm.bc64[11] = tn;
     }
 }
 
@@ -576,127 +573,212 @@ __device__ __forceinline__ uint32_t tp_first_key(uint32_t tauk, P&& pred) {
     return lo;
 }
 
-// Wide rows (the boundary bucket bstar reaches the values below the candidates), once bstar is
-// known: the race over the survivors below the candidates that top-p keeps (buckets above
-// bstar), and bstar's members below the candidates appended to the gather list (key(y) << 32 |
-// index, counter sm.bc[4]).  The bucket of a value never rises as the value grows (x / T, y - m
-// and the bucket all round monotonically), and neither does min-p's test fail, so kept, boundary
-// and removed survivors are key ranges, found by bisection; the pass compares keys, and only
-// kept elements compute their race key (from the uniforms streamed with the logits).  Thread 0
-// leaves the race's best (RowRace::best), second (RowRace::second), the kept and the removed
-// counts in sm.bc64[10..13].
-template <typename T>
-__device__ __forceinline__ void topp_wide_race(const KArgs& a, TopPSmem& sm, int r, float Tt,
-                                               float m, float lp_min, uint32_t tauk, int bstar) {
-    constexpr int VEC = Elem<T>::kVec;
-    const int tid = threadIdx.x, lane = tid & 63;
-    auto bucket_of_key = [&](uint32_t k) __attribute__((always_inline)) { return tp_bucket(val_of(k) / Tt - m); };
-    const uint32_t ksv = lp_min > -__builtin_inff()
-        ? tp_first_key(tauk, [&](uint32_t k) __attribute__((always_inline)) { return val_of(k) / Tt - m >= lp_min; })
-        : 0x007FFFFFu;
-    uint32_t kkeep = tp_first_key(tauk, [&](uint32_t k) __attribute__((always_inline)) { return bucket_of_key(k) < bstar; });
-    uint32_t kmem = tp_first_key(tauk, [&](uint32_t k) __attribute__((always_inline)) { return bucket_of_key(k) <= bstar; });
-    kkeep = tp_u(kkeep > ksv ? kkeep : ksv);
-    kmem = tp_u(kmem > ksv ? kmem : ksv);
-    RowRace rs;
-    uint32_t nrem = 0u;
-    // gen: the uniforms are generated (at the kept elements only) instead of streamed
-    const uint64_t gseed = a.u ? 0ull : a.rng_seed[r];
-    const uint64_t goff = (a.u || !a.rng_offset) ? 0ull : a.rng_offset[r];
-    auto body = [&](const float* v, const float* u, int i0, bool ok, bool gen) __attribute__((always_inline)) {
-        // generated uniforms: one Philox block per 4 tokens when the vector starts on a block
-        // (the body's vectors all do when the row's aligned start does), else token by token
-        float ug[VEC];
-        const bool blocks = gen && (i0 & 3) == 0;
-        bool anykept = false;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            const uint32_t kx = ok ? key_of(v[j]) : 0u;
-            anykept = anykept || (kx < tauk && kx >= kkeep);
-        }
-        if (blocks && anykept) philox_uniforms_aligned<VEC>(gseed, goff, (uint32_t)i0, ug);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            const uint32_t kx = ok ? key_of(v[j]) : 0u;
-            if (kx >= tauk) continue;
-            if (kx >= kkeep) {
-                const float d = v[j] / Tt - m;
-                rs.nkept++;
-                const float uu = !gen ? u[j] : (blocks ? ug[j] : row_uniform(a, r, i0 + j));
-                rs.add_key(exp_det(d) / (0.0f - log_det(uu)), i0 + j);
-            } else if (kx >= kmem) {
-                const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
-                if (pos < (uint32_t)kTpGather)
-                    sm.g.key[pos] = ((uint64_t)key_of(v[j] / Tt) << 32) | (uint32_t)(i0 + j);
-            } else {
-                nrem += kx >= ksv ? 1u : 0u;
-            }
-        }
-    };
-    if (a.u) {
-        tp_row_pass<T, true>(a, r, [&](const float* v, const float* u, int i0, bool ok)
-                                       __attribute__((always_inline)) { body(v, u, i0, ok, false); });
-    } else {
-        tp_row_pass<T, false>(a, r, [&](const float* v, const float* u, int i0, bool ok)
-                                        __attribute__((always_inline)) { body(v, u, i0, ok, true); });
+// Wide rows (the boundary bucket bstar reaches the values below the candidates): the bucket of a
+// value never rises as the value grows (x / T, y - m and the bucket all round monotonically),
+// and neither does min-p's test fail, so the survivors below the candidates that top-p keeps,
+// bstar's members and the removed ones are key ranges, found by bisection: min-p survivors
+// from ksv on, kept ones from kkeep on, bstar's members from kmem on (all below tauk).  The
+// three bisections run in lanes 0-2 of wave 0; the keys reach every thread through LDS (*out,
+// read after the next barrier).
+__device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out) {
+    if (threadIdx.x >= 3) return;
+    const int which = threadIdx.x;
+    const float Tt = d.Tt, m = d.m, lp_min = d.lp_min;
+    const uint32_t tauk = d.key;
+    const int bstar = d.bstar;
+    uint32_t k = 0x007FFFFFu;
+    if (which > 0 || lp_min > -__builtin_inff()) {
+        k = tp_first_key(tauk, [&](uint32_t x) __attribute__((always_inline)) {
+            const float dd = val_of(x) / Tt - m;
+            if (which == 0) return dd >= lp_min;
+            const int bk = tp_bucket(dd);
+            return which == 1 ? bk < bstar : bk <= bstar;
+        });
     }
-    rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
-    rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);
-    const uint64_t nr = wave_sum_u64(nrem);
-    __syncthreads();
+    out[which] = k;
+}
+
+// A workgroup's share of a pass over row r: the body vectors [v0, v1), and the unaligned head
+// and tail when `edges`.
+//   * exact pass (rows whose decision the interval leaves open or puts below the candidates,
+//     min-p rows with survivors below them): the exact masses of the survivors below the
+//     candidates (key below tauk) into their buckets of sm.h.hmass, their total mass and number
+//     into acc.sw and acc.n;
+//   * wide race (once bstar is known): the race over the survivors below the candidates that
+//     top-p keeps (buckets above bstar) into acc.rs, bstar's members there appended to sm.g.key
+//     (key(y) << 32 | index, counter sm.bc[4]), the removed survivors counted in acc.nrem.  The
+//     pass compares keys, and only kept elements compute their race key (from the uniforms
+//     streamed with the logits, or generated);
+//   * rank pass: the elements at or above the key (the rank of a sampled token that is not a
+//     candidate) into acc.n.
+template <typename T>
+__device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int r, const TpPassDesc& d,
+                                              int v0, int v1, bool edges, TpPassAcc& acc) {
+    constexpr int VEC = Elem<T>::kVec;
+    const uint32_t tauk = d.key;
+    const float Tt = d.Tt, m = d.m, lp_min = d.lp_min;
+    if (d.kind == kTpPassExact) {
+        tp_row_range<T, false>(a, r, v0, v1, edges, [&](const float* v, const float*, int, bool ok)
+                                                       __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                const uint32_t kx = key_of(v[j]);
+                const float y = v[j] / Tt;
+                const float dd = y - m;
+                const bool s = ok && kx != 0u && kx < tauk && key_of(y) != 0u && dd >= lp_min;
+                const uint64_t w = s ? mass_of(exp_det(dd)) : 0ull;
+                if (w) atomicAdd((unsigned long long*)&sm.h.hmass[tp_bucket(dd)], (unsigned long long)w);
+                acc.sw += w;
+                acc.n += s ? 1ull : 0ull;
+            }
+        });
+    } else if (d.kind == kTpPassWideRace) {
+        const uint32_t ksv = d.ksv, kkeep = d.kkeep, kmem = d.kmem;
+        // gen: the uniforms are generated (at the kept elements only) instead of streamed
+        const uint64_t gseed = a.u ? 0ull : a.rng_seed[r];
+        const uint64_t goff = (a.u || !a.rng_offset) ? 0ull : a.rng_offset[r];
+        auto body = [&](const float* v, const float* u, int i0, bool ok, bool gen) __attribute__((always_inline)) {
+            // generated uniforms: one Philox block per 4 tokens when the vector starts on a
+            // block (the body's vectors all do when the row's aligned start does), else token
+            // by token
+            float ug[VEC];
+            const bool blocks = gen && (i0 & 3) == 0;
+            bool anykept = false;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                const uint32_t kx = ok ? key_of(v[j]) : 0u;
+                anykept = anykept || (kx < tauk && kx >= kkeep);
+            }
+            if (blocks && anykept) philox_uniforms_aligned<VEC>(gseed, goff, (uint32_t)i0, ug);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                const uint32_t kx = ok ? key_of(v[j]) : 0u;
+                if (kx >= tauk) continue;
+                if (kx >= kkeep) {
+                    const float dd = v[j] / Tt - m;
+                    acc.rs.nkept++;
+                    const float uu = !gen ? u[j] : (blocks ? ug[j] : row_uniform(a, r, i0 + j));
+                    acc.rs.add_key(exp_det(dd) / (0.0f - log_det(uu)), i0 + j);
+                } else if (kx >= kmem) {
+                    const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
+                    if (pos < (uint32_t)kTpGather)
+                        sm.g.key[pos] = ((uint64_t)key_of(v[j] / Tt) << 32) | (uint32_t)(i0 + j);
+                } else {
+                    acc.nrem += kx >= ksv ? 1u : 0u;
+                }
+            }
+        };
+        if (a.u) {
+            tp_row_range<T, true>(a, r, v0, v1, edges, [&](const float* v, const float* u, int i0, bool ok)
+                                                          __attribute__((always_inline)) { body(v, u, i0, ok, false); });
+        } else {
+            tp_row_range<T, false>(a, r, v0, v1, edges, [&](const float* v, const float* u, int i0, bool ok)
+                                                           __attribute__((always_inline)) { body(v, u, i0, ok, true); });
+        }
+    } else {
+        tp_row_range<T, false>(a, r, v0, v1, edges, [&](const float* v, const float*, int, bool ok)
+                                                       __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) acc.n += (ok && key_of(v[j]) >= tauk) ? 1ull : 0ull;
+        });
+    }
+}
+
+// Workgroup totals of acc: thread 0 leaves them in sm.bc64[10..13] (exact pass: mass, number;
+// wide race: best, second, kept, removed (RowRace fields); rank pass: number), for every thread
+// after the next barrier.  Every thread calls it.
+__device__ __forceinline__ void tp_pass_reduce(TopPSmem& sm, int kind, TpPassAcc& acc) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    uint64_t x0, x1, x2 = 0ull;
+    if (kind == kTpPassWideRace) {
+        acc.rs.shfl_merge(32); acc.rs.shfl_merge(16); acc.rs.shfl_merge(8);
+        acc.rs.shfl_merge(4); acc.rs.shfl_merge(2); acc.rs.shfl_merge(1);
+        x0 = acc.rs.best;
+        x1 = ((uint64_t)acc.rs.second << 32) | acc.rs.nkept;
+        x2 = wave_sum_u64(acc.nrem);
+    } else {
+        x0 = wave_sum_u64(acc.sw);
+        x1 = wave_sum_u64(acc.n);
+    }
+    __syncthreads();  // the per-wave records' last readers are done
     if (lane == 0) {
-        sm.red[tid >> 6][0] = rs.best;
-        sm.red[tid >> 6][1] = ((uint64_t)rs.second << 32) | rs.nkept;
-        sm.red[tid >> 6][2] = nr;
+        sm.red[w][0] = x0;
+        sm.red[w][1] = x1;
+        sm.red[w][2] = x2;
     }
     __syncthreads();
     if (tid == 0) {
-        RowRace all;
-        uint64_t nremt = 0ull;
-        for (int w = 0; w < kTpWaves; ++w) {
-            RowRace o;
-            o.best = sm.red[w][0];
-            o.second = (uint32_t)(sm.red[w][1] >> 32);
-            o.nkept = (uint32_t)sm.red[w][1];
-            all.merge(o);
-            nremt += sm.red[w][2];
+        if (kind == kTpPassWideRace) {
+            RowRace all;
+            uint64_t nremt = 0ull;
+            for (int i = 0; i < kTpWaves; ++i) {
+                RowRace o;
+                o.best = sm.red[i][0];
+                o.second = (uint32_t)(sm.red[i][1] >> 32);
+                o.nkept = (uint32_t)sm.red[i][1];
+                all.merge(o);
+                nremt += sm.red[i][2];
+            }
+            sm.bc64[10] = all.best;
+            sm.bc64[11] = all.second;
+            sm.bc64[12] = all.nkept;
+            sm.bc64[13] = nremt;
+        } else {
+            uint64_t t0 = 0ull, t1 = 0ull;
+            for (int i = 0; i < kTpWaves; ++i) {
+                t0 += sm.red[i][0];
+                t1 += sm.red[i][1];
+            }
+            sm.bc64[10] = kind == kTpPassRank ? t1 : t0;
+            sm.bc64[11] = t1;
         }
-        sm.bc64[10] = all.best;
-        sm.bc64[11] = all.second;
-        sm.bc64[12] = all.nkept;
-        sm.bc64[13] = nremt;
     }
 }
 
-// Number of elements of row r whose raw value is at or above the one with key ks (> 0): the
-// rank of a sampled token that is not a candidate.  Scalar result; every thread calls it.
-template <typename T>
-__device__ __forceinline__ uint32_t topp_rank_pass(const KArgs& a, TopPSmem& sm, int r, uint32_t ks) {
-    constexpr int VEC = Elem<T>::kVec;
-    const int tid = threadIdx.x;
-    uint64_t n = 0ull;
-    tp_row_pass<T, false>(a, r, [&](const float* v, const float*, int, bool ok) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) n += (ok && key_of(v[j]) >= ks) ? 1ull : 0ull;
-    });
-    n = wave_sum_u64(n);
-    __syncthreads();
-    if (lane_id() == 0) sm.red[tid >> 6][0] = n;
-    __syncthreads();
-    const uint64_t t = tp_sum16(sm, 0);
-    if (tid == 0) sm.bc64[10] = t;
-    return (uint32_t)t;
+// ---- cooperative passes ------------------------------------------------------------------
+//
+// A row that needs a further pass over V >= kCoopMinChunks chunks takes a free slot of the
+// workspace's CoopState, describes the pass there, opens its chunks and works through them
+// itself; workgroups that have no row left (or that are between rows) claim chunks too, run
+// them, add their totals into the slot (global atomics: bucket masses, sums, gathered members;
+// per-chunk race records) and count them done.  The owner waits until every chunk it did not
+// run is done, adds the slot's totals to its own and frees the slot.  Every sum is of integers
+// (masses, counts) and the race merge is order-independent, so the result does not depend on
+// who ran which chunk.
+//
+// claim: generation (bits 40-63) | chunks of the pass (bits 32-39) | next chunk (bits 0-31).
+// One atomic add claims a chunk and tells whether it exists; only the owner changes the
+// generation and the chunk count (nothing open: 0 chunks).  The owner describes the pass
+// before it opens the chunks, and a claimed chunk keeps the owner waiting, so a helper that
+// claimed one reads a stable description.
+constexpr int kCoopMinChunks = 4;
+constexpr uint32_t kCoopNone = 0xFFFFFFFFu;
+constexpr int kCoopWaitPolls = 1 << 20;  // the owner's wait for chunks run by others
+constexpr int kCoopHelpPolls = 1 << 16;  // a helper's polls for chunks while rows hold slots
+static_assert(kCoopBuckets == kTpBuckets && kCoopGather == kTpGather, "cooperative slot sizes");
+static_assert(kCoopMaxChunks < 256, "chunk count field");
+
+__device__ __forceinline__ uint64_t coop_claim_word(uint32_t gen, uint32_t nch) {
+    return ((uint64_t)(gen & 0xFFFFFFu) << 40) | ((uint64_t)nch << 32);
+}
+// the chunk a claim returned, or kCoopNone
+__device__ __forceinline__ uint32_t coop_chunk_of(uint64_t x) {
+    const uint32_t nch = (uint32_t)(x >> 32) & 0xFFu;
+    return (uint32_t)x < nch ? (uint32_t)x : kCoopNone;
 }
 
-// The finish's further passes over the row (the rarer cases) run out of line, so that their
-// registers stay out of the stream and the finish; defined next to the LDS they use.  Every
-// thread calls it; its scalar results are in sm.bc64[10..13] after a barrier.
-constexpr int kTpPassExact = 0;     // topp_exact_pass
-constexpr int kTpPassWideRace = 1;  // topp_wide_race (bstar)
-constexpr int kTpPassRank = 2;      // topp_rank_pass (key)
+// The finish's further passes run out of line, so that their registers stay out of the stream
+// and the finish; defined next to the LDS they use.  Every thread calls them.
+//   topp_pass_entry: one whole pass over row r (cooperative when a slot is free); its scalar
+//     results are in sm.bc64[10..13] after a barrier; sets sm.coop_fail when a cooperative
+//     pass was not completed (the row then takes the multi-pass path);
+//   topp_range_entry: the pass sm.pd over the body vectors [v0, v1) of row r (and the edges),
+//     its workgroup totals into sm.bc64[10..13] as tp_pass_reduce leaves them.
 template <typename T>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar);
+template <typename T>
+__device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
 
 // Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
 // take the multi-pass path (VWS_FALLBACK_*).  Every return decision is uniform over the
@@ -711,6 +793,10 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     const int L = a.L;
     const bool greedy = prm.greedy;
     const float Tt = tp_uf(greedy ? 1.0f : prm.T);
+    if (tid == 0) {
+        sm.coop_hold = 0u;  // read by thread 0 once the row is done
+        sm.coop_fail = 0u;
+    }
     __syncthreads();  // every wave's stream results are published
     if (sm.status != 0u) return (sm.status & 1u) ? VWS_FALLBACK_OVERFLOW : VWS_FALLBACK_SUM;
     uint32_t tauk = 0u, maxk = 0u;
@@ -729,6 +815,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     const float lp_min = (!greedy && prm.min_p > 0.0f)
                              ? tp_uf(log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)) : -__builtin_inff();
     const float aw = tp_uf(sm.anchor);
+    // a cooperative pass that was not completed marks sm.coop_fail; the row is handed over
+    // before anything is written (the rest of the finish runs on, on values of no use)
     auto pass = [&](int kind, uint32_t key, int bs) __attribute__((always_inline)) {
         topp_pass_entry<T>(kind, r, kernarg, Tt, m, lp_min, key, bs);
         __syncthreads();
@@ -1213,6 +1301,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (tp_u(sm.bc[7]) > (uint32_t)kTpLpCap) return VWS_FALLBACK_TOPL;
         }
     }
+
+    if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
 
     // ---- outputs (nothing was written before this point)
     if (tid == 0) {
