@@ -38,11 +38,9 @@ constexpr int kCoopMaxChunks = 64;
 constexpr int kCoopBuckets = 2048;                // the top-p path's exact-mass buckets
 constexpr int kCoopGather = 2048;                 // boundary-bucket members a slot gathers
 constexpr int kCoopChunkVecs = 2 * kGenThreads;   // vectors per chunk (a multiple of this)
-constexpr uint32_t kCoopIdle = 0xFFFFFF00u;       // claim counter of a slot with nothing posted
 
 struct CoopSlot {
-    uint64_t claim;    // generation << 32 | next chunk to hand out
-    uint64_t posted;   // generation << 32 | chunks of the pass
+    uint64_t claim;    // generation (bits 40-63) | chunks of the pass (32-39) | next chunk (0-31)
     uint64_t sw, n, nrem;                  // totals added by the workgroups that helped
     uint32_t done;     // chunks finished by workgroups other than the owner
     uint32_t owner;    // row + 1 while a row holds the slot, 0 when free
@@ -51,7 +49,7 @@ struct CoopSlot {
     uint32_t key, ksv, kkeep, kmem;
     float Tt, m, lp_min;
     int32_t cvecs;     // vectors per chunk
-    uint32_t pad[2];
+    uint32_t pad[4];
     uint64_t race[kCoopMaxChunks][2];      // wide race per chunk: best, second << 32 | kept
     uint64_t hmass[kCoopBuckets];          // exact pass: bucket masses
     uint64_t gkey[kCoopGather];            // wide race: boundary-bucket members
