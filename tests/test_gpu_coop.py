@@ -21,8 +21,8 @@ WIDE = 0x800
 RECOUNT = 0x400
 
 # CoopState layout (vllm_webgpu_amd/csrc/vws_internal.h): wgs (u64) at 0, then 16 slots of
-# 33896 bytes from byte 256; a slot's claim word (u64) at +0, done (u32) at +32, owner at +36.
-SLOTS, SLOT0, SLOT_BYTES = 16, 256, 33896
+# 34408 bytes from byte 256; a slot's claim word (u64) at +0, done (u32) at +32, owner at +36.
+SLOTS, SLOT0, SLOT_BYTES = 16, 256, 34408
 
 
 def _mixed(B, V, n_wide, seed):

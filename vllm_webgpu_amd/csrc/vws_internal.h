@@ -50,7 +50,7 @@ struct CoopSlot {
     float Tt, m, lp_min;
     int32_t cvecs;     // vectors per chunk
     uint32_t pad[4];
-    uint64_t race[kCoopMaxChunks][2];      // wide race per chunk: best, second << 32 | kept
+    uint64_t race[kCoopMaxChunks][3];      // wide race per chunk: best, second << 32 | kept, last
     uint64_t hmass[kCoopBuckets];          // exact pass: bucket masses
     uint64_t gkey[kCoopGather];            // wide race: boundary-bucket members
 };

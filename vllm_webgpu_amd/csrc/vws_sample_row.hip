@@ -256,6 +256,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     if (kind == kTpPassWideRace && tid < kCoopMaxChunks) {
         ag_store64(&S.race[tid][0], 0ull);
         ag_store64(&S.race[tid][1], 0ull);
+        ag_store64(&S.race[tid][2], 0ull);
     }
     if (tid == 0) {
         ag_store64(&S.sw, 0ull);
@@ -305,6 +306,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
                 o.best = sm.bc64[10];
                 o.second = (uint32_t)sm.bc64[11];
                 o.nkept = (uint32_t)sm.bc64[12];
+                o.last = sm.bc64[14];
                 tr.merge(o);
                 t3 += sm.bc64[13];
             } else {
@@ -340,6 +342,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
         const uint64_t x = ag_load64(&S.race[tid][1]);
         hr.second = (uint32_t)(x >> 32);
         hr.nkept = (uint32_t)x;
+        hr.last = ag_load64(&S.race[tid][2]);
     }
     if (kind == kTpPassWideRace && tid < kWave) {
         hr.shfl_merge(32); hr.shfl_merge(16); hr.shfl_merge(8);
@@ -379,6 +382,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
             sm.bc64[11] = tr.second;
             sm.bc64[12] = tr.nkept;
             sm.bc64[13] = t3 + hrem;
+            sm.bc64[14] = tr.last;
             sm.bc[4] = base + ngh;
         } else {
             sm.bc64[10] = t0 + hn;
@@ -516,6 +520,7 @@ __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
             if (tid == 0) {
                 ag_store64(&S.race[c][0], sm.bc64[10]);
                 ag_store64(&S.race[c][1], (sm.bc64[11] << 32) | (uint32_t)sm.bc64[12]);
+                ag_store64(&S.race[c][2], sm.bc64[14]);
                 ag_add64(&S.nrem, sm.bc64[13]);
                 sm.cp[4] = ng ? ag_add32(&S.ngather, ng) : 0u;
             }

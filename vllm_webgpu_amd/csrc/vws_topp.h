@@ -575,11 +575,11 @@ __device__ __forceinline__ uint32_t tp_first_key(uint32_t tauk, P&& pred) {
 
 // Wide rows (the boundary bucket bstar reaches the values below the candidates): the bucket of a
 // value never rises as the value grows (x / T, y - m and the bucket all round monotonically),
-// and neither does min-p's test fail, so the survivors below the candidates that top-p keeps,
-// bstar's members and the removed ones are key ranges, found by bisection: min-p survivors
-// from ksv on, kept ones from kkeep on, bstar's members from kmem on (all below tauk).  The
-// three bisections run in lanes 0-2 of wave 0; the keys reach every thread through LDS (*out,
-// read after the next barrier).
+// and neither does min-p's test fail, so the survivors top-p keeps, bstar's members and the
+// removed ones are key ranges, found by bisection over the whole key range (the candidates top-p
+// keeps are kept survivors too): min-p survivors from ksv on, bstar's members from kmem on, kept
+// survivors from kkeep on.  The three bisections run in lanes 0-2 of wave 0; the keys reach
+// every thread through LDS (*out, read after the next barrier).
 __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out) {
     if (threadIdx.x >= 3) return;
     const int which = threadIdx.x;
@@ -588,7 +588,7 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
     const int bstar = d.bstar;
     uint32_t k = 0x007FFFFFu;
     if (which > 0 || lp_min > -__builtin_inff()) {
-        k = tp_first_key(tauk, [&](uint32_t x) __attribute__((always_inline)) {
+        k = tp_first_key(0xFF800000u, [&](uint32_t x) __attribute__((always_inline)) {
             const float dd = val_of(x) / Tt - m;
             if (which == 0) return dd >= lp_min;
             const int bk = tp_bucket(dd);
@@ -604,9 +604,10 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
 //     min-p rows with survivors below them): the exact masses of the survivors below the
 //     candidates (key below tauk) into their buckets of sm.h.hmass, their total mass and number
 //     into acc.sw and acc.n;
-//   * wide race (once bstar is known): the race over the survivors below the candidates that
-//     top-p keeps (buckets above bstar) into acc.rs, bstar's members there appended to sm.g.key
-//     (key(y) << 32 | index, counter sm.bc[4]), the removed survivors counted in acc.nrem.  The
+//   * wide race (once bstar is known): the race over every survivor top-p keeps (buckets above
+//     bstar: the candidates among them too, so the finish races only the boundary members) into
+//     acc.rs, bstar's members below the candidates appended to sm.g.key (key(y) << 32 | index,
+//     counter sm.bc[4]), the removed survivors below the candidates counted in acc.nrem.  The
 //     pass compares keys, and only kept elements compute their race key (from the uniforms
 //     streamed with the logits, or generated);
 //   * rank pass: the elements at or above the key (the rank of a sampled token that is not a
@@ -647,18 +648,22 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
 #pragma unroll
             for (int j = 0; j < VEC; ++j) {
                 const uint32_t kx = ok ? key_of(v[j]) : 0u;
-                anykept = anykept || (kx < tauk && kx >= kkeep);
+                anykept = anykept || kx >= kkeep;
             }
             if (blocks && anykept) philox_uniforms_aligned<VEC>(gseed, goff, (uint32_t)i0, ug);
 #pragma unroll
             for (int j = 0; j < VEC; ++j) {
                 const uint32_t kx = ok ? key_of(v[j]) : 0u;
-                if (kx >= tauk) continue;
                 if (kx >= kkeep) {
-                    const float dd = v[j] / Tt - m;
+                    const float y = v[j] / Tt;
+                    const float dd = y - m;
                     acc.rs.nkept++;
+                    const uint64_t lk = ((uint64_t)key_of(y) << 32) | (uint32_t)(i0 + j);
+                    acc.rs.last = acc.rs.last > lk ? acc.rs.last : lk;
                     const float uu = !gen ? u[j] : (blocks ? ug[j] : row_uniform(a, r, i0 + j));
                     acc.rs.add_key(exp_det(dd) / (0.0f - log_det(uu)), i0 + j);
+                } else if (kx >= tauk) {
+                    continue;  // a candidate member of bstar: gathered from the buffers
                 } else if (kx >= kmem) {
                     const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
                     if (pos < (uint32_t)kTpGather)
@@ -684,18 +689,19 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
     }
 }
 
-// Workgroup totals of acc: thread 0 leaves them in sm.bc64[10..13] (exact pass: mass, number;
-// wide race: best, second, kept, removed (RowRace fields); rank pass: number), for every thread
-// after the next barrier.  Every thread calls it.
+// Workgroup totals of acc: thread 0 leaves them in sm.bc64[10..14] (exact pass: mass, number;
+// wide race: best, second, kept, removed, last (RowRace fields); rank pass: number), for every
+// thread after the next barrier.  Every thread calls it.
 __device__ __forceinline__ void tp_pass_reduce(TopPSmem& sm, int kind, TpPassAcc& acc) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    uint64_t x0, x1, x2 = 0ull;
+    uint64_t x0, x1, x2 = 0ull, x3 = 0ull;
     if (kind == kTpPassWideRace) {
         acc.rs.shfl_merge(32); acc.rs.shfl_merge(16); acc.rs.shfl_merge(8);
         acc.rs.shfl_merge(4); acc.rs.shfl_merge(2); acc.rs.shfl_merge(1);
         x0 = acc.rs.best;
         x1 = ((uint64_t)acc.rs.second << 32) | acc.rs.nkept;
         x2 = wave_sum_u64(acc.nrem);
+        x3 = acc.rs.last;
     } else {
         x0 = wave_sum_u64(acc.sw);
         x1 = wave_sum_u64(acc.n);
@@ -705,6 +711,7 @@ __device__ __forceinline__ void tp_pass_reduce(TopPSmem& sm, int kind, TpPassAcc
         sm.red[w][0] = x0;
         sm.red[w][1] = x1;
         sm.red[w][2] = x2;
+        sm.red[w][3] = x3;
     }
     __syncthreads();
     if (tid == 0) {
@@ -716,6 +723,7 @@ __device__ __forceinline__ void tp_pass_reduce(TopPSmem& sm, int kind, TpPassAcc
                 o.best = sm.red[i][0];
                 o.second = (uint32_t)(sm.red[i][1] >> 32);
                 o.nkept = (uint32_t)sm.red[i][1];
+                o.last = sm.red[i][3];
                 all.merge(o);
                 nremt += sm.red[i][2];
             }
@@ -723,6 +731,7 @@ __device__ __forceinline__ void tp_pass_reduce(TopPSmem& sm, int kind, TpPassAcc
             sm.bc64[11] = all.second;
             sm.bc64[12] = all.nkept;
             sm.bc64[13] = nremt;
+            sm.bc64[14] = all.last;
         } else {
             uint64_t t0 = 0ull, t1 = 0ull;
             for (int i = 0; i < kTpWaves; ++i) {
@@ -964,9 +973,10 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         bool ranked = false;
         bool exact = false, wide = false, go_exact = tp_u(sm.bc[10]) != 0u;
         int bnc = kTpBuckets;       // bucket of the largest value below the candidates
-        uint64_t wide_kept = 0ull;  // survivors below the candidates kept (wide rows)
-        uint64_t wbest = 0ull;      // and their race (RowRace fields)
-        uint32_t wsec = 0u;
+        uint64_t wide_kept = 0ull;  // survivors kept by the wide race pass (wide rows: every one
+        uint64_t wbest = 0ull;      // outside the boundary bucket) and their race (RowRace
+        uint32_t wsec = 0u;         // fields)
+        uint64_t wlast = 0ull;
         for (;;) {
             if (go_exact && !exact) {
                 pass(kTpPassExact, tauk, 0);
@@ -1034,6 +1044,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                             wbest = tp_u64(sm.bc64[10]);
                             wsec = (uint32_t)tp_u64(sm.bc64[11]);
                             wide_kept = tp_u64(sm.bc64[12]);
+                            wlast = tp_u64(sm.bc64[14]);
                             any_below_nc = tp_u64(sm.bc64[13]) > 0ull;
                             flags |= VWS_FLAG_TOPP_WIDE;
                         }
@@ -1146,7 +1157,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         uint32_t below_cands = 0u;  // surviving candidates in buckets below the boundary
         // four entries per lane at a time, their uniforms loaded together: a lane waits for one
         // memory latency per four entries, not per kept entry
-        for (int i0 = lane; i0 < cnt; i0 += 4 * kWave) {
+        // (wide rows: the pass raced the kept candidates too, and no candidate lies in a bucket
+        // below the boundary one)
+        for (int i0 = lane; i0 < (wide ? 0 : cnt); i0 += 4 * kWave) {
             float dq[4], uq[4];
             uint32_t yq[4];
             int32_t iq[4];
@@ -1208,8 +1221,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         __syncthreads();
         if (tid == 0) {
             RowRace all;
-            all.best = wbest;  // the race below the candidates (wide rows), counted once
+            all.best = wbest;  // the wide race pass's survivors (wide rows), counted once
             all.second = wsec;
+            all.last = wlast;
             uint64_t nbelow = 0ull;
             for (int w = 0; w < kTpWaves; ++w) {
                 RowRace o;
