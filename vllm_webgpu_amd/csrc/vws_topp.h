@@ -844,28 +844,37 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         uint64_t wc = 0ull, sx = 0ull;
         uint32_t nxs = 0u;
         float s0b = 0.0f;
-        for (int i = lane; i < cnt; i += kWave) {
-            const float x = u2f(sm.ck[wave][i]);
-            const uint32_t kk = key_of(x);
-            const float y = greedy ? x : x / Tt;
-            const float d = y - m;
-            const bool surv = !greedy && key_of(y) != 0u && d >= lp_min;
-            const float e = exp_det(d);
-            const uint64_t w = surv ? mass_of(e) : 0ull;
-            // raw logprobs' normaliser: x - max x is d itself for greedy rows and T = 1
-            if (L >= 0) s0b += (greedy || Tt == 1.0f) ? e : exp_det(x - xmax);
-            const int b = tp_bucket(d);
-            sm.ck[wave][i] = kk;
-            sm.ci[wave][i] = (int32_t)(((uint32_t)sm.ci[wave][i] & kTpIdxMask) | ((uint32_t)b << 19) |
-                                       (surv ? kTpSurv : 0u) | (kk < tauk ? kTpBelow : 0u));
-            if (kk >= tauk) {
-                if (L > 0) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
-                if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
-                wc += w;
-            } else {
-                sx += w;
-                nxs += surv ? 1u : 0u;
+        // unit: y = x (greedy rows and T = 1, where x / T is x itself): the loop without the
+        // division, chosen once for the wave
+        auto masses = [&](auto unit) __attribute__((always_inline)) {
+            for (int i = lane; i < cnt; i += kWave) {
+                const float x = u2f(sm.ck[wave][i]);
+                const uint32_t kk = key_of(x);
+                const float y = decltype(unit)::value ? x : x / Tt;
+                const float d = y - m;
+                const bool surv = !greedy && key_of(y) != 0u && d >= lp_min;
+                const float e = exp_det(d);
+                const uint64_t w = surv ? mass_of(e) : 0ull;
+                // raw logprobs' normaliser: x - max x is d itself for greedy rows and T = 1
+                if (L >= 0) s0b += decltype(unit)::value ? e : exp_det(x - xmax);
+                const int b = tp_bucket(d);
+                sm.ck[wave][i] = kk;
+                sm.ci[wave][i] = (int32_t)(((uint32_t)sm.ci[wave][i] & kTpIdxMask) | ((uint32_t)b << 19) |
+                                           (surv ? kTpSurv : 0u) | (kk < tauk ? kTpBelow : 0u));
+                if (kk >= tauk) {
+                    if (L > 0) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
+                    if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
+                    wc += w;
+                } else {
+                    sx += w;
+                    nxs += surv ? 1u : 0u;
+                }
             }
+        };
+        if (greedy || Tt == 1.0f) {
+            masses(BoolC<true>{});
+        } else {
+            masses(BoolC<false>{});
         }
         wc = wave_sum_u64(wc);
         sx = wave_sum_u64(sx);
