@@ -34,7 +34,7 @@ namespace vws {
 
 constexpr int kTpWaves = kGenWaves;       // 16
 constexpr int kTpCapW = 832;              // candidate slots per wave
-constexpr int kTpSlots = kTpCapW;         // slots per wave
+constexpr int kTpSlots = kTpCapW + kWave; // slots per wave: the candidates, then one spare per lane
 constexpr int kTpSoft = 704;              // a wave holding more after half an iteration compacts
 constexpr int kTpKeep = 512;              // entries a compaction keeps (ties included)
 constexpr float kTpFill = 0.65f;          // share of the slots the seed threshold aims to fill
@@ -190,10 +190,11 @@ struct TpBuf {
     }
     // Stores the candidates of one vector of every lane (elements v[j] >= tauf of a vector in
     // the row, okv; first index i0; bal[j] the wave's ballot of element j's test), with one
-    // capacity check for the whole vector; each candidate lane writes its own slot (exec-masked
-    // stores, placed by mbcnt).  Wave-uniform call.  A full buffer marks the row for the
-    // multi-pass path (the stream compacts every half iteration, from kTpSoft entries on, so
-    // this takes more than kTpCapW - kTpSoft candidates in half an iteration of one wave).
+    // capacity check for the whole vector: every lane writes, without branches, a candidate into
+    // its slot (placed by mbcnt) and anything else into its spare slot past the capacity.
+    // Wave-uniform call.  A full buffer marks the row for the multi-pass path (the stream
+    // compacts every half iteration, from kTpSoft entries on, so this takes more than
+    // kTpCapW - kTpSoft candidates in half an iteration of one wave).
     template <int VEC>
     __device__ __forceinline__ void append_vec(TopPSmem& sm, const float* v, const uint64_t* bal,
                                                bool okv, int i0) {
@@ -206,13 +207,15 @@ struct TpBuf {
             return;
         }
         int base = cnt;
+        const int spare = kTpCapW + lane_id();
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            if (okv && v[j] >= tauf) {  // the lanes of bal[j]
-                const int pos = base + lane_prefix(bal[j]);
-                sm.ck[w][pos] = f2u(v[j]);
-                sm.ci[w][pos] = i0 + j;
-            }
+            const int at = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[j] >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal[j], (uint32_t)base));
+            const bool c = okv & (v[j] >= tauf);  // the lanes of bal[j] (no short-circuit branch)
+            const int pos = c ? at : spare;
+            sm.ck[w][pos] = f2u(v[j]);
+            sm.ci[w][pos] = i0 + j;
             base += __popcll(bal[j]);
         }
         cnt = base;
