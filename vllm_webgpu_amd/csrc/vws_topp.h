@@ -1167,17 +1167,43 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         // boundary bucket's members from the cut on
         RowRace rs;
         uint32_t below_cands = 0u;  // surviving candidates in buckets below the boundary
+        // the boundary bucket's kept members, at most two per thread (ng <= kTpGather = 2 NT),
+        // with their uniforms loaded first: that latency overlaps the candidates' race below
+        static_assert(kTpGather <= 2 * NT, "two boundary members per thread");
+        bool mk[2];
+        uint64_t mg[2];
+        float mu[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t j = (uint32_t)tid + (uint32_t)(h * NT);
+            mk[h] = false;
+            mg[h] = 0ull;
+            if (j < ng) {
+                const uint64_t g = sm.g.key[j];
+                if (ranked) {
+                    // kept: at or after the cut in ascending order
+                    uint32_t rankj = 0u;
+                    for (uint32_t i = 0; i < ng; ++i) rankj += sm.rk.key[i] <= g ? 1u : 0u;
+                    mk[h] = !(rankj - 1u < cpos);
+                } else {
+                    mk[h] = j >= cpos;
+                }
+                mg[h] = g;
+            }
+            mu[h] = mk[h] ? row_uniform(a, r, (int32_t)(uint32_t)mg[h]) : 0.5f;
+        }
         // four entries per lane at a time, their uniforms loaded together: a lane waits for one
         // memory latency per four entries, not per kept entry
+        constexpr int kRq = 4;
         // (wide rows: the pass raced the kept candidates too, and no candidate lies in a bucket
         // below the boundary one)
-        for (int i0 = lane; i0 < (wide ? 0 : cnt); i0 += 4 * kWave) {
-            float dq[4], uq[4];
-            uint32_t yq[4];
-            int32_t iq[4];
-            bool kq[4];
+        for (int i0 = lane; i0 < (wide ? 0 : cnt); i0 += kRq * kWave) {
+            float dq[kRq], uq[kRq];
+            uint32_t yq[kRq];
+            int32_t iq[kRq];
+            bool kq[kRq];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kRq; ++q) {
                 const int i = i0 + q * kWave;
                 const uint32_t c = i < cnt ? (uint32_t)sm.ci[wave][i] : kTpBelow;
                 const bool sv = tp_code_cand(c);
@@ -1187,16 +1213,16 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 iq[q] = (int32_t)(c & kTpIdxMask);
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) uq[q] = kq[q] ? row_uniform(a, r, iq[q]) : 0.5f;
+            for (int q = 0; q < kRq; ++q) uq[q] = kq[q] ? row_uniform(a, r, iq[q]) : 0.5f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kRq; ++q) {
                 if (!kq[q]) continue;
                 const float y = val_of(sm.ck[wave][i0 + q * kWave]) / Tt;
                 dq[q] = y - m;
                 yq[q] = key_of(y);
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kRq; ++q) {
                 if (!kq[q]) continue;
                 const uint64_t lk = ((uint64_t)yq[q] << 32) | (uint32_t)iq[q];
                 rs.nkept++;
@@ -1204,21 +1230,14 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 rs.add_key(exp_det(dq[q]) / (0.0f - log_det(uq[q])), iq[q]);
             }
         }
-        for (uint32_t j = (uint32_t)tid; j < ng; j += NT) {
-            const uint64_t g = sm.g.key[j];
-            if (ranked) {
-                // kept: at or after the cut in ascending order
-                uint32_t rankj = 0u;
-                for (uint32_t i = 0; i < ng; ++i) rankj += sm.rk.key[i] <= g ? 1u : 0u;
-                if (rankj - 1u < cpos) continue;
-            } else if (j < cpos) {
-                continue;
-            }
-            const int32_t idx = (int32_t)(uint32_t)g;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (!mk[h]) continue;
+            const uint64_t g = mg[h];
             rs.nkept++;
             rs.last = rs.last > g ? rs.last : g;
-            rs.add_key(exp_det(val_of((uint32_t)(g >> 32)) - m) /
-                           (0.0f - log_det(row_uniform(a, r, idx))), idx);
+            rs.add_key(exp_det(val_of((uint32_t)(g >> 32)) - m) / (0.0f - log_det(mu[h])),
+                       (int32_t)(uint32_t)g);
         }
         rs.shfl_merge(32); rs.shfl_merge(16); rs.shfl_merge(8);
         rs.shfl_merge(4); rs.shfl_merge(2); rs.shfl_merge(1);
