@@ -40,7 +40,7 @@ constexpr int kTpKeep = 512;              // entries a compaction keeps (ties in
 constexpr float kTpFill = 0.65f;          // share of the slots the seed threshold aims to fill
 constexpr int kTpBuckets = 2048;          // exact-mass buckets of width 1/64 over max - y in [0, 32)
 constexpr int kTpGather = 2048;           // members of the boundary bucket resolved in LDS
-constexpr int kTpRankCap = 256;           // up to this many, without sorting them
+constexpr int kTpRankCap = 64;            // up to this many, without sorting them (O(n^2) ranks)
 constexpr int kTpLpCap = 256;             // candidates gathered for the top-L logprobs
 constexpr float kLog2e = 0x1.715476p+0f;  // log2(e) rounded to fp32
 
