@@ -62,7 +62,7 @@ def test_wide_rows_share_their_passes(cuda, B, V, n_wide):
     w, wide = _mixed(B, V, n_wide, seed=60 + B)
     g = gpu_run(w, cuda)
     assert_same(g, oracle_run(w), w.name)
-    # most of the flat rows need the exact pass and the wide race (16 chunks of 2048 vectors
+    # most of the flat rows need the exact pass and the wide race (4 chunks of 4096 vectors
     # at this V, so they are shared)
     assert int(((g["flags"][wide] & WIDE) != 0).sum()) >= n_wide // 2
     _region_clean(cuda)

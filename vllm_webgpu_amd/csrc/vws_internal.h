@@ -37,7 +37,7 @@ constexpr int kCoopSlots = 16;
 constexpr int kCoopMaxChunks = 64;
 constexpr int kCoopBuckets = 2048;                // the top-p path's exact-mass buckets
 constexpr int kCoopGather = 2048;                 // boundary-bucket members a slot gathers
-constexpr int kCoopChunkVecs = 2 * kGenThreads;   // vectors per chunk (a multiple of this)
+constexpr int kCoopChunkVecs = 4 * kGenThreads;   // vectors per chunk (a multiple of this)
 
 struct CoopSlot {
     uint64_t claim;    // generation (bits 40-63) | chunks of the pass (32-39) | next chunk (0-31)
