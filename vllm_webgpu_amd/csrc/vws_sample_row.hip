@@ -136,6 +136,10 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
     return topp_compact(g_row_sh.t, w, cnt, aw, c, want_raw != 0);
 }
 
+__device__ __noinline__ void topp_rank_members_entry(uint32_t ng, float m) {
+    topp_rank_members(g_row_sh.t, tp_u(ng), tp_uf(m));
+}
+
 // lane l's value of v, in every lane (wave-uniform l)
 __device__ __forceinline__ uint64_t lane_bcast64(uint64_t v, int l) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);

@@ -40,7 +40,8 @@ constexpr int kTpKeep = 512;              // entries a compaction keeps (ties in
 constexpr float kTpFill = 0.65f;          // share of the slots the seed threshold aims to fill
 constexpr int kTpBuckets = 2048;          // exact-mass buckets of width 1/64 over max - y in [0, 32)
 constexpr int kTpGather = 2048;           // members of the boundary bucket resolved in LDS
-constexpr int kTpRankCap = 64;            // up to this many, without sorting them (O(n^2) ranks)
+constexpr int kTpRankCap = 512;           // up to this many, ranked without sorting them
+constexpr int kTpRankSerial = 64;         // up to this many, one thread ranks each member
 constexpr int kTpLpCap = 256;             // candidates gathered for the top-L logprobs
 constexpr float kLog2e = 0x1.715476p+0f;  // log2(e) rounded to fp32
 
@@ -93,7 +94,9 @@ struct TopPSmem {
         } g;
         struct {
             uint64_t key[kTpRankCap];     // the same, for up to kTpRankCap members
-            uint64_t w[kTpRankCap];       // and their exact masses
+            uint64_t w[kTpRankCap];       // their exact masses,
+            uint64_t cum[kTpRankCap];     // the mass of the members at or below each one
+            uint32_t rnk[kTpRankCap];     // and their number
         } rk;
         struct {
             uint32_t key[kTpLpCap];
@@ -221,6 +224,41 @@ struct TpBuf {
         cnt = base;
     }
 };
+
+// Boundary buckets of kTpRankSerial < ng <= kTpRankCap members (sm.rk.key, in any order): each
+// member's exact mass (sm.rk.w), rank (the members at or below it, itself included: sm.rk.rnk)
+// and the mass of the members at or below it (sm.rk.cum), counted by S threads per member over
+// slices of at least 32 members each and added up in LDS (the keys are distinct: they hold the
+// index).  Every thread calls it; the results are read after the caller's next barrier.
+__device__ __forceinline__ void topp_rank_members(TopPSmem& sm, uint32_t ng, float m) {
+    constexpr int NT = kGenThreads;
+    const int tid = threadIdx.x;
+    const int S = min(NT / (int)ng, (int)ng / 32);
+    if (tid < (int)ng) {
+        sm.rk.w[tid] = mass_of(exp_det(val_of((uint32_t)(sm.rk.key[tid] >> 32)) - m));
+        sm.rk.cum[tid] = 0ull;
+        sm.rk.rnk[tid] = 0u;
+    }
+    __syncthreads();
+    if (tid < S * (int)ng) {
+        const int c = tid % (int)ng, sl = tid / (int)ng;
+        const int i0 = sl * (int)ng / S, i1 = (sl + 1) * (int)ng / S;
+        const uint64_t gc = sm.rk.key[c];
+        uint64_t cj = 0ull;
+        uint32_t rj = 0u;
+#pragma unroll 8
+        for (int i = i0; i < i1; ++i) {
+            const bool le = sm.rk.key[i] <= gc;
+            cj += le ? sm.rk.w[i] : 0ull;
+            rj += le ? 1u : 0u;
+        }
+        if (cj) atomicAdd((unsigned long long*)&sm.rk.cum[c], (unsigned long long)cj);
+        if (rj) atomicAdd(&sm.rk.rnk[c], rj);
+    }
+}
+
+// Out of line (defined next to the LDS it works on).
+__device__ __noinline__ void topp_rank_members_entry(uint32_t ng, float m);
 
 // Keeps the kTpKeep largest values (ties included) of wave w's buffer and raises its threshold
 // to the smallest kept value; the dropped entries are returned as terms of the approximate sum.
@@ -768,6 +806,7 @@ constexpr uint32_t kCoopNone = 0xFFFFFFFFu;
 constexpr int kCoopWaitPolls = 1 << 20;  // the owner's wait for chunks run by others
 constexpr int kCoopHelpPolls = 1 << 16;  // a helper's polls for chunks while rows hold slots
 static_assert(kCoopBuckets == kTpBuckets && kCoopGather == kTpGather, "cooperative slot sizes");
+static_assert(kTpRankCap * 28 <= kTpGather * 8 && 2 * kTpRankCap <= kGenThreads, "ranked members fit the gather buffer");
 static_assert(kCoopMaxChunks < 256, "chunk count field");
 
 __device__ __forceinline__ uint64_t coop_claim_word(uint32_t gen, uint32_t nch) {
@@ -982,7 +1021,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         // kept survivors below the candidates and gathers the boundary bucket's members there.
         int bstar = -1, gathered = -1;
         uint32_t ng = 0u, cpos = 0u, tflags = 0u;
-        bool ranked = false;
+        bool ranked = false, serial = false;
         bool exact = false, wide = false, go_exact = tp_u(sm.bc[10]) != 0u;
         int bnc = kTpBuckets;       // bucket of the largest value below the candidates
         uint64_t wide_kept = 0ull;  // survivors kept by the wide race pass (wide rows: every one
@@ -1064,10 +1103,13 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                         ng = tp_u(sm.bc[4]);
                         if (ng == 0u || ng > (uint32_t)kTpGather) return VWS_FALLBACK_GATHER;
                         ranked = ng <= (uint32_t)kTpRankCap;
-                        if (ranked) {
+                        serial = ng <= (uint32_t)kTpRankSerial;
+                        if (serial) {
                             // members in any order, with their exact masses
                             if (tid < (int)ng)
                                 sm.rk.w[tid] = mass_of(exp_det(val_of((uint32_t)(sm.rk.key[tid] >> 32)) - m));
+                        } else if (ranked) {
+                            topp_rank_members_entry(ng, m);  // out of line: rare, and large
                         } else {
                             uint32_t P = 1u;
                             while (P < ng) P <<= 1;
@@ -1098,14 +1140,19 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                     if (ranked) {
                         // a member's cumulative mass counts the members at or below it
                         if (tid < (int)ng) {
-                            const uint64_t gj = sm.rk.key[tid];
                             const uint64_t wj = sm.rk.w[tid];
                             uint64_t cj = 0ull;
                             uint32_t rankj = 0u;
-                            for (uint32_t i = 0; i < ng; ++i) {
-                                const bool le = sm.rk.key[i] <= gj;
-                                cj += le ? sm.rk.w[i] : 0ull;
-                                rankj += le ? 1u : 0u;
+                            if (serial) {
+                                const uint64_t gj = sm.rk.key[tid];
+                                for (uint32_t i = 0; i < ng; ++i) {
+                                    const bool le = sm.rk.key[i] <= gj;
+                                    cj += le ? sm.rk.w[i] : 0ull;
+                                    rankj += le ? 1u : 0u;
+                                }
+                            } else {
+                                cj = sm.rk.cum[tid];
+                                rankj = sm.rk.rnk[tid];
                             }
 #pragma unroll
                             for (int e = 0; e < 2; ++e) {
@@ -1183,7 +1230,11 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 if (ranked) {
                     // kept: at or after the cut in ascending order
                     uint32_t rankj = 0u;
-                    for (uint32_t i = 0; i < ng; ++i) rankj += sm.rk.key[i] <= g ? 1u : 0u;
+                    if (serial) {
+                        for (uint32_t i = 0; i < ng; ++i) rankj += sm.rk.key[i] <= g ? 1u : 0u;
+                    } else {
+                        rankj = sm.rk.rnk[j];
+                    }
                     mk[h] = !(rankj - 1u < cpos);
                 } else {
                     mk[h] = j >= cpos;
