@@ -180,3 +180,18 @@ def test_wide_rows(cuda, dtype, L):
     w.min_p[::4] = np.float32(0.001)
     got = _check(w, cuda, f"wide {dtype} L={L}")
     assert int(((got["flags"] & WIDE) != 0).sum()) >= B - 2
+
+
+def test_boundary_bucket_sizes(cuda):
+    """Boundary buckets (1/64 of a unit of y) of about 1000, 340, 100 and 20 members: values
+    uniform over [-a, 0], V = 262144, p = 0.5.  For a = 4 and 12 the nucleus is far larger than
+    the candidate buffers (wide rows: most members come from the pass over the logits); for
+    a = 40 and 200 it lies among the candidates.  The members are sorted above 512, ranked by
+    several threads per member from 65 to 512 and by one thread up to 64."""
+    rng = np.random.default_rng(77)
+    V = 262144
+    spans = [4.0, 4.0, 12.0, 12.0, 40.0, 40.0, 200.0, 200.0]
+    x = np.stack([-rng.uniform(0.0, a, V) for a in spans]).astype(np.float32)
+    w = _wl(x, 1.0, 0.5, seed=77)
+    got = _check(w, cuda, "boundary bucket sizes")
+    assert int(((got["flags"][:4] & WIDE) != 0).sum()) == 4
