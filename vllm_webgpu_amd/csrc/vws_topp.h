@@ -602,14 +602,30 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
 }
 
 // Smallest key k in [key(-inf), tauk) with P(k), for a predicate that holds from some key on;
-// tauk when none does.  Uniform bisection (scalar).
+// tauk when none does.  One wave searches together: each round the 64 lanes test 64 evenly
+// spaced keys of the open range (keys at or above its end count as holding) and the range
+// shrinks to the gap below the first key that holds, so the 32-bit range takes six rounds.
+// Wave-uniform call; the result is uniform.
 template <typename P>
 __device__ __forceinline__ uint32_t tp_first_key(uint32_t tauk, P&& pred) {
+    const uint32_t lane = (uint32_t)lane_id();
     uint32_t lo = 0x007FFFFFu, hi = tauk > lo ? tauk : lo;
     while (lo < hi) {
-        const uint32_t mid = lo + ((hi - lo) >> 1);
-        if (pred(mid)) hi = mid;
-        else lo = mid + 1u;
+        const uint32_t n = hi - lo;                             // < 2^32 - 2^23
+        const uint32_t step = n <= (uint32_t)kWave ? 1u : (n + (uint32_t)kWave - 1u) / (uint32_t)kWave;
+        const uint32_t p = lo + (lane + 1u) * step - 1u;       // 64 step <= n + 63: no overflow
+        const uint64_t b = wave_ballot(p >= hi || pred(p));
+        if (b == 0ull) {
+            lo = hi;  // every key of the range fails
+        } else {
+            const uint32_t f = (uint32_t)__builtin_ctzll(b);
+            const uint32_t pf = lo + (f + 1u) * step - 1u;
+            const uint32_t nlo = f == 0u ? lo : lo + f * step;  // just above the last failing key
+            hi = pf < hi ? pf : hi;
+            lo = nlo;
+        }
+        lo = __builtin_amdgcn_readfirstlane(lo);
+        hi = __builtin_amdgcn_readfirstlane(hi);
     }
     return lo;
 }
@@ -619,13 +635,12 @@ __device__ __forceinline__ uint32_t tp_first_key(uint32_t tauk, P&& pred) {
 // and neither does min-p's test fail, so the survivors top-p keeps, bstar's members and the
 // removed ones are key ranges, found by bisection over the whole key range (the candidates top-p
 // keeps are kept survivors too): min-p survivors from ksv on, bstar's members from kmem on, kept
-// survivors from kkeep on.  The three bisections run in lanes 0-2 of wave 0; the keys reach
-// every thread through LDS (*out, read after the next barrier).
+// survivors from kkeep on.  The three searches run in waves 0-2; the keys reach every thread
+// through LDS (*out, read after the next barrier).
 __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out) {
-    if (threadIdx.x >= 3) return;
-    const int which = threadIdx.x;
+    const int which = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (which >= 3) return;
     const float Tt = d.Tt, m = d.m, lp_min = d.lp_min;
-    const uint32_t tauk = d.key;
     const int bstar = d.bstar;
     uint32_t k = 0x007FFFFFu;
     if (which > 0 || lp_min > -__builtin_inff()) {
@@ -636,7 +651,7 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
             return which == 1 ? bk < bstar : bk <= bstar;
         });
     }
-    out[which] = k;
+    if (lane_id() == 0) out[which] = k;
 }
 
 // A workgroup's share of a pass over row r: the body vectors [v0, v1), and the unaligned head
