@@ -1018,17 +1018,17 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // past the resource's num_records, so the prefetches past the row's end never leave the row.
     // The loads are non-temporal (nt): the row is read once, and streaming it with the default
     // policy evicts the kernel's own code and small operands from L2 and the infinity cache.
-    auto load_iter = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
+    auto load_iter = [&](float (&buf)[U][VEC], int it, auto keep) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-                lrs, 16u * (uint32_t)(tid_now() + (it * U + q) * NT), 0u, kLoadNT);
+                lrs, 16u * (uint32_t)(tid_now() + (it * U + q) * NT), 0u, decltype(keep)::value ? 0 : kLoadNT);
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
     // the first iteration depends only on the preloaded arguments: issued before anything
     // waits for the rest of the kernel arguments
-    load_iter(A, 0);
+    load_iter(A, 0, BoolC<true>{});
     __builtin_amdgcn_sched_barrier(0);
     const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
     const bool has_a = a.adj_ids && a.adjwidth > 0;
@@ -1045,7 +1045,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const __amdgpu_buffer_rsrc_t avs = make_rsrc(avrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
     const int ha_id = __builtin_amdgcn_raw_buffer_load_b32(ais, 4u * (uint32_t)tid, 0u, 0);
     const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
-    load_iter(Bq, 1);
+    load_iter(Bq, 1, BoolC<false>{});
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
     if (k == 0) {
@@ -1214,9 +1214,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     }
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
         examine(A, it);
-        load_iter(A, it + 2);
+        load_iter(A, it + 2, BoolC<false>{});
         if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
-        load_iter(Bq, it + 3);
+        load_iter(Bq, it + 3, BoolC<false>{});
     }
     if (wave == 0) {
         // unaligned head (thread 0) and tail (thread 1), fewer than 2 vectors in total; handled
