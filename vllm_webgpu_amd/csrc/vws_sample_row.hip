@@ -1018,17 +1018,22 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // past the resource's num_records, so the prefetches past the row's end never leave the row.
     // The loads are non-temporal (nt): the row is read once, and streaming it with the default
     // policy evicts the kernel's own code and small operands from L2 and the infinity cache.
-    auto load_iter = [&](float (&buf)[U][VEC], int it, auto keep) __attribute__((always_inline)) {
+    auto load_part = [&](float (&buf)[U][VEC], int it, auto keep, int q0, int q1) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < U; ++q) {
+        for (int q = q0; q < q1; ++q) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(
                 lrs, 16u * (uint32_t)(tid_now() + (it * U + q) * NT), 0u, decltype(keep)::value ? 0 : kLoadNT);
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
-    // the first iteration depends only on the preloaded arguments: issued before anything
-    // waits for the rest of the kernel arguments
-    load_iter(A, 0, BoolC<true>{});
+    auto load_iter = [&](float (&buf)[U][VEC], int it, auto keep) __attribute__((always_inline)) {
+        load_part(buf, it, keep, 0, U);
+    };
+    // the first half of the first iteration depends only on the preloaded arguments: issued
+    // before anything waits for the rest of the kernel arguments; the history ids follow it
+    // and the rest of the iteration follows them, so the history hash is built while that
+    // rest is still arriving (a wait for a load waits for every load issued before it)
+    load_part(A, 0, BoolC<true>{}, 0, U / 2);
     __builtin_amdgcn_sched_barrier(0);
     const bool has_p = a.prompt && a.pwidth > 0, has_o = a.output && a.owidth > 0;
     const bool has_a = a.adj_ids && a.adjwidth > 0;
@@ -1045,6 +1050,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const __amdgpu_buffer_rsrc_t avs = make_rsrc(avrow, has_a ? 4u * (uint32_t)a.adjwidth : 0u);
     const int ha_id = __builtin_amdgcn_raw_buffer_load_b32(ais, 4u * (uint32_t)tid, 0u, 0);
     const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
+    __builtin_amdgcn_sched_barrier(0);
+    load_part(A, 0, BoolC<true>{}, U / 2, U);
     load_iter(Bq, 1, BoolC<false>{});
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
