@@ -63,6 +63,37 @@ def build_args(lib_mod, logits, T, K, P, MP, R, PR, FR, hist, U, out, flags, nke
     return a
 
 
+def timed_region(step, steps: int, stream, launches_per_step: int = 1, kernel_events: bool = True):
+    """Runs ``step(i)`` for i < steps between two hipEvents on ``stream``; with
+    ``kernel_events`` every library launch in between carries its own kernel-stamped event pair
+    (vws_profile_begin).  Returns the raw figures: region ms, wall s, and per kernel kind the
+    summed kernel ms and launches.  (The per-launch events cost host time and stretch the region
+    by a few microseconds per launch, so the region that defines ms/step runs without them.)"""
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    torch.cuda.synchronize()
+    if kernel_events:
+        ops.profile_begin(steps * launches_per_step + 8)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern = ops.profile_end() if kernel_events else {}
+    return {"steps": steps, "region_ms": e0.elapsed_time(e1), "wall_s": wall,
+            "kernels": {k: {"ms": v[0], "launches": v[1]} for k, v in kern.items()}}
+
+
+def kernel_us(t, kind="sample"):
+    k = t["kernels"].get(kind)
+    return None if not k else k["ms"] / k["launches"] * 1e3
+
+
 def v1_forward_timing(w, logits, T, K, P, MP, R, PR, FR, hist, dev, steps: int, warmup: int):
     """Sampler.forward (vLLM-v1 signature) on device-resident metadata: wall time per call
     (host work included, synchronised at both ends) and stream time per call (hipEvents)."""
@@ -81,25 +112,16 @@ def v1_forward_timing(w, logits, T, K, P, MP, R, PR, FR, hist, dev, steps: int, 
     sampler = Sampler()
     for _ in range(warmup):
         sampler(logits, m)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        sampler(logits, m)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps * 1e6
-    return {"wall_us": wall, "gpu_us": e0.elapsed_time(e1) / steps * 1e3, "steps": steps,
+    t = timed_region(lambda i: sampler(logits, m), steps, torch.cuda.current_stream(),
+                     kernel_events=False)
+    return {"wall_us": t["wall_s"] / steps * 1e6, "gpu_us": t["region_ms"] / steps * 1e3,
+            "timing": t,
             "uniforms": "generated in the kernel (Philox-4x32-10, one key per row and step)"}
 
 
-def history_free_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
-                           stream, steps: int, warmup: int) -> float:
+def history_free_timing(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
+                        stream, steps: int, warmup: int) -> dict:
     """The sampling kernel on the same logits and uniforms with no history (penalties off)."""
-    import torch
-
     argv = []
     for lg, u, _ in sets:
         a = build_args(lib_mod, lg, T, K, P, MP, R, PR, FR, None, u, out, flags, nkept, ws, lp)
@@ -107,18 +129,11 @@ def history_free_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags,
         argv.append(a)
     for i in range(warmup):
         lib_mod.check(L.vws_sample(ctypes.byref(argv[i % len(argv)])))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(steps):
-        L.vws_sample(ctypes.byref(argv[i % len(argv)]))
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps * 1e3
+    return timed_region(lambda i: L.vws_sample(ctypes.byref(argv[i % len(argv)])), steps, stream)
 
 
-def generated_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
-                        stream, B, steps: int, warmup: int) -> float:
+def generated_timing(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
+                     stream, B, steps: int, warmup: int) -> dict:
     """The sampling kernel alone with generated uniforms (keys instead of a [B, V] tensor)."""
     import torch
 
@@ -132,14 +147,49 @@ def generated_kernel_us(lib_mod, L, sets, T, K, P, MP, R, PR, FR, out, flags, nk
         argv.append(a)
     for i in range(warmup):
         lib_mod.check(L.vws_sample(ctypes.byref(argv[i % len(argv)])))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(steps):
-        L.vws_sample(ctypes.byref(argv[i % len(argv)]))
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps * 1e3
+    return timed_region(lambda i: L.vws_sample(ctypes.byref(argv[i % len(argv)])), steps, stream)
+
+
+def token_state_timing(lib_mod, L, W, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, lp,
+                       stream, steps: int, warmup: int) -> dict:
+    """The sampling kernel with the penalties' history in a per-request token-state table
+    instead of id lists: (a) C3's own 512-token output histories, (b) a 4096-token prompt plus a
+    1024-token output per row (more distinct ids than the single pass's LDS hash holds), each
+    checked against the oracle on the id lists for its first 16 rows."""
+    import torch
+
+    from oracle import sampler as O  # checker only
+
+    B, V = w.shape
+    res = {}
+    for name, (prompt, outp) in (("c3_history", (None, w.output_ids)),
+                                 ("long_history_4096_1024", W.long_history(w))):
+        st = torch.from_numpy(W.token_state_table(B, V, prompt, outp).view(np.int32)).to(out.device)
+        tabs = [st] + [torch.roll(st, shifts=i, dims=0).contiguous() for i in range(1, len(sets))]
+        argv = []
+        for (lg, u, _), tb in zip(sets, tabs):
+            a = build_args(lib_mod, lg, T, K, P, MP, R, PR, FR, None, u, out, flags, nkept, ws, lp)
+            a.token_state, a.token_state_row_stride = tb.data_ptr(), tb.stride(0)
+            a.stream = stream.cuda_stream
+            argv.append(a)
+        lib_mod.check(L.vws_sample(ctypes.byref(argv[0])))
+        torch.cuda.synchronize()
+        n = 16
+        got = out.cpu().numpy()[:n]
+        gflags = flags.cpu().numpy().view(np.uint32)
+        prm = O.make_params(n, w.temperature[:n], w.top_k[:n], w.top_p[:n], w.min_p[:n],
+                            w.repetition[:n], w.presence[:n], w.frequency[:n])
+        ref = O.sample(w.logits_f32()[:n], prm, w.uniforms[:n],
+                       prompt_ids=None if prompt is None else prompt[:n], output_ids=outp[:n])
+        for i in range(warmup):
+            lib_mod.check(L.vws_sample(ctypes.byref(argv[i % len(argv)])))
+        t = timed_region(lambda i: L.vws_sample(ctypes.byref(argv[i % len(argv)])), steps, stream)
+        res[name] = {"kernel_us": kernel_us(t), "timing": t,
+                     "parity_rows": n, "token_mismatches": int((got != ref["token"]).sum()),
+                     "general_path_rows": int(((gflags & 0x100) != 0).sum()),
+                     "history": {"prompt": 0 if prompt is None else int(prompt.shape[1]),
+                                 "output": int(outp.shape[1])}}
+    return res
 
 
 def cpu_baseline(w, rows: int, iters: int):
@@ -352,59 +402,57 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # timed region: exactly `steps` calls, bracketed by synchronisation
-    # hipEvents on the launch stream bracket the same region: it holds only sampling-kernel
-    # launches (the input sets rotate by pointer), so region time / steps is the kernel's
-    # average launch duration, back-to-back dispatch gaps included.
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    kern_ms = ev0.elapsed_time(ev1) / args.steps
+    # timed region: exactly `steps` calls, bracketed by synchronisation (wall clock: ms/step and
+    # the rows/s value) and by two hipEvents on the launch stream (region time, dispatch gaps
+    # included).  Then the same `steps` calls once more with every launch carrying an event
+    # pair that the runtime stamps when the kernel itself begins and ends (hipExtLaunchKernel,
+    # on the launch stream): their mean is the sampling kernel's average launch duration, the
+    # figure a rocprofv3 kernel trace reports, from which the roofline is computed.
+    nls = 2 if w.return_probs else 1
+    tr = timed_region(step, args.steps, stream, nls, kernel_events=False)
+    tk = timed_region(step, args.steps, stream, nls, kernel_events=True)
     st = L.vws_last_error()
     if st:
         log(f"last error: {st}")
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    rows_per_s = B * args.steps / (t1 - t0)
-
-    # one hipEvent pair around each launch (up to 500 more calls): adds the event packets' cost
-    npair = min(args.steps, 500)
-    ops.profile_begin(4 * npair + 8)
-    for i in range(npair):
-        step(i)
-    prof = ops.profile_end()
+    ms_per_step = tr["wall_s"] * 1e3 / args.steps
+    rows_per_s = B * args.steps / tr["wall_s"]
+    kern_us = kernel_us(tk)
+    kern_ms = kern_us * 1e-3 if probs_out is None else (kern_us + kernel_us(tk, "softmax")) * 1e-3
+    region_us = tr["region_ms"] / args.steps * 1e3
 
     alg_bytes = W.algorithmic_bytes(w, gpu_kept)
     gbps_e2e = alg_bytes / (ms_per_step * 1e-3) / 1e9
     gbps_kern = alg_bytes / (kern_ms * 1e-3) / 1e9
-    log(f"ms/step {ms_per_step:.4f}  sampling kernel {kern_ms * 1e3:.2f} us  alg bytes {alg_bytes}  "
-        f"e2e {gbps_e2e:.0f} GB/s ({gbps_e2e / PEAK_HBM_GBPS:.1%})  kernel {gbps_kern:.0f} GB/s "
-        f"({gbps_kern / PEAK_HBM_GBPS:.1%})")
+    log(f"ms/step {ms_per_step:.4f}  sampling kernel {kern_us:.2f} us (region {region_us:.2f} us "
+        f"per step)  alg bytes {alg_bytes}  e2e {gbps_e2e:.0f} GB/s ({gbps_e2e / PEAK_HBM_GBPS:.1%})"
+        f"  kernel {gbps_kern:.0f} GB/s ({gbps_kern / PEAK_HBM_GBPS:.1%})  raw {tr} {tk}")
 
     # the same step through the vLLM-v1 front end (Sampler.forward on a SamplingMetadata), with
     # the uniforms generated in the kernel from one key per row (no [B, V] tensor), and the
     # kernel alone in that mode
     # the same launch without the history (the penalty step skipped): what re-hashing the
     # padded histories every step costs inside the launch
-    nohist_us = None
+    nohist = None
     if H0 is not None and not args.skip_v1:
-        nohist_us = history_free_kernel_us(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags,
-                                           nkept, ws, lp, stream, min(args.steps, 300),
-                                           min(args.warmup, 30))
-        log(f"the same launch without the history: {nohist_us:.2f} us")
-    v1 = gen_us = None
+        nohist = history_free_timing(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept,
+                                     ws, lp, stream, min(args.steps, 300), min(args.warmup, 30))
+        log(f"the same launch without the history: {kernel_us(nohist):.2f} us  raw {nohist}")
+    tstate = None
+    if H0 is not None and not args.skip_v1:
+        tstate = token_state_timing(_lib, L, W, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept,
+                                    ws, lp, stream, min(args.steps, 300), min(args.warmup, 30))
+        log("token-state table: " + ", ".join(
+            f"{k} {v['kernel_us']:.2f} us ({v['token_mismatches']} of {v['parity_rows']} rows "
+            f"differ, {v['general_path_rows']} on the multi-pass path)" for k, v in tstate.items()))
+    v1 = gen = None
     if not args.skip_v1:
         v1 = v1_forward_timing(w, sets[0][0], T, K, P, MP, R, PR, FR, sets[0][2], dev,
                                min(args.steps, 300), min(args.warmup, 30))
-        gen_us = generated_kernel_us(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws,
-                                     lp, stream, B, min(args.steps, 300), min(args.warmup, 30))
+        gen = generated_timing(_lib, L, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws,
+                               lp, stream, B, min(args.steps, 300), min(args.warmup, 30))
         log(f"v1 Sampler.forward: {v1['wall_us']:.1f} us/step wall, {v1['gpu_us']:.1f} us/step on "
-            f"the stream; kernel with generated uniforms {gen_us:.2f} us")
+            f"the stream; kernel with generated uniforms "
+            f"{kernel_us(gen):.2f} us  raw {gen}")
 
     if args.calibrate_copy:
         a = torch.empty(1 << 27, dtype=torch.float32, device=dev)
@@ -453,11 +501,20 @@ def main():
         "parity": parity,
         "near_tie_rows": near_tie,
         "kernel_us": {"sample" if probs_out is None else "sample+softmax": kern_ms * 1e3},
-        "kernel_us_generated_uniforms": gen_us,
-        "kernel_us_without_history": nohist_us,
+        "region_us_per_step": region_us,
+        # raw figures of every timed region: hipEvent-bracketed region ms, wall seconds, and per
+        # kernel kind the summed kernel-stamped ms and the number of launches they cover
+        "timing": tr,
+        "timing_kernel_events": tk,
+        "kernel_us_generated_uniforms": None if gen is None else kernel_us(gen),
+        "timing_generated_uniforms": gen,
+        "kernel_us_without_history": None if nohist is None else kernel_us(nohist),
+        "timing_without_history": nohist,
+        "kernel_us_long_history": (None if tstate is None
+                                   else tstate["long_history_4096_1024"]["kernel_us"]),
+        "token_state": tstate,
         "v1_sampler_forward": None if v1 is None else {
             **v1, "kernel_us": kern_ms * 1e3, "wall_vs_kernel": v1["wall_us"] / (kern_ms * 1e3)},
-        "kernel_us_event_pairs": {k: v[0] / v[1] * 1e3 for k, v in prof.items()},
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": gbps_kern / PEAK_HBM_GBPS, "traffic": pmc_traffic_bytes(args.config),

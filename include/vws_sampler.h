@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 5
+#define VWS_ABI_VERSION 6
 
 /* status codes */
 #define VWS_OK 0
@@ -105,6 +105,19 @@ typedef struct vws_sample_args {
     int32_t output_width;
     const int32_t* output_lens;
 
+    /* Per-request token state, instead of the two lists above (optional; prompt_ids and
+     * output_ids must then be NULL): uint32 [rows, >= V] with the given row stride (elements);
+     * logits row r uses table row token_state_rows[r] (device int32 [B]; NULL = row r).  Word t
+     * of a row = 0x80000000 when token t is in the request's prompt, plus the number of times t
+     * occurs in its output (< 2^29; bits 29-30 are ignored) -- the prompt mask and output bin
+     * counts vLLM-v1 rebuilds from the histories every step (apply_penalties), kept on the
+     * device instead (vws_token_state_update).  The single-pass paths read only the words of
+     * the tokens that reach a row's candidates, so a history of any length costs the same; the
+     * multi-pass path scans the row's words once. */
+    const uint32_t* token_state;
+    int64_t token_state_row_stride;
+    const int32_t* token_state_rows;
+
     /* vLLM-v1 logits processors, applied before the penalties (raw logprobs never see them).
      * allowed_mask: uint32 [B, ceil(V/32)] words with the given row stride, bit (t & 31) of word
      * t >> 5 set = token t allowed, others become -inf (allowed_token_ids); NULL = all allowed.
@@ -142,7 +155,10 @@ typedef struct vws_sample_args {
     float* logprob_vals;    /* [B, L+1] */
     int32_t* logprob_ranks; /* [B]: #{j : logprob_j >= logprob_sampled} */
 
-    void* workspace; /* device scratch, >= vws_sample_workspace_size(); see vws_workspace_init */
+    /* Device scratch, >= vws_sample_workspace_size(); see vws_workspace_init.  Without any
+     * history (prompt, output and processor lists all absent or of width 0) it may be NULL or
+     * smaller: the launch then runs without the cooperative passes (same results). */
+    void* workspace;
     size_t workspace_bytes;
     void* stream; /* hipStream_t */
 } vws_sample_args;
@@ -187,6 +203,19 @@ int vws_sample(const vws_sample_args* args);
 #define VWS_NOALLOC_SCRATCH_BYTES (16 << 20)
 int vws_sample_noalloc(const vws_sample_args* args);
 
+/* Token-state table maintenance on `stream` (no counterpart in the reference, which has no
+ * sampler state; vLLM-v1 rebuilds the same counts from the histories every step).  For each
+ * i < n with 0 <= tokens[i] < vocab: VWS_STATE_OUTPUT adds one output occurrence to word
+ * tokens[i] of table row rows[i], VWS_STATE_PROMPT sets that word's prompt flag (atomics: ids and
+ * rows may repeat).  rows and tokens are device int32 [n]; rows NULL sends every id to table
+ * row `row`.  Ids outside [0, vocab) and negative rows are padding and skipped.  A row is
+ * cleared by zeroing its words (the caller's memory). */
+#define VWS_STATE_OUTPUT 0
+#define VWS_STATE_PROMPT 1
+int vws_token_state_update(uint32_t* state, int64_t row_stride, int32_t vocab, int32_t n,
+                           const int32_t* rows, int32_t row, const int32_t* tokens, int32_t kind,
+                           void* stream);
+
 /* Greedy argmax of each row (lowest index on ties; NaN never selected). */
 int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,
                int64_t row_stride, int32_t* out_ids, void* stream);
@@ -214,9 +243,20 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
                         const int32_t* output_lens, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* Test hook (no counterpart in the reference): the bound, in polls of a few dozen cycles each,
+ * of a top-p row's wait for the chunks of its shared passes that other workgroups run (default
+ * 2^20; process-wide, read by each vws_sample launch).  A row that stops waiting takes the
+ * multi-pass path (same results) and leaves its slot to the last of those chunks to finish,
+ * which frees it.  0 gives every shared pass up as soon as the row's own chunks are done,
+ * finished elsewhere or not, so that tests reach that path whatever the timing.  Returns the
+ * previous bound, or -1 (with vws_last_error) for polls < 0. */
+int32_t vws_set_coop_wait_polls(int32_t polls);
+
 /* Per-kernel timing.  vws_profile_begin(n) makes the next n kernel launches of this library
- * (on any stream) record a hipEvent pair around themselves; vws_profile_end() waits for those
- * events, writes the summed milliseconds and launch counts per kernel kind into
+ * (on any stream) carry a hipEvent pair that the runtime stamps when the kernel itself begins
+ * and ends (hipExtLaunchKernel; no marker packets between launches, so the sum is the kernels'
+ * own durations, as a kernel trace reports them); vws_profile_end() waits for those events,
+ * writes the summed milliseconds and launch counts per kernel kind into
  * ms[VWS_KERNEL_KINDS] / count[VWS_KERNEL_KINDS] and turns recording off. */
 #define VWS_KERNEL_SAMPLE 0    /* the sampling kernel of vws_sample (one workgroup per row) */
 #define VWS_KERNEL_TOPK 1      /* the kernels of vws_topk */

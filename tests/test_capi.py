@@ -134,6 +134,10 @@ def test_valid_args_pass(L):
     (dict(logit_softcap=-1.0), _lib.ERR_INVALID_ARGUMENT, "logit_softcap"),
     (dict(logit_softcap=float("nan")), _lib.ERR_INVALID_ARGUMENT, "logit_softcap"),
     (dict(logit_softcap=float("inf")), _lib.ERR_INVALID_ARGUMENT, "logit_softcap"),
+    (dict(token_state=FAKE, token_state_row_stride=999), _lib.ERR_INVALID_ARGUMENT,
+     "token_state_row_stride"),
+    (dict(HIST, token_state=FAKE, token_state_row_stride=1000), _lib.ERR_INVALID_ARGUMENT,
+     "token_state replaces"),
 ])
 def test_invalid_args_rejected(L, over, code, msg):
     assert _status(L, _args(L, **over)) == code
@@ -155,11 +159,32 @@ def test_processor_lists_grow_the_required_workspace(L):
     assert _status(L, _args(L, allowed_mask=FAKE, allowed_row_stride=32)) == _lib.OK
 
 
-def test_sampling_always_needs_the_shared_region(L):
-    assert _status(L, _args(L, workspace=None, workspace_bytes=0)) == _lib.ERR_WORKSPACE_TOO_SMALL
+def test_workspace_optional_without_history(L):
+    """Without a history the workspace only carries the cooperative region: NULL or a smaller
+    one is accepted (the launch then runs without the shared passes); with a history the hash
+    needs it."""
+    assert _status(L, _args(L, workspace=None, workspace_bytes=0)) == _lib.OK
     c0 = L.vws_sample_workspace_size(4, 1000, 0)
-    assert _status(L, _args(L, workspace_bytes=c0 - 256)) == _lib.ERR_WORKSPACE_TOO_SMALL
+    assert _status(L, _args(L, workspace_bytes=c0 - 256)) == _lib.OK
     assert _status(L, _args(L, workspace_bytes=c0)) == _lib.OK
+    assert _status(L, _args(L, **HIST, workspace=None, workspace_bytes=0)) == _lib.ERR_WORKSPACE_TOO_SMALL
+
+
+def test_penalties_without_history_touch_nothing(L):
+    """vws_apply_penalties with no history returns before looking at the workspace."""
+    assert L.vws_apply_penalties(FAKE, 4, 1000, 1000, None, None, None, None, 0, 0, None, None,
+                                 0, 0, None, None, 0, None) == _lib.OK
+
+
+def test_coop_wait_polls_hook(L):
+    prev = L.vws_set_coop_wait_polls(0)
+    try:
+        assert prev >= 0
+        assert L.vws_set_coop_wait_polls(-1) == -1
+        assert "polls" in _lib.last_error()
+        assert L.vws_set_coop_wait_polls(7) == 0
+    finally:
+        L.vws_set_coop_wait_polls(prev)
 
 
 def test_greedy_batches_need_no_uniforms(L):
@@ -182,3 +207,20 @@ def test_noalloc_checks_before_touching_the_device(L):
     assert L.vws_sample_noalloc(ctypes.byref(_args(L, **HIST, logits=None))) == _lib.ERR_INVALID_ARGUMENT
     assert "logits is NULL" in _lib.last_error()
     assert L.vws_sample_noalloc(ctypes.byref(_args(L, **HIST, struct_size=8))) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_token_state_args(L):
+    """The table replaces the lists: valid without a history list (and without a workspace),
+    and its maintenance entry point checks its arguments on the host."""
+    assert _status(L, _args(L, token_state=FAKE, token_state_row_stride=1000, workspace=None,
+                            workspace_bytes=0)) == _lib.OK
+    up = L.vws_token_state_update
+    assert up(None, 1000, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 999, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "row_stride" in _lib.last_error()
+    assert up(FAKE, 1000, 1000, 1, None, 0, FAKE, 2, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "kind" in _lib.last_error()
+    assert up(FAKE, 1000, 1000, 1, None, -1, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 1000, 1000, 1, None, 0, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 1000, 0, 1, None, 0, FAKE, 0, None) == _lib.ERR_LIMIT
+    assert up(FAKE, 1000, 1000, 0, None, 0, None, 0, None) == _lib.OK   # nothing to do

@@ -102,3 +102,33 @@ def test_wide_rows_with_logprobs_and_bf16(cuda):
     assert_same(g, oracle_run(w), w.name + " bf16")
     assert int(((g["flags"][wide] & (WIDE | RECOUNT)) != 0).sum()) >= w.shape[0] // 40
     _region_clean(cuda)
+
+
+@pytest.mark.parametrize("B", [48, 320])
+def test_given_up_passes_fall_back_and_free_their_slots(cuda, B):
+    """With the owners' wait set to 0 polls from the host, every row that opens a shared pass
+    gives it up once its own chunks are done and hands itself to the multi-pass path (reason 9
+    in bits 16-23); the slot is freed by the owner when no other workgroup still runs a chunk
+    of it, else by the last such chunk.  Every kernel still ends normally; every row must match
+    the oracle, and the region must be clean after each launch and serve the next one at the
+    default bound."""
+    from vllm_webgpu_amd import _lib
+
+    L = _lib.lib()
+    w, wide = _mixed(B, 65536, 24, seed=81 + B)
+    ref = oracle_run(w)
+    gave_up = 0
+    prev = L.vws_set_coop_wait_polls(0)
+    try:
+        for i in range(3):
+            g = gpu_run(w, cuda)
+            assert_same(g, ref, f"{w.name} polls=0 launch {i}")
+            _region_clean(cuda)
+            gave_up += int((((g["flags"] >> 16) & 0xFF) == 9).sum())
+    finally:
+        L.vws_set_coop_wait_polls(prev)
+    print(f"B={B}: {gave_up} rows gave up a shared pass over 3 launches", flush=True)
+    assert gave_up > 0
+    g = gpu_run(w, cuda)
+    assert_same(g, ref, w.name + " default bound")
+    _region_clean(cuda)

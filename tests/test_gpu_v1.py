@@ -91,11 +91,14 @@ def _sp(**kw):
     return NS(**base)
 
 
-def test_runner_steps_match_oracle(cuda):
+@pytest.mark.parametrize("token_state", [True, False])
+def test_runner_steps_match_oracle(cuda, token_state):
+    """Six runner steps of mixed requests against the oracle on the id lists; the runner keeps
+    the penalties' history as its device token-state table or as gathered id lists."""
     V = 4096
     model = _FakeModel(V, cuda)
     runner = ROCmModelRunner(None, cuda, model, max_num_reqs=8, max_prompt_len=64,
-                             max_output_len=32)
+                             max_output_len=32, token_state=token_state)
     params = {
         "g": _sp(temperature=0.0, repetition_penalty=1.5),
         "k": _sp(temperature=0.8, top_k=20, seed=11, presence_penalty=0.4),
@@ -154,13 +157,20 @@ def test_runner_steps_match_oracle(cuda):
                                        atol=1e-6)
         for r, tok in zip(active, got):
             outputs[r].append(tok)
-    # the device history table agrees with the host lists
+    # the device history table agrees with the host lists, and so does the token-state table
     b = runner.input_batch
+    assert (b.token_state is not None) == token_state
     for r in active:
         st = b.requests[r]
         n = len(outputs[r])
         assert b.output_ids[st.slot, :n].tolist() == outputs[r] and st.output_token_ids == outputs[r]
         assert int(b.output_lens[st.slot]) == n
+        if token_state:
+            want = np.zeros(V, np.uint32)
+            np.add.at(want, np.array(outputs[r], np.int64), np.uint32(1))
+            want[np.array(prompts[r], np.int64)] |= np.uint32(0x80000000)
+            got = b.token_state[st.slot].cpu().numpy().view(np.uint32)
+            assert np.array_equal(got, want), f"request {r}: token-state row differs"
 
 
 def test_runner_logits_processors_match_oracle(cuda):

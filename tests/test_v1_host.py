@@ -186,6 +186,27 @@ def test_input_batch_processor_fields():
     assert m.allowed_token_ids_mask[1].sum() == V - 3 and not m.allowed_token_ids_mask[1, 1:4].any()
 
 
+def test_min_tokens_and_bad_words_with_an_output_in_flight():
+    """While a step's output is in flight (async output) the host copy of a request's output
+    lags the device by a token: min-tokens is decided on the device-side count, and bad words
+    (which match the host copy) refuse to sample until get_output() has caught it up."""
+    b = InputBatch(2, 4, 8, V, torch.device("cpu"))
+    b.add_request("a", [1], NS(temperature=1.0, min_tokens=2, stop_token_ids=[7], eos_token_id=0))
+    b.add_request("w", [2], NS(temperature=1.0, bad_words_token_ids=[[5, 6]]))
+    st = b.requests["a"]
+    st.output_token_ids, st.num_sampled = [4], 2     # second sampled id not on the host yet
+    m = b.make_sampling_metadata(["a"])
+    assert m.min_tokens == {}                        # the minimum is reached on the device
+    st.num_sampled = 1
+    st.output_token_ids = []
+    assert b.make_sampling_metadata(["a"]).min_tokens == {0: (2, {0, 7})}
+    b.requests["w"].num_sampled = 1                  # its host list is still empty
+    with pytest.raises(RuntimeError, match="get_output"):
+        b.make_sampling_metadata(["a", "w"])
+    b.requests["w"].output_token_ids = [5]
+    assert b.make_sampling_metadata(["a", "w"]).bad_words_token_ids == {1: [[5, 6]]}
+
+
 def test_runner_without_model_and_grammar():
     r = WebGPUModelRunner(None, device="cpu")
     assert r is not None and WebGPUModelRunner is ROCmModelRunner

@@ -14,7 +14,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2
@@ -39,13 +39,16 @@ MAX_VOCAB = 1 << 19
 MAX_LOGPROBS = 64
 TOPK_MAX = 256
 NOALLOC_SCRATCH_BYTES = 16 << 20
+STATE_OUTPUT = 0
+STATE_PROMPT = 1
+STATE_PROMPT_FLAG = 0x80000000
 
 EXPORTED = (
     "vws_abi_version", "vws_last_error", "vws_sample_workspace_size", "vws_workspace_init",
     "vws_validate_sample_args", "vws_sample", "vws_sample_noalloc", "vws_argmax",
     "vws_topk_workspace_size",
     "vws_topk", "vws_softmax", "vws_apply_penalties", "vws_math_selftest",
-    "vws_profile_begin", "vws_profile_end",
+    "vws_profile_begin", "vws_profile_end", "vws_set_coop_wait_polls", "vws_token_state_update",
 )
 
 KERNEL_KINDS = ("sample", "topk", "argmax", "softmax", "penalties", "other")
@@ -68,6 +71,7 @@ class SampleArgs(ctypes.Structure):
         ("repetition_penalty", _P), ("presence_penalty", _P), ("frequency_penalty", _P),
         ("prompt_ids", _P), ("prompt_row_stride", _I64), ("prompt_width", _I32), ("prompt_lens", _P),
         ("output_ids", _P), ("output_row_stride", _I64), ("output_width", _I32), ("output_lens", _P),
+        ("token_state", _P), ("token_state_row_stride", _I64), ("token_state_rows", _P),
         ("allowed_mask", _P), ("allowed_row_stride", _I64),
         ("adjust_ids", _P), ("adjust_vals", _P), ("adjust_row_stride", _I64), ("adjust_width", _I32),
         ("adjust_lens", _P),
@@ -122,6 +126,10 @@ def _declare(L):
     L.vws_profile_begin.argtypes = [_I32]
     L.vws_profile_end.restype = ctypes.c_int
     L.vws_profile_end.argtypes = [_P, _P]
+    L.vws_set_coop_wait_polls.restype = _I32
+    L.vws_set_coop_wait_polls.argtypes = [_I32]
+    L.vws_token_state_update.restype = ctypes.c_int
+    L.vws_token_state_update.argtypes = [_P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P]
 
 
 def lib() -> ctypes.CDLL:

@@ -1,7 +1,9 @@
 // vws_capi.hip -- extern "C" entry points of _vws.so: argument validation (pure host code),
 // workspace layout, shape-dependent launch decisions and kernel launches on the caller's stream.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -21,6 +23,7 @@ __global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, flo
 __global__ void penalties_kernel(KArgs, float*);
 __global__ void selftest_kernel(int, uint32_t, uint32_t, unsigned long long*);
 __global__ void fill_u32_kernel(uint32_t*, size_t, uint32_t);
+__global__ void token_state_kernel(uint32_t*, int64_t, int, int, const int32_t*, int, const int32_t*, int);
 }  // namespace vws
 
 using namespace vws;
@@ -33,6 +36,10 @@ static __device__ __align__(256) unsigned char scratch[VWS_NOALLOC_SCRATCH_BYTES
 namespace {
 
 thread_local std::string g_err;
+
+// Bound of a top-p row's wait for the chunks of its cooperative passes run by other workgroups
+// (vws_set_coop_wait_polls), read at every launch.
+std::atomic<int> g_coop_wait_polls{kCoopWaitPolls};
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -109,6 +116,11 @@ int esize_of(int dtype) { return dtype == VWS_DTYPE_F32 ? 4 : 2; }
 
 // Per-device address of `scratch`, looked up once per device with that device current and
 // cleared once by a fill kernel on the caller's stream (the kernels also clear what they use).
+// The array is zero when the code object is loaded (static storage), which is the state the
+// kernels need; the first call outside graph capture also clears it once and waits for that
+// clear before any call can use the address, so that a first call from another stream cannot
+// overtake it.  Under capture nothing is enqueued (the clear would otherwise be recorded into
+// the caller's graph and replayed with it).
 struct ScratchSlot {
     void* ptr = nullptr;
 };
@@ -126,9 +138,17 @@ int scratch_address(hipStream_t s, void** out) {
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
             return fail(VWS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
-        const size_t n = VWS_NOALLOC_SCRATCH_BYTES / 4;
-        hipLaunchKernelGGL(fill_u32_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint32_t*>(p), n, 0u);
-        if (int st = check_launch("vws_sample_noalloc (scratch clear)")) return st;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+        (void)hipGetLastError();
+        if (cs == hipStreamCaptureStatusNone) {
+            const size_t n = VWS_NOALLOC_SCRATCH_BYTES / 4;
+            hipLaunchKernelGGL(fill_u32_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint32_t*>(p), n, 0u);
+            if (int st = check_launch("vws_sample_noalloc (scratch clear)")) return st;
+            const hipError_t se = hipStreamSynchronize(s);
+            if (se != hipSuccess)
+                return fail(VWS_ERR_HIP, "vws_sample_noalloc (scratch clear): %s", hipGetErrorString(se));
+        }
         slot.ptr = p;
     }
     *out = slot.ptr;
@@ -145,20 +165,27 @@ struct Profiler {
 };
 Profiler g_prof;
 
-// Records the start event of the next launch; returns the slot or -1.
-int prof_start(hipStream_t s, int kind) {
+// The event pair of the next launch while profiling is on (else both null).
+void prof_events(int kind, hipEvent_t* e0, hipEvent_t* e1) {
+    *e0 = *e1 = nullptr;
     std::lock_guard<std::mutex> lock(g_prof.mu);
-    if (!g_prof.on || g_prof.n >= g_prof.cap) return -1;
+    if (!g_prof.on || g_prof.n >= g_prof.cap) return;
     const int i = g_prof.n++;
     g_prof.kind[i] = kind;
-    (void)hipEventRecord(g_prof.ev[2 * i], s);
-    return i;
+    *e0 = g_prof.ev[2 * i];
+    *e1 = g_prof.ev[2 * i + 1];
 }
 
-void prof_stop(hipStream_t s, int slot) {
-    if (slot < 0) return;
-    std::lock_guard<std::mutex> lock(g_prof.mu);
-    (void)hipEventRecord(g_prof.ev[2 * slot + 1], s);
+// Launches kernel k on stream s.  While profiling is on, the launch carries its own event pair
+// (hipExtLaunchKernel), which the runtime stamps when the kernel begins and ends: the elapsed
+// time is the kernel's duration, as a kernel trace reports it, with no marker packets between
+// back-to-back launches.
+template <typename F, typename... A>
+void launch(int kind, F k, dim3 g, dim3 b, hipStream_t s, A... args) {
+    hipEvent_t e0, e1;
+    prof_events(kind, &e0, &e1);
+    if (e0) hipExtLaunchKernelGGL(k, g, b, 0, s, e0, e1, 0u, args...);
+    else hipLaunchKernelGGL(k, g, b, 0, s, args...);
 }
 
 int validate_rows(const void* logits, int32_t dtype, int32_t B, int32_t V, int64_t stride) {
@@ -208,19 +235,34 @@ int validate_sample(const vws_sample_args* a) {
     if ((st = validate_history(a->output_ids, a->output_row_stride, a->output_width, "output"))) return st;
     if ((st = validate_history(a->adjust_ids, a->adjust_row_stride, a->adjust_width, "adjust"))) return st;
     if (a->adjust_ids && !a->adjust_vals) return fail(VWS_ERR_INVALID_ARGUMENT, "adjust_vals is NULL while adjust_ids is set");
+    if (a->token_state) {
+        if (a->prompt_ids || a->output_ids)
+            return fail(VWS_ERR_INVALID_ARGUMENT, "token_state replaces prompt_ids/output_ids: pass one or the other");
+        if (a->token_state_row_stride < a->vocab)
+            return fail(VWS_ERR_INVALID_ARGUMENT, "token_state_row_stride < vocab");
+    }
     if (!(a->logit_softcap >= 0.0f) || a->logit_softcap == __builtin_inff())
         return fail(VWS_ERR_INVALID_ARGUMENT, "logit_softcap must be finite and >= 0 (got %g)", (double)a->logit_softcap);
     if (a->allowed_mask && a->allowed_row_stride < (int64_t)(a->vocab + 31) / 32)
         return fail(VWS_ERR_INVALID_ARGUMENT, "allowed_row_stride < ceil(vocab / 32) words");
     const int hw = sample_history_width(a);
     const size_t need = ws_layout(a->batch, a->vocab, hw, false).total;
-    if (need == 0) return VWS_OK;
+    // without a history the workspace carries only the cooperative region: a NULL or smaller
+    // workspace turns the cooperative passes off (sample_workspace)
+    if (hw == 0 && (!a->workspace || a->workspace_bytes < need)) return VWS_OK;
     if (!a->workspace) return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace is NULL (need %zu bytes)", need);
     if (a->workspace_bytes < need)
         return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", a->workspace_bytes, need);
     if (reinterpret_cast<uintptr_t>(a->workspace) & 255u)
         return fail(VWS_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     return VWS_OK;
+}
+
+// The workspace vws_sample uses (after validate_sample): NULL when it is absent or too small to
+// hold the cooperative region of a launch without a history.
+void* sample_workspace(const vws_sample_args* a, int hw) {
+    const size_t need = ws_layout(a->batch, a->vocab, hw, false).total;
+    return (a->workspace && a->workspace_bytes >= need) ? a->workspace : nullptr;
 }
 
 KArgs make_kargs(int B, int V, const void* logits, int64_t stride, void* ws, int hw, bool parts) {
@@ -278,7 +320,7 @@ int vws_sample(const vws_sample_args* a) {
     int st = validate_sample(a);
     if (st) return st;
     const int hw = sample_history_width(a);
-    KArgs k = make_kargs(a->batch, a->vocab, a->logits, a->logits_row_stride, a->workspace, hw, false);
+    KArgs k = make_kargs(a->batch, a->vocab, a->logits, a->logits_row_stride, sample_workspace(a, hw), hw, false);
     k.temperature = a->temperature;
     k.top_k = a->top_k;
     k.top_p = a->top_p;
@@ -294,6 +336,9 @@ int vws_sample(const vws_sample_args* a) {
     k.ostride = a->output_row_stride;
     k.owidth = a->output_ids ? a->output_width : 0;
     k.olens = a->output_lens;
+    k.tstate = a->token_state;
+    k.tstride = a->token_state_row_stride;
+    k.trows = a->token_state_rows;
     k.allowed = a->allowed_mask;
     k.astride = a->allowed_row_stride;
     k.adj_ids = a->adjust_ids;
@@ -326,16 +371,17 @@ int vws_sample(const vws_sample_args* a) {
         if (a->batch > kCoopMaxGrid) k.coop = nullptr;
         else if (a->batch > d.cus * d.row_blocks_per_cu) k.coop_count = 1;
     }
-    const int cf = (k.coop ? 1 : 0) | (k.coop_count ? 2 : 0);
+    k.coop_wait_polls = g_coop_wait_polls.load(std::memory_order_relaxed);
+    const int cf = (k.coop ? 1 : 0) | (k.coop_count ? 2 : 0) |
+                   ((k.coop_count && a->batch <= kRowOrderMaxBatch) ? 4 : 0);
     hipStream_t s = (hipStream_t)a->stream;
-    const int ps = prof_start(s, VWS_KERNEL_SAMPLE);
+    const int K = VWS_KERNEL_SAMPLE;
     if (a->dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(row_kernel<float>, dim3(grid), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, cf, k);
+        launch(K, row_kernel<float>, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
     else if (a->dtype == VWS_DTYPE_BF16)
-        hipLaunchKernelGGL(row_kernel<uint16_t>, dim3(grid), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, cf, k);
+        launch(K, row_kernel<uint16_t>, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
     else
-        hipLaunchKernelGGL(row_kernel<_Float16>, dim3(grid), dim3(kGenThreads), 0, s, k.logits, k.lstride, k.V, cf, k);
-    prof_stop(s, ps);
+        launch(K, row_kernel<_Float16>, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();
 }
@@ -369,23 +415,41 @@ int vws_sample_noalloc(const vws_sample_args* a) {
     return vws_sample(&b);
 }
 
+int vws_token_state_update(uint32_t* state, int64_t row_stride, int32_t vocab, int32_t n,
+                           const int32_t* rows, int32_t row, const int32_t* tokens, int32_t kind,
+                           void* stream) {
+    if (!state) return fail(VWS_ERR_INVALID_ARGUMENT, "state is NULL");
+    if (vocab < 1 || vocab > VWS_MAX_VOCAB)
+        return fail(VWS_ERR_LIMIT, "vocab must be in [1, %d] (got %d)", VWS_MAX_VOCAB, vocab);
+    if (row_stride < vocab) return fail(VWS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+    if (n < 0) return fail(VWS_ERR_INVALID_ARGUMENT, "n must be >= 0 (got %d)", n);
+    if (kind != VWS_STATE_OUTPUT && kind != VWS_STATE_PROMPT)
+        return fail(VWS_ERR_INVALID_ARGUMENT, "kind must be VWS_STATE_OUTPUT or VWS_STATE_PROMPT (got %d)", kind);
+    if (n == 0) return ok();
+    if (!tokens) return fail(VWS_ERR_INVALID_ARGUMENT, "tokens is NULL");
+    if (!rows && row < 0) return fail(VWS_ERR_INVALID_ARGUMENT, "row must be >= 0 when rows is NULL (got %d)", row);
+    launch(VWS_KERNEL_OTHER, token_state_kernel, dim3((n + 255) / 256), dim3(256), (hipStream_t)stream,
+           state, row_stride, (int)vocab, (int)n, rows, (int)row, tokens, (int)kind);
+    if (int st = check_launch("vws_token_state_update")) return st;
+    return ok();
+}
+
 int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, int64_t row_stride,
                int32_t* out_ids, void* stream) {
     int st = validate_rows(logits, dtype, batch, vocab, row_stride);
     if (st) return st;
     if (!out_ids) return fail(VWS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
     hipStream_t s = (hipStream_t)stream;
-    const int ps = prof_start(s, VWS_KERNEL_ARGMAX);
+    const int K = VWS_KERNEL_ARGMAX;
     if (dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(argmax_kernel<float>, dim3(batch), dim3(1024), 0, s,
-                           static_cast<const float*>(logits), row_stride, vocab, out_ids);
+        launch(K, argmax_kernel<float>, dim3(batch), dim3(1024), s,
+               static_cast<const float*>(logits), row_stride, vocab, out_ids);
     else if (dtype == VWS_DTYPE_BF16)
-        hipLaunchKernelGGL(argmax_kernel<uint16_t>, dim3(batch), dim3(1024), 0, s,
-                           static_cast<const uint16_t*>(logits), row_stride, vocab, out_ids);
+        launch(K, argmax_kernel<uint16_t>, dim3(batch), dim3(1024), s,
+               static_cast<const uint16_t*>(logits), row_stride, vocab, out_ids);
     else
-        hipLaunchKernelGGL(argmax_kernel<_Float16>, dim3(batch), dim3(1024), 0, s,
-                           static_cast<const _Float16*>(logits), row_stride, vocab, out_ids);
-    prof_stop(s, ps);
+        launch(K, argmax_kernel<_Float16>, dim3(batch), dim3(1024), s,
+               static_cast<const _Float16*>(logits), row_stride, vocab, out_ids);
     if ((st = check_launch("vws_argmax"))) return st;
     return ok();
 }
@@ -413,24 +477,21 @@ int vws_topk(const void* logits, int32_t dtype, int32_t batch, int32_t vocab, in
     choose_parts(batch, vocab, esize_of(dtype), &ka.S, &ka.part_len);
     hipStream_t s = (hipStream_t)stream;
     const int bp = (batch + 7) / 8 * 8;
-    const int ps = prof_start(s, VWS_KERNEL_TOPK);
+    const int K = VWS_KERNEL_TOPK;
     if (dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(fast_kernel<float>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
+        launch(K, fast_kernel<float>, dim3(bp * ka.S), dim3(kFastThreads), s, ka);
     else if (dtype == VWS_DTYPE_BF16)
-        hipLaunchKernelGGL(fast_kernel<uint16_t>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
+        launch(K, fast_kernel<uint16_t>, dim3(bp * ka.S), dim3(kFastThreads), s, ka);
     else
-        hipLaunchKernelGGL(fast_kernel<_Float16>, dim3(bp * ka.S), dim3(kFastThreads), 0, s, ka);
-    prof_stop(s, ps);
+        launch(K, fast_kernel<_Float16>, dim3(bp * ka.S), dim3(kFastThreads), s, ka);
     if ((st = check_launch("vws_topk"))) return st;
     // rows whose single-pass candidate lists overflowed (ties) are finished exactly here
-    const int pg = prof_start(s, VWS_KERNEL_TOPK);
     if (dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(general_kernel<float>, dim3(batch), dim3(kGenThreads), 0, s, ka);
+        launch(K, general_kernel<float>, dim3(batch), dim3(kGenThreads), s, ka);
     else if (dtype == VWS_DTYPE_BF16)
-        hipLaunchKernelGGL(general_kernel<uint16_t>, dim3(batch), dim3(kGenThreads), 0, s, ka);
+        launch(K, general_kernel<uint16_t>, dim3(batch), dim3(kGenThreads), s, ka);
     else
-        hipLaunchKernelGGL(general_kernel<_Float16>, dim3(batch), dim3(kGenThreads), 0, s, ka);
-    prof_stop(s, pg);
+        launch(K, general_kernel<_Float16>, dim3(batch), dim3(kGenThreads), s, ka);
     if ((st = check_launch("vws_topk (general kernel)"))) return st;
     return ok();
 }
@@ -441,20 +502,16 @@ int vws_softmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,
     if (st) return st;
     if (!probs) return fail(VWS_ERR_INVALID_ARGUMENT, "probs is NULL");
     hipStream_t s = (hipStream_t)stream;
-    const int ps = prof_start(s, VWS_KERNEL_SOFTMAX);
+    const int K = VWS_KERNEL_SOFTMAX;
     if (dtype == VWS_DTYPE_F32)
-        hipLaunchKernelGGL(softmax_kernel<float>, dim3(batch), dim3(1024), 0, s,
-                           static_cast<const float*>(logits), row_stride, vocab, temperature, probs,
-                           row_max, log_sum);
+        launch(K, softmax_kernel<float>, dim3(batch), dim3(1024), s,
+               static_cast<const float*>(logits), row_stride, vocab, temperature, probs, row_max, log_sum);
     else if (dtype == VWS_DTYPE_BF16)
-        hipLaunchKernelGGL(softmax_kernel<uint16_t>, dim3(batch), dim3(1024), 0, s,
-                           static_cast<const uint16_t*>(logits), row_stride, vocab, temperature,
-                           probs, row_max, log_sum);
+        launch(K, softmax_kernel<uint16_t>, dim3(batch), dim3(1024), s,
+               static_cast<const uint16_t*>(logits), row_stride, vocab, temperature, probs, row_max, log_sum);
     else
-        hipLaunchKernelGGL(softmax_kernel<_Float16>, dim3(batch), dim3(1024), 0, s,
-                           static_cast<const _Float16*>(logits), row_stride, vocab, temperature,
-                           probs, row_max, log_sum);
-    prof_stop(s, ps);
+        launch(K, softmax_kernel<_Float16>, dim3(batch), dim3(1024), s,
+               static_cast<const _Float16*>(logits), row_stride, vocab, temperature, probs, row_max, log_sum);
     if ((st = check_launch("vws_softmax"))) return st;
     return ok();
 }
@@ -471,10 +528,10 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
     if ((st = validate_history(prompt_ids, prompt_row_stride, prompt_width, "prompt"))) return st;
     if ((st = validate_history(output_ids, output_row_stride, output_width, "output"))) return st;
     const int hw = (prompt_ids ? prompt_width : 0) + (output_ids ? output_width : 0);
+    if (hw == 0) return ok();  // nothing to penalise: the workspace is not touched
     const size_t need = ws_layout(batch, vocab, hw, false).total;
-    if (need && (!workspace || workspace_bytes < need))
+    if (!workspace || workspace_bytes < need)
         return fail(VWS_ERR_WORKSPACE_TOO_SMALL, "workspace has %zu bytes, need %zu", workspace_bytes, need);
-    if (hw == 0) return ok();
     KArgs k = make_kargs(batch, vocab, logits, row_stride, workspace, hw, false);
     k.rep = repetition;
     k.pres = presence;
@@ -487,9 +544,7 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
     k.ostride = output_row_stride;
     k.owidth = output_ids ? output_width : 0;
     k.olens = output_lens;
-    const int ps = prof_start((hipStream_t)stream, VWS_KERNEL_PENALTIES);
-    hipLaunchKernelGGL(penalties_kernel, dim3(batch), dim3(1024), 0, (hipStream_t)stream, k, logits);
-    prof_stop((hipStream_t)stream, ps);
+    launch(VWS_KERNEL_PENALTIES, penalties_kernel, dim3(batch), dim3(1024), (hipStream_t)stream, k, logits);
     if ((st = check_launch("vws_apply_penalties"))) return st;
     return ok();
 }
@@ -506,6 +561,14 @@ int vws_math_selftest(int32_t fn, uint32_t key_lo, uint32_t key_hi, uint64_t* ou
                        reinterpret_cast<unsigned long long*>(out2));
     if ((st = check_launch("vws_math_selftest"))) return st;
     return ok();
+}
+
+int32_t vws_set_coop_wait_polls(int32_t polls) {
+    if (polls < 0) {
+        fail(VWS_ERR_INVALID_ARGUMENT, "polls must be >= 0 (got %d)", polls);
+        return -1;
+    }
+    return g_coop_wait_polls.exchange(polls);
 }
 
 int vws_profile_begin(int32_t max_launches) {

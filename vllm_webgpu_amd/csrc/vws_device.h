@@ -221,6 +221,9 @@ __device__ __forceinline__ float apply_penalty(float x, bool in_prompt, uint32_t
 // History hash value word: output occurrences (bits 0-28), a logit bias present (bit 29),
 // banned by a logits processor (bit 30), token in the prompt (bit 31).
 constexpr uint32_t kHCount = 0x1FFFFFFFu;
+// The bits of a token-state word (prompt flag, output count) the penalties read; the word has
+// the hash value's layout without the processor flags.
+constexpr uint32_t kStateMask = 0x80000000u | kHCount;
 constexpr uint32_t kHBias = 1u << 29;
 constexpr uint32_t kHBan = 1u << 30;
 constexpr uint32_t kHPrompt = 1u << 31;

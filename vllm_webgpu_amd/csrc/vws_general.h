@@ -77,16 +77,19 @@ __device__ __forceinline__ void ghash_insert(uint32_t* hkey, uint32_t* hval, uin
     }
 }
 
-__device__ __forceinline__ float ghash_pen(const uint32_t* hkey, const uint32_t* hpen, int hs, int t, float raw) {
+// The processed value of hashed token t into *out; false when t is not in the hash.
+__device__ __forceinline__ bool ghash_pen(const uint32_t* hkey, const uint32_t* hpen, int hs, int t, float* out) {
     uint32_t s = ghash_slot(t, hs);
     for (int probe = 0; probe < hs; ++probe) {
         const uint32_t k = __hip_atomic_load(&hkey[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (k == (uint32_t)t + 1u)
-            return u2f(__hip_atomic_load(&hpen[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (k == (uint32_t)t + 1u) {
+            *out = u2f(__hip_atomic_load(&hpen[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            return true;
+        }
         if (k == 0u) break;
         s = (s + 1u) & (uint32_t)(hs - 1);
     }
-    return raw;
+    return false;
 }
 
 // ---- block helpers for 1024 threads ---------------------------------------------------------
@@ -226,6 +229,10 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
     const int nch = sl.nchunks();
     const int nit = (nch + 2 * NT - 1) / (2 * NT);
     const bool hh = prm.need_hash;
+    // penalties from the token-state table: the tokens with a non-zero word are marked in the
+    // bitmap (one scan of the row's words) and penalised from their word where they are read
+    const bool tb = prm.tab;
+    const uint32_t* tabrow = tb ? a.tstate + (size_t)prm.trow * (size_t)a.tstride : nullptr;
     const int hs = a.hs_row;
     uint32_t* hkey = a.hist_hash + (size_t)r * (size_t)hs * 4;
     uint32_t* hval = hkey + hs;
@@ -236,12 +243,24 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
     const int L = a.L;
 
     // ---- history: hash in the workspace + bitmap of positions in LDS
-    if (hh) {
+    if (hh || tb) {
         const int nw = (V + 31) / 32 + 2;
         for (int i = tid; i < nw; i += NT) sm.bitmap[i] = 0u;
-        for (int i = tid; i < hs; i += NT) { hkey[i] = 0u; hval[i] = 0u; hpen[i] = 0u; }
+        if (hh)
+            for (int i = tid; i < hs; i += NT) { hkey[i] = 0u; hval[i] = 0u; hpen[i] = 0u; }
         __threadfence();
         __syncthreads();
+        if (tb) {
+            // each wave marks 64 consecutive tokens per step (two bitmap words)
+            for (int i0 = wave * kWave; i0 < V; i0 += NT) {
+                const int i = i0 + lane;
+                const uint64_t nz = wave_ballot(i < V && (tabrow[i] & kStateMask) != 0u);
+                if (lane == 0 && nz) {
+                    atomicOr(&sm.bitmap[i0 >> 5], (uint32_t)nz);
+                    atomicOr(&sm.bitmap[(i0 >> 5) + 1], (uint32_t)(nz >> 32));
+                }
+            }
+        }
         if (prm.has_hist && prm.np > 0) {
             const int32_t* pr = a.prompt + (size_t)r * a.pstride;
             for (int i = tid; i < prm.np; i += NT) {
@@ -279,7 +298,8 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
         for (int s = tid; s < hs; s += NT) {
             const uint32_t kk = __hip_atomic_load(&hkey[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (kk) {
-                const uint32_t v = __hip_atomic_load(&hval[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                uint32_t v = __hip_atomic_load(&hval[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (tb) v |= tabrow[kk - 1u] & kStateMask;
                 float raw = Elem<T>::load1(row + (kk - 1u));
                 if (a.softcap > 0.0f) raw = softcap_out(raw, a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 const float bias = u2f(__hip_atomic_load(&hadj[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -293,14 +313,20 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
     // processed values of a chunk: hashed tokens (processors, then penalties), then the
     // allowed-token mask (masked tokens are -inf whatever the hash did to them)
     auto finalize = [&](float* v, int i0) {
-        if (hh) {
+        if (hh || tb) {
             const uint32_t w = (uint32_t)i0 >> 5, sh = (uint32_t)i0 & 31u;
             const uint64_t win = (uint64_t)sm.bitmap[w] | ((uint64_t)sm.bitmap[w + 1] << 32);
             const uint32_t bits = (uint32_t)(win >> sh) & ((1u << VEC) - 1u);
             if (bits) {
 #pragma unroll
-                for (int j = 0; j < VEC; ++j)
-                    if ((bits >> j) & 1u) v[j] = ghash_pen(hkey, hpen, hs, i0 + j, v[j]);
+                for (int j = 0; j < VEC; ++j) {
+                    if (!((bits >> j) & 1u)) continue;
+                    // processor tokens are hashed (their word folded in); others are table tokens
+                    if (hh && ghash_pen(hkey, hpen, hs, i0 + j, &v[j])) continue;
+                    if (tb)
+                        v[j] = apply_hashed(v[j], tabrow[i0 + j] & kStateMask, 0.0f, prm.rep,
+                                            prm.inv_rep, prm.freq, prm.pres);
+                }
             }
         }
         if (mrow) {
@@ -499,7 +525,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
         const float q32 = 1.0f - prm.top_p;
         const bool topp = q32 > 0.0f;
         const bool abl = topp && !(q32 < 1.0f);
-        const bool share_lse = (L >= 0) && !hh && Tt == 1.0f && kth_y == -__builtin_inff() &&
+        const bool share_lse = (L >= 0) && !hh && !tb && Tt == 1.0f && kth_y == -__builtin_inff() &&
                                lp_min == -__builtin_inff();
         auto survivor = [&](float x, float& y, float& d) -> bool {
             y = (Tt == 1.0f) ? x : x / Tt;

@@ -38,6 +38,11 @@ constexpr int kCoopMaxChunks = 64;
 constexpr int kCoopBuckets = 2048;                // the top-p path's exact-mass buckets
 constexpr int kCoopGather = 2048;                 // boundary-bucket members a slot gathers
 constexpr int kCoopChunkVecs = 4 * kGenThreads;   // vectors per chunk (a multiple of this)
+constexpr int kCoopWaitPolls = 1 << 20;           // default bound of the owner's wait for helpers
+// An owner that stops waiting adds kCoopAbandon - (chunks helpers still owe) to the slot's done
+// count; the completion that brings it to exactly kCoopAbandon (the owner's own add when every
+// chunk was already done, or the last late helper's increment) frees the slot.
+constexpr uint32_t kCoopAbandon = 1u << 30;
 
 struct CoopSlot {
     uint64_t claim;    // generation (bits 40-63) | chunks of the pass (32-39) | next chunk (0-31)
@@ -63,6 +68,10 @@ constexpr uint64_t kCoopFinished = 1ull << 20;
 constexpr uint64_t kCoopActive = 1ull << 40;
 constexpr uint64_t kCoopPending = 1ull << 52;
 constexpr int kCoopMaxGrid = (1 << 20) - 1;
+// Largest counted batch whose rows are served longest first (each workgroup of such a launch
+// reads every row's parameters twice to find its row, O(B^2) in all); larger batches run in
+// index order.
+constexpr int kRowOrderMaxBatch = 16384;
 inline __host__ __device__ uint32_t coop_started(uint64_t w) { return (uint32_t)(w & 0xFFFFFu); }
 inline __host__ __device__ uint32_t coop_finished(uint64_t w) { return (uint32_t)((w >> 20) & 0xFFFFFu); }
 inline __host__ __device__ uint32_t coop_active(uint64_t w) { return (uint32_t)((w >> 40) & 0xFFFu); }
@@ -93,6 +102,11 @@ struct KArgs {
     int64_t ostride;
     int owidth;
     const int32_t* olens;
+    // per-request token state instead of the history lists (or null): word t of table row
+    // trows[r] (r when trows is null) = prompt flag (bit 31) | output occurrences of token t
+    const uint32_t* tstate;
+    int64_t tstride;
+    const int32_t* trows;
     const uint32_t* allowed;   // [B, astride] words, bit set = token allowed (or null)
     int64_t astride;
     const int32_t* adj_ids;    // [B, adjstride] sparse processor list (or null)
@@ -129,6 +143,7 @@ struct KArgs {
     int32_t* topk_ids;      // [B, k]
     CoopState* coop;        // cooperative passes (sampling workspace), or null
     int coop_count;         // B exceeds the workgroups resident at once: count them in coop->wgs
+    int coop_wait_polls;    // bound of an owner's wait for the chunks helpers run (>= 0)
 };
 
 // Workspace layout (bytes, 256-aligned sections).

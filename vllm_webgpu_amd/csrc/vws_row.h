@@ -12,8 +12,10 @@ struct RowP {
     float T, top_p, min_p, rep, pres, freq, inv_rep;
     int k, np, no;
     int na;          // logits-processor entries (bans, logit bias) of the row
+    int trow;        // the row's row of the token-state table
     bool greedy;
     bool has_hist;   // penalties apply: a history and not every penalty the identity
+    bool tab;        // ... read from the token-state table (no history lists)
     bool need_hash;  // the row's hash holds history or processor tokens
 };
 
@@ -28,14 +30,23 @@ __device__ __forceinline__ RowP row_params(const KArgs& a, int r) {
     p.pres = a.pres ? a.pres[r] : 0.0f;
     p.freq = a.freq ? a.freq[r] : 0.0f;
     p.inv_rep = 1.0f / p.rep;
-    p.np = a.prompt ? (a.plens ? min(max(a.plens[r], 0), a.pwidth) : a.pwidth) : 0;
+    // prompt tokens take only the repetition penalty: at r = 1 (x * 1 and x * fl(1 / 1) are x)
+    // they change nothing and are not hashed
+    p.np = (a.prompt && p.rep != 1.0f) ? (a.plens ? min(max(a.plens[r], 0), a.pwidth) : a.pwidth) : 0;
     p.no = a.output ? (a.olens ? min(max(a.olens[r], 0), a.owidth) : a.owidth) : 0;
     // vLLM skips the penalty step when every penalty is the identity; the result is the same
     const bool identity = (p.rep == 1.0f && p.pres == 0.0f && p.freq == 0.0f);
-    p.has_hist = (p.np > 0 || p.no > 0) && !identity;
+    p.tab = a.tstate != nullptr && !identity;
+    p.trow = a.trows ? a.trows[r] : r;
+    p.has_hist = p.tab || ((p.np > 0 || p.no > 0) && !identity);
     p.na = a.adj_ids ? (a.adjlens ? min(max(a.adjlens[r], 0), a.adjwidth) : a.adjwidth) : 0;
-    p.need_hash = p.has_hist || p.na > 0;
+    p.need_hash = (p.has_hist && !p.tab) || p.na > 0;
     return p;
+}
+
+// The token-state word of token t in table row trow (prompt flag | output count).
+__device__ __forceinline__ uint32_t state_word(const KArgs& a, int trow, int t) {
+    return a.tstate[(size_t)trow * (size_t)a.tstride + (uint32_t)t] & kStateMask;
 }
 
 // The race's uniform of token t in row r: the caller's [B, V] uniforms, or the generated one

@@ -75,9 +75,11 @@ struct RowSmem {
     uint32_t ymax, tmaxk;                    // largest packed y key; largest threshold used
     uint32_t adjraise;                       // a positive logit bias was inserted
     uint32_t bc[8];
-    // penalty context of the row for the out-of-line fix-up: mode 0 none, 1 penalise, 2 drop
-    uint32_t pmode;
+    // penalty context of the row for the out-of-line fix-up: mode 0 none, 1 penalise, 2 drop;
+    // whether the hash holds tokens, and the row's token-state words (0 without a table)
+    uint32_t pmode, phash;
     float prep, pinv, ppres, pfreq;
+    uint64_t ptab;
 };
 
 union RowShared {
@@ -323,19 +325,36 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
         __syncthreads();
         c = tp_u(sm.cp[6 + (k & 1)]);
     }
-    // the chunks other workgroups claimed: every one is running, so the wait ends
+    // the chunks other workgroups claimed: every one is running, so the wait ends; it is bounded
+    // all the same (a.coop_wait_polls; 0, a test setting, gives every pass up here).  Giving up
+    // hands the slot to whoever completes it: the owner adds kCoopAbandon - others to the done
+    // count, and the completion that brings the count to exactly kCoopAbandon frees the slot --
+    // the owner itself when every chunk was done meanwhile (with a non-zero bound the pass then
+    // counts as completed), else the last helper's increment (coop_help_entry).  No chunk is
+    // open at this point (the owner's own claims ran out), so a freed slot has no late chunk
+    // left to add into it.
     if (tid == 0) {
         const uint32_t others = (uint32_t)nch - own;
+        const int polls = a.coop_wait_polls;
         uint32_t done = ag_load32(&S.done);
-        for (int poll = 0; done < others && poll < kCoopWaitPolls; ++poll) {
+        for (int poll = 0; done < others && poll < polls; ++poll) {
             __builtin_amdgcn_s_sleep(1);
             done = ag_load32(&S.done);
         }
-        sm.cp[4] = done >= others ? 1u : 0u;
+        uint32_t ok = done >= others ? 1u : 0u;
+        if (!ok || polls == 0) {
+            const uint32_t prev = ag_add32(&S.done, kCoopAbandon - others);
+            ok = (prev == others && polls != 0) ? 1u : 0u;
+            if (prev == others && polls == 0) {
+                ag_store64(&S.claim, coop_claim_word(gen, 0u));
+                ag_store32(&S.owner, 0u);
+            }
+        }
+        sm.cp[4] = ok;
     }
     __syncthreads();
     if (!tp_u(sm.cp[4])) {
-        // the slot stays held: a late chunk may still add into it
+        // abandoned: the slot is the late helpers' to free; the row takes the multi-pass path
         if (tid == 0) sm.coop_fail = 1u;
         return;
     }
@@ -539,7 +558,12 @@ __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
         stores_complete();
         __syncthreads();
         if (tid == 0) {
-            ag_add32(&S.done, 1u);
+            // the last chunk of a pass its owner gave up on: free the slot (no chunk of it is
+            // open or running any more)
+            if (ag_add32(&S.done, 1u) + 1u == kCoopAbandon) {
+                ag_store64(&S.claim, coop_claim_word(gen, 0u));
+                ag_store32(&S.owner, 0u);
+            }
             // the claimed next chunk: of this pass (same generation) it runs with the same
             // description; of a later pass the description is read again (a claimed chunk always
             // runs); none: look again
@@ -585,12 +609,16 @@ __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
 // value bounds the processed one from above, so nothing is missed and the key is corrected
 // here.  In mode 2 (something may raise a logit) the processed values of the hashed tokens were
 // added up front with bit 31 of the index set; stream entries of hashed tokens are dropped.
+// Penalties from a token-state table (whose tokens are never hashed) are monotone here: the
+// table's words are read at the candidates, in both modes.
 __device__ __noinline__ int row_fixup(int w, int from, int cnt) {
     RowSmem& sm = g_row_sh.f;
     const uint32_t mode = sm.pmode;
     if (mode == 0u || from >= cnt) return cnt;
     uint32_t* ck = sm.ckey[w];
     int32_t* ci = sm.cidx[w];
+    const bool hashed = sm.phash != 0u;
+    const uint32_t* tab = reinterpret_cast<const uint32_t*>(sm.ptab);
     const int lane = lane_id();
     int out = from;
     for (int base = from; base < cnt; base += kWave) {
@@ -605,11 +633,15 @@ __device__ __noinline__ int row_fixup(int w, int from, int cnt) {
             if (ii < 0) {
                 ii &= 0x7FFFFFFF;  // added up front, already penalised
             } else {
-                const int hs = rhash_find(sm, ii);
-                if (hs >= 0) {
-                    if (mode == 2u) keep = false;
-                    else kk = key_of(apply_hashed(val_of(kk), sm.hval[hs], sm.hadj[hs], sm.prep,
-                                                  sm.pinv, sm.pfreq, sm.ppres));
+                const int hs = hashed ? rhash_find(sm, ii) : -1;
+                if (hs >= 0 && mode == 2u) {
+                    keep = false;
+                } else {
+                    uint32_t hv = hs >= 0 ? sm.hval[hs] : 0u;
+                    if (tab) hv |= tab[ii] & kStateMask;
+                    if (hs >= 0 || hv != 0u)
+                        kk = key_of(apply_hashed(val_of(kk), hv, hs >= 0 ? sm.hadj[hs] : 0.0f, sm.prep,
+                                                 sm.pinv, sm.pfreq, sm.ppres));
                 }
             }
         }
@@ -755,7 +787,8 @@ struct RowCand {
 // never written; they are not const so that they live in the global address space, like the
 // arrays they stand in for, and the pointer select between the two stays global.
 __device__ float kRowDefaultsF[8] = {0.0f, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-// top_k (0 = off), and a length that clamps to the history width (absent lengths = full width)
+// top_k (0 = off), a length that clamps to the history width (absent lengths = full width), and
+// a token-state row (replaced by the row itself when the table has no row map)
 __device__ int32_t kRowDefaultsI[4] = {0, 0x7FFFFFFF, 0, 0};
 
 // Per-row parameters, all issued as scalar loads before the first one is used.  Scalar loads
@@ -771,34 +804,39 @@ __device__ __forceinline__ RowP row_params_scalar(const KArgs& a, int r) {
     const int32_t* pPL = a.plens ? a.plens + r : &kRowDefaultsI[1];
     const int32_t* pOL = a.olens ? a.olens + r : &kRowDefaultsI[1];
     const int32_t* pAL = a.adjlens ? a.adjlens + r : &kRowDefaultsI[1];
+    const int32_t* pTR = a.trows ? a.trows + r : &kRowDefaultsI[2];
     RowP p;
-    int pl, ol, al;
+    int pl, ol, al, tr;
     // scalar loads on the scalar counter; the compiler would otherwise issue vector loads, and
     // waiting for those would also wait for every logits load issued before them
     asm volatile(
-        "s_load_dword %0, %10, 0x0\n\t"
-        "s_load_dword %1, %11, 0x0\n\t"
-        "s_load_dword %2, %12, 0x0\n\t"
-        "s_load_dword %3, %13, 0x0\n\t"
-        "s_load_dword %4, %14, 0x0\n\t"
-        "s_load_dword %5, %15, 0x0\n\t"
-        "s_load_dword %6, %16, 0x0\n\t"
-        "s_load_dword %7, %17, 0x0\n\t"
-        "s_load_dword %8, %18, 0x0\n\t"
-        "s_load_dword %9, %19, 0x0\n\t"
+        "s_load_dword %0, %11, 0x0\n\t"
+        "s_load_dword %1, %12, 0x0\n\t"
+        "s_load_dword %2, %13, 0x0\n\t"
+        "s_load_dword %3, %14, 0x0\n\t"
+        "s_load_dword %4, %15, 0x0\n\t"
+        "s_load_dword %5, %16, 0x0\n\t"
+        "s_load_dword %6, %17, 0x0\n\t"
+        "s_load_dword %7, %18, 0x0\n\t"
+        "s_load_dword %8, %19, 0x0\n\t"
+        "s_load_dword %9, %20, 0x0\n\t"
+        "s_load_dword %10, %21, 0x0\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&s"(p.T), "=&s"(p.top_p), "=&s"(p.min_p), "=&s"(p.rep), "=&s"(p.pres), "=&s"(p.freq),
-          "=&s"(p.k), "=&s"(pl), "=&s"(ol), "=&s"(al)
-        : "s"(pT), "s"(pP), "s"(pM), "s"(pR), "s"(pS), "s"(pF), "s"(pK), "s"(pPL), "s"(pOL), "s"(pAL)
+          "=&s"(p.k), "=&s"(pl), "=&s"(ol), "=&s"(al), "=&s"(tr)
+        : "s"(pT), "s"(pP), "s"(pM), "s"(pR), "s"(pS), "s"(pF), "s"(pK), "s"(pPL), "s"(pOL), "s"(pAL),
+          "s"(pTR)
         : "memory");
     p.greedy = is_greedy(p.T);
     p.inv_rep = 1.0f / p.rep;
-    p.np = a.prompt ? min(max(pl, 0), a.pwidth) : 0;
+    p.np = (a.prompt && p.rep != 1.0f) ? min(max(pl, 0), a.pwidth) : 0;  // see row_params
     p.no = a.output ? min(max(ol, 0), a.owidth) : 0;
     const bool identity = (p.rep == 1.0f && p.pres == 0.0f && p.freq == 0.0f);
-    p.has_hist = (p.np > 0 || p.no > 0) && !identity;
+    p.tab = a.tstate != nullptr && !identity;
+    p.trow = a.trows ? tr : r;
+    p.has_hist = p.tab || ((p.np > 0 || p.no > 0) && !identity);
     p.na = a.adj_ids ? min(max(al, 0), a.adjwidth) : 0;
-    p.need_hash = p.has_hist || p.na > 0;
+    p.need_hash = (p.has_hist && !p.tab) || p.na > 0;
     return p;
 }
 
@@ -1064,6 +1102,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // processors and penalties that never raise a logit let hashed candidates be found by their
     // raw value (a positive logit bias is only seen once the hash is built)
     const bool mono = !hh || (prm.rep >= 1.0f && prm.pres >= 0.0f && prm.freq >= 0.0f);
+    // penalties that may raise a logit need every penalised token up front, which a token-state
+    // table cannot list: the multi-pass path serves such rows
+    if (prm.tab && !mono) return false;
+    // the row's token-state words (read at the candidates only)
+    const uint32_t* tabrow = prm.tab ? a.tstate + (size_t)prm.trow * (size_t)a.tstride : nullptr;
     const int32_t* pr = hh && prm.np > 0 ? prow : nullptr;
     const int32_t* ou = hh && prm.no > 0 ? orow : nullptr;
 
@@ -1071,7 +1114,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     if (tid == 0) {
         sm.tau = 0u; sm.status = 0u; sm.nhash = 0u; sm.nkeep = 0u; sm.npack = 0u; sm.bc[4] = 0u;
         sm.ymax = 0u; sm.tmaxk = 0u;
-        sm.pmode = hx ? 1u : 0u;
+        sm.pmode = (hx || prm.tab) ? 1u : 0u;
+        sm.phash = hx ? 1u : 0u;
+        sm.ptab = (uint64_t)tabrow;
         sm.adjraise = 0u;
         sm.prep = prm.rep; sm.pinv = prm.inv_rep; sm.ppres = prm.pres; sm.pfreq = prm.freq;
     }
@@ -1163,7 +1208,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         for (int s = tid; s < kRowHash; s += NT) {
             const uint32_t kk = sm.hkey[s];
             if (kk) {
-                sm.hpen[s] = apply_hashed(Elem<T>::load1(row + (kk - 1u)), sm.hval[s], sm.hadj[s],
+                const uint32_t hv = sm.hval[s] | (tabrow ? tabrow[kk - 1u] & kStateMask : 0u);
+                sm.hpen[s] = apply_hashed(Elem<T>::load1(row + (kk - 1u)), hv, sm.hadj[s],
                                           prm.rep, prm.inv_rep, prm.freq, prm.pres);
             }
         }
@@ -1261,10 +1307,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         auto pack_one = [&](int pos, uint32_t kx, int32_t ii, bool fixed, bool first)
             __attribute__((always_inline)) {
             if (capped) kx = key_of(softcap_out(val_of(kx), a.inv_softcap, a.softcap, a.softcap_f16 != 0));
-            if (!fixed && rhash_maybe(sm, ii)) {
-                const int hs = rhash_find(sm, ii);
-                if (hs >= 0)
-                    kx = key_of(apply_hashed(val_of(kx), sm.hval[hs], sm.hadj[hs], sm.prep,
+            if (!fixed) {
+                const int hs = (hx && rhash_maybe(sm, ii)) ? rhash_find(sm, ii) : -1;
+                uint32_t hv = hs >= 0 ? sm.hval[hs] : 0u;
+                if (tabrow) hv |= tabrow[ii] & kStateMask;
+                if (hs >= 0 || hv != 0u)
+                    kx = key_of(apply_hashed(val_of(kx), hv, hs >= 0 ? sm.hadj[hs] : 0.0f, sm.prep,
                                              sm.pinv, sm.pfreq, sm.ppres));
             }
             const uint32_t ky = sampling ? key_of(val_of(kx) / Tt) : kx;
@@ -1671,7 +1719,9 @@ __device__ __noinline__ int row_order_entry(uint64_t kernarg, int b) {
 
 // One workgroup per row (the grid is exactly B workgroups).  `coop` (preloaded with the row's
 // address, stride and V, so that testing it costs no argument read): bit 0, the cooperative
-// region is present; bit 1, the workgroups are counted (KArgs::coop_count).
+// region is present; bit 1, the workgroups are counted (KArgs::coop_count); bit 2, the rows are
+// served longest first (row_order_entry: every workgroup scans the batch's parameters, so the
+// launcher asks for it only up to kRowOrderMaxBatch rows).
 template <typename T>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
                                                           int coop, KArgs a) {
@@ -1679,7 +1729,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
     int r = blockIdx.x;
     if (coop & 2) {
         if (threadIdx.x == 0) ag_add64(&a.coop->wgs, kCoopStarted);
-        r = __builtin_amdgcn_readfirstlane(row_order_entry(kernarg, r));
+        if (coop & 4) r = __builtin_amdgcn_readfirstlane(row_order_entry(kernarg, r));
     }
     const bool long_row = row_one<T>(a, r, logits, lstride, V, kernarg);
     if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T>(kernarg, long_row ? 1 : 0);

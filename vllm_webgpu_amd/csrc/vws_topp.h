@@ -139,7 +139,7 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
 
 // Whether the single-pass top-p path may serve the row.
 __device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
-    if (p.need_hash || a.allowed || a.softcap > 0.0f) return false;
+    if (p.need_hash || p.has_hist || a.allowed || a.softcap > 0.0f) return false;
     if (p.greedy) return a.L >= 0;
     const bool topk_off = p.k <= 0 || p.k >= a.V;
     return topk_off && p.top_p > 0.0f && p.top_p < 1.0f;
@@ -818,7 +818,6 @@ __device__ __forceinline__ void tp_pass_reduce(TopPSmem& sm, int kind, TpPassAcc
 // claimed one reads a stable description.
 constexpr int kCoopMinChunks = 4;
 constexpr uint32_t kCoopNone = 0xFFFFFFFFu;
-constexpr int kCoopWaitPolls = 1 << 20;  // the owner's wait for chunks run by others
 constexpr int kCoopHelpPolls = 1 << 16;  // a helper's polls for chunks while rows hold slots
 static_assert(kCoopBuckets == kTpBuckets && kCoopGather == kTpGather, "cooperative slot sizes");
 static_assert(kTpRankCap * 28 <= kTpGather * 8 && 2 * kTpRankCap <= kGenThreads, "ranked members fit the gather buffer");
@@ -881,8 +880,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     const float lp_min = (!greedy && prm.min_p > 0.0f)
                              ? tp_uf(log_det(prm.min_p < 1.0f ? prm.min_p : 1.0f)) : -__builtin_inff();
     const float aw = tp_uf(sm.anchor);
-    // a cooperative pass that was not completed marks sm.coop_fail; the row is handed over
-    // before anything is written (the rest of the finish runs on, on values of no use)
+    // a cooperative pass that was not completed marks sm.coop_fail; the row is handed over right
+    // after it, before anything is written
     auto pass = [&](int kind, uint32_t key, int bs) __attribute__((always_inline)) {
         topp_pass_entry<T>(kind, r, kernarg, Tt, m, lp_min, key, bs);
         __syncthreads();
@@ -1046,6 +1045,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         for (;;) {
             if (go_exact && !exact) {
                 pass(kTpPassExact, tauk, 0);
+                if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
                 Wc += tp_u64(sm.bc64[10]);
                 any_below_nc = tp_u64(sm.bc64[11]) > 0ull;
                 S[0] = S[1] = 0ull;
@@ -1107,6 +1107,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                         }
                         if (wide) {
                             pass(kTpPassWideRace, tauk, bstar);
+                            if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
                             wbest = tp_u64(sm.bc64[10]);
                             wsec = (uint32_t)tp_u64(sm.bc64[11]);
                             wide_kept = tp_u64(sm.bc64[12]);
@@ -1369,6 +1370,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         uint32_t rk = 0u;
         if (rank_pass) {
             pass(kTpPassRank, ks, 0);
+            if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
             rk = wave == 0 ? (uint32_t)tp_u64(sm.bc64[10]) : 0u;  // the per-wave records below add up
         } else {
             for (int i = lane; i < cnt; i += kWave) rk += sm.ck[wave][i] >= ks ? 1u : 0u;
@@ -1412,8 +1414,6 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (tp_u(sm.bc[7]) > (uint32_t)kTpLpCap) return VWS_FALLBACK_TOPL;
         }
     }
-
-    if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
 
     // ---- outputs (nothing was written before this point)
     if (tid == 0) {

@@ -103,7 +103,8 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
            allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
            adjust_lens=None, logit_softcap: float | None = None,
            logit_softcap_f16: bool = False, rng_seeds: torch.Tensor | None = None,
-           rng_offsets: torch.Tensor | None = None) -> SampleResult:
+           rng_offsets: torch.Tensor | None = None, token_state: torch.Tensor | None = None,
+           token_state_rows: torch.Tensor | None = None) -> SampleResult:
     """Samples one token per row of ``logits`` [B, V] (float32, bfloat16 or float16, on the
     GPU; each widened exactly to fp32).
 
@@ -118,7 +119,9 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     value is added to its logit.  ``logit_softcap`` > 0: ``logits`` are the lm_head output
     before Gemma's final soft cap, which is applied first (cap * tanh(x / cap)); with
     ``logit_softcap_f16`` each capped value is rounded to float16 (the reference's shader
-    stores the cap's output in an f16 buffer).
+    stores the cap's output in an f16 buffer).  ``token_state`` int32 [R, >= V] (uint32 words,
+    see ``token_state_update``) replaces ``prompt_ids``/``output_ids`` as the penalties' history;
+    ``token_state_rows`` int32 [B] picks each row's table row (None = row i).
     """
     _check_device(logits, "logits")
     cap = 0.0 if logit_softcap is None else float(logit_softcap)
@@ -140,6 +143,18 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     pid, pstride, pwidth, plens = _history(prompt_ids, prompt_lens, B, dev, "prompt_ids")
     oid, ostride, owidth, olens = _history(output_ids, output_lens, B, dev, "output_ids")
     aid, astride, awidth, alens = _history(adjust_ids, adjust_lens, B, dev, "adjust_ids")
+    TS = TR = None
+    if token_state is not None:
+        _check_device(token_state, "token_state")
+        if token_state.dtype != torch.int32 or token_state.dim() != 2 or token_state.stride(1) != 1:
+            raise ValueError("token_state must be an int32 [rows, >= V] table with contiguous rows")
+        if token_state.shape[1] < V:
+            raise ValueError(f"token_state rows hold {token_state.shape[1]} words < vocab {V}")
+        TS = token_state
+        if token_state_rows is not None:
+            TR = token_state_rows.to(device=dev, dtype=torch.int32).contiguous()
+            if TR.shape != (B,):
+                raise ValueError(f"token_state_rows must have shape ({B},)")
     aval = None
     if aid is not None:
         if adjust_vals is None:
@@ -194,6 +209,8 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     a.repetition_penalty, a.presence_penalty, a.frequency_penalty = _ptr(R), _ptr(PR), _ptr(FR)
     a.prompt_ids, a.prompt_row_stride, a.prompt_width, a.prompt_lens = _ptr(pid), pstride, pwidth, _ptr(plens)
     a.output_ids, a.output_row_stride, a.output_width, a.output_lens = _ptr(oid), ostride, owidth, _ptr(olens)
+    if TS is not None:
+        a.token_state, a.token_state_row_stride, a.token_state_rows = TS.data_ptr(), TS.stride(0), _ptr(TR)
     if AM is not None:
         a.allowed_mask, a.allowed_row_stride = AM.data_ptr(), AM.stride(0)
     if aid is not None:
@@ -210,6 +227,31 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     _lib.check(L_lib.vws_sample(ctypes.byref(a)))
     # keep the argument tensors alive until the work is enqueued (it is, on return)
     return SampleResult(sampled, flags, nkept, lp_ids, lp_vals, ranks)
+
+
+def token_state_update(state: torch.Tensor, tokens: torch.Tensor, rows=None, prompt: bool = False,
+                       vocab: int | None = None) -> None:
+    """Counts ``tokens`` (int32 [n] on the device) as output occurrences in the token-state
+    table ``state`` (int32 [R, >= V], uint32 words: bit 31 prompt flag, low bits output count),
+    or with ``prompt`` sets their prompt flags.  ``rows``: int32 [n] table rows, or one int for
+    every id.  Ids outside [0, vocab) are padding (vocab defaults to the table's width)."""
+    _check_device(state, "state")
+    if state.dtype != torch.int32 or state.dim() != 2 or state.stride(1) != 1:
+        raise ValueError("state must be an int32 [rows, V] table with contiguous rows")
+    V = state.shape[1] if vocab is None else int(vocab)
+    tok = tokens.to(device=state.device, dtype=torch.int32).contiguous().view(-1)
+    n = tok.numel()
+    R = None
+    row = 0
+    if rows is None or isinstance(rows, int):
+        row = 0 if rows is None else int(rows)
+    else:
+        R = rows.to(device=state.device, dtype=torch.int32).contiguous().view(-1)
+        if R.numel() != n:
+            raise ValueError(f"rows has {R.numel()} entries for {n} ids")
+    kind = _lib.STATE_PROMPT if prompt else _lib.STATE_OUTPUT
+    _lib.check(_lib.lib().vws_token_state_update(state.data_ptr(), state.stride(0), V, n, _ptr(R), row,
+                                                 tok.data_ptr(), kind, _stream_ptr()))
 
 
 def pack_allowed(allowed: torch.Tensor) -> torch.Tensor:

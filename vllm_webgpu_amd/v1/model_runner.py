@@ -10,7 +10,12 @@ Where the reference argmaxes numpy logits on the host and returns ``None`` from
 
 The persistent batch (``InputBatch``) holds every running request's prompt and generated ids in
 device tables padded with ``vocab_size``; each step gathers the scheduled rows and, after
-sampling, appends the sampled ids on the device, so histories are never re-uploaded.  Host
+sampling, appends the sampled ids on the device, so histories are never re-uploaded.  On a GPU
+it also keeps a token-state table, one uint32 word per (request slot, token): prompt flag and
+output count, set when a request is admitted and counted once per sampled id
+(``vws_token_state_update``).  The penalties read that table at the tokens that reach the
+sampler's candidates, so a long prompt or output costs nothing per step (vLLM-v1 rebuilds the
+same prompt mask and output bin counts from the histories every step).  Host
 copies of the generated ids (needed by ``SamplingMetadata.output_token_ids`` and the engine)
 come from the one device-to-host copy of the sampled ids per step.
 
@@ -66,7 +71,7 @@ class InputBatch:
     """
 
     def __init__(self, max_num_reqs: int, max_prompt_len: int, max_output_len: int,
-                 vocab_size: int, device: torch.device) -> None:
+                 vocab_size: int, device: torch.device, token_state: bool = True) -> None:
         self.max_num_reqs = max_num_reqs
         self.max_prompt_len = max_prompt_len
         self.max_output_len = max_output_len
@@ -77,6 +82,12 @@ class InputBatch:
         self.output_ids = torch.full((max_num_reqs, max(max_output_len, 1)), vocab_size,
                                      dtype=torch.int32, device=device)
         self.output_lens = torch.zeros(max_num_reqs, dtype=torch.int32, device=device)
+        # per-slot token state (prompt flag | output count), on a ROCm device only: the table
+        # is maintained by the library's kernels
+        self.token_state = None
+        if token_state and torch.device(device).type == "cuda":
+            self.token_state = torch.zeros((max_num_reqs, vocab_size), dtype=torch.int32,
+                                           device=device)
         self.requests: dict[str, CachedRequestState] = {}
         self._free = list(range(max_num_reqs - 1, -1, -1))
 
@@ -102,6 +113,13 @@ class InputBatch:
         self.prompt_ids[slot].copy_(row, non_blocking=False)
         self.output_ids[slot].fill_(self.vocab_size)
         self.output_lens[slot] = 0
+        if self.token_state is not None:
+            from .. import ops
+
+            self.token_state[slot].zero_()
+            if prompt_token_ids:
+                ops.token_state_update(self.token_state, self.prompt_ids[slot, :len(prompt_token_ids)],
+                                       rows=slot, prompt=True)
         return slot
 
     def remove_request(self, req_id: str) -> None:
@@ -129,10 +147,19 @@ class InputBatch:
         bias = [_param(sp, "logit_bias", None) for sp in sps]
         bad = {i: [list(w) for w in _param(sp, "bad_words_token_ids", [])]
                for i, sp in enumerate(sps) if _param(sp, "bad_words_token_ids", None)}
+        # bad words match the end of the host copy of the output, which lags the device while a
+        # step's output is in flight (async output): refuse rather than match stale ids
+        stale = [states[i].req_id for i in bad
+                 if states[i].num_sampled != len(states[i].output_token_ids)]
+        if stale:
+            raise RuntimeError(f"requests {stale} use bad words while a step's output is still in "
+                               "flight: call get_output() on it before sampling the next step")
         mint = {}
         for i, sp in enumerate(sps):
             mt = int(_param(sp, "min_tokens", 0))
-            if mt > 0:
+            # counted on the device side (num_sampled), which is current even while the host
+            # copy of the output lags (async output); rows past the minimum are left out
+            if mt > 0 and states[i].num_sampled < mt:
                 stop = set(_param(sp, "stop_token_ids", [])) | set(_param(sp, "all_stop_token_ids", []))
                 eos = _param(sp, "eos_token_id", None)
                 if eos is not None:
@@ -154,6 +181,7 @@ class InputBatch:
         all_greedy = all(greedy)
         no_penalties = all(r == 1.0 for r in rep) and not any(pres) and not any(freq)
         slots = t([s.slot for s in states], torch.int64)
+        table = self.token_state is not None and not no_penalties
         # gather only the populated columns: the kernel reads every history column it is given
         pw = max(1, max((len(s.prompt_token_ids) for s in states), default=1))
         ow = max(1, min(self.output_ids.shape[1],
@@ -170,7 +198,8 @@ class InputBatch:
             generators=gens,
             max_num_logprobs=max(lps) if lps else None,
             no_penalties=no_penalties,
-            prompt_token_ids=None if no_penalties else self.prompt_ids[:, :pw].index_select(0, slots),
+            prompt_token_ids=(None if no_penalties or table
+                              else self.prompt_ids[:, :pw].index_select(0, slots)),
             frequency_penalties=t(freq, torch.float32),
             presence_penalties=t(pres, torch.float32),
             repetition_penalties=t(rep, torch.float32),
@@ -180,9 +209,12 @@ class InputBatch:
             bad_words_token_ids=bad,
             min_tokens=mint,
             logit_bias=bias if any(bias) else None,
-            output_token_ids_tensor=(None if no_penalties
+            output_token_ids_tensor=(None if no_penalties or table
                                     else self.output_ids[:, :ow].index_select(0, slots)),
-            output_token_lens=None if no_penalties else self.output_lens.index_select(0, slots),
+            output_token_lens=(None if no_penalties or table
+                               else self.output_lens.index_select(0, slots)),
+            token_state=self.token_state if table else None,
+            token_state_rows=slots.to(torch.int32) if table else None,
         ) if B else None
 
     def decode_inputs(self, req_ids: list[str]) -> tuple[torch.Tensor, torch.Tensor]:
@@ -223,6 +255,10 @@ class InputBatch:
         ok = pos < self.output_ids.shape[1]
         self.output_ids[slots[ok], pos[ok]] = sampled.to(torch.int32)[ok]
         self.output_lens.index_add_(0, slots, ok.to(torch.int32))
+        if self.token_state is not None:
+            from .. import ops
+
+            ops.token_state_update(self.token_state, sampled, rows=slots.to(torch.int32))
 
 
 class AsyncModelRunnerOutput:
@@ -270,11 +306,14 @@ class ROCmModelRunner:
     def __init__(self, vllm_config: Any, device: torch.device | str | None = None,
                  model: Any = None, max_num_reqs: int = 1024, max_prompt_len: int = 8192,
                  max_output_len: int = 8192, vocab_size: int | None = None,
-                 logit_softcap: float | None = None, logit_softcap_f16: bool = False) -> None:
+                 logit_softcap: float | None = None, logit_softcap_f16: bool = False,
+                 token_state: bool = True) -> None:
         """``logit_softcap``: set when ``model`` returns logits before Gemma's final soft cap;
         the sampler then applies the cap inside its launch (``logit_softcap_f16``: rounding
         each capped value to float16, as the reference stores it).  The model's logits may be
-        float32, bfloat16 or float16 (sampled without a cast)."""
+        float32, bfloat16 or float16 (sampled without a cast).  ``token_state``: keep the
+        penalties' history as a per-slot token-state table on the device (``max_num_reqs`` x
+        vocab words) instead of gathering id lists every step."""
         self.vllm_config = vllm_config
         self.device = torch.device(device if device is not None else "cuda")
         self.model = model
@@ -282,13 +321,15 @@ class ROCmModelRunner:
         self._last_logits: torch.Tensor | None = None
         self._last_req_ids: list[str] = []
         self._max = (max_num_reqs, max_prompt_len, max_output_len)
+        self._token_state = token_state
         self._vocab_size = vocab_size
         self.input_batch: InputBatch | None = None
 
     # -- state ---------------------------------------------------------------------------
     def _batch(self, vocab_size: int) -> InputBatch:
         if self.input_batch is None:
-            self.input_batch = InputBatch(*self._max, vocab_size, self.device)
+            self.input_batch = InputBatch(*self._max, vocab_size, self.device,
+                                          token_state=self._token_state)
         elif self.input_batch.vocab_size != vocab_size:
             raise ValueError(f"vocab size changed from {self.input_batch.vocab_size} to {vocab_size}")
         return self.input_batch
@@ -345,9 +386,10 @@ class ROCmModelRunner:
         returned: its ``get_output()`` waits for the copy, so the host can schedule the next
         step while the device finishes this one (the device-side history tables are updated on
         the device either way).  The next step may be executed before ``get_output()``: its
-        inputs and penalty histories come from the device tables.  Bad-words matching reads the
-        host copies of the generated ids, which ``get_output()`` appends, so a batch that uses
-        bad words must call it before the next step samples.
+        inputs, penalty histories and min-tokens counts come from the device-side state.
+        Bad-words matching reads the host copies of the generated ids, which ``get_output()``
+        appends, so a batch that uses bad words must call it before the next step samples
+        (sampling raises otherwise).
         """
         if self._last_logits is None:
             return None

@@ -22,6 +22,11 @@ Conventions the kernels rely on:
   ``bad_words_token_ids`` row -> token sequences (the last token of a sequence is banned when the
   output ends with the rest of it), ``min_tokens`` row -> (minimum output length, stop token
   ids banned until it is reached), ``logit_bias`` per row (token -> bias) or None.
+* ``token_state`` (this package's extension): int32 ``[R, V]`` per-request token-state table
+  kept on the device by a persistent batch (bit 31: the token is in the prompt; low bits: its
+  count in the output), with ``token_state_rows`` int32 ``[B]`` giving each row's table row.
+  When set, the penalties read it instead of ``prompt_token_ids`` / ``output_token_ids``: the
+  prompt mask and output bin counts vLLM-v1 rebuilds every step, kept up to date instead.
 """
 from __future__ import annotations
 
@@ -52,3 +57,5 @@ class SamplingMetadata:
     output_token_lens: torch.Tensor | None = None
     min_tokens: dict[int, tuple[int, set[int]]] = field(default_factory=dict)
     logit_bias: list[dict[int, float] | None] | None = None
+    token_state: torch.Tensor | None = None
+    token_state_rows: torch.Tensor | None = None

@@ -132,7 +132,12 @@ class Sampler:
             seeds = draw_seeds(B, m.generators, dev)
 
         penalties = {}
-        if not m.no_penalties:
+        if not m.no_penalties and m.token_state is not None:
+            penalties = dict(repetition_penalty=m.repetition_penalties,
+                             presence_penalty=m.presence_penalties,
+                             frequency_penalty=m.frequency_penalties,
+                             token_state=m.token_state, token_state_rows=m.token_state_rows)
+        elif not m.no_penalties:
             out_ids, out_lens = m.output_token_ids_tensor, m.output_token_lens
             if out_ids is None and any(m.output_token_ids):
                 out_ids, out_lens = pad_output_ids(m.output_token_ids, V, dev)

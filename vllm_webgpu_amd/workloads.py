@@ -136,6 +136,38 @@ def config(i: int, scale: float = 1.0) -> Workload:
     raise ValueError(f"unknown config {i}")
 
 
+def token_state_table(B: int, V: int, prompt_ids: np.ndarray | None = None,
+                      output_ids: np.ndarray | None = None) -> np.ndarray:
+    """uint32 [B, V] token-state words from padded id lists: bit 31 set for prompt tokens, the
+    low bits counting output occurrences (ids outside [0, V) are padding)."""
+    st = np.zeros((B, V), np.uint32)
+    for ids, prompt in ((prompt_ids, True), (output_ids, False)):
+        if ids is None:
+            continue
+        ok = (ids >= 0) & (ids < V)
+        rows = np.broadcast_to(np.arange(B)[:, None], ids.shape)[ok]
+        t = ids[ok].astype(np.int64)
+        if prompt:
+            np.bitwise_or.at(st, (rows, t), np.uint32(0x80000000))
+        else:
+            np.add.at(st, (rows, t), np.uint32(1))
+    return st
+
+
+def long_history(w: Workload, n_prompt: int = 4096, n_output: int = 1024):
+    """C3's rows with a longer history: ``n_prompt`` prompt ids and ``n_output`` output ids per
+    row, uniform over V from ``default_rng(SEED_BASE + 30)`` (the first ``H`` output ids are the
+    workload's own history)."""
+    B, V = w.shape
+    rng = np.random.default_rng(SEED_BASE + 30)
+    prompt = rng.integers(0, V, size=(B, n_prompt), dtype=np.int64).astype(np.int32)
+    out = rng.integers(0, V, size=(B, n_output), dtype=np.int64).astype(np.int32)
+    if w.output_ids is not None:
+        h = min(n_output, w.output_ids.shape[1])
+        out[:, :h] = w.output_ids[:, :h]
+    return prompt, out
+
+
 def algorithmic_bytes(w: Workload, n_kept: np.ndarray | None) -> int:
     """Lower-bound HBM bytes for one pass of the sampler over workload ``w``.
 
