@@ -192,6 +192,61 @@ def token_state_timing(lib_mod, L, W, w, sets, T, K, P, MP, R, PR, FR, out, flag
     return res
 
 
+def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, stream,
+                   steps: int, warmup: int, num_logprobs=None, parity_rows: int = 16,
+                   allowed=None, hist=None) -> dict:
+    """The launch with one thing changed (raw logprobs requested, an allowed mask [B, V] bool,
+    or a [B, H] output history replacing the workload's), timed with kernel-stamped events and
+    checked against the oracle on its first rows."""
+    import torch
+
+    from oracle import sampler as O  # checker only
+
+    B, V = w.shape
+    words = hist_d = None
+    if allowed is not None:
+        wb = np.zeros((B, (V + 31) // 32 * 32), np.uint64)
+        wb[:, :V] = allowed
+        words = (wb.reshape(B, -1, 32) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
+        words_d = torch.from_numpy(words.view(np.int32)).to(out.device)
+    if hist is not None:
+        hist_d = torch.from_numpy(hist).to(out.device)
+    out_ids = w.output_ids if hist is None else hist
+    lp = None
+    if num_logprobs is not None:
+        lp = (num_logprobs, torch.empty((B, num_logprobs + 1), dtype=torch.int32, device=out.device),
+              torch.empty((B, num_logprobs + 1), dtype=torch.float32, device=out.device),
+              torch.empty(B, dtype=torch.int32, device=out.device))
+    argv, keep = [], []
+    for i, (lg, u, h) in enumerate(sets):
+        if hist_d is not None:
+            h = torch.roll(hist_d, shifts=i, dims=0).contiguous() if i else hist_d
+            keep.append(h)
+        a = build_args(lib_mod, lg, T, K, P, MP, R, PR, FR, h, u, out, flags, nkept, ws, lp)
+        if words is not None:
+            a.allowed_mask, a.allowed_row_stride = words_d.data_ptr(), words_d.stride(0)
+        a.stream = stream.cuda_stream
+        argv.append(a)
+    lib_mod.check(L.vws_sample(ctypes.byref(argv[0])))
+    torch.cuda.synchronize()
+    n = parity_rows
+    gflags = flags.cpu().numpy().view(np.uint32)
+    prm = O.make_params(n, w.temperature[:n], w.top_k[:n], w.top_p[:n], w.min_p[:n],
+                        w.repetition[:n], w.presence[:n], w.frequency[:n])
+    ref = O.sample(w.logits_f32()[:n], prm, w.uniforms[:n],
+                   output_ids=None if out_ids is None else out_ids[:n],
+                   num_logprobs=num_logprobs, allowed=None if words is None else words[:n])
+    mism = int((out.cpu().numpy()[:n] != ref["token"]).sum())
+    if lp is not None:
+        mism += int((lp[1].cpu().numpy()[:n] != ref["lp_ids"]).any(axis=1).sum())
+        mism += int((lp[3].cpu().numpy()[:n] != ref["ranks"]).sum())
+    for i in range(warmup):
+        lib_mod.check(L.vws_sample(ctypes.byref(argv[i % len(argv)])))
+    t = timed_region(lambda i: L.vws_sample(ctypes.byref(argv[i % len(argv)])), steps, stream)
+    return {"kernel_us": kernel_us(t), "timing": t, "parity_rows": n, "mismatches": mism,
+            "general_path_rows": int(((gflags & 0x100) != 0).sum())}
+
+
 def cpu_baseline(w, rows: int, iters: int):
     """torch CPU restatement of vLLM's sampler on `rows` rows of the workload, all host cores."""
     import torch
@@ -444,6 +499,37 @@ def main():
         log("token-state table: " + ", ".join(
             f"{k} {v['kernel_us']:.2f} us ({v['token_mismatches']} of {v['parity_rows']} rows "
             f"differ, {v['general_path_rows']} on the multi-pass path)" for k, v in tstate.items()))
+    variants = None
+    vsteps, vwarm = min(args.steps, 300), min(args.warmup, 30)
+    if args.config == 3 and not args.skip_v1:
+        one_masked = np.ones((B, V), bool)   # row 0 restricted to 20 tokens, the rest allowed
+        one_masked[0] = False
+        one_masked[0, np.random.default_rng(62).choice(V, 20, replace=False)] = True
+        variants = {
+            "logprobs_20": variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out, flags,
+                                          nkept, ws, stream, vsteps, vwarm, num_logprobs=20),
+            "one_masked_row": variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out, flags,
+                                             nkept, ws, stream, vsteps, vwarm, allowed=one_masked)}
+    elif args.config == 5 and not args.skip_v1:
+        # C5 with C3's penalties (a 512-token output history per row; repetition 1.1,
+        # presence 0.5, frequency 0.3)
+        hist5 = np.random.default_rng(W.SEED_BASE + 35).integers(0, V, (B, 512), dtype=np.int64).astype(np.int32)
+        w.repetition[:], w.presence[:], w.frequency[:] = 1.1, 0.5, 0.3
+        R.fill_(1.1)
+        PR.fill_(0.5)
+        FR.fill_(0.3)
+        ws5 = ops.workspace(L.vws_sample_workspace_size(B, V, 512), dev)
+        variants = {"c3_penalties": variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out,
+                                                   flags, nkept, ws5, stream, vsteps, vwarm,
+                                                   num_logprobs=w.num_logprobs, hist=hist5)}
+        w.repetition[:], w.presence[:], w.frequency[:] = 1.0, 0.0, 0.0
+        R.fill_(1.0)
+        PR.fill_(0.0)
+        FR.fill_(0.0)
+    if variants:
+        log("variants: " + ", ".join(
+            f"{k} {v['kernel_us']:.2f} us ({v['mismatches']} mismatches in {v['parity_rows']} rows, "
+            f"{v['general_path_rows']} rows on the multi-pass path)" for k, v in variants.items()))
     v1 = gen = None
     if not args.skip_v1:
         v1 = v1_forward_timing(w, sets[0][0], T, K, P, MP, R, PR, FR, sets[0][2], dev,
@@ -513,6 +599,7 @@ def main():
         "kernel_us_long_history": (None if tstate is None
                                    else tstate["long_history_4096_1024"]["kernel_us"]),
         "token_state": tstate,
+        "variants": variants,
         "v1_sampler_forward": None if v1 is None else {
             **v1, "kernel_us": kern_ms * 1e3, "wall_vs_kernel": v1["wall_us"] / (kern_ms * 1e3)},
         "roofline": {

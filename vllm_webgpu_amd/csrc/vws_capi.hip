@@ -16,7 +16,7 @@
 namespace vws {
 template <typename T> __global__ void fast_kernel(KArgs);
 template <typename T> __global__ void general_kernel(KArgs);
-template <typename T> __global__ void row_kernel(const void*, int64_t, int, int, KArgs);
+template <typename T, bool LP, bool MASK> __global__ void row_kernel(const void*, int64_t, int, int, KArgs);
 template <typename T> __global__ void argmax_kernel(const T*, int64_t, int, int32_t*);
 template <typename T>
 __global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, float*, float*);
@@ -83,7 +83,7 @@ DeviceInfo device_info() {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fast_kernel<float>, kFastThreads, 0) != hipSuccess || n <= 0) n = 4;
         d.fast_blocks_per_cu = n;
         int nr = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nr, row_kernel<float>, kGenThreads, 0) != hipSuccess || nr <= 0) nr = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nr, row_kernel<float, false, false>, kGenThreads, 0) != hipSuccess || nr <= 0) nr = 1;
         d.row_blocks_per_cu = nr;
         (void)hipGetLastError();
     }
@@ -362,7 +362,7 @@ int vws_sample(const vws_sample_args* a) {
     k.lp_ranks = a->logprob_ranks;
     // every row would leave the single-pass kernel at once: rows go straight to the top-p
     // stream or the general path, without the single pass's first loads
-    k.nofast = (a->num_logprobs >= 0 || a->allowed_mask) ? 1 : 0;
+    k.nofast = (a->allowed_mask && a->num_logprobs >= 0) ? 1 : 0;
     // more rows than workgroups resident at once: the kernel counts its workgroups, so that one
     // whose row is done waits for other rows' passes only once no workgroup is left to start
     const int grid = a->batch;
@@ -375,13 +375,19 @@ int vws_sample(const vws_sample_args* a) {
     const int cf = (k.coop ? 1 : 0) | (k.coop_count ? 2 : 0) |
                    ((k.coop_count && a->batch <= kRowOrderMaxBatch) ? 4 : 0);
     hipStream_t s = (hipStream_t)a->stream;
+    // the kernel with the raw-logprob epilogue only for launches that ask for logprobs, the one
+    // that masks as it streams only for launches with an allowed mask (and no logprobs)
     const int K = VWS_KERNEL_SAMPLE;
+    const int var = a->num_logprobs >= 0 ? 1 : (a->allowed_mask ? 2 : 0);
+    using Kern = void (*)(const void*, int64_t, int, int, KArgs);
+    Kern kern;
     if (a->dtype == VWS_DTYPE_F32)
-        launch(K, row_kernel<float>, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
+        kern = var == 1 ? row_kernel<float, true, false> : var == 2 ? row_kernel<float, false, true> : row_kernel<float, false, false>;
     else if (a->dtype == VWS_DTYPE_BF16)
-        launch(K, row_kernel<uint16_t>, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
+        kern = var == 1 ? row_kernel<uint16_t, true, false> : var == 2 ? row_kernel<uint16_t, false, true> : row_kernel<uint16_t, false, false>;
     else
-        launch(K, row_kernel<_Float16>, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
+        kern = var == 1 ? row_kernel<_Float16, true, false> : var == 2 ? row_kernel<_Float16, false, true> : row_kernel<_Float16, false, false>;
+    launch(K, kern, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();
 }

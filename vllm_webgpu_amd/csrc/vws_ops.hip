@@ -61,6 +61,11 @@ __global__ __launch_bounds__(kOpThreads) void argmax_kernel(const T* logits, int
 }
 
 // probs = exp_det(x/T - m) / S, m = max x/T, S = sum exp_det(x/T - m); one workgroup per row.
+// Rows of up to 32 values per thread (V <= 32768: 8 chunks of fp32, 4 of 16-bit values) are
+// read once: each thread keeps its chunks in registers through the max, the sum and the write
+// (one read and one write of the row);
+// longer rows are read three times (max, sum, write).  S is summed in double, in a different
+// order than the sequential oracle (the probabilities agree to within a few fp32 ulps).
 template <typename T>
 __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, int64_t stride, int V,
                                                               const float* temperature, float* probs,
@@ -72,32 +77,73 @@ __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, in
     Slice<T> sl;
     sl.init(logits + (size_t)r * stride, 0, V);
     constexpr int VEC = Elem<T>::kVec;
+    constexpr int kSoftmaxRegs = 32 / VEC;  // chunks a thread keeps in registers
+    const int nch = sl.nchunks();
+    // element i of chunk c (head and tail chunks are NaN-padded) lies in the row
+    auto inside = [&](int c, int i) {
+        const bool in = (c == 0) ? (i < sl.a) : (c <= sl.nbody ? true : i < V);
+        return c <= sl.nbody + 1 && in && i < V;
+    };
+    float* out = probs + (size_t)r * V;
     uint64_t mk = 0;
-    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
-        float v[VEC];
-        sl.load(c, v);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[j] / Tt); mk = mk > k ? mk : k; }
-    }
-    mk = op_block_max(mk, red);
-    const float m = val_of((uint32_t)mk);
     double s = 0.0;
-    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
-        float v[VEC];
-        sl.load(c, v);
+    float m;
+    double S;
+    if (nch <= kSoftmaxRegs * kOpThreads) {
+        float v[kSoftmaxRegs][VEC];
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) if (v[j] == v[j]) s += (double)exp_det(v[j] / Tt - m);
-    }
-    const double S = op_block_sum_f64(s, redd);
-    for (int c = threadIdx.x; c < sl.nchunks(); c += kOpThreads) {
-        float v[VEC];
-        const int i0 = sl.load(c, v);
+        for (int q = 0; q < kSoftmaxRegs; ++q) {
+            const int c = threadIdx.x + q * kOpThreads;
+            if (c < nch) {
+                sl.load(c, v[q]);
+            } else {
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            const int i = i0 + j;
-            const bool inside = (c == 0) ? (i < sl.a) : (c <= sl.nbody ? true : i < V);
-            if (c <= sl.nbody + 1 && inside && i < V)
-                probs[(size_t)r * V + i] = (float)((double)exp_det(v[j] / Tt - m) / S);
+                for (int j = 0; j < VEC; ++j) v[q][j] = __builtin_nanf("");
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kSoftmaxRegs; ++q)
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[q][j] / Tt); mk = mk > k ? mk : k; }
+        mk = op_block_max(mk, red);
+        m = val_of((uint32_t)mk);
+#pragma unroll
+        for (int q = 0; q < kSoftmaxRegs; ++q)
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) if (v[q][j] == v[q][j]) s += (double)exp_det(v[q][j] / Tt - m);
+        S = op_block_sum_f64(s, redd);
+#pragma unroll
+        for (int q = 0; q < kSoftmaxRegs; ++q) {
+            const int c = threadIdx.x + q * kOpThreads;
+            // first element of chunk c: the row's start (head), the body vectors, the tail
+            const int i0 = c == 0 ? 0 : sl.a + (c - 1) * VEC;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j)
+                if (c < nch && inside(c, i0 + j))
+                    out[i0 + j] = (float)((double)exp_det(v[q][j] / Tt - m) / S);
+        }
+    } else {
+        for (int c = threadIdx.x; c < nch; c += kOpThreads) {
+            float v[VEC];
+            sl.load(c, v);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[j] / Tt); mk = mk > k ? mk : k; }
+        }
+        mk = op_block_max(mk, red);
+        m = val_of((uint32_t)mk);
+        for (int c = threadIdx.x; c < nch; c += kOpThreads) {
+            float v[VEC];
+            sl.load(c, v);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) if (v[j] == v[j]) s += (double)exp_det(v[j] / Tt - m);
+        }
+        S = op_block_sum_f64(s, redd);
+        for (int c = threadIdx.x; c < nch; c += kOpThreads) {
+            float v[VEC];
+            const int i0 = sl.load(c, v);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j)
+                if (inside(c, i0 + j)) out[i0 + j] = (float)((double)exp_det(v[j] / Tt - m) / S);
         }
     }
     if (threadIdx.x == 0) {

@@ -56,9 +56,12 @@ __device__ __forceinline__ float row_uniform(const KArgs& a, int r, int t) {
     return philox_uniform(a.rng_seed[r], a.rng_offset ? a.rng_offset[r] : 0ull, (uint32_t)t);
 }
 
-// k served by the single-pass kernel for this row, or 0 when the row needs the general kernel.
+// k served by the single-pass kernel for this row, or 0 when the row needs another path (top-k
+// off or above kKMax; an allowed mask together with logprobs).  With raw logprobs the single
+// pass keeps at least L candidates and finishes the logprobs from them (row_logprobs_entry);
+// with an allowed mask it masks every element as it streams.
 __device__ __forceinline__ int fast_k(const KArgs& a, const RowP& p) {
-    if (a.L >= 0 || a.allowed) return 0;
+    if (a.allowed && a.L >= 0) return 0;
     if (p.greedy) return 1;
     if (p.k > 0 && p.k < a.V && p.k <= kKMax) return p.k;
     return 0;

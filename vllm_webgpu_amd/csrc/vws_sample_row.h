@@ -1,4 +1,6 @@
-// vws_sample_row.hip -- the sampling kernel: one workgroup of 1024 threads per row.
+// vws_sample_row.h -- the sampling kernel: one workgroup of 1024 threads per row.  Instantiated
+// per logits type in vws_row_f32.hip, vws_row_bf16.hip and vws_row_f16.hip (each a code object
+// of its own, compiled in parallel), with and without raw logprobs.
 //
 // Greedy rows and top-k rows (k <= 256) are finished in one streaming pass over the row:
 //   1. the history ids are loaded, then the first two iterations of logits (8 x 16-byte loads
@@ -23,6 +25,8 @@
 // Every other row (top-k off or k > 256, logprobs requested, candidate or hash overflow, a
 // seed above the k-th value, degenerate maxima, temperature ties across a threshold) runs the
 // multi-pass path of vws_general.h in the same workgroup, so one launch serves the whole batch.
+#pragma once
+
 #include "vws_general.h"
 #include "vws_topp.h"
 
@@ -80,6 +84,15 @@ struct RowSmem {
     uint32_t pmode, phash;
     float prep, pinv, ppres, pfreq;
     uint64_t ptab;
+    // raw logprobs (launches that ask for them): each wave's sum of 2^(x log2 e - lpA) over its share
+    // of the row; the tail's token, packing layout, greedy flag and largest threshold; then
+    // the sampled token's raw key, candidates at or above the threshold, the largest raw key
+    // and the rank (row_logprobs_entry)
+    uint32_t plp;
+    double lpS[kRowWaves];
+    float lpA[kRowWaves];
+    uint32_t lpk[8];
+    float lplog;
 };
 
 union RowShared {
@@ -658,6 +671,9 @@ __device__ __noinline__ int row_fixup(int w, int from, int cnt) {
 // (k-th key << 32) | new count (k-th key 0 when fewer than k candidates remain).  Compaction is
 // rare, so it lives out of line and the unrolled streaming loop stays small.
 __device__ __noinline__ uint64_t row_compact(int w, int nfix, int cnt, int k) {
+    // raw logprobs need the candidates' raw keys, which a fix-up replaces (and a cut by
+    // processed values may drop an element of the raw top L): the row takes the multi-pass path
+    if (g_row_sh.f.plp && g_row_sh.f.pmode != 0u) atomicOr(&g_row_sh.f.status, 8u);
     cnt = row_fixup(w, nfix, cnt);
     if (cnt <= k) return (uint64_t)(uint32_t)cnt;
     RowSmem& sm = g_row_sh.f;
@@ -786,10 +802,10 @@ struct RowCand {
 // unconditional scalar load: T, top_p, min_p, repetition, presence, frequency.  The arrays are
 // never written; they are not const so that they live in the global address space, like the
 // arrays they stand in for, and the pointer select between the two stays global.
-__device__ float kRowDefaultsF[8] = {0.0f, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+static __device__ float kRowDefaultsF[8] = {0.0f, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 // top_k (0 = off), a length that clamps to the history width (absent lengths = full width), and
 // a token-state row (replaced by the row itself when the table has no row map)
-__device__ int32_t kRowDefaultsI[4] = {0, 0x7FFFFFFF, 0, 0};
+static __device__ int32_t kRowDefaultsI[4] = {0, 0x7FFFFFFF, 0, 0};
 
 // Per-row parameters, all issued as scalar loads before the first one is used.  Scalar loads
 // complete on their own counter, so waiting for them never waits for the logits in flight.
@@ -866,7 +882,8 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
 // Exact when the k-th key is strictly above the largest y a dropped element can have (ylim).
 // Returns false (uniformly over the workgroup) when the row must take the general path.
 __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int r, const RowP& prm,
-                                               int k, int total, uint32_t seed, bool sampling) {
+                                               int k, int total, uint32_t seed, bool sampling,
+                                               bool short_ok) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool mine = tid < total;
@@ -924,14 +941,17 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
     __syncthreads();
     // tie or hash overflow, a k-th key not above a dropped element, or fewer than k candidates
     // with a threshold used
-    if (sm.status != 0u || (tmax != 0u && total < k)) return false;
+    if (sm.status != 0u || (tmax != 0u && total < k && !(short_ok && tmax == 0x00800000u))) return false;
     const uint64_t top = total > 0 ? sm.tk[0] : 0ull;
     if (!sampling) {
         // greedy: the lowest index at the maximum of the processed logits (0 without candidates)
         if (tid == 0) {
-            a.sampled[r] = (top >> 32) != 0ull ? (int32_t)(0x7FFFFFFFu - (uint32_t)top) : 0;
+            const int32_t tok = (top >> 32) != 0ull ? (int32_t)(0x7FFFFFFFu - (uint32_t)top) : 0;
+            a.sampled[r] = tok;
             if (a.flags) a.flags[r] = VWS_FLAG_GREEDY;
             if (a.nkept) a.nkept[r] = 1;
+            // for row_logprobs_entry: the token, 64-bit packing, greedy, the largest threshold
+            sm.lpk[0] = (uint32_t)tok; sm.lpk[1] = 1u; sm.lpk[2] = 1u; sm.lpk[3] = tmax;
         }
         return true;
     }
@@ -1017,14 +1037,22 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
         a.sampled[r] = tok;
         if (a.flags) a.flags[r] = fl;
         if (a.nkept) a.nkept[r] = nkept;
+        sm.lpk[0] = (uint32_t)tok; sm.lpk[1] = 1u; sm.lpk[2] = 0u; sm.lpk[3] = tmax;
     }
     return true;
 }
 
 // Serves greedy and top-k rows; returns false when the row must take the general path (nothing
 // has been written for it then); *topp_row tells whether the single-pass top-p path may serve
-// the row instead.
-template <typename T>
+// the row instead.  LP (launches with raw logprobs): the stream also sums exp(x - a) over every
+// element (a the wave's largest value of its first iteration), the candidates keep their raw
+// keys, and the threshold keeps at least max(k, L) candidates, so that row_logprobs_entry can
+// finish the logprobs from the candidates.  MASK (launches with an allowed-token mask and no
+// logprobs): every element outside the row's mask becomes -inf as it is loaded, before the seed
+// and the threshold see it.  One mask word per lane and iteration covers the wave's whole
+// iteration (U vectors of 64 lanes x VEC elements = 64 words; row starts 16-byte aligned), and
+// each lane takes its vector's bits from the lane that loaded them (ds_bpermute).
+template <typename T, bool LP, bool MASK>
 __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, const void* logits,
                                          int64_t lstride, int V, bool* topp_row) {
     constexpr int NT = kRowThreads;
@@ -1044,6 +1072,17 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     //    so nothing is clamped.
     //    The row addresses are computed without branches (an absent list gets a zero-sized
     //    buffer, whatever its address), so that the kernel arguments are read in one batch.
+    // LP: the row's parameters first.  Launches with logprobs also hold rows the single pass does
+    // not serve (top-p without top-k: most of such a batch); those must not issue the first two
+    // iterations (256 KB of fp32 logits) only to stream the row again on the top-p path.
+    // Without logprobs the first loads wait for no argument read.
+    if (LP) {
+        const RowP p0 = row_params_scalar(a, r);
+        if (fast_k(a, p0) == 0) {
+            *topp_row = topp_eligible(a, p0);
+            return false;
+        }
+    }
     Slice<T> sl;
     sl.init(row, 0, V);
     const int nbody = sl.nbody;
@@ -1090,13 +1129,48 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
     __builtin_amdgcn_sched_barrier(0);
     load_part(A, 0, BoolC<true>{}, U / 2, U);
+    // MASK: the row's allowed-token words; lane l loads word l of the wave's share of an
+    // iteration (vector l / (2 VEC), word l % (2 VEC) of it); words past the mask read 0
+    const uint32_t* mrow = MASK ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(mrow, MASK ? 4u * (uint32_t)((V + 31) >> 5) : 0u);
+    auto load_mask = [&](uint32_t& mw, int it) __attribute__((always_inline)) {
+        if (MASK) {
+            const int ln = lane_now();
+            const uint32_t wi = (uint32_t)((((it * U + ln / (2 * VEC)) * NT + wave * kWave) * VEC) >> 5) +
+                                (uint32_t)(ln % (2 * VEC));
+            mw = __builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * wi, 0u, 0);
+        }
+    };
+    // elements of buf outside the mask become -inf (mw: this lane's word of the iteration)
+    auto mask_iter = [&](float (&buf)[U][VEC], uint32_t mw) __attribute__((always_inline)) {
+        if (MASK) {
+            const int ln = lane_now();
+#pragma unroll
+            for (int q = 0; q < U; ++q) {
+                const int src = q * 2 * VEC + ((ln * VEC) >> 5);
+                const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mw);
+                const uint32_t bits = w >> ((ln * VEC) & 31);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) buf[q][j] = ((bits >> j) & 1u) ? buf[q][j] : -__builtin_inff();
+            }
+        }
+    };
+    uint32_t MA = 0u, MB = 0u;
+    load_mask(MA, 0);
     load_iter(Bq, 1, BoolC<false>{});
+    load_mask(MB, 1);
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
     if (k == 0) {
         *topp_row = topp_eligible(a, prm);
         return false;
     }
+    // raw logprobs are of the capped logits, which the stream does not compute
+    if (LP && a.softcap > 0.0f) return false;
+    // MASK: the mask words line up with the vectors only when the row starts 16-byte aligned
+    if (MASK && sl.a != 0) return false;
+    // the threshold keeps at least kc candidates: the top-L raw logits must be among them
+    const int kc = LP ? max(k, a.L) : k;
     const bool hh = prm.has_hist;     // penalties
     const bool hx = prm.need_hash;    // penalties or logits processors
     // processors and penalties that never raise a logit let hashed candidates be found by their
@@ -1119,6 +1193,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         sm.ptab = (uint64_t)tabrow;
         sm.adjraise = 0u;
         sm.prep = prm.rep; sm.pinv = prm.inv_rep; sm.ppres = prm.pres; sm.pfreq = prm.freq;
+        sm.plp = LP ? 1u : 0u;
+        if (LP)
+            for (int i = 0; i < 8; ++i) sm.lpk[i] = 0u;
     }
     if (hx) {
         for (int s = tid; s < kRowHash; s += NT) { sm.hkey[s] = 0u; sm.hval[s] = 0u; }
@@ -1167,12 +1244,28 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     //    for any lambda, and keeps about m * V / sample candidates (k = 1: the sample's
     //    maximum, never above the k-th).
     const int sample = nbody > 0 ? min(NT * U, nbody) * VEC : 0;
-    const float lam = (float)(k - 1) * (float)sample / (float)V;
-    const int m_seed = sample > 0 ? (k > 1 ? (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f) : 1) : 0;
+    const float lam = (float)(kc - 1) * (float)sample / (float)V;
+    const int m_seed = sample > 0 ? (kc > 1 ? (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f) : 1) : 0;
     const bool seeded = sample > 0 && m_seed <= kRowWaves * kSeedPerWave;
     // m <= 64: the pool is every wave's 4 largest lane maxima, and every wave selects the m-th
     // largest of it for itself; otherwise the 16 largest of every wave, selected by wave 0
     const bool small_pool = m_seed <= kRowWaves * 4;
+    // LP: the wave's anchor, its largest value over the first iteration (0 when it has none
+    // that is finite), so that its sum of exp(x - anchor) starts near 1 and cannot overflow
+    // unless a later value lies ~88 above it (the row then takes the multi-pass path)
+    mask_iter(A, MA);
+    float aw = 0.0f;
+    if (LP) {
+        float lm = __builtin_nanf("");
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            const bool ok = q * NT + tid < nbody;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) lm = ok ? fmaxf(lm, A[q][j]) : lm;
+        }
+        const uint32_t km = wave_max_u32(key_of(lm));
+        aw = (km > 0x007FFFFFu && km < 0xFF800000u) ? val_of(km) : 0.0f;
+    }
     if (seeded) {
         float mx = __builtin_nanf("");  // fmaxf ignores NaN; clamped duplicate loads are skipped
 #pragma unroll
@@ -1203,14 +1296,17 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const bool gather = hx && (!mono || sm.adjraise != 0u);
     // something may raise a logit and the logits are capped: the general path serves the row
     if (gather && a.softcap > 0.0f) return false;
+    // LP: the up-front processed values would leave the candidates without their raw keys
+    if (LP && gather) return false;
     if (gather) {
         if (lane == 0) sm.pmode = 2u;  // every wave writes the same value before its stream
         for (int s = tid; s < kRowHash; s += NT) {
             const uint32_t kk = sm.hkey[s];
             if (kk) {
                 const uint32_t hv = sm.hval[s] | (tabrow ? tabrow[kk - 1u] & kStateMask : 0u);
-                sm.hpen[s] = apply_hashed(Elem<T>::load1(row + (kk - 1u)), hv, sm.hadj[s],
-                                          prm.rep, prm.inv_rep, prm.freq, prm.pres);
+                float xr = Elem<T>::load1(row + (kk - 1u));
+                if (MASK && !((mrow[(kk - 1u) >> 5] >> ((kk - 1u) & 31u)) & 1u)) xr = -__builtin_inff();
+                sm.hpen[s] = apply_hashed(xr, hv, sm.hadj[s], prm.rep, prm.inv_rep, prm.freq, prm.pres);
             }
         }
     }
@@ -1227,15 +1323,29 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         if (wave_ballot(c) == 0ull) return;
         cb.append(c, key_of(v), idx);  // raw value; penalties are applied by RowCand::finish
     };
+    // LP: this lane's sum of exp(x - aw) = 2^(x log2 e - aw log2 e) (one fma and the hardware
+    // exp2; the product aw log2 e rounded once for the whole wave, which scales every term of
+    // the wave alike and is undone exactly by the rescale in row_logprobs_entry; each
+    // iteration's float partial sum added in double)
+    const float awc = aw * kLog2e;
+    double lacc = 0.0;
     // One vector (VEC elements per lane) at a time: the lane maximum against the threshold
     // decides for the whole wave whether any element of the vector is examined one by one.
-    auto examine = [&](float (&buf)[U][VEC], int it) __attribute__((always_inline)) {
+    auto examine = [&](float (&buf)[U][VEC], uint32_t mw, int it) __attribute__((always_inline)) {
+        mask_iter(buf, mw);
         cb.refresh();
         const int t = tid_now();
+        float lit = 0.0f;
 #pragma unroll
         for (int q = 0; q < U; ++q) {
             const int vi = (it * U + q) * NT + t;
             const bool ok = vi < nbody;
+            if (LP) {
+                float tq = 0.0f;
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) tq += __builtin_amdgcn_exp2f(__builtin_fmaf(buf[q][j], kLog2e, -awc));
+                lit += ok ? tq : 0.0f;
+            }
             float mq = buf[q][0];
 #pragma unroll
             for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
@@ -1243,6 +1353,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             if (__builtin_expect(hm == 0ull, 1)) continue;
             cb.template append_vec<VEC>(buf[q], sl.a + vi * VEC, hm);
         }
+        if (LP) lacc += (double)lit;
     };
     const bool sampling = !prm.greedy;
     // With the soft cap the buffer keeps raw values throughout (the cap is applied at the pack),
@@ -1254,7 +1365,18 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // it by twice the margin in capped units.
     if (capped && seed > 0x007FFFFFu)
         seed = key_of(softcap_lower(val_of(seed), a.inv_softcap, a.softcap));
-    cb.init(wave, k, !capped);
+    // MASK: the elements outside the mask are -inf; the threshold admits finite values only
+    // (the smallest key above -inf), so that they never become candidates
+    if (MASK && seed < 0x00800000u) seed = 0x00800000u;
+    // Fewer candidates than k are exact when no threshold was used.  With the finite-only
+    // threshold alone (MASK), every finite value is a candidate and the top k also holds every
+    // -inf element (y = -inf >= the k-th value): those have zero mass, fail min-p, are removed
+    // by top-p when it is on (their cumulative mass 0 is at most the cut; the near-tie term they
+    // would add needs 1 - p within 2e-6 of 0, which is left to the multi-pass path), and lose
+    // every race, so they change nothing when min-p or top-p is on.
+    const bool short_ok = MASK && seed == 0x00800000u &&
+                          (prm.min_p > 0.0f || (1.0f - prm.top_p) > 2e-6f);
+    cb.init(wave, kc, !capped);
     cb.set_tau(seed);
     if (gather) {
         constexpr int per = kRowHash / kRowWaves;
@@ -1266,10 +1388,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         }
     }
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
-        examine(A, it);
+        examine(A, MA, it);
         load_iter(A, it + 2, BoolC<false>{});
-        if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
+        load_mask(MA, it + 2);
+        if (it + 1 < nit && !cb.ovf) examine(Bq, MB, it + 1);
         load_iter(Bq, it + 3, BoolC<false>{});
+        load_mask(MB, it + 3);
     }
     if (wave == 0) {
         // unaligned head (thread 0) and tail (thread 1), fewer than 2 vectors in total; handled
@@ -1280,8 +1404,31 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         int i0 = 0;
         if (tid <= 1) i0 = sl.load_edge(tid, v);
         const int end = tid == 0 ? sl.a : V;
+        if (MASK && tid <= 1) {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) {
+                const int t = i0 + j;
+                if (t < end && !((mrow[t >> 5] >> (t & 31)) & 1u)) v[j] = -__builtin_inff();
+            }
+        }
 #pragma unroll
         for (int j = 0; j < VEC; ++j) slot(v[j], i0 + j, tid <= 1 && i0 + j < end);
+        if (LP) {
+#pragma unroll
+            for (int j = 0; j < VEC; ++j)
+                if (tid <= 1 && i0 + j < end) lacc += (double)__builtin_amdgcn_exp2f(__builtin_fmaf(v[j], kLog2e, -awc));
+        }
+    }
+    if (LP) {
+        // the wave's sum (a NaN or an overflow sends the row to the multi-pass path)
+        double sw = lacc;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sw += __shfl_xor(sw, o, kWave);
+        if (lane == 0) {
+            sm.lpS[wave] = sw;
+            sm.lpA[wave] = awc;  // the wave's terms are 2^(x log2 e - awc)
+            if (!(sw < 1e300)) atomicOr(&sm.status, 16u);
+        }
     }
     // each wave packs its candidates into the row's arrays as soon as its own stream ends, while
     // other waves are still streaming: the key of y (the processed logit over T; the processed
@@ -1306,6 +1453,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         // unless a compaction has applied them) and its packed entry at slot pos
         auto pack_one = [&](int pos, uint32_t kx, int32_t ii, bool fixed, bool first)
             __attribute__((always_inline)) {
+            // LP: the raw key of every packed candidate (the soft cap and up-front processed
+            // values never occur with LP; a compaction that processed keys set status bit 8)
+            if (LP) reinterpret_cast<uint32_t*>(sm.hpen)[pos] = kx;
             if (capped) kx = key_of(softcap_out(val_of(kx), a.inv_softcap, a.softcap, a.softcap_f16 != 0));
             if (!fixed) {
                 const int hs = (hx && rhash_maybe(sm, ii)) ? rhash_find(sm, ii) : -1;
@@ -1375,11 +1525,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const int total = (int)sm.npack;
     if (total > kRowPack) return false;  // too many candidates
     // the single-wave finish checks the status and the thresholds once its count is running
-    if (small) return row_tail_small(a, sm, r, prm, k, total, seed, sampling);
+    if (small) return row_tail_small(a, sm, r, prm, k, total, seed, sampling, short_ok);
     if (sm.status != 0u) return false;  // tie or hash overflow
     const uint32_t tmax = seed > sm.tmaxk ? seed : sm.tmaxk;  // every threshold used (raw keys)
     // fewer than k candidates can only be exact when no threshold was used
-    if (tmax != 0u && total < k) return false;
+    if (tmax != 0u && total < k && !(short_ok && tmax == 0x00800000u)) return false;
     // the largest y an element below the thresholds can have (with the soft cap, a bound on
     // it); -inf when only NaNs were dropped
     float vlim = val_of(tmax - 1u);
@@ -1562,8 +1712,86 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         a.sampled[r] = tok;
         if (a.flags) a.flags[r] = fl;
         if (a.nkept) a.nkept[r] = (int32_t)rs.nkept;
+        sm.lpk[0] = (uint32_t)tok; sm.lpk[1] = 0u; sm.lpk[2] = 0u; sm.lpk[3] = tmax;
     }
     return true;
+}
+
+// Raw logprobs of a row the single pass has sampled (launches that ask for them; every thread
+// calls it after row_fast succeeded).  The packed candidates are every element of the row at
+// or above its wave's final threshold, with their raw keys (sm.hpen) and indices (packed
+// keys); every element left out lies below the largest threshold any wave used (tmax).  So the
+// L largest raw logits (value desc, index asc) are the L largest candidates as long as at
+// least L candidates lie at or above tmax, and the sampled token's rank (#{j : x_j >= x_s})
+// is counted among the candidates as long as x_s >= tmax.  The log-normaliser is the stream's
+// per-wave sums of exp(x - a_w), rescaled to the row maximum in double.  Returns 0 (nothing of
+// the logprobs written; the row's token is written again by the multi-pass path) when a
+// condition fails.
+__device__ __noinline__ int row_logprobs_entry(int r, uint64_t kernarg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KArgs a = kargs_at(kernarg);
+    r = __builtin_amdgcn_readfirstlane(r);
+    RowSmem& sm = g_row_sh.f;
+    const int tid = threadIdx.x, lane = tid & 63;
+    __syncthreads();  // the tail's hand-off (sm.lpk[0..3])
+    const int total = (int)sm.npack;
+    const bool small = sm.lpk[1] != 0u, greedy = sm.lpk[2] != 0u;
+    const uint32_t tok = sm.lpk[0], tmax = sm.lpk[3];
+    const uint32_t* rawk = reinterpret_cast<const uint32_t*>(sm.hpen);
+    const bool mine = tid < total;
+    const uint32_t rk = mine ? rawk[tid] : 0u;
+    uint32_t ix = 0u;
+    if (mine) {
+        const uint32_t lo = small ? (uint32_t)sm.pk64[tid] : (uint32_t)sm.pidx[tid];
+        ix = (small && greedy) ? 0x7FFFFFFFu - lo : lo;
+    }
+    if (mine && ix == tok) sm.lpk[4] = rk;
+    const uint32_t nge = (uint32_t)__popcll(wave_ballot(mine && rk >= tmax));
+    const uint32_t mxk = wave_max_u32(rk);
+    if (lane == 0) {
+        if (nge) atomicAdd(&sm.lpk[5], nge);
+        atomicMax(&sm.lpk[6], mxk);
+    }
+    __syncthreads();
+    const uint32_t ks = sm.lpk[4], ngeq = sm.lpk[5], km = sm.lpk[6];
+    const int L = a.L;
+    if (!(ks != 0u && ks >= tmax && (int)ngeq >= L && km > 0x007FFFFFu && km < 0xFF800000u)) return 0;
+    // the rank, and each candidate's position in (raw desc, index asc) order, counted over a
+    // 64-bit copy of the candidates in the (now free) candidate buffers
+    const uint32_t nrk = (uint32_t)__popcll(wave_ballot(mine && rk >= ks));
+    if (lane == 0 && nrk) atomicAdd(&sm.lpk[7], nrk);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(&sm.ckey[0][0]);
+    const uint64_t me = ((uint64_t)rk << 32) | (0x7FFFFFFFu - ix);
+    if (mine) keys[tid] = me;
+    const float A = val_of(km);  // the row maximum: the largest candidate
+    if (tid == 0) {
+        double S = 0.0;
+        for (int w = 0; w < kRowWaves; ++w)
+            if (sm.lpS[w] > 0.0) S += sm.lpS[w] * exp2((double)sm.lpA[w] - (double)A * (double)kLog2e);
+        sm.lplog = (float)log(S);
+    }
+    __syncthreads();
+    uint32_t pos = 0u;
+    if (mine && rk >= tmax) {
+        for (int j = 0; j < total; ++j) pos += keys[j] > me ? 1u : 0u;
+    }
+    const float logS = sm.lplog;
+    const int stride = L + 1;
+    if (tid == 0) {
+        a.lp_ids[(size_t)r * stride] = (int32_t)tok;
+        a.lp_vals[(size_t)r * stride] = (val_of(ks) - A) - logS;
+        a.lp_ranks[r] = (int32_t)sm.lpk[7];
+    }
+    if (mine && rk >= tmax && pos < (uint32_t)L) {
+        a.lp_ids[(size_t)r * stride + 1 + pos] = (int32_t)ix;
+        a.lp_vals[(size_t)r * stride + 1 + pos] = (val_of(rk) - A) - logS;
+    }
+    return 1;
+#else
+    (void)r;
+    (void)kernarg;
+    return 0;
+#endif
 }
 
 // The general path runs in a function of its own so that its register allocation (it needs
@@ -1585,14 +1813,14 @@ __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
 // One row: the single pass, the single-pass top-p path or the multi-pass path.  Returns whether
 // the row took one of the longer paths (top-p or multi-pass), whose workgroup then looks for
 // chunks of other rows' passes.
-template <typename T>
+template <typename T, bool LP, bool MASK>
 __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logits, int64_t lstride,
                                         int V, uint64_t kernarg) {
     bool topp = false;
     if (a.nofast) {
         topp = topp_eligible(a, row_params(a, r));
-    } else if (row_fast<T>(a, g_row_sh.f, r, logits, lstride, V, &topp)) {
-        return false;
+    } else if (row_fast<T, LP, MASK>(a, g_row_sh.f, r, logits, lstride, V, &topp)) {
+        if (!LP || row_logprobs_entry(r, kernarg)) return false;
     }
     int why = 0;
     if (topp) {
@@ -1722,7 +1950,7 @@ __device__ __noinline__ int row_order_entry(uint64_t kernarg, int b) {
 // region is present; bit 1, the workgroups are counted (KArgs::coop_count); bit 2, the rows are
 // served longest first (row_order_entry: every workgroup scans the batch's parameters, so the
 // launcher asks for it only up to kRowOrderMaxBatch rows).
-template <typename T>
+template <typename T, bool LP, bool MASK>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
                                                           int coop, KArgs a) {
     const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u;
@@ -1731,12 +1959,8 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
         if (threadIdx.x == 0) ag_add64(&a.coop->wgs, kCoopStarted);
         if (coop & 4) r = __builtin_amdgcn_readfirstlane(row_order_entry(kernarg, r));
     }
-    const bool long_row = row_one<T>(a, r, logits, lstride, V, kernarg);
+    const bool long_row = row_one<T, LP, MASK>(a, r, logits, lstride, V, kernarg);
     if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T>(kernarg, long_row ? 1 : 0);
 }
-
-template __global__ void row_kernel<float>(const void*, int64_t, int, int, KArgs);
-template __global__ void row_kernel<uint16_t>(const void*, int64_t, int, int, KArgs);
-template __global__ void row_kernel<_Float16>(const void*, int64_t, int, int, KArgs);
 
 }  // namespace vws
