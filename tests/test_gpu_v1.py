@@ -15,7 +15,7 @@ from oracle import sampler as O
 from vllm_webgpu_amd import workloads as W
 from vllm_webgpu_amd.v1.model_runner import ROCmModelRunner
 from vllm_webgpu_amd.v1.sample.metadata import SamplingMetadata
-from vllm_webgpu_amd.v1.sample.sampler import Sampler, draw_seeds
+from vllm_webgpu_amd.v1.sample.sampler import KeyStream, Sampler, draw_seeds
 
 pytestmark = pytest.mark.gpu
 
@@ -109,7 +109,7 @@ def test_runner_steps_match_oracle(cuda, token_state):
     }
     prompts = {"g": [1, 2, 3], "k": [5, 5, 9, 4000], "p": [17], "m": [2, 3, 5, 7, 11, 13],
                "late": [100, 200]}
-    mirror = {r: torch.Generator(device=cuda).manual_seed(params[r].seed)
+    mirror = {r: KeyStream(params[r].seed)
               for r in params if params[r].seed is not None}
     outputs = {r: [] for r in params}
     active = []
@@ -129,9 +129,7 @@ def test_runner_steps_match_oracle(cuda, token_state):
         u = np.full((B, V), 0.5, np.float32)
         for i, r in enumerate(active):
             if r in mirror:
-                sd = torch.randint(-2 ** 63, 2 ** 63 - 1, (1,), dtype=torch.int64, device=cuda,
-                                   generator=mirror[r])
-                u[i] = O.philox_uniforms(sd.cpu().numpy(), V)[0]
+                u[i] = O.philox_uniforms(np.array([mirror[r].next_key()], np.int64), V)[0]
         sps = [params[r] for r in active]
         prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
                             [s.top_p for s in sps], [s.min_p for s in sps],
@@ -187,7 +185,7 @@ def test_runner_logits_processors_match_oracle(cuda):
         "allow": _sp(temperature=1.0, seed=32, allowed_token_ids=[10, 11, 12, 13, 400]),
     }
     prompts = {"bias": [4], "mint": [1], "bad": [1], "allow": [10, 11]}
-    mirror = {r: torch.Generator(device=cuda).manual_seed(params[r].seed)
+    mirror = {r: KeyStream(params[r].seed)
               for r in params if params[r].seed is not None}
     outputs = {r: [] for r in params}
     active = list(params)
@@ -202,9 +200,7 @@ def test_runner_logits_processors_match_oracle(cuda):
         u = np.full((B, V), 0.5, np.float32)
         for i, r in enumerate(active):
             if r in mirror:
-                sd = torch.randint(-2 ** 63, 2 ** 63 - 1, (1,), dtype=torch.int64, device=cuda,
-                                   generator=mirror[r])
-                u[i] = O.philox_uniforms(sd.cpu().numpy(), V)[0]
+                u[i] = O.philox_uniforms(np.array([mirror[r].next_key()], np.int64), V)[0]
         sps = [params[r] for r in active]
         prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
                             [s.top_p for s in sps], [s.min_p for s in sps],
@@ -296,3 +292,59 @@ def test_async_next_step_before_get_output(cuda):
     (tok, seen) = runs[0]
     assert seen[1][0] == [t[0] for t in tok[0]] and seen[1][1] == [2, 2]
     assert [p for _, p in seen] == [[1, 1], [2, 2], [3, 3], [4, 4]]
+
+
+@pytest.mark.parametrize("logprobs", [None, 3])
+def test_runner_structured_output_bitmask(cuda, logprobs):
+    """sample_tokens(grammar_output): the structured-output rows sample inside their bitmask
+    (without logprobs through the kernel's allowed mask; with logprobs the logits are masked
+    first, so the raw logprobs see the mask, as in vLLM-v1), the other rows are untouched."""
+    from vllm_webgpu_amd.v1.model_runner import grammar_words
+
+    V = 3000
+    model = _FakeModel(V, cuda)
+    runner = ROCmModelRunner(None, cuda, model, max_num_reqs=4, max_prompt_len=8, max_output_len=8)
+    params = {"free": _sp(temperature=0.9, top_k=40, seed=71, logprobs=logprobs),
+              "json": _sp(temperature=0.9, top_p=0.9, seed=72, logprobs=logprobs),
+              "g": _sp(temperature=0.0, logprobs=logprobs)}
+    rng = np.random.default_rng(73)
+    mirror = {r: KeyStream(params[r].seed)
+              for r in params if params[r].seed is not None}
+    active = list(params)
+    so = NS(scheduled_new_reqs=[NS(req_id=r, prompt_token_ids=[1, 2], sampling_params=params[r])
+                                for r in active], finished_req_ids=set(),
+            num_scheduled_tokens={r: 1 for r in active})
+    runner.execute_model(so)
+    W = (V + 31) // 32
+    bm = np.zeros((2, W), np.int64)
+    for i in range(2):
+        for t in rng.choice(V, 25, replace=False):
+            bm[i, t >> 5] |= 1 << (t & 31)
+    bm = (bm - (bm >= 2 ** 31) * 2 ** 32).astype(np.int32)
+    go = NS(structured_output_request_ids=["json", "g"], grammar_bitmask=bm)
+    mro = runner.sample_tokens(go)
+    words = grammar_words(go, active, V, torch.device("cpu")).numpy().view(np.uint32)
+    B = len(active)
+    u = np.full((B, V), 0.5, np.float32)
+    for i, r in enumerate(active):
+        if r in mirror:
+            u[i] = O.philox_uniforms(np.array([mirror[r].next_key()], np.int64), V)[0]
+    sps = [params[r] for r in active]
+    prm = O.make_params(B, [s.temperature for s in sps], [s.top_k for s in sps],
+                        [s.top_p for s in sps], [s.min_p for s in sps],
+                        [s.repetition_penalty for s in sps], [s.presence_penalty for s in sps],
+                        [s.frequency_penalty for s in sps])
+    x = model.history[-1].copy()
+    allowed_bits = ((words[:, :, None] >> np.arange(32, dtype=np.uint32)) & 1).reshape(B, -1)[:, :V]
+    if logprobs is None:
+        ref = O.sample(x, prm, u, allowed=words)
+    else:
+        x[allowed_bits == 0] = -np.inf
+        ref = O.sample(x, prm, u, num_logprobs=logprobs)
+    got = [t[0] for t in mro.sampled_token_ids]
+    assert got == ref["token"].tolist()
+    for i in (1, 2):
+        assert allowed_bits[i, got[i]] == 1
+    if logprobs is not None:
+        assert mro.logprobs.logprob_token_ids == ref["lp_ids"].tolist()
+        np.testing.assert_allclose(np.array(mro.logprobs.logprobs), ref["lp_vals"], rtol=1e-5, atol=1e-6)

@@ -21,7 +21,7 @@ def _runtime():
 
 @pytest.mark.skipif(_runtime() is None, reason="clang's AddressSanitizer runtime is not installed")
 def test_host_code_under_asan_and_ubsan():
-    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "vllm_webgpu_amd", "csrc"), "san"],
+    subprocess.run(["make", "-s", "-j6", "-C", os.path.join(ROOT, "vllm_webgpu_amd", "csrc"), "san"],
                    check=True)
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "_san/liboracle.so"], check=True)
     env = dict(os.environ, LD_PRELOAD=_runtime(),

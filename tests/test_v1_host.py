@@ -3,6 +3,7 @@ device-side history appends (exercised on CPU tensors), uniform draws, padding, 
 failures the sampler owes its callers (no CPU fallback, unsupported processors refused)."""
 from types import SimpleNamespace as NS
 
+import numpy as np
 import pytest
 import torch
 
@@ -238,3 +239,70 @@ def test_platform_routes_to_worker():
     import importlib
     assert getattr(importlib.import_module(mod), cls) is not None
     assert MI355XPlatform.is_pin_memory_available()
+
+
+def test_grammar_words_and_in_place_mask():
+    """vLLM-v1 GrammarOutput -> per-row allowed words in request order (rows without a grammar
+    allow everything), and the in-place -inf mask used when logprobs are requested."""
+    from vllm_webgpu_amd.v1.model_runner import apply_grammar_words, grammar_words
+    Vg = 70
+    bm = np.zeros((2, 3), np.int32)
+    bm[0] = [0b101, 0, 1 << 5]          # tokens 0, 2 and 69
+    bm[1, 0] = -1                       # tokens 0..31
+    go = NS(structured_output_request_ids=["b", "c"], grammar_bitmask=bm)
+    w = grammar_words(go, ["a", "b", "c"], Vg, torch.device("cpu"))
+    assert w[0].tolist() == [-1, -1, -1] and w[1].tolist() == bm[0].tolist()
+    assert grammar_words(NS(structured_output_request_ids={"c": 0}, grammar_bitmask=bm), ["c"], Vg,
+                         torch.device("cpu"))[0].tolist() == bm[0].tolist()
+    assert grammar_words(None, ["a"], Vg, torch.device("cpu")) is None
+    x = torch.zeros(3, Vg)
+    apply_grammar_words(x, w)
+    assert torch.isfinite(x[0]).all()
+    assert torch.isfinite(x[1]).nonzero().flatten().tolist() == [0, 2, 69]
+    assert torch.isfinite(x[2]).nonzero().flatten().tolist() == list(range(32))
+    with pytest.raises(ValueError):
+        grammar_words(NS(structured_output_request_ids=["a"], grammar_bitmask=bm[:, :2]), ["a"], Vg,
+                      torch.device("cpu"))
+
+
+def test_sampler_config_from_env(monkeypatch):
+    """The VLLM_WEBGPU_AMD_* variables in the reference's envs/config pattern: defaults,
+    parsing and validation that names the variable."""
+    from vllm_webgpu_amd import config, envs
+    for k in list(envs.environment_variables):
+        monkeypatch.delenv(k, raising=False)
+    config.reset_config()
+    c = config.get_config()
+    assert (c.token_state, c.async_output, c.coop_wait_polls, c.max_num_reqs, c.debug) == \
+        (True, False, 1 << 20, 1024, False)
+    monkeypatch.setenv("VLLM_WEBGPU_AMD_TOKEN_STATE", "0")
+    monkeypatch.setenv("VLLM_WEBGPU_AMD_ASYNC_OUTPUT", "true")
+    monkeypatch.setenv("VLLM_WEBGPU_AMD_MAX_NUM_REQS", "64")
+    config.reset_config()
+    c = config.get_config()
+    assert (c.token_state, c.async_output, c.max_num_reqs) == (False, True, 64)
+    monkeypatch.setenv("VLLM_WEBGPU_AMD_COOP_WAIT_POLLS", "-3")
+    with pytest.raises(ValueError, match="VLLM_WEBGPU_AMD_COOP_WAIT_POLLS"):
+        config.SamplerConfig.from_env()
+    monkeypatch.setenv("VLLM_WEBGPU_AMD_COOP_WAIT_POLLS", "x")
+    with pytest.raises(ValueError, match="sampler environment"):
+        config.SamplerConfig.from_env()
+    with pytest.raises(AttributeError):
+        envs.VLLM_WEBGPU_AMD_NOPE
+    config.reset_config()
+
+
+def test_key_stream_splitmix64():
+    """Seeded requests' per-step keys: SplitMix64 (Steele, Lea, Flood 2014) of the seed advanced
+    by the golden-ratio increment -- the first outputs for seed 0 are the published
+    0xe220a8397b1dcdaf, 0x6e789e6aa1b965f4, 0x06c45d188009454f -- and draw_seeds advances
+    each stream by one key per step, computing a batch's keys together."""
+    from vllm_webgpu_amd.v1.sample.sampler import KeyStream
+    k = KeyStream(0)
+    got = [k.next_key() & 0xFFFFFFFFFFFFFFFF for _ in range(3)]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    a, b = KeyStream(1234), KeyStream(1234)
+    s = draw_seeds(4, {1: a, 3: KeyStream(99)}, torch.device("cpu"))
+    assert int(s[1]) == b.next_key() and a.step == 1
+    s2 = draw_seeds(4, {1: a}, torch.device("cpu"))
+    assert int(s2[1]) == b.next_key() and int(s2[1]) != int(s[1])

@@ -1242,10 +1242,13 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     //    average (about Poisson); m = ceil(lambda + 5 sqrt(lambda) + 3) puts the seed above
     //    the k-th value (the row then takes the general path) with probability at most 1.2e-6
     //    for any lambda, and keeps about m * V / sample candidates (k = 1: the sample's
-    //    maximum, never above the k-th).
+    //    maximum, never above the k-th).  m = k is never above the k-th value: at least k lane
+    //    maxima, so at least k elements, lie at or above the m-th largest lane maximum (and the
+    //    pool's m-th largest is at most that).  So m is capped at k, which the rule exceeds when
+    //    the sample is most of the row (short rows: fewer candidates, and no 256-entry pool).
     const int sample = nbody > 0 ? min(NT * U, nbody) * VEC : 0;
     const float lam = (float)(kc - 1) * (float)sample / (float)V;
-    const int m_seed = sample > 0 ? (kc > 1 ? (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f) : 1) : 0;
+    const int m_seed = sample > 0 ? min(kc, (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f)) : 0;
     const bool seeded = sample > 0 && m_seed <= kRowWaves * kSeedPerWave;
     // m <= 64: the pool is every wave's 4 largest lane maxima, and every wave selects the m-th
     // largest of it for itself; otherwise the 16 largest of every wave, selected by wave 0

@@ -33,7 +33,7 @@ import torch
 
 from .outputs import ModelRunnerOutput
 from .sample.metadata import SamplingMetadata
-from .sample.sampler import Sampler
+from .sample.sampler import KeyStream, Sampler
 
 logger = logging.getLogger(__name__)
 
@@ -50,7 +50,7 @@ class CachedRequestState:
     req_id: str
     prompt_token_ids: list[int]
     sampling_params: Any
-    generator: torch.Generator | None
+    generator: KeyStream | None
     slot: int
     output_token_ids: list[int] = field(default_factory=list)
     # ids sampled on the device so far; counted when the step samples, so it leads the host
@@ -101,10 +101,7 @@ class InputBatch:
             raise RuntimeError(f"batch is full ({self.max_num_reqs} requests)")
         slot = self._free.pop()
         seed = _param(sampling_params, "seed", None)
-        gen = None
-        if seed is not None:
-            gen = torch.Generator(device=self.device)
-            gen.manual_seed(int(seed))
+        gen = KeyStream(int(seed)) if seed is not None else None
         self.requests[req_id] = CachedRequestState(req_id, list(prompt_token_ids),
                                                    sampling_params, gen, slot)
         row = torch.full((self.prompt_ids.shape[1],), self.vocab_size, dtype=torch.int32)
@@ -261,6 +258,40 @@ class InputBatch:
             ops.token_state_update(self.token_state, sampled, rows=slots.to(torch.int32))
 
 
+def grammar_words(grammar_output: Any, req_ids: list[str], vocab_size: int,
+                  device: torch.device) -> torch.Tensor | None:
+    """int32 [B, ceil(V/32)] allowed-token words of a step's structured-output rows, rows in
+    ``req_ids`` order (bit t & 31 of word t >> 5 set = token t allowed; rows without a grammar
+    allow everything), from vLLM-v1's ``GrammarOutput``: ``grammar_bitmask`` int32
+    [n, ceil(V/32)] and ``structured_output_request_ids`` (a list of request ids, or a dict of
+    request id -> bitmask row).  None when the step has no bitmask."""
+    bm = getattr(grammar_output, "grammar_bitmask", None) if grammar_output is not None else None
+    if bm is None:
+        return None
+    ids = getattr(grammar_output, "structured_output_request_ids", None) or []
+    row_of = dict(ids) if isinstance(ids, dict) else {r: i for i, r in enumerate(ids)}
+    bm = torch.as_tensor(bm, dtype=torch.int32)
+    W = (vocab_size + 31) // 32
+    if bm.dim() != 2 or bm.shape[1] < W:
+        raise ValueError(f"grammar_bitmask must be [n, >= {W}] int32 words (got {tuple(bm.shape)})")
+    words = torch.full((len(req_ids), W), -1, dtype=torch.int32)
+    for i, r in enumerate(req_ids):
+        j = row_of.get(r)
+        if j is not None:
+            words[i] = bm[j, :W]
+    return words.to(device, non_blocking=True)
+
+
+def apply_grammar_words(logits: torch.Tensor, words: torch.Tensor) -> torch.Tensor:
+    """Sets the logits of tokens outside ``words`` to -inf, in place (vLLM-v1 applies the
+    grammar bitmask to the logits before its sampler, so raw logprobs see the mask)."""
+    B, V = logits.shape
+    shifts = torch.arange(32, dtype=torch.int32, device=logits.device)
+    bits = (words.unsqueeze(-1) >> shifts) & 1
+    allowed = bits.reshape(B, -1)[:, :V].bool()
+    return logits.masked_fill_(~allowed, float("-inf"))
+
+
 class AsyncModelRunnerOutput:
     """A step's output whose device-to-host copy is in flight (vLLM-v1's async output)."""
 
@@ -389,16 +420,24 @@ class ROCmModelRunner:
         inputs, penalty histories and min-tokens counts come from the device-side state.
         Bad-words matching reads the host copies of the generated ids, which ``get_output()``
         appends, so a batch that uses bad words must call it before the next step samples
-        (sampling raises otherwise).
+        (sampling raises otherwise).  ``grammar_output`` (vLLM-v1's ``GrammarOutput``) restricts
+        its structured-output rows to their bitmask's tokens.
         """
         if self._last_logits is None:
             return None
-        if grammar_output is not None and getattr(grammar_output, "grammar_bitmask", None) is not None:
-            raise NotImplementedError("structured-output bitmasks are not applied by the device sampler")
         req_ids, logits = self._last_req_ids, self._last_logits
         self._last_logits = None
         batch = self.input_batch
         md = batch.make_sampling_metadata(req_ids)
+        # structured output: without logprobs the grammar bitmask joins the kernel's allowed
+        # mask (the result is the same as masking the logits); with logprobs the logits are
+        # masked first, as vLLM-v1 does, so that the raw logprobs see the mask
+        words = grammar_words(grammar_output, req_ids, logits.shape[1], logits.device)
+        if words is not None:
+            if md.max_num_logprobs is None:
+                md.allowed_words = words
+            else:
+                logits = apply_grammar_words(logits.clone() if not logits.is_contiguous() else logits, words)
         out = self.sampler(logits, md)
         sampled = out.sampled_token_ids[:, 0]
         batch.append_sampled(req_ids, sampled)

@@ -27,6 +27,9 @@ Conventions the kernels rely on:
   count in the output), with ``token_state_rows`` int32 ``[B]`` giving each row's table row.
   When set, the penalties read it instead of ``prompt_token_ids`` / ``output_token_ids``: the
   prompt mask and output bin counts vLLM-v1 rebuilds every step, kept up to date instead.
+* ``allowed_words`` (extension): int32 ``[B, ceil(V/32)]`` allowed-token bit words (bit set =
+  allowed), ANDed with ``allowed_token_ids_mask``; the runner puts a step's structured-output
+  grammar bitmask here.
 """
 from __future__ import annotations
 
@@ -59,3 +62,4 @@ class SamplingMetadata:
     logit_bias: list[dict[int, float] | None] | None = None
     token_state: torch.Tensor | None = None
     token_state_rows: torch.Tensor | None = None
+    allowed_words: torch.Tensor | None = None

@@ -21,6 +21,7 @@ There is no host fallback: without the HIP library, or for logits that are not o
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from ... import ops
@@ -28,18 +29,66 @@ from ..outputs import LogprobsTensors, SamplerOutput
 from .metadata import SamplingMetadata
 
 _SEED_LO, _SEED_HI = -2 ** 63, 2 ** 63 - 1
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
 
 
-def draw_seeds(B: int, generators: dict[int, torch.Generator],
-               device: torch.device) -> torch.Tensor:
+def splitmix64(x: np.ndarray) -> np.ndarray:
+    """SplitMix64's output function (Steele, Lea and Flood, OOPSLA 2014) on uint64 states."""
+    with np.errstate(over="ignore"):
+        z = x.astype(np.uint64)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+class KeyStream:
+    """A seeded request's per-step race keys: step n's key is SplitMix64 of
+    ``seed + (n + 1) * 0x9E3779B97F4A7C15``, so the request draws the same keys, and samples
+    the same tokens, whenever it runs again with its seed.  Stands in for a ``torch.Generator``
+    in ``SamplingMetadata.generators`` so that a whole batch's keys come from one host-side
+    computation (``draw_seeds``)."""
+
+    _GOLDEN = 0x9E3779B97F4A7C15
+
+    def __init__(self, seed: int) -> None:
+        self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+        self.step = 0
+
+    @staticmethod
+    def keys(seeds: np.ndarray, steps: np.ndarray) -> np.ndarray:
+        """int64 keys of the given (seed, step) pairs."""
+        with np.errstate(over="ignore"):
+            st = seeds.astype(np.uint64) + (steps.astype(np.uint64) + np.uint64(1)) * np.uint64(KeyStream._GOLDEN)
+        return splitmix64(st).view(np.int64)
+
+    def next_key(self) -> int:
+        k = int(self.keys(np.array([self.seed], np.uint64), np.array([self.step], np.uint64))[0])
+        self.step += 1
+        return k
+
+
+def draw_seeds(B: int, generators: dict, device: torch.device) -> torch.Tensor:
     """int64 ``[B]`` keys of the race's generated uniforms, one fresh draw per row and step: row
     ``i`` draws from ``generators[i]`` if present (a seeded request samples the same tokens
-    again), the others from torch's default generator."""
-    seeds = torch.randint(_SEED_LO, _SEED_HI, (B,), dtype=torch.int64, device=device)
+    again), the others from torch's default CPU generator.  ``KeyStream`` entries (the
+    persistent batch's seeded requests) are computed together on the host; a ``torch.Generator``
+    entry draws from its own stream.  One host-to-device copy."""
+    keys = torch.randint(_SEED_LO, _SEED_HI, (B,), dtype=torch.int64)
+    ks = [(i, g) for i, g in generators.items() if isinstance(g, KeyStream)]
+    if ks:
+        rows = np.array([i for i, _ in ks], np.int64)
+        seeds = np.array([g.seed for _, g in ks], np.uint64)
+        steps = np.array([g.step for _, g in ks], np.uint64)
+        keys[torch.from_numpy(rows)] = torch.from_numpy(KeyStream.keys(seeds, steps))
+        for _, g in ks:
+            g.step += 1
     for i, g in generators.items():
-        seeds[i] = torch.randint(_SEED_LO, _SEED_HI, (1,), dtype=torch.int64, device=device,
-                                 generator=g)[0]
-    return seeds
+        if not isinstance(g, KeyStream):
+            keys[i] = torch.randint(_SEED_LO, _SEED_HI, (1,), dtype=torch.int64,
+                                    device=g.device, generator=g)[0].cpu()
+    if device.type == "cuda":
+        keys = keys.pin_memory()
+    return keys.to(device, non_blocking=True)
 
 
 def pad_output_ids(output_token_ids: list[list[int]], vocab_size: int,
@@ -150,6 +199,10 @@ class Sampler:
         processors = {}
         if m.allowed_token_ids_mask is not None:
             processors["allowed_mask"] = ops.pack_allowed(~m.allowed_token_ids_mask.to(dev, torch.bool))
+        if m.allowed_words is not None:
+            w = m.allowed_words.to(dev, torch.int32)
+            processors["allowed_mask"] = (w if "allowed_mask" not in processors
+                                          else processors["allowed_mask"] & w)
         adj = processor_lists(m, B, V)
         if adj is not None:
             ids, vals = adj

@@ -14,6 +14,7 @@ from typing import Any
 
 import torch
 
+from ..config import get_config
 from .model_runner import ROCmModelRunner
 
 logger = logging.getLogger(__name__)
@@ -38,8 +39,14 @@ class ROCmWorker:
             raise RuntimeError("no ROCm device is visible to this process")
         self.device = torch.device(f"cuda:{self.local_rank}")
         torch.cuda.set_device(self.device)
-        self.model_runner = ROCmModelRunner(self.vllm_config, self.device, self._model,
-                                            **self._runner_kwargs)
+        # the sampler's settings from the environment (VLLM_WEBGPU_AMD_*); explicit runner
+        # arguments take precedence
+        cfg = get_config()
+        cfg.apply()
+        kwargs = dict(token_state=cfg.token_state, max_num_reqs=cfg.max_num_reqs)
+        kwargs.update(self._runner_kwargs)
+        self._async_output = cfg.async_output
+        self.model_runner = ROCmModelRunner(self.vllm_config, self.device, self._model, **kwargs)
 
     def load_model(self) -> None:
         self.model_runner.load_model()
@@ -48,7 +55,8 @@ class ROCmWorker:
         return self.model_runner.execute_model(scheduler_output)
 
     def sample_tokens(self, grammar_output: Any) -> Any:
-        return self.model_runner.sample_tokens(grammar_output)
+        return self.model_runner.sample_tokens(grammar_output,
+                                               async_output=getattr(self, "_async_output", False))
 
     def get_model(self) -> Any:
         return self.model_runner.model
