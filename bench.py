@@ -194,10 +194,11 @@ def token_state_timing(lib_mod, L, W, w, sets, T, K, P, MP, R, PR, FR, out, flag
 
 def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, stream,
                    steps: int, warmup: int, num_logprobs=None, parity_rows: int = 16,
-                   allowed=None, hist=None) -> dict:
+                   allowed=None, hist=None, table: bool = False) -> dict:
     """The launch with one thing changed (raw logprobs requested, an allowed mask [B, V] bool,
-    or a [B, H] output history replacing the workload's), timed with kernel-stamped events and
-    checked against the oracle on its first rows."""
+    or a [B, H] output history replacing the workload's: as padded id lists, or with `table` as
+    the token-state table and its bitmap the runner keeps, built by vws_token_state_update),
+    timed with kernel-stamped events and checked against the oracle on its first rows."""
     import torch
 
     from oracle import sampler as O  # checker only
@@ -211,6 +212,15 @@ def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkep
         words_d = torch.from_numpy(words.view(np.int32)).to(out.device)
     if hist is not None:
         hist_d = torch.from_numpy(hist).to(out.device)
+    state = bits = None
+    if table:
+        from vllm_webgpu_amd import ops
+
+        state = torch.zeros((B, V), dtype=torch.int32, device=out.device)
+        bits = torch.zeros((B, (V + 31) // 32), dtype=torch.int32, device=out.device)
+        rows = torch.arange(B, dtype=torch.int32, device=out.device).repeat_interleave(hist.shape[1])
+        ops.token_state_update(state, hist_d.reshape(-1), rows=rows, bits=bits)
+        torch.cuda.synchronize()
     out_ids = w.output_ids if hist is None else hist
     lp = None
     if num_logprobs is not None:
@@ -219,10 +229,20 @@ def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkep
               torch.empty(B, dtype=torch.int32, device=out.device))
     argv, keep = [], []
     for i, (lg, u, h) in enumerate(sets):
-        if hist_d is not None:
+        trows = None
+        if table:
+            # the rotated set's row r has history row (r - i) mod B: the table's row map
+            trows = torch.remainder(torch.arange(B, device=out.device) - i, B).to(torch.int32)
+            keep.append(trows)
+            h = None
+        elif hist_d is not None:
             h = torch.roll(hist_d, shifts=i, dims=0).contiguous() if i else hist_d
             keep.append(h)
         a = build_args(lib_mod, lg, T, K, P, MP, R, PR, FR, h, u, out, flags, nkept, ws, lp)
+        if table:
+            a.token_state, a.token_state_row_stride = state.data_ptr(), state.stride(0)
+            a.token_state_rows = trows.data_ptr()
+            a.token_state_bits, a.token_state_bits_stride = bits.data_ptr(), bits.stride(0)
         if words is not None:
             a.allowed_mask, a.allowed_row_stride = words_d.data_ptr(), words_d.stride(0)
         a.stream = stream.cuda_stream
@@ -519,9 +539,16 @@ def main():
         PR.fill_(0.5)
         FR.fill_(0.3)
         ws5 = ops.workspace(L.vws_sample_workspace_size(B, V, 512), dev)
-        variants = {"c3_penalties": variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out,
-                                                   flags, nkept, ws5, stream, vsteps, vwarm,
-                                                   num_logprobs=w.num_logprobs, hist=hist5)}
+        variants = {
+            # the history as the runner keeps it: the token-state table and its bitmap
+            "c3_penalties_table": variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out,
+                                                 flags, nkept, ws5, stream, vsteps, vwarm,
+                                                 num_logprobs=w.num_logprobs, hist=hist5,
+                                                 table=True),
+            # the same history as padded id lists (the multi-pass path serves such rows)
+            "c3_penalties": variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out,
+                                           flags, nkept, ws5, stream, vsteps, vwarm,
+                                           num_logprobs=w.num_logprobs, hist=hist5)}
         w.repetition[:], w.presence[:], w.frequency[:] = 1.0, 0.0, 0.0
         R.fill_(1.0)
         PR.fill_(0.0)

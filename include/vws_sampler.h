@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 6
+#define VWS_ABI_VERSION 7
 
 /* status codes */
 #define VWS_OK 0
@@ -117,6 +117,14 @@ typedef struct vws_sample_args {
     const uint32_t* token_state;
     int64_t token_state_row_stride;
     const int32_t* token_state_rows;
+    /* Optional with token_state: uint32 [rows, >= ceil(V/32)] (row stride in words, rows as
+     * for the table), bit (t & 31) of word t >> 5 set when word t of the table row is non-zero;
+     * vws_token_state_update keeps it with the table.  With it, rows whose survivors top-p
+     * alone cuts (top-k off) keep the single-pass top-p path with their penalties when
+     * V <= 196608 (the bitmap is staged in LDS); without it such rows take the multi-pass
+     * path.  NULL otherwise. */
+    const uint32_t* token_state_bits;
+    int64_t token_state_bits_stride;
 
     /* vLLM-v1 logits processors, applied before the penalties (raw logprobs never see them).
      * allowed_mask: uint32 [B, ceil(V/32)] words with the given row stride, bit (t & 31) of word
@@ -208,13 +216,15 @@ int vws_sample_noalloc(const vws_sample_args* args);
  * i < n with 0 <= tokens[i] < vocab: VWS_STATE_OUTPUT adds one output occurrence to word
  * tokens[i] of table row rows[i], VWS_STATE_PROMPT sets that word's prompt flag (atomics: ids and
  * rows may repeat).  rows and tokens are device int32 [n]; rows NULL sends every id to table
- * row `row`.  Ids outside [0, vocab) and negative rows are padding and skipped.  A row is
- * cleared by zeroing its words (the caller's memory). */
+ * row `row`.  Ids outside [0, vocab) and negative rows are padding and skipped.  `bits` (or
+ * NULL): the table's bitmap of non-zero words (vws_sample_args::token_state_bits, row stride
+ * bits_stride >= ceil(vocab/32) words), whose bit of every id updated is set.  A row is cleared
+ * by zeroing its words and its bitmap row (the caller's memory). */
 #define VWS_STATE_OUTPUT 0
 #define VWS_STATE_PROMPT 1
-int vws_token_state_update(uint32_t* state, int64_t row_stride, int32_t vocab, int32_t n,
-                           const int32_t* rows, int32_t row, const int32_t* tokens, int32_t kind,
-                           void* stream);
+int vws_token_state_update(uint32_t* state, int64_t row_stride, uint32_t* bits,
+                           int64_t bits_stride, int32_t vocab, int32_t n, const int32_t* rows,
+                           int32_t row, const int32_t* tokens, int32_t kind, void* stream);
 
 /* Greedy argmax of each row (lowest index on ties; NaN never selected). */
 int vws_argmax(const void* logits, int32_t dtype, int32_t batch, int32_t vocab,

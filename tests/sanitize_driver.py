@@ -53,7 +53,10 @@ def capi():
            dict(allowed_mask=FAKE, allowed_row_stride=31), dict(logit_softcap=-1.0),
            dict(logit_softcap=float("nan")), dict(logit_softcap=float("inf")),
            dict(token_state=FAKE, token_state_row_stride=999),
-           dict(hist, token_state=FAKE, token_state_row_stride=1000)]
+           dict(hist, token_state=FAKE, token_state_row_stride=1000),
+           dict(token_state=FAKE, token_state_row_stride=1000, token_state_bits=FAKE,
+                token_state_bits_stride=31),
+           dict(token_state_bits=FAKE, token_state_bits_stride=32)]
     for over in bad:
         a = args(**over)
         st = L.vws_validate_sample_args(ctypes.byref(a))
@@ -64,6 +67,8 @@ def capi():
     assert L.vws_validate_sample_args(None) == _lib.ERR_INVALID_ARGUMENT
     for over in (dict(), dict(workspace=None, workspace_bytes=0),
                  dict(token_state=FAKE, token_state_row_stride=1000, workspace=None),
+                 dict(token_state=FAKE, token_state_row_stride=1000, token_state_bits=FAKE,
+                      token_state_bits_stride=32, workspace=None),
                  dict(hist, workspace_bytes=L.vws_sample_workspace_size(4, 1000, 8)),
                  dict(temperature=None, uniforms=None), dict(uniforms=None, rng_seeds=FAKE)):
         assert L.vws_validate_sample_args(ctypes.byref(args(**over))) == 0, over
@@ -87,12 +92,13 @@ def capi():
     assert L.vws_apply_penalties(FAKE, 4, 1000, 1000, None, None, None, FAKE, 8, 8, None, None,
                                  0, 0, None, None, 0, None) == _lib.ERR_WORKSPACE_TOO_SMALL
     up = L.vws_token_state_update
-    assert up(None, 1000, 1000, 1, None, 0, FAKE, 0, None) != 0
-    assert up(FAKE, 999, 1000, 1, None, 0, FAKE, 0, None) != 0
-    assert up(FAKE, 1000, 1000, 1, None, 0, FAKE, 5, None) != 0
-    assert up(FAKE, 1000, 1000, 1, None, -1, FAKE, 0, None) != 0
-    assert up(FAKE, 1000, 1000, -1, None, 0, FAKE, 0, None) != 0
-    assert up(FAKE, 1000, 1000, 0, None, 0, None, 0, None) == 0
+    assert up(None, 1000, None, 0, 1000, 1, None, 0, FAKE, 0, None) != 0
+    assert up(FAKE, 999, None, 0, 1000, 1, None, 0, FAKE, 0, None) != 0
+    assert up(FAKE, 1000, FAKE, 31, 1000, 1, None, 0, FAKE, 0, None) != 0
+    assert up(FAKE, 1000, None, 0, 1000, 1, None, 0, FAKE, 5, None) != 0
+    assert up(FAKE, 1000, None, 0, 1000, 1, None, -1, FAKE, 0, None) != 0
+    assert up(FAKE, 1000, None, 0, 1000, -1, None, 0, FAKE, 0, None) != 0
+    assert up(FAKE, 1000, FAKE, 32, 1000, 0, None, 0, None, 0, None) == 0
     assert L.vws_math_selftest(9, 0, 1, FAKE, None) != 0
     assert L.vws_math_selftest(0, 5, 1, FAKE, None) != 0
     prev = L.vws_set_coop_wait_polls(3)

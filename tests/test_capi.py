@@ -138,6 +138,10 @@ def test_valid_args_pass(L):
      "token_state_row_stride"),
     (dict(HIST, token_state=FAKE, token_state_row_stride=1000), _lib.ERR_INVALID_ARGUMENT,
      "token_state replaces"),
+    (dict(token_state=FAKE, token_state_row_stride=1000, token_state_bits=FAKE,
+          token_state_bits_stride=31), _lib.ERR_INVALID_ARGUMENT, "token_state_bits_stride"),
+    (dict(token_state_bits=FAKE, token_state_bits_stride=32), _lib.ERR_INVALID_ARGUMENT,
+     "without token_state"),
 ])
 def test_invalid_args_rejected(L, over, code, msg):
     assert _status(L, _args(L, **over)) == code
@@ -214,13 +218,17 @@ def test_token_state_args(L):
     and its maintenance entry point checks its arguments on the host."""
     assert _status(L, _args(L, token_state=FAKE, token_state_row_stride=1000, workspace=None,
                             workspace_bytes=0)) == _lib.OK
+    assert _status(L, _args(L, token_state=FAKE, token_state_row_stride=1000, token_state_bits=FAKE,
+                            token_state_bits_stride=32, workspace=None, workspace_bytes=0)) == _lib.OK
     up = L.vws_token_state_update
-    assert up(None, 1000, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    assert up(FAKE, 999, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(None, 1000, None, 0, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 999, None, 0, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
     assert "row_stride" in _lib.last_error()
-    assert up(FAKE, 1000, 1000, 1, None, 0, FAKE, 2, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 1000, FAKE, 31, 1000, 1, None, 0, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "bits_stride" in _lib.last_error()
+    assert up(FAKE, 1000, None, 0, 1000, 1, None, 0, FAKE, 2, None) == _lib.ERR_INVALID_ARGUMENT
     assert "kind" in _lib.last_error()
-    assert up(FAKE, 1000, 1000, 1, None, -1, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    assert up(FAKE, 1000, 1000, 1, None, 0, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    assert up(FAKE, 1000, 0, 1, None, 0, FAKE, 0, None) == _lib.ERR_LIMIT
-    assert up(FAKE, 1000, 1000, 0, None, 0, None, 0, None) == _lib.OK   # nothing to do
+    assert up(FAKE, 1000, None, 0, 1000, 1, None, -1, FAKE, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 1000, None, 0, 1000, 1, None, 0, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert up(FAKE, 1000, None, 0, 0, 1, None, 0, FAKE, 0, None) == _lib.ERR_LIMIT
+    assert up(FAKE, 1000, FAKE, 32, 1000, 0, None, 0, None, 0, None) == _lib.OK   # nothing to do

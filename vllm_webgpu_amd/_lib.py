@@ -14,7 +14,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2
@@ -72,6 +72,7 @@ class SampleArgs(ctypes.Structure):
         ("prompt_ids", _P), ("prompt_row_stride", _I64), ("prompt_width", _I32), ("prompt_lens", _P),
         ("output_ids", _P), ("output_row_stride", _I64), ("output_width", _I32), ("output_lens", _P),
         ("token_state", _P), ("token_state_row_stride", _I64), ("token_state_rows", _P),
+        ("token_state_bits", _P), ("token_state_bits_stride", _I64),
         ("allowed_mask", _P), ("allowed_row_stride", _I64),
         ("adjust_ids", _P), ("adjust_vals", _P), ("adjust_row_stride", _I64), ("adjust_width", _I32),
         ("adjust_lens", _P),
@@ -129,7 +130,7 @@ def _declare(L):
     L.vws_set_coop_wait_polls.restype = _I32
     L.vws_set_coop_wait_polls.argtypes = [_I32]
     L.vws_token_state_update.restype = ctypes.c_int
-    L.vws_token_state_update.argtypes = [_P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P]
+    L.vws_token_state_update.argtypes = [_P, _I64, _P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P]
 
 
 def lib() -> ctypes.CDLL:

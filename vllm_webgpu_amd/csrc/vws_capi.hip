@@ -23,7 +23,8 @@ __global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, flo
 __global__ void penalties_kernel(KArgs, float*);
 __global__ void selftest_kernel(int, uint32_t, uint32_t, unsigned long long*);
 __global__ void fill_u32_kernel(uint32_t*, size_t, uint32_t);
-__global__ void token_state_kernel(uint32_t*, int64_t, int, int, const int32_t*, int, const int32_t*, int);
+__global__ void token_state_kernel(uint32_t*, int64_t, uint32_t*, int64_t, int, int, const int32_t*, int,
+                                   const int32_t*, int);
 }  // namespace vws
 
 using namespace vws;
@@ -240,6 +241,10 @@ int validate_sample(const vws_sample_args* a) {
             return fail(VWS_ERR_INVALID_ARGUMENT, "token_state replaces prompt_ids/output_ids: pass one or the other");
         if (a->token_state_row_stride < a->vocab)
             return fail(VWS_ERR_INVALID_ARGUMENT, "token_state_row_stride < vocab");
+        if (a->token_state_bits && a->token_state_bits_stride < (int64_t)(a->vocab + 31) / 32)
+            return fail(VWS_ERR_INVALID_ARGUMENT, "token_state_bits_stride < ceil(vocab / 32) words");
+    } else if (a->token_state_bits) {
+        return fail(VWS_ERR_INVALID_ARGUMENT, "token_state_bits is set without token_state");
     }
     if (!(a->logit_softcap >= 0.0f) || a->logit_softcap == __builtin_inff())
         return fail(VWS_ERR_INVALID_ARGUMENT, "logit_softcap must be finite and >= 0 (got %g)", (double)a->logit_softcap);
@@ -339,6 +344,8 @@ int vws_sample(const vws_sample_args* a) {
     k.tstate = a->token_state;
     k.tstride = a->token_state_row_stride;
     k.trows = a->token_state_rows;
+    k.tbits = a->token_state ? a->token_state_bits : nullptr;
+    k.tbstride = a->token_state_bits_stride;
     k.allowed = a->allowed_mask;
     k.astride = a->allowed_row_stride;
     k.adj_ids = a->adjust_ids;
@@ -421,13 +428,15 @@ int vws_sample_noalloc(const vws_sample_args* a) {
     return vws_sample(&b);
 }
 
-int vws_token_state_update(uint32_t* state, int64_t row_stride, int32_t vocab, int32_t n,
-                           const int32_t* rows, int32_t row, const int32_t* tokens, int32_t kind,
-                           void* stream) {
+int vws_token_state_update(uint32_t* state, int64_t row_stride, uint32_t* bits,
+                           int64_t bits_stride, int32_t vocab, int32_t n, const int32_t* rows,
+                           int32_t row, const int32_t* tokens, int32_t kind, void* stream) {
     if (!state) return fail(VWS_ERR_INVALID_ARGUMENT, "state is NULL");
     if (vocab < 1 || vocab > VWS_MAX_VOCAB)
         return fail(VWS_ERR_LIMIT, "vocab must be in [1, %d] (got %d)", VWS_MAX_VOCAB, vocab);
     if (row_stride < vocab) return fail(VWS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+    if (bits && bits_stride < (vocab + 31) / 32)
+        return fail(VWS_ERR_INVALID_ARGUMENT, "bits_stride %lld < ceil(vocab / 32) = %d", (long long)bits_stride, (vocab + 31) / 32);
     if (n < 0) return fail(VWS_ERR_INVALID_ARGUMENT, "n must be >= 0 (got %d)", n);
     if (kind != VWS_STATE_OUTPUT && kind != VWS_STATE_PROMPT)
         return fail(VWS_ERR_INVALID_ARGUMENT, "kind must be VWS_STATE_OUTPUT or VWS_STATE_PROMPT (got %d)", kind);
@@ -435,7 +444,7 @@ int vws_token_state_update(uint32_t* state, int64_t row_stride, int32_t vocab, i
     if (!tokens) return fail(VWS_ERR_INVALID_ARGUMENT, "tokens is NULL");
     if (!rows && row < 0) return fail(VWS_ERR_INVALID_ARGUMENT, "row must be >= 0 when rows is NULL (got %d)", row);
     launch(VWS_KERNEL_OTHER, token_state_kernel, dim3((n + 255) / 256), dim3(256), (hipStream_t)stream,
-           state, row_stride, (int)vocab, (int)n, rows, (int)row, tokens, (int)kind);
+           state, row_stride, bits, bits_stride, (int)vocab, (int)n, rows, (int)row, tokens, (int)kind);
     if (int st = check_launch("vws_token_state_update")) return st;
     return ok();
 }

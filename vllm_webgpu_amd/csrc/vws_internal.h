@@ -107,6 +107,8 @@ struct KArgs {
     const uint32_t* tstate;
     int64_t tstride;
     const int32_t* trows;
+    const uint32_t* tbits;     // bitmap of the table's non-zero words (same rows), or null
+    int64_t tbstride;
     const uint32_t* allowed;   // [B, astride] words, bit set = token allowed (or null)
     int64_t astride;
     const int32_t* adj_ids;    // [B, adjstride] sparse processor list (or null)

@@ -240,8 +240,9 @@ __global__ void fill_u32_kernel(uint32_t* p, size_t n, uint32_t v) {
 
 // vws_token_state_update: one id per thread, counted (output) or flagged (prompt) in its row's
 // word with a vector atomic (ids and rows may repeat within a call).
-__global__ void token_state_kernel(uint32_t* st, int64_t stride, int V, int n, const int32_t* rows,
-                                   int row, const int32_t* tok, int kind) {
+__global__ void token_state_kernel(uint32_t* st, int64_t stride, uint32_t* bits, int64_t bstride,
+                                   int V, int n, const int32_t* rows, int row, const int32_t* tok,
+                                   int kind) {
     const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= n) return;
     const int t = tok[i];
@@ -250,6 +251,7 @@ __global__ void token_state_kernel(uint32_t* st, int64_t stride, int V, int n, c
     uint32_t* w = st + (size_t)rr * (size_t)stride + (uint32_t)t;
     if (kind == VWS_STATE_OUTPUT) atomicAdd(w, 1u);
     else atomicOr(w, 0x80000000u);
+    if (bits) atomicOr(bits + (size_t)rr * (size_t)bstride + ((uint32_t)t >> 5), 1u << (t & 31));
 }
 
 template __global__ void argmax_kernel<float>(const float*, int64_t, int, int32_t*);

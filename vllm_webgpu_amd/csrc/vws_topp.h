@@ -23,8 +23,12 @@
 //   * the race runs over the kept candidates (uniforms read at their positions only), and raw
 //     logprobs come from the candidates (top-L, rank) and the sums (log-sum-exp); a sampled
 //     token below the candidates is ranked by one more pass.
-// Rows with penalties, logits processors, an allowed mask or the soft cap, rows whose buffers
-// overflow (ties) and the rare rows listed under VWS_FALLBACK_* take the multi-pass path
+// Rows with penalties from a token-state table that comes with its bitmap of non-zero words
+// stage that bitmap in LDS and buffer every history token whatever its value, so that nothing
+// outside the buffers is penalised (the sums see raw values, which are then the processed ones);
+// the finish gives the buffered history tokens their processed values from their words.  Rows
+// with penalties from id lists, logits processors, an allowed mask or the soft cap, rows whose
+// buffers overflow (ties) and the rare rows listed under VWS_FALLBACK_* take the multi-pass path
 // instead; nothing is written for them here.
 #pragma once
 
@@ -44,6 +48,12 @@ constexpr int kTpRankCap = 512;           // up to this many, ranked without sor
 constexpr int kTpRankSerial = 64;         // up to this many, one thread ranks each member
 constexpr int kTpLpCap = 256;             // candidates gathered for the top-L logprobs
 constexpr float kLog2e = 0x1.715476p+0f;  // log2(e) rounded to fp32
+constexpr int kTpHistMaxV = 196608;       // history rows: V up to the LDS bitmap's bits
+constexpr int kTpHistWords = kTpHistMaxV / 32 + 2;  // (two words of padding for 64-bit windows)
+// Index-word mark of a buffered history token (history rows only: their indices are below 2^18,
+// so bit 18 is free; other rows use it for the index).
+constexpr uint32_t kTpHist = 1u << 18;
+constexpr int kTpRawCap = 512;            // history tokens at or above the threshold by raw value
 
 // Why a row left the single-pass top-p path (recorded in bits 16-23 of its result flags, which
 // are diagnostic like VWS_FLAG_GENERAL_PATH).
@@ -82,13 +92,14 @@ struct TopPSmem {
     uint32_t ck[kTpWaves][kTpSlots];
     int32_t ci[kTpWaves][kTpSlots];
     union {
-        uint32_t rhist[kTpWaves][256];    // stream: per-wave radix-select scratch
+        uint32_t hb[kTpHistWords];        // stream of a history row: bit t = token t's word is non-zero
         struct {
             uint64_t hmass[kTpBuckets];   // finish: exact masses of the surviving candidates
             uint32_t hcnt[kTpBuckets];    // and the number of candidates per bucket (top-L logprobs)
         } h;
     };
     union {
+        uint32_t rhist[kTpWaves][256];    // stream: per-wave radix-select scratch
         struct {
             uint64_t key[kTpGather];      // boundary bucket: key(y) << 32 | index
         } g;
@@ -109,11 +120,26 @@ struct TopPSmem {
     float wZ[kTpWaves];                   // sum of |z| * term (error bound)
     uint32_t wTau[kTpWaves];              // final threshold key
     uint32_t wCnt[kTpWaves];              // buffered entries
-    uint32_t wMax[kTpWaves];              // largest buffered key
+    uint32_t wMax[kTpWaves];              // largest buffered key (raw values)
+    uint32_t wMaxP[kTpWaves];             // history rows: largest processed key
+    float wS0h[kTpWaves];                 // history rows: their history tokens' raw normaliser terms
+    // history rows with raw logprobs: the history tokens at or above the threshold by raw value
+    // (their buffered entries hold processed values): raw keys and indices
+    uint32_t rl_key[kTpRawCap];
+    int32_t rl_idx[kTpRawCap];
+    uint32_t rl_n;
     // finish
     uint64_t red[kTpWaves][4];            // per-wave records of the finish's reductions
     double redd[kTpWaves];
     float anchor;                         // the row's anchor a
+    // totals of the finish kept here rather than in registers across it: the candidates' mass
+    // (updated by an exact pass), the number of survivors buffered below the threshold, the
+    // buffered part of the raw log-sum-exp, the raw maximum
+    uint64_t tot_wc, tot_nxs;
+    double tot_s0b;
+    float xr;
+    // the wide race pass's results (wide rows): best, second, kept, last (RowRace fields)
+    uint64_t wrace[4];
     uint32_t status;                      // bit 0: buffer overflow, bit 1: non-finite sum
     uint32_t bc[16];
     uint64_t bc64[16];
@@ -135,11 +161,13 @@ struct TpDrop {
 };
 
 // Out of line (compaction is rare); defined next to the LDS it works on.
-__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw);
+__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw, int hist);
 
 // Whether the single-pass top-p path may serve the row.
 __device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
-    if (p.need_hash || p.has_hist || a.allowed || a.softcap > 0.0f) return false;
+    if (p.need_hash || a.allowed || a.softcap > 0.0f) return false;
+    // penalties: from the token-state table with its bitmap (need_hash covers the lists)
+    if (p.has_hist && !(p.tab && a.tbits && a.V <= kTpHistMaxV)) return false;
     if (p.greedy) return a.L >= 0;
     const bool topk_off = p.k <= 0 || p.k >= a.V;
     return topk_off && p.top_p > 0.0f && p.top_p < 1.0f;
@@ -192,15 +220,15 @@ struct TpBuf {
         }
     }
     // Stores the candidates of one vector of every lane (elements v[j] >= tauf of a vector in
-    // the row, okv; first index i0; bal[j] the wave's ballot of element j's test), with one
-    // capacity check for the whole vector: every lane writes, without branches, a candidate into
-    // its slot (placed by mbcnt) and anything else into its spare slot past the capacity.
-    // Wave-uniform call.  A full buffer marks the row for the multi-pass path (the stream
-    // compacts every half iteration, from kTpSoft entries on, so this takes more than
-    // kTpCapW - kTpSoft candidates in half an iteration of one wave).
+    // the row, okv, and history tokens: bit j of hb; first index i0; bal[j] the wave's ballot of
+    // element j's test), with one capacity check for the whole vector: every lane writes,
+    // without branches, a candidate into its slot (placed by mbcnt) and anything else into its
+    // spare slot past the capacity.  Wave-uniform call.  A full buffer marks the row for the
+    // multi-pass path (the stream compacts every half iteration, from kTpSoft entries on, so
+    // this takes more than kTpCapW - kTpSoft candidates in half an iteration of one wave).
     template <int VEC>
     __device__ __forceinline__ void append_vec(TopPSmem& sm, const float* v, const uint64_t* bal,
-                                               bool okv, int i0) {
+                                               bool okv, int i0, uint32_t hb) {
         int tot = 0;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) tot += __popcll(bal[j]);
@@ -215,10 +243,11 @@ struct TpBuf {
         for (int j = 0; j < VEC; ++j) {
             const int at = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[j] >> 32),
                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal[j], (uint32_t)base));
-            const bool c = okv & (v[j] >= tauf);  // the lanes of bal[j] (no short-circuit branch)
+            const bool hj = ((hb >> j) & 1u) != 0u;
+            const bool c = okv & ((v[j] >= tauf) | hj);  // the lanes of bal[j] (no short-circuit branch)
             const int pos = c ? at : spare;
             sm.ck[w][pos] = f2u(v[j]);
-            sm.ci[w][pos] = i0 + j;
+            sm.ci[w][pos] = (int32_t)((uint32_t)(i0 + j) | (hj ? kTpHist : 0u));
             base += __popcll(bal[j]);
         }
         cnt = base;
@@ -260,17 +289,23 @@ __device__ __forceinline__ void topp_rank_members(TopPSmem& sm, uint32_t ng, flo
 // Out of line (defined next to the LDS it works on).
 __device__ __noinline__ void topp_rank_members_entry(uint32_t ng, float m);
 
-// Keeps the kTpKeep largest values (ties included) of wave w's buffer and raises its threshold
-// to the smallest kept value; the dropped entries are returned as terms of the approximate sum.
+// Keeps the kTpKeep largest values (ties included) of wave w's buffer, and its history tokens,
+// and raises its threshold to the smallest kept value; the dropped entries are returned as terms
+// of the approximate sum.
 __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, float aw, float c,
-                                               bool want_raw) {
+                                               bool want_raw, bool hist) {
     TpDrop d{0.0, 0.0, 0.0f, 0u, 0};
     const int lane = lane_id();
     uint32_t* ck = sm.ck[w];
     int32_t* ci = sm.ci[w];
-    for (int i = lane; i < cnt; i += kWave) ck[i] = key_of(u2f(ck[i]));  // raw bits -> keys
+    int nh = 0;  // history tokens (kept whatever their value: the rest make up kTpKeep)
+    for (int base = 0; base < cnt; base += kWave) {
+        const int i = base + lane;
+        if (i < cnt) ck[i] = key_of(u2f(ck[i]));  // raw bits -> keys
+        if (hist) nh += __popcll(wave_ballot(i < cnt && ((uint32_t)ci[i] & kTpHist)));
+    }
     wave_sync();
-    const uint32_t kth = wave_kth_largest(ck, cnt, kTpKeep, sm.rhist[w]);
+    const uint32_t kth = wave_kth_largest(ck, cnt, kTpKeep - nh > 1 ? kTpKeep - nh : 1, sm.rhist[w]);
     int out = 0;
     for (int base = 0; base < cnt; base += kWave) {
         const int i = base + lane;
@@ -280,7 +315,7 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
         if (i < cnt) {
             kk = ck[i];
             ii = ci[i];
-            keep = kk >= kth;
+            keep = kk >= kth || (hist && ((uint32_t)ii & kTpHist));  // history tokens stay buffered
             if (!keep) {
                 const float x = val_of(kk);
                 float z;
@@ -308,7 +343,9 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
 }
 
 // The stream over row r.  Publishes each wave's results into sm; topp_finish completes the row.
-template <typename T>
+// HIST: a row with penalties from the token-state table; its bitmap is staged in sm.hb and every
+// history token is buffered.
+template <typename T, bool HIST>
 __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r, const RowP& prm) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
@@ -332,9 +369,27 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
+    // history rows: the bitmap's words are read first (their stores into LDS wait only for them)
+    constexpr int kHbPer = (kTpHistWords + NT - 1) / NT;
+    uint32_t hbw[HIST ? kHbPer : 1];
+    const int nhw = (V + 31) >> 5;
+    if (HIST) {
+        const uint32_t* brow = a.tbits + (size_t)prm.trow * (size_t)a.tbstride;
+#pragma unroll
+        for (int q = 0; q < kHbPer; ++q) {
+            const int i = q * NT + tid;
+            hbw[q] = i < nhw ? brow[i] : 0u;
+            if (i == nhw - 1 && (V & 31)) hbw[q] &= (1u << (V & 31)) - 1u;  // no token past V
+        }
+    }
     float A[U][VEC], Bq[U][VEC];
     load_iter(A, 0);
     load_iter(Bq, 1);
+    if (HIST) {
+#pragma unroll
+        for (int q = 0; q < kHbPer; ++q)
+            if (q * NT + tid < kTpHistWords) sm.hb[q * NT + tid] = hbw[q];
+    }
 
     // seed: a threshold from the lane maxima over the first iteration.  A lane's maximum over its
     // E elements reaches tau with probability 1 - (1 - phi)^E when a fraction phi of the
@@ -350,7 +405,22 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         for (int j = 0; j < VEC; ++j) lmax = ok ? __builtin_fmaxf(lmax, A[q][j]) : lmax;
     }
     const float share = (float)V / (float)kTpWaves;
-    const float phi = __builtin_fminf(1.0f, kTpFill * (float)kTpCapW / share);
+    float fill = kTpFill * (float)kTpCapW;
+    if (HIST) {
+        // history tokens take slots of their own: the estimate of a wave's share of them (from
+        // the bitmap words this wave staged, a 1/16 sample of the row's) leaves the fill target
+        uint32_t nb = 0u, nwd = 0u;
+#pragma unroll
+        for (int q = 0; q < kHbPer; ++q) {
+            nb += (uint32_t)__popc(hbw[q]);
+            nwd += (q * NT + tid < nhw) ? 1u : 0u;
+        }
+        nb = (uint32_t)wave_sum_u64(nb);
+        nwd = (uint32_t)wave_sum_u64(nwd);
+        const float est = nwd ? (float)nb * (float)nhw / (float)nwd : 0.0f;  // the row's
+        fill = __builtin_fmaxf(fill - est / (float)kTpWaves, (float)kWave);
+    }
+    const float phi = __builtin_fminf(1.0f, fill / share);
     const bool seeded = phi < 1.0f && nbody > 0;
     uint32_t tw = 0u;
     if (seeded) {
@@ -362,7 +432,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     }
     if (tid == 0) sm.status = 0u;
     if (lane == 0) sm.bc[wave] = tw;  // bc is free until the finish's first barrier
-    __syncthreads();
+    __syncthreads();  // (also publishes the history bitmap)
     uint32_t tau0 = 0u;
     if (seeded) tau0 = wave_mth_largest64(lane < kTpWaves ? sm.bc[lane] : 0u, kTpWaves / 2);
     if (tau0 <= 0x007FFFFFu || tau0 >= 0xFF800000u) tau0 = 0u;  // -inf, or +inf (degenerate row)
@@ -376,25 +446,33 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     cb.set_tau(tau0);
     double acc = 0.0, accr = 0.0;
     float accz = 0.0f;
-    // one vector of VEC elements starting at element i0 (okv: in the row): candidates into the
-    // buffer, every other element into the sums (a zero term for NaN and -inf).  The ballots of
-    // the element tests decide whether any lane appends (no separate vector test: a wave almost
-    // always has a candidate somewhere in a vector position).
-    auto consume = [&](const float* v, int i0, bool okv) __attribute__((always_inline)) {
+    // one vector of VEC elements starting at element i0 (okv: in the row; hv: the elements whose
+    // history bit counts): candidates into the buffer, every other element into the sums (a zero
+    // term for NaN and -inf).  The ballots of the element tests decide whether any lane appends
+    // (no separate vector test: a wave almost always has a candidate somewhere in a vector
+    // position).
+    auto consume = [&](const float* v, int i0, bool okv, uint32_t hv) __attribute__((always_inline)) {
+        uint32_t hb = 0u;
+        if (HIST) {
+            // bits i0 .. i0 + VEC - 1 of the bitmap (i0 need not be aligned: a 64-bit window)
+            const uint32_t w = okv ? ((uint32_t)i0 >> 5) : 0u;
+            const uint64_t win = (uint64_t)sm.hb[w] | ((uint64_t)sm.hb[w + 1] << 32);
+            hb = (uint32_t)(win >> ((uint32_t)i0 & 31u)) & hv;
+        }
         uint64_t bal[VEC];
         uint64_t any = 0ull;
         // ballots of single compares (the compiler takes their lane masks as they are)
         const uint64_t okm = wave_ballot(okv);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            bal[j] = wave_ballot(v[j] >= cb.tauf) & okm;
+            bal[j] = wave_ballot((v[j] >= cb.tauf) || (HIST && ((hb >> j) & 1u))) & okm;
             any |= bal[j];
         }
-        if (any) cb.append_vec<VEC>(sm, v, bal, okv, i0);
+        if (any) cb.append_vec<VEC>(sm, v, bal, okv, i0, hb);
         float s = 0.0f, z = 0.0f, sr = 0.0f;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            const bool inc = okv && !(v[j] >= cb.tauf);
+            const bool inc = okv && !(v[j] >= cb.tauf) && !(HIST && ((hb >> j) & 1u));
             float zj;
             const float t = tp_term(v[j], aw, c, zj);
             const float tt = inc ? t : 0.0f;
@@ -413,7 +491,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     // keeps the buffer's fill at most kTpSoft every half iteration: the dropped entries join the sum
     auto shrink = [&]() __attribute__((always_inline)) {
         if (cb.cnt > kTpSoft && !cb.ovf) {
-            const TpDrop d = topp_compact_entry(wave, cb.cnt, aw, c, want_raw ? 1 : 0);
+            const TpDrop d = topp_compact_entry(wave, cb.cnt, aw, c, want_raw ? 1 : 0, HIST ? 1 : 0);
             acc += d.s;
             accr += d.sr;
             accz += d.z;
@@ -427,7 +505,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         for (int q = 0; q < U; ++q) {
             if (q == U / 2) shrink();
             const int vi = (it * U + q) * NT + t;
-            consume(buf[q], sl.a + vi * VEC, vi < nbody);
+            consume(buf[q], sl.a + vi * VEC, vi < nbody, (1u << VEC) - 1u);
         }
     };
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
@@ -446,10 +524,14 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         int i0 = 0;
         if (tid <= 1) i0 = sl.load_edge(tid, v);
         const int end = tid == 0 ? sl.a : V;
+        uint32_t hv = 0u;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j)
-            if (!(tid <= 1 && i0 + j < end)) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
-        consume(v, i0, true);
+        for (int j = 0; j < VEC; ++j) {
+            const bool in = tid <= 1 && i0 + j < end;
+            if (!in) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
+            hv |= in ? (1u << j) : 0u;
+        }
+        consume(v, i0, true, hv);
     }
 
     // publish the wave's results
@@ -521,17 +603,26 @@ __device__ __forceinline__ double tp_wave_sum_f64(double v) {
 
 // ---- further passes over the row ------------------------------------------------------
 
+// Penalties of a history row in a further pass: the row's token-state words and parameters.
+struct TpPen {
+    const uint32_t* wrow;
+    float rep, inv_rep, freq, pres;
+};
+
 // The aligned body vectors [v0, v1) of row r, and its unaligned head and tail when `edges`
 // (every thread calls it): 16-byte buffer loads over just that range (loads past its end read
 // zeros and fetch nothing), one vector per thread per step with the next step's load in flight
 // (a range is a chunk of a few steps: the second load overlaps the first step's work).  f(v, u, i0, ok) gets the VEC elements of one vector from element i0 on (ok: the
 // vector lies in the range; head and tail are NaN-padded) and, with WITH_U, their uniforms
-// (dword-aligned 16-byte loads).
-template <typename T, bool WITH_U, typename F>
-__device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int v1, bool edges, F&& f) {
+// (dword-aligned 16-byte loads).  PEN: the elements are penalised first from their token-state
+// words (streamed like the uniforms), so that f sees processed values.
+template <typename T, bool WITH_U, bool PEN, typename F>
+__device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int v1, bool edges,
+                                             const TpPen& pen, F&& f) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int UW = WITH_U ? VEC / 4 : 0;  // uniform loads per vector
+    constexpr int WW = PEN ? VEC / 4 : 0;     // token-state word loads per vector
     constexpr int UP = 1;                     // vectors per thread per step
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -546,11 +637,19 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
     const __amdgpu_buffer_rsrc_t lrs = make_rsrc(row + e0, 16u * (uint32_t)nv);
     const __amdgpu_buffer_rsrc_t urs = make_rsrc(WITH_U ? (const void*)(urow + e0) : (const void*)row,
                                                  WITH_U ? 4u * (uint32_t)(nv * VEC) : 0u);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(PEN ? (const void*)(pen.wrow + e0) : (const void*)row,
+                                                 PEN ? 4u * (uint32_t)(nv * VEC) : 0u);
     auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
     using W4 = decltype(__builtin_amdgcn_raw_buffer_load_b128(lrs, 0u, 0u, 0));
+    // a history token's processed value (a zero word: the value itself)
+    auto penal = [&](float x, uint32_t wd) __attribute__((always_inline)) {
+        wd &= kStateMask;
+        return wd ? apply_hashed(x, wd, 0.0f, pen.rep, pen.inv_rep, pen.freq, pen.pres) : x;
+    };
     // vectors (it * UP + q) * NT + tid lie past the range for every thread once
     // (it * UP + q) * NT >= nv: such loads and their work are skipped (a uniform test)
-    auto load = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], int it) __attribute__((always_inline)) {
+    auto load = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], W4 (&ww)[UP][WW > 0 ? WW : 1], int it)
+                    __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < UP; ++q) {
             if ((it * UP + q) * NT >= nv) break;
@@ -560,9 +659,14 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
             for (int g = 0; g < UW; ++g)
                 uw[q][g] = __builtin_amdgcn_raw_buffer_load_b128(
                     urs, 4u * (vi * (uint32_t)VEC + 4u * (uint32_t)g), 0u, 2);
+#pragma unroll
+            for (int g = 0; g < WW; ++g)
+                ww[q][g] = __builtin_amdgcn_raw_buffer_load_b128(
+                    wrs, 4u * (vi * (uint32_t)VEC + 4u * (uint32_t)g), 0u, 2);
         }
     };
-    auto consume = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], int it) __attribute__((always_inline)) {
+    auto consume = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], W4 (&ww)[UP][WW > 0 ? WW : 1], int it)
+                       __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < UP; ++q) {
             if ((it * UP + q) * NT >= nv) break;
@@ -572,18 +676,23 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
                                 (uint32_t)lw[q][3], v);
 #pragma unroll
             for (int j = 0; j < VEC; ++j) u[j] = WITH_U ? u2f((uint32_t)uw[q][j / 4][j % 4]) : 0.0f;
+            if (PEN) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[j] = penal(v[j], (uint32_t)ww[q][j / 4][j % 4]);
+            }
             f(v, u, e0 + vi * VEC, vi < nv);
         }
     };
     W4 la[UP], lb[UP];
     W4 ua[UP][UW > 0 ? UW : 1], ub[UP][UW > 0 ? UW : 1];
-    load(la, ua, 0);
-    load(lb, ub, 1);
+    W4 wa[UP][WW > 0 ? WW : 1], wb[UP][WW > 0 ? WW : 1];
+    load(la, ua, wa, 0);
+    load(lb, ub, wb, 1);
     for (int it = 0; it < nit; it += 2) {
-        consume(la, ua, it);
-        load(la, ua, it + 2);
-        if (it + 1 < nit) consume(lb, ub, it + 1);
-        load(lb, ub, it + 3);
+        consume(la, ua, wa, it);
+        load(la, ua, wa, it + 2);
+        if (it + 1 < nit) consume(lb, ub, wb, it + 1);
+        load(lb, ub, wb, it + 3);
     }
     if (edges && wave == 0) {
         float v[VEC], u[VEC];
@@ -596,7 +705,10 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
             for (int j = 0; j < VEC; ++j) v[j] = __builtin_nanf("");
         }
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) u[j] = (WITH_U && i0 + j < end) ? urow[i0 + j] : 0.0f;
+        for (int j = 0; j < VEC; ++j) {
+            u[j] = (WITH_U && i0 + j < end) ? urow[i0 + j] : 0.0f;
+            if (PEN && i0 + j < end) v[j] = penal(v[j], pen.wrow[i0 + j]);
+        }
         f(v, u, i0, tid <= 1);
     }
 }
@@ -668,15 +780,33 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
 //     streamed with the logits, or generated);
 //   * rank pass: the elements at or above the key (the rank of a sampled token that is not a
 //     candidate) into acc.n.
+// In rows with penalties from the token-state table the exact and wide passes see processed
+// values (the rank pass ranks raw ones).
 template <typename T>
 __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int r, const TpPassDesc& d,
                                               int v0, int v1, bool edges, TpPassAcc& acc) {
     constexpr int VEC = Elem<T>::kVec;
     const uint32_t tauk = d.key;
     const float Tt = d.Tt, m = d.m, lp_min = d.lp_min;
+    TpPen pen{nullptr, 1.0f, 1.0f, 0.0f, 0.0f};
+    bool hist = false;
+    if (a.tstate) {
+        pen.rep = a.rep ? a.rep[r] : 1.0f;
+        pen.pres = a.pres ? a.pres[r] : 0.0f;
+        pen.freq = a.freq ? a.freq[r] : 0.0f;
+        pen.inv_rep = 1.0f / pen.rep;
+        hist = !(pen.rep == 1.0f && pen.pres == 0.0f && pen.freq == 0.0f);
+        pen.wrow = a.tstate + (size_t)(a.trows ? a.trows[r] : r) * (size_t)a.tstride;
+        hist = __builtin_amdgcn_readfirstlane(hist ? 1 : 0) != 0;
+    }
+    // the pass over the range, with or without the penalties
+    auto range = [&](auto with_u, auto&& f) __attribute__((always_inline)) {
+        if (hist) tp_row_range<T, decltype(with_u)::value, true>(a, r, v0, v1, edges, pen, f);
+        else tp_row_range<T, decltype(with_u)::value, false>(a, r, v0, v1, edges, pen, f);
+    };
     if (d.kind == kTpPassExact) {
-        tp_row_range<T, false>(a, r, v0, v1, edges, [&](const float* v, const float*, int, bool ok)
-                                                       __attribute__((always_inline)) {
+        range(BoolC<false>{}, [&](const float* v, const float*, int, bool ok)
+                                  __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) {
                 const uint32_t kx = key_of(v[j]);
@@ -730,15 +860,15 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
             }
         };
         if (a.u) {
-            tp_row_range<T, true>(a, r, v0, v1, edges, [&](const float* v, const float* u, int i0, bool ok)
-                                                          __attribute__((always_inline)) { body(v, u, i0, ok, false); });
+            range(BoolC<true>{}, [&](const float* v, const float* u, int i0, bool ok)
+                                     __attribute__((always_inline)) { body(v, u, i0, ok, false); });
         } else {
-            tp_row_range<T, false>(a, r, v0, v1, edges, [&](const float* v, const float* u, int i0, bool ok)
-                                                           __attribute__((always_inline)) { body(v, u, i0, ok, true); });
+            range(BoolC<false>{}, [&](const float* v, const float* u, int i0, bool ok)
+                                      __attribute__((always_inline)) { body(v, u, i0, ok, true); });
         }
     } else {
-        tp_row_range<T, false>(a, r, v0, v1, edges, [&](const float* v, const float*, int, bool ok)
-                                                       __attribute__((always_inline)) {
+        tp_row_range<T, false, false>(a, r, v0, v1, edges, pen, [&](const float* v, const float*, int, bool ok)
+                                                                   __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) acc.n += (ok && key_of(v[j]) >= tauk) ? 1ull : 0ull;
         });
@@ -864,17 +994,85 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     }
     __syncthreads();  // every wave's stream results are published
     if (sm.status != 0u) return (sm.status & 1u) ? VWS_FALLBACK_OVERFLOW : VWS_FALLBACK_SUM;
-    uint32_t tauk = 0u, maxk = 0u;
+    const bool hist = prm.has_hist;
+    // an entry's element index (history rows mark their history tokens in bit 18)
+    const uint32_t imask = hist ? kTpHist - 1u : kTpIdxMask;
+    uint32_t tauk = 0u, maxr = 0u;
 #pragma unroll
     for (int w = 0; w < kTpWaves; ++w) {
         tauk = sm.wTau[w] > tauk ? sm.wTau[w] : tauk;
-        maxk = sm.wMax[w] > maxk ? sm.wMax[w] : maxk;
+        maxr = sm.wMax[w] > maxr ? sm.wMax[w] : maxr;
     }
     tauk = tp_u(tauk);
-    maxk = tp_u(maxk);
+    maxr = tp_u(maxr);
     // a finite row maximum (always a candidate: no threshold exceeds a wave's own maximum)
-    if (maxk <= 0x007FFFFFu || maxk >= 0xFF800000u) return VWS_FALLBACK_DEGENERATE;
-    const float xmax = val_of(maxk);
+    if (maxr <= 0x007FFFFFu || maxr >= 0xFF800000u) return VWS_FALLBACK_DEGENERATE;
+    const float xmaxr = val_of(maxr);  // raw maximum (the raw logprobs)
+    uint32_t maxk = maxr;
+    if (hist) {
+        // the buffered history tokens take their processed values from their token-state words
+        // (gathered G entries per lane at a time), in place, keeping their mark; with raw
+        // logprobs, their raw normaliser terms are added up here and those at or above the
+        // threshold by raw value are listed (the raw top-L and rank need them)
+        const uint32_t* trw = a.tstate + (size_t)prm.trow * (size_t)a.tstride;
+        const int cnt0 = (int)tp_u(sm.wCnt[wave]);
+        uint32_t mx = 0u;
+        float s0h = 0.0f;
+        if (tid == 0) sm.rl_n = 0u;
+        __syncthreads();
+        constexpr int G = 8;
+        for (int base = 0; base < cnt0; base += G * kWave) {
+            uint32_t cw[G], wd[G];
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+                const int i = base + q * kWave + lane;
+                cw[q] = i < cnt0 ? (uint32_t)sm.ci[wave][i] : 0u;
+            }
+#pragma unroll
+            for (int q = 0; q < G; ++q)
+                wd[q] = (cw[q] & kTpHist) ? (trw[cw[q] & (kTpHist - 1u)] & kStateMask) : 0u;
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+                const int i = base + q * kWave + lane;
+                if (i >= cnt0) continue;
+                const float x = u2f(sm.ck[wave][i]);
+                float y = x;
+                if (cw[q] & kTpHist) {
+                    y = apply_hashed(x, wd[q], 0.0f, prm.rep, prm.inv_rep, prm.freq, prm.pres);
+                    sm.ck[wave][i] = f2u(y);
+                    if (L >= 0) {
+                        s0h += exp_det(x - xmaxr);
+                        const uint32_t kx = key_of(x);
+                        if (kx >= tauk) {
+                            const uint32_t pos = atomicAdd(&sm.rl_n, 1u);
+                            if (pos < (uint32_t)kTpRawCap) {
+                                sm.rl_key[pos] = kx;
+                                sm.rl_idx[pos] = (int32_t)(cw[q] & (kTpHist - 1u));
+                            }
+                        }
+                    }
+                }
+                const uint32_t ky = key_of(y);
+                mx = ky > mx ? ky : mx;
+            }
+        }
+        mx = wave_max_u32(mx);
+        s0h = (float)tp_wave_sum_f64((double)s0h);
+        if (lane == 0) {
+            sm.wMaxP[wave] = mx;
+            sm.wS0h[wave] = s0h;
+        }
+        __syncthreads();
+        if (tp_u(sm.rl_n) > (uint32_t)kTpRawCap) return VWS_FALLBACK_TOPL;
+        maxk = 0u;
+#pragma unroll
+        for (int w = 0; w < kTpWaves; ++w) maxk = sm.wMaxP[w] > maxk ? sm.wMaxP[w] : maxk;
+        maxk = tp_u(maxk);
+    }
+    // the processed maximum: finite, and in history rows at or above every threshold (nothing
+    // outside the buffers, whose values are raw, can then exceed it)
+    if (maxk <= 0x007FFFFFu || maxk >= 0xFF800000u || maxk < tauk) return VWS_FALLBACK_DEGENERATE;
+    const float xmax = val_of(maxk);   // processed maximum (top-p)
     const float m = greedy ? xmax : xmax / Tt;  // max y (the division is monotone)
     if (!(m > -__builtin_inff() && m < __builtin_inff())) return VWS_FALLBACK_DEGENERATE;
     const float lp_min = (!greedy && prm.min_p > 0.0f)
@@ -890,13 +1088,19 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         sm.h.hmass[i] = 0ull;
         sm.h.hcnt[i] = 0u;
     }
-    if (tid == 0) sm.bc[7] = 0u;  // top-L members gathered
+    if (tid == 0) {
+        sm.bc[7] = 0u;  // top-L members gathered
+        sm.xr = xmaxr;
+    }
     __syncthreads();
 
     // exact masses of the buffered entries (now turned into order keys): candidates into the
     // buckets, the others into Sx
     const int cnt = (int)tp_u(sm.wCnt[wave]);
+    // history rows: the marked entries hold processed values; their raw parts (normaliser terms,
+    // raw entries at or above the threshold) come from the pre-pass
     {
+        const float mr = (greedy || Tt == 1.0f) ? xmaxr : xmaxr / Tt;  // history rows: raw buckets
         uint64_t wc = 0ull, sx = 0ull;
         uint32_t nxs = 0u;
         float s0b = 0.0f;
@@ -904,6 +1108,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         // division, chosen once for the wave
         auto masses = [&](auto unit) __attribute__((always_inline)) {
             for (int i = lane; i < cnt; i += kWave) {
+                const uint32_t c0 = (uint32_t)sm.ci[wave][i];
+                const bool hm = hist && (c0 & kTpHist);  // a history token (processed value)
                 const float x = u2f(sm.ck[wave][i]);
                 const uint32_t kk = key_of(x);
                 const float y = decltype(unit)::value ? x : x / Tt;
@@ -912,19 +1118,23 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 const float e = exp_det(d);
                 const uint64_t w = surv ? mass_of(e) : 0ull;
                 // raw logprobs' normaliser: x - max x is d itself for greedy rows and T = 1
-                if (L >= 0) s0b += decltype(unit)::value ? e : exp_det(x - xmax);
+                // (without a history)
+                if (L >= 0 && !hm) s0b += hist ? exp_det(x - xmaxr) : (decltype(unit)::value ? e : exp_det(x - xmax));
                 const int b = tp_bucket(d);
+                const bool below = kk < tauk;
                 sm.ck[wave][i] = kk;
-                sm.ci[wave][i] = (int32_t)(((uint32_t)sm.ci[wave][i] & kTpIdxMask) | ((uint32_t)b << 19) |
-                                           (surv ? kTpSurv : 0u) | (kk < tauk ? kTpBelow : 0u));
-                if (kk >= tauk) {
-                    if (L > 0) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
+                sm.ci[wave][i] = (int32_t)((c0 & kTpIdxMask) | ((uint32_t)b << 19) |
+                                           (surv ? kTpSurv : 0u) | (below ? kTpBelow : 0u));
+                if (!below) {
+                    if (L > 0 && !hist) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
                     if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
                     wc += w;
                 } else {
                     sx += w;
                     nxs += surv ? 1u : 0u;
                 }
+                // history rows: the top-L counts by raw bucket
+                if (hist && L > 0 && !hm && kk >= tauk) atomicAdd(&sm.h.hcnt[tp_bucket(y - mr)], 1u);
             }
         };
         if (greedy || Tt == 1.0f) {
@@ -932,10 +1142,19 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         } else {
             masses(BoolC<false>{});
         }
+        if (hist && L > 0) {
+            // the listed raw entries in the top-L counts
+            const uint32_t nrl = tp_u(sm.rl_n);
+            for (uint32_t j = (uint32_t)tid; j < nrl; j += NT) {
+                const float xr = val_of(sm.rl_key[j]);
+                atomicAdd(&sm.h.hcnt[tp_bucket(((greedy || Tt == 1.0f) ? xr : xr / Tt) - mr)], 1u);
+            }
+        }
         wc = wave_sum_u64(wc);
         sx = wave_sum_u64(sx);
         const uint64_t nn = wave_sum_u64(nxs);
-        const double sb = tp_wave_sum_f64((double)s0b);
+        double sb = tp_wave_sum_f64((double)s0b);
+        if (hist && L >= 0) sb += (double)sm.wS0h[wave];
         if (lane == 0) {
             sm.red[wave][0] = wc;
             sm.red[wave][1] = sx;
@@ -944,12 +1163,20 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         }
     }
     __syncthreads();
-    uint64_t Wc = tp_sum16(sm, 0);  // candidates' mass (wide rows: every survivor's)
-    const uint64_t Sx = tp_sum16(sm, 1);
-    const uint64_t NXS = tp_sum16(sm, 2);
-    double S0b = 0.0;
-#pragma unroll
-    for (int w = 0; w < kTpWaves; ++w) S0b += sm.redd[w];
+    if (tid == 0) {
+        // candidates' mass (wide rows: every survivor's), survivors below the threshold, the
+        // buffered raw normaliser: read from LDS after the next barrier
+        uint64_t wc = 0ull, nx = 0ull;
+        double sb = 0.0;
+        for (int w = 0; w < kTpWaves; ++w) {
+            wc += sm.red[w][0];
+            nx += sm.red[w][2];
+            sb += sm.redd[w];
+        }
+        sm.tot_wc = wc;
+        sm.tot_nxs = nx;
+        sm.tot_s0b = sb;
+    }
 
     int32_t token = 0;
     uint32_t flags = VWS_FLAG_STREAM_TOPP;
@@ -960,7 +1187,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         for (int i = lane; i < cnt; i += kWave) {
             if (sm.ck[wave][i] == maxk) {
                 const uint64_t pk = ((uint64_t)maxk << 32) |
-                                    (0x7FFFFFFFu - ((uint32_t)sm.ci[wave][i] & kTpIdxMask));
+                                    (0x7FFFFFFFu - ((uint32_t)sm.ci[wave][i] & imask));
                 best = pk > best ? pk : best;
             }
         }
@@ -996,6 +1223,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             const double sap = tp_wave_sum_f64(mw * ws);
             const double err0 = tp_wave_sum_f64(mw * (k0 * ws + k1 * wz * (1.0 + 0x1p-8)));
             if (lane == 0) {
+                uint64_t Sx = 0ull;  // exact mass of the survivors buffered below the threshold
+                for (int w = 0; w < kTpWaves; ++w) Sx += sm.red[w][1];
                 int why = 0;
                 // every element of the row outside the buffers may be a term (the floor of each
                 // exact mass loses less than one unit)
@@ -1025,7 +1254,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         if (const int why = (int)tp_u(sm.bc[8])) return why;
         // survivors below every candidate: the stream's terms (all survive without min-p) and
         // the buffered ones below the threshold
-        bool any_below_nc = tp_u(sm.bc[9]) != 0u || NXS > 0ull;
+        bool any_below_nc = tp_u(sm.bc[9]) != 0u || tp_u64(sm.tot_nxs) > 0ull;
         uint64_t S[2] = {tp_u64(sm.bc64[0]), tp_u64(sm.bc64[1])};
 
         // decides top-p for S[0] and S[1]; when they differ, or when the boundary lies below
@@ -1038,15 +1267,17 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         bool ranked = false, serial = false;
         bool exact = false, wide = false, go_exact = tp_u(sm.bc[10]) != 0u;
         int bnc = kTpBuckets;       // bucket of the largest value below the candidates
-        uint64_t wide_kept = 0ull;  // survivors kept by the wide race pass (wide rows: every one
-        uint64_t wbest = 0ull;      // outside the boundary bucket) and their race (RowRace
-        uint32_t wsec = 0u;         // fields)
-        uint64_t wlast = 0ull;
+        if (tid == 0) {
+            // the wide race pass's survivors (wide rows: every one outside the boundary bucket)
+            // and their race: none until that pass runs
+            sm.wrace[0] = sm.wrace[1] = sm.wrace[2] = sm.wrace[3] = 0ull;
+        }
         for (;;) {
             if (go_exact && !exact) {
                 pass(kTpPassExact, tauk, 0);
                 if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
-                Wc += tp_u64(sm.bc64[10]);
+                if (tid == 0) sm.tot_wc += sm.bc64[10];
+                __syncthreads();
                 any_below_nc = tp_u64(sm.bc64[11]) > 0ull;
                 S[0] = S[1] = 0ull;
                 exact = true;
@@ -1056,7 +1287,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             uint64_t thr[2], W[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                W[e] = S[e] + Wc;
+                W[e] = S[e] + tp_u64(sm.tot_wc);
                 thr[e] = scale_floor(q32, W[e]);
             }
             bool decided = false;
@@ -1103,15 +1334,17 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                             const float y = val_of(sm.ck[wave][i]) / Tt;
                             const uint32_t pos = atomicAdd(&sm.bc[4], 1u);
                             if (pos < (uint32_t)kTpGather)
-                                sm.g.key[pos] = ((uint64_t)key_of(y) << 32) | (c & kTpIdxMask);
+                                sm.g.key[pos] = ((uint64_t)key_of(y) << 32) | (c & imask);
                         }
                         if (wide) {
                             pass(kTpPassWideRace, tauk, bstar);
                             if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
-                            wbest = tp_u64(sm.bc64[10]);
-                            wsec = (uint32_t)tp_u64(sm.bc64[11]);
-                            wide_kept = tp_u64(sm.bc64[12]);
-                            wlast = tp_u64(sm.bc64[14]);
+                            if (tid == 0) {
+                                sm.wrace[0] = sm.bc64[10];
+                                sm.wrace[1] = sm.bc64[11];
+                                sm.wrace[2] = sm.bc64[12];
+                                sm.wrace[3] = sm.bc64[14];
+                            }
                             any_below_nc = tp_u64(sm.bc64[13]) > 0ull;
                             flags |= VWS_FLAG_TOPP_WIDE;
                         }
@@ -1277,7 +1510,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 const int b = tp_code_bucket(c);
                 below_cands += (sv && b > bstar) ? 1u : 0u;
                 kq[q] = sv && b < bstar;
-                iq[q] = (int32_t)(c & kTpIdxMask);
+                iq[q] = (int32_t)(c & imask);
             }
 #pragma unroll
             for (int q = 0; q < kRq; ++q) uq[q] = kq[q] ? row_uniform(a, r, iq[q]) : 0.5f;
@@ -1319,9 +1552,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         __syncthreads();
         if (tid == 0) {
             RowRace all;
-            all.best = wbest;  // the wide race pass's survivors (wide rows), counted once
-            all.second = wsec;
-            all.last = wlast;
+            all.best = sm.wrace[0];  // the wide race pass's survivors (wide rows), counted once
+            all.second = (uint32_t)sm.wrace[1];
+            all.last = sm.wrace[3];
             uint64_t nbelow = 0ull;
             for (int w = 0; w < kTpWaves; ++w) {
                 RowRace o;
@@ -1350,7 +1583,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             }
             sm.bc[12] = (uint32_t)tok;
             sm.bc[13] = f;
-            sm.bc[14] = all.nkept + (uint32_t)wide_kept;
+            sm.bc[14] = all.nkept + (uint32_t)sm.wrace[2];
         }
         __syncthreads();
         token = (int32_t)tp_u(sm.bc[12]);
@@ -1373,7 +1606,11 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
             rk = wave == 0 ? (uint32_t)tp_u64(sm.bc64[10]) : 0u;  // the per-wave records below add up
         } else {
-            for (int i = lane; i < cnt; i += kWave) rk += sm.ck[wave][i] >= ks ? 1u : 0u;
+            // raw values: history rows count their unmarked entries and the listed raw ones
+            for (int i = lane; i < cnt; i += kWave)
+                rk += (sm.ck[wave][i] >= ks && !(hist && ((uint32_t)sm.ci[wave][i] & kTpHist))) ? 1u : 0u;
+            if (hist)
+                for (uint32_t j = (uint32_t)tid; j < tp_u(sm.rl_n); j += NT) rk += sm.rl_key[j] >= ks ? 1u : 0u;
             rk = (uint32_t)wave_sum_u64(rk);
         }
         uint32_t ncand = 0u;
@@ -1391,7 +1628,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (wave == 0) {
                 // log-sum-exp of the raw logits: the buffered part plus the stream's terms
                 const double sw = lane < kTpWaves ? ((greedy || Tt == 1.0f) ? sm.wS[lane] : sm.wSR[lane]) : 0.0;
-                const double s0 = S0b + tp_wave_sum_f64(sw) * exp((double)aw - (double)xmax);
+                const double s0 = sm.tot_s0b + tp_wave_sum_f64(sw) * exp((double)aw - (double)sm.xr);
                 if (lane == 0) sm.bc64[8] = (uint64_t)__double_as_longlong(s0);
             }
         }
@@ -1401,13 +1638,31 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         if (L > 0) {
             if (ncand < (uint32_t)L) return VWS_FALLBACK_TOPL;  // the top-L reaches below the candidates
             const int bl = (int)tp_u(sm.bc[15]);
+            const bool unitT = greedy || Tt == 1.0f;
+            const float mr = unitT ? tp_uf(sm.xr) : tp_uf(sm.xr) / Tt;
+            // history rows: raw values (unmarked entries and the listed raw ones) against the
+            // threshold and the raw buckets
+            auto raw_in = [&](uint32_t kr) __attribute__((always_inline)) {
+                return kr >= tauk && tp_bucket((unitT ? val_of(kr) : val_of(kr) / Tt) - mr) <= bl;
+            };
             for (int i = lane; i < cnt; i += kWave) {
                 const uint32_t c = (uint32_t)sm.ci[wave][i];
-                if ((c & kTpBelow) || tp_code_bucket(c) > bl) continue;
+                if (hist ? ((c & kTpHist) || !raw_in(sm.ck[wave][i])) : ((c & kTpBelow) || tp_code_bucket(c) > bl))
+                    continue;
                 const uint32_t pos = atomicAdd(&sm.bc[7], 1u);
                 if (pos < (uint32_t)kTpLpCap) {
                     sm.lp.key[pos] = sm.ck[wave][i];
-                    sm.lp.idx[pos] = (int32_t)(c & kTpIdxMask);
+                    sm.lp.idx[pos] = (int32_t)(c & imask);
+                }
+            }
+            if (hist) {
+                for (uint32_t j = (uint32_t)tid; j < tp_u(sm.rl_n); j += NT) {
+                    if (!raw_in(sm.rl_key[j])) continue;
+                    const uint32_t pos = atomicAdd(&sm.bc[7], 1u);
+                    if (pos < (uint32_t)kTpLpCap) {
+                        sm.lp.key[pos] = sm.rl_key[j];
+                        sm.lp.idx[pos] = sm.rl_idx[j];
+                    }
                 }
             }
             __syncthreads();
@@ -1425,7 +1680,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         const int stride = L + 1;
         if (tid == 0) {
             a.lp_ids[(size_t)r * stride] = token;
-            a.lp_vals[(size_t)r * stride] = (xs - xmax) - logS;
+            a.lp_vals[(size_t)r * stride] = (xs - sm.xr) - logS;
             a.lp_ranks[r] = (int32_t)rank;
         }
         if (L > 0) {
@@ -1440,7 +1695,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 }
                 if (pos < L) {
                     a.lp_ids[(size_t)r * stride + 1 + pos] = ij;
-                    a.lp_vals[(size_t)r * stride + 1 + pos] = (val_of(kj) - xmax) - logS;
+                    a.lp_vals[(size_t)r * stride + 1 + pos] = (val_of(kj) - tp_uf(sm.xr)) - logS;
                 }
             }
         }

@@ -104,7 +104,8 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
            adjust_lens=None, logit_softcap: float | None = None,
            logit_softcap_f16: bool = False, rng_seeds: torch.Tensor | None = None,
            rng_offsets: torch.Tensor | None = None, token_state: torch.Tensor | None = None,
-           token_state_rows: torch.Tensor | None = None) -> SampleResult:
+           token_state_rows: torch.Tensor | None = None,
+           token_state_bits: torch.Tensor | None = None) -> SampleResult:
     """Samples one token per row of ``logits`` [B, V] (float32, bfloat16 or float16, on the
     GPU; each widened exactly to fp32).
 
@@ -121,7 +122,10 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     ``logit_softcap_f16`` each capped value is rounded to float16 (the reference's shader
     stores the cap's output in an f16 buffer).  ``token_state`` int32 [R, >= V] (uint32 words,
     see ``token_state_update``) replaces ``prompt_ids``/``output_ids`` as the penalties' history;
-    ``token_state_rows`` int32 [B] picks each row's table row (None = row i).
+    ``token_state_rows`` int32 [B] picks each row's table row (None = row i);
+    ``token_state_bits`` int32 [R, >= ceil(V/32)], the table's bitmap of non-zero words (kept by
+    ``token_state_update``), lets rows that top-p alone cuts keep the single-pass top-p path
+    with their penalties.
     """
     _check_device(logits, "logits")
     cap = 0.0 if logit_softcap is None else float(logit_softcap)
@@ -151,6 +155,16 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
         if token_state.shape[1] < V:
             raise ValueError(f"token_state rows hold {token_state.shape[1]} words < vocab {V}")
         TS = token_state
+        if token_state_bits is not None:
+            _check_device(token_state_bits, "token_state_bits")
+            if (token_state_bits.dtype != torch.int32 or token_state_bits.dim() != 2
+                    or token_state_bits.stride(1) != 1):
+                raise ValueError("token_state_bits must be an int32 [rows, >= ceil(V/32)] bitmap")
+            if token_state_bits.shape[1] < (V + 31) // 32:
+                raise ValueError(f"token_state_bits rows hold {token_state_bits.shape[1]} words < "
+                                 f"ceil(vocab / 32) = {(V + 31) // 32}")
+            if token_state_bits.shape[0] != token_state.shape[0]:
+                raise ValueError("token_state_bits must have the table's rows")
         if token_state_rows is not None:
             TR = token_state_rows.to(device=dev, dtype=torch.int32).contiguous()
             if TR.shape != (B,):
@@ -211,6 +225,8 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     a.output_ids, a.output_row_stride, a.output_width, a.output_lens = _ptr(oid), ostride, owidth, _ptr(olens)
     if TS is not None:
         a.token_state, a.token_state_row_stride, a.token_state_rows = TS.data_ptr(), TS.stride(0), _ptr(TR)
+        if token_state_bits is not None:
+            a.token_state_bits, a.token_state_bits_stride = token_state_bits.data_ptr(), token_state_bits.stride(0)
     if AM is not None:
         a.allowed_mask, a.allowed_row_stride = AM.data_ptr(), AM.stride(0)
     if aid is not None:
@@ -230,15 +246,23 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
 
 
 def token_state_update(state: torch.Tensor, tokens: torch.Tensor, rows=None, prompt: bool = False,
-                       vocab: int | None = None) -> None:
+                       vocab: int | None = None, bits: torch.Tensor | None = None) -> None:
     """Counts ``tokens`` (int32 [n] on the device) as output occurrences in the token-state
     table ``state`` (int32 [R, >= V], uint32 words: bit 31 prompt flag, low bits output count),
     or with ``prompt`` sets their prompt flags.  ``rows``: int32 [n] table rows, or one int for
-    every id.  Ids outside [0, vocab) are padding (vocab defaults to the table's width)."""
+    every id.  Ids outside [0, vocab) are padding (vocab defaults to the table's width).
+    ``bits`` (int32 [R, >= ceil(V/32)]): the table's bitmap of non-zero words, whose bits of the
+    updated ids are set."""
     _check_device(state, "state")
     if state.dtype != torch.int32 or state.dim() != 2 or state.stride(1) != 1:
         raise ValueError("state must be an int32 [rows, V] table with contiguous rows")
     V = state.shape[1] if vocab is None else int(vocab)
+    if bits is not None:
+        _check_device(bits, "bits")
+        if bits.dtype != torch.int32 or bits.dim() != 2 or bits.stride(1) != 1:
+            raise ValueError("bits must be an int32 [rows, >= ceil(V/32)] bitmap")
+        if bits.shape[0] != state.shape[0] or bits.shape[1] < (V + 31) // 32:
+            raise ValueError("bits must have the table's rows and >= ceil(V/32) words per row")
     tok = tokens.to(device=state.device, dtype=torch.int32).contiguous().view(-1)
     n = tok.numel()
     R = None
@@ -250,8 +274,9 @@ def token_state_update(state: torch.Tensor, tokens: torch.Tensor, rows=None, pro
         if R.numel() != n:
             raise ValueError(f"rows has {R.numel()} entries for {n} ids")
     kind = _lib.STATE_PROMPT if prompt else _lib.STATE_OUTPUT
-    _lib.check(_lib.lib().vws_token_state_update(state.data_ptr(), state.stride(0), V, n, _ptr(R), row,
-                                                 tok.data_ptr(), kind, _stream_ptr()))
+    _lib.check(_lib.lib().vws_token_state_update(state.data_ptr(), state.stride(0), _ptr(bits),
+                                                 bits.stride(0) if bits is not None else 0, V, n,
+                                                 _ptr(R), row, tok.data_ptr(), kind, _stream_ptr()))
 
 
 def pack_allowed(allowed: torch.Tensor) -> torch.Tensor:

@@ -13,9 +13,10 @@ device tables padded with ``vocab_size``; each step gathers the scheduled rows a
 sampling, appends the sampled ids on the device, so histories are never re-uploaded.  On a GPU
 it also keeps a token-state table, one uint32 word per (request slot, token): prompt flag and
 output count, set when a request is admitted and counted once per sampled id
-(``vws_token_state_update``).  The penalties read that table at the tokens that reach the
-sampler's candidates, so a long prompt or output costs nothing per step (vLLM-v1 rebuilds the
-same prompt mask and output bin counts from the histories every step).  Host
+(``vws_token_state_update``), with a bitmap of its non-zero words.  The penalties read that
+table at the tokens that reach the sampler's candidates, and the bitmap lets rows that top-p
+alone cuts buffer their history tokens, so a long prompt or output costs nothing per step
+(vLLM-v1 rebuilds the same prompt mask and output bin counts from the histories every step).  Host
 copies of the generated ids (needed by ``SamplingMetadata.output_token_ids`` and the engine)
 come from the one device-to-host copy of the sampled ids per step.
 
@@ -84,8 +85,10 @@ class InputBatch:
         self.output_lens = torch.zeros(max_num_reqs, dtype=torch.int32, device=device)
         # per-slot token state (prompt flag | output count), on a ROCm device only: the table
         # is maintained by the library's kernels
-        self.token_state = None
+        self.token_state = self.token_state_bits = None
         if token_state and torch.device(device).type == "cuda":
+            self.token_state_bits = torch.zeros((max_num_reqs, (vocab_size + 31) // 32),
+                                                dtype=torch.int32, device=device)
             self.token_state = torch.zeros((max_num_reqs, vocab_size), dtype=torch.int32,
                                            device=device)
         self.requests: dict[str, CachedRequestState] = {}
@@ -114,9 +117,10 @@ class InputBatch:
             from .. import ops
 
             self.token_state[slot].zero_()
+            self.token_state_bits[slot].zero_()
             if prompt_token_ids:
                 ops.token_state_update(self.token_state, self.prompt_ids[slot, :len(prompt_token_ids)],
-                                       rows=slot, prompt=True)
+                                       rows=slot, prompt=True, bits=self.token_state_bits)
         return slot
 
     def remove_request(self, req_id: str) -> None:
@@ -212,6 +216,7 @@ class InputBatch:
                                else self.output_lens.index_select(0, slots)),
             token_state=self.token_state if table else None,
             token_state_rows=slots.to(torch.int32) if table else None,
+            token_state_bits=self.token_state_bits if table else None,
         ) if B else None
 
     def decode_inputs(self, req_ids: list[str]) -> tuple[torch.Tensor, torch.Tensor]:
@@ -255,7 +260,8 @@ class InputBatch:
         if self.token_state is not None:
             from .. import ops
 
-            ops.token_state_update(self.token_state, sampled, rows=slots.to(torch.int32))
+            ops.token_state_update(self.token_state, sampled, rows=slots.to(torch.int32),
+                                   bits=self.token_state_bits)
 
 
 def grammar_words(grammar_output: Any, req_ids: list[str], vocab_size: int,

@@ -24,7 +24,8 @@ Conventions the kernels rely on:
   ids banned until it is reached), ``logit_bias`` per row (token -> bias) or None.
 * ``token_state`` (this package's extension): int32 ``[R, V]`` per-request token-state table
   kept on the device by a persistent batch (bit 31: the token is in the prompt; low bits: its
-  count in the output), with ``token_state_rows`` int32 ``[B]`` giving each row's table row.
+  count in the output), with ``token_state_rows`` int32 ``[B]`` giving each row's table row and
+  ``token_state_bits`` int32 ``[R, ceil(V/32)]`` the bitmap of its non-zero words (or None).
   When set, the penalties read it instead of ``prompt_token_ids`` / ``output_token_ids``: the
   prompt mask and output bin counts vLLM-v1 rebuilds every step, kept up to date instead.
 * ``allowed_words`` (extension): int32 ``[B, ceil(V/32)]`` allowed-token bit words (bit set =
@@ -62,4 +63,5 @@ class SamplingMetadata:
     logit_bias: list[dict[int, float] | None] | None = None
     token_state: torch.Tensor | None = None
     token_state_rows: torch.Tensor | None = None
+    token_state_bits: torch.Tensor | None = None
     allowed_words: torch.Tensor | None = None

@@ -185,7 +185,8 @@ class Sampler:
             penalties = dict(repetition_penalty=m.repetition_penalties,
                              presence_penalty=m.presence_penalties,
                              frequency_penalty=m.frequency_penalties,
-                             token_state=m.token_state, token_state_rows=m.token_state_rows)
+                             token_state=m.token_state, token_state_rows=m.token_state_rows,
+                             token_state_bits=m.token_state_bits)
         elif not m.no_penalties:
             out_ids, out_lens = m.output_token_ids_tensor, m.output_token_lens
             if out_ids is None and any(m.output_token_ids):
