@@ -189,8 +189,11 @@ __device__ __noinline__ void topp_stream_hist_entry(int r, uint64_t kernarg) {
 #endif
 }
 
-template <typename T>
-__device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
+// The pass sm.pd over row r's body vectors [v0, v1) (and the edges): without, and with the
+// penalties from the token-state table (separate functions, so that the plain pass keeps its
+// registers).
+template <typename T, bool PEN>
+__device__ __forceinline__ void topp_range_body(int r, uint64_t kernarg, int v0, int v1, int edges) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
     r = __builtin_amdgcn_readfirstlane(r);
@@ -209,7 +212,7 @@ __device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, i
     d.kkeep = tp_u(sm.pd.kkeep);
     d.kmem = tp_u(sm.pd.kmem);
     TpPassAcc acc;
-    tp_pass_range<T>(a, sm, r, d, v0, v1, edges != 0, acc);
+    tp_pass_range<T, PEN>(a, sm, r, d, v0, v1, edges != 0, acc);
     tp_pass_reduce(sm, d.kind, acc);
 #else
     (void)r; (void)kernarg; (void)v0; (void)v1; (void)edges;
@@ -217,6 +220,16 @@ __device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, i
 }
 
 template <typename T>
+__device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
+    topp_range_body<T, false>(r, kernarg, v0, v1, edges);
+}
+
+template <typename T>
+__device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
+    topp_range_body<T, true>(r, kernarg, v0, v1, edges);
+}
+
+template <typename T, bool PEN>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -279,8 +292,10 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     }
     __syncthreads();
     const uint32_t slot = tp_u(sm.cp[4]);
+    const bool pen = PEN && tp_pass_pen(a, r, kind);
     if (slot == kCoopNone) {
-        topp_range_entry<T>(r, kernarg, 0, nbody, 1);
+        if (pen) topp_range_hist_entry<T>(r, kernarg, 0, nbody, 1);
+        else topp_range_entry<T>(r, kernarg, 0, nbody, 1);
         return;
     }
     CoopSlot& S = st->slot[slot];
@@ -331,7 +346,8 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     for (int k = 0; c != kCoopNone; ++k) {
         const int v0 = (int)c * cvecs;
         const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
-        topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        if (pen) topp_range_hist_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        else topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
         __syncthreads();
         if (tid == 0) {
             ++own;
@@ -450,8 +466,9 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
 // A workgroup without a row (or between two rows) runs chunks of the passes other rows opened,
 // adding its totals into their slots.  spin: poll again while rows hold slots (no row of the
 // launch is left to start, so no row waits for this workgroup's CU); otherwise return once no
-// chunk is open.
-template <typename T>
+// chunk is open.  PEN: the launch has penalties from a token-state table with its bitmap (some
+// chunks are of penalised passes; without, the function calls only the plain range function).
+template <typename T, bool PEN>
 __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int NT = kGenThreads;
@@ -549,7 +566,8 @@ __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
         const int nbody = __builtin_amdgcn_readfirstlane(sl.nbody);
         const int v0 = (int)c * cvecs;
         const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
-        topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        if (PEN && tp_pass_pen(a, r, kind)) topp_range_hist_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        else topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
         __syncthreads();
         // the next chunk, claimed while this one's totals go out (before this one counts as
         // done, so the pass cannot have been replaced meanwhile)
@@ -1878,7 +1896,8 @@ __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
     if (!a.coop_count) {
         if (long_row) {
             __syncthreads();
-            coop_help_entry<T>(kernarg, 1);
+            if (a.tbits) coop_help_entry<T, true>(kernarg, 1);
+            else coop_help_entry<T, false>(kernarg, 1);
         }
         return;
     }
@@ -1895,7 +1914,8 @@ __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
     const uint32_t how = tp_u(sm.cp[6]);
     if (how) {
         __syncthreads();
-        coop_help_entry<T>(kernarg, how == 2u ? 1 : 0);
+        if (a.tbits) coop_help_entry<T, true>(kernarg, how == 2u ? 1 : 0);
+        else coop_help_entry<T, false>(kernarg, how == 2u ? 1 : 0);
     }
 #else
     (void)kernarg;

@@ -780,29 +780,24 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
 //     streamed with the logits, or generated);
 //   * rank pass: the elements at or above the key (the rank of a sampled token that is not a
 //     candidate) into acc.n.
-// In rows with penalties from the token-state table the exact and wide passes see processed
-// values (the rank pass ranks raw ones).
-template <typename T>
+// PEN (rows with penalties from the token-state table, exact and wide passes only): the pass
+// sees processed values (the rank pass ranks raw ones).
+template <typename T, bool PEN>
 __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int r, const TpPassDesc& d,
                                               int v0, int v1, bool edges, TpPassAcc& acc) {
     constexpr int VEC = Elem<T>::kVec;
     const uint32_t tauk = d.key;
     const float Tt = d.Tt, m = d.m, lp_min = d.lp_min;
     TpPen pen{nullptr, 1.0f, 1.0f, 0.0f, 0.0f};
-    bool hist = false;
-    if (a.tstate) {
+    if (PEN) {
         pen.rep = a.rep ? a.rep[r] : 1.0f;
         pen.pres = a.pres ? a.pres[r] : 0.0f;
         pen.freq = a.freq ? a.freq[r] : 0.0f;
         pen.inv_rep = 1.0f / pen.rep;
-        hist = !(pen.rep == 1.0f && pen.pres == 0.0f && pen.freq == 0.0f);
         pen.wrow = a.tstate + (size_t)(a.trows ? a.trows[r] : r) * (size_t)a.tstride;
-        hist = __builtin_amdgcn_readfirstlane(hist ? 1 : 0) != 0;
     }
-    // the pass over the range, with or without the penalties
     auto range = [&](auto with_u, auto&& f) __attribute__((always_inline)) {
-        if (hist) tp_row_range<T, decltype(with_u)::value, true>(a, r, v0, v1, edges, pen, f);
-        else tp_row_range<T, decltype(with_u)::value, false>(a, r, v0, v1, edges, pen, f);
+        tp_row_range<T, decltype(with_u)::value, PEN>(a, r, v0, v1, edges, pen, f);
     };
     if (d.kind == kTpPassExact) {
         range(BoolC<false>{}, [&](const float* v, const float*, int, bool ok)
@@ -966,14 +961,28 @@ __device__ __forceinline__ uint32_t coop_chunk_of(uint64_t x) {
 // and the finish; defined next to the LDS they use.  Every thread calls them.
 //   topp_pass_entry: one whole pass over row r (cooperative when a slot is free); its scalar
 //     results are in sm.bc64[10..13] after a barrier; sets sm.coop_fail when a cooperative
-//     pass was not completed (the row then takes the multi-pass path);
+//     pass was not completed (the row then takes the multi-pass path).  PEN: a row with
+//     penalties from the token-state table (its range functions are separate, and so are the
+//     functions that call them, so that the others keep their registers);
 //   topp_range_entry: the pass sm.pd over the body vectors [v0, v1) of row r (and the edges),
 //     its workgroup totals into sm.bc64[10..13] as tp_pass_reduce leaves them.
-template <typename T>
+template <typename T, bool PEN>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar);
 template <typename T>
 __device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
+template <typename T>
+__device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
+
+// Whether a pass of `kind` over row r reads the rows' token-state words (penalties from the
+// table, exact and wide passes): such passes run in topp_range_hist_entry.
+__device__ __forceinline__ bool tp_pass_pen(const KArgs& a, int r, int kind) {
+    if (!a.tstate || kind == kTpPassRank) return false;
+    const float rp = a.rep ? a.rep[r] : 1.0f;
+    const float pr = a.pres ? a.pres[r] : 0.0f;
+    const float fr = a.freq ? a.freq[r] : 0.0f;
+    return __builtin_amdgcn_readfirstlane((rp == 1.0f && pr == 0.0f && fr == 0.0f) ? 0 : 1) != 0;
+}
 
 // Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
 // take the multi-pass path (VWS_FALLBACK_*).  Every return decision is uniform over the
@@ -1081,7 +1090,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     // a cooperative pass that was not completed marks sm.coop_fail; the row is handed over right
     // after it, before anything is written
     auto pass = [&](int kind, uint32_t key, int bs) __attribute__((always_inline)) {
-        topp_pass_entry<T>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        if (hist) topp_pass_entry<T, true>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        else topp_pass_entry<T, false>(kind, r, kernarg, Tt, m, lp_min, key, bs);
         __syncthreads();
     };
     for (int i = tid; i < kTpBuckets; i += NT) {
@@ -1105,11 +1115,13 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         uint32_t nxs = 0u;
         float s0b = 0.0f;
         // unit: y = x (greedy rows and T = 1, where x / T is x itself): the loop without the
-        // division, chosen once for the wave
-        auto masses = [&](auto unit) __attribute__((always_inline)) {
+        // division, chosen once for the wave; hc: a history row (a separate loop, so that rows
+        // without one compute nothing of it)
+        auto masses = [&](auto unit, auto hc) __attribute__((always_inline)) {
+            constexpr bool H = decltype(hc)::value;
             for (int i = lane; i < cnt; i += kWave) {
                 const uint32_t c0 = (uint32_t)sm.ci[wave][i];
-                const bool hm = hist && (c0 & kTpHist);  // a history token (processed value)
+                const bool hm = H && (c0 & kTpHist);  // a history token (processed value)
                 const float x = u2f(sm.ck[wave][i]);
                 const uint32_t kk = key_of(x);
                 const float y = decltype(unit)::value ? x : x / Tt;
@@ -1119,14 +1131,14 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 const uint64_t w = surv ? mass_of(e) : 0ull;
                 // raw logprobs' normaliser: x - max x is d itself for greedy rows and T = 1
                 // (without a history)
-                if (L >= 0 && !hm) s0b += hist ? exp_det(x - xmaxr) : (decltype(unit)::value ? e : exp_det(x - xmax));
+                if (L >= 0 && !hm) s0b += H ? exp_det(x - xmaxr) : (decltype(unit)::value ? e : exp_det(x - xmax));
                 const int b = tp_bucket(d);
                 const bool below = kk < tauk;
                 sm.ck[wave][i] = kk;
                 sm.ci[wave][i] = (int32_t)((c0 & kTpIdxMask) | ((uint32_t)b << 19) |
                                            (surv ? kTpSurv : 0u) | (below ? kTpBelow : 0u));
                 if (!below) {
-                    if (L > 0 && !hist) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
+                    if (L > 0 && !H) atomicAdd(&sm.h.hcnt[b], 1u);  // counts for the top-L logprobs
                     if (w) atomicAdd((unsigned long long*)&sm.h.hmass[b], (unsigned long long)w);
                     wc += w;
                 } else {
@@ -1134,13 +1146,15 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                     nxs += surv ? 1u : 0u;
                 }
                 // history rows: the top-L counts by raw bucket
-                if (hist && L > 0 && !hm && kk >= tauk) atomicAdd(&sm.h.hcnt[tp_bucket(y - mr)], 1u);
+                if (H && L > 0 && !hm && kk >= tauk) atomicAdd(&sm.h.hcnt[tp_bucket(y - mr)], 1u);
             }
         };
-        if (greedy || Tt == 1.0f) {
-            masses(BoolC<true>{});
+        if (hist) {
+            if (greedy || Tt == 1.0f) masses(BoolC<true>{}, BoolC<true>{});
+            else masses(BoolC<false>{}, BoolC<true>{});
         } else {
-            masses(BoolC<false>{});
+            if (greedy || Tt == 1.0f) masses(BoolC<true>{}, BoolC<false>{});
+            else masses(BoolC<false>{}, BoolC<false>{});
         }
         if (hist && L > 0) {
             // the listed raw entries in the top-L counts
@@ -1168,6 +1182,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         // buffered raw normaliser: read from LDS after the next barrier
         uint64_t wc = 0ull, nx = 0ull;
         double sb = 0.0;
+#pragma unroll
         for (int w = 0; w < kTpWaves; ++w) {
             wc += sm.red[w][0];
             nx += sm.red[w][2];
@@ -1224,6 +1239,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             const double err0 = tp_wave_sum_f64(mw * (k0 * ws + k1 * wz * (1.0 + 0x1p-8)));
             if (lane == 0) {
                 uint64_t Sx = 0ull;  // exact mass of the survivors buffered below the threshold
+#pragma unroll
                 for (int w = 0; w < kTpWaves; ++w) Sx += sm.red[w][1];
                 int why = 0;
                 // every element of the row outside the buffers may be a term (the floor of each
@@ -1606,11 +1622,14 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (tp_u(sm.coop_fail)) return VWS_FALLBACK_COOP;
             rk = wave == 0 ? (uint32_t)tp_u64(sm.bc64[10]) : 0u;  // the per-wave records below add up
         } else {
-            // raw values: history rows count their unmarked entries and the listed raw ones
-            for (int i = lane; i < cnt; i += kWave)
-                rk += (sm.ck[wave][i] >= ks && !(hist && ((uint32_t)sm.ci[wave][i] & kTpHist))) ? 1u : 0u;
-            if (hist)
+            if (hist) {
+                // raw values: the unmarked entries and the listed raw ones
+                for (int i = lane; i < cnt; i += kWave)
+                    rk += (sm.ck[wave][i] >= ks && !((uint32_t)sm.ci[wave][i] & kTpHist)) ? 1u : 0u;
                 for (uint32_t j = (uint32_t)tid; j < tp_u(sm.rl_n); j += NT) rk += sm.rl_key[j] >= ks ? 1u : 0u;
+            } else {
+                for (int i = lane; i < cnt; i += kWave) rk += sm.ck[wave][i] >= ks ? 1u : 0u;
+            }
             rk = (uint32_t)wave_sum_u64(rk);
         }
         uint32_t ncand = 0u;
@@ -1645,16 +1664,21 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             auto raw_in = [&](uint32_t kr) __attribute__((always_inline)) {
                 return kr >= tauk && tp_bucket((unitT ? val_of(kr) : val_of(kr) / Tt) - mr) <= bl;
             };
-            for (int i = lane; i < cnt; i += kWave) {
-                const uint32_t c = (uint32_t)sm.ci[wave][i];
-                if (hist ? ((c & kTpHist) || !raw_in(sm.ck[wave][i])) : ((c & kTpBelow) || tp_code_bucket(c) > bl))
-                    continue;
-                const uint32_t pos = atomicAdd(&sm.bc[7], 1u);
-                if (pos < (uint32_t)kTpLpCap) {
-                    sm.lp.key[pos] = sm.ck[wave][i];
-                    sm.lp.idx[pos] = (int32_t)(c & imask);
+            auto gather = [&](auto hc) __attribute__((always_inline)) {
+                for (int i = lane; i < cnt; i += kWave) {
+                    const uint32_t c = (uint32_t)sm.ci[wave][i];
+                    if (decltype(hc)::value ? ((c & kTpHist) || !raw_in(sm.ck[wave][i]))
+                                            : ((c & kTpBelow) || tp_code_bucket(c) > bl))
+                        continue;
+                    const uint32_t pos = atomicAdd(&sm.bc[7], 1u);
+                    if (pos < (uint32_t)kTpLpCap) {
+                        sm.lp.key[pos] = sm.ck[wave][i];
+                        sm.lp.idx[pos] = (int32_t)(c & imask);
+                    }
                 }
-            }
+            };
+            if (hist) gather(BoolC<true>{});
+            else gather(BoolC<false>{});
             if (hist) {
                 for (uint32_t j = (uint32_t)tid; j < tp_u(sm.rl_n); j += NT) {
                     if (!raw_in(sm.rl_key[j])) continue;
