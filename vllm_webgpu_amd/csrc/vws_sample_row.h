@@ -147,8 +147,8 @@ __device__ __forceinline__ int rhash_find(const RowSmem& sm, int t) {
 // share it.
 __shared__ RowShared g_row_sh;
 
-__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw, int hist) {
-    return topp_compact(g_row_sh.t, w, cnt, aw, c, want_raw != 0, hist != 0);
+__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw) {
+    return topp_compact(g_row_sh.t, w, cnt, aw, c, want_raw != 0);
 }
 
 __device__ __noinline__ void topp_rank_members_entry(uint32_t ng, float m) {
@@ -174,18 +174,33 @@ __device__ __forceinline__ KArgs kargs_at(uint64_t kernarg) {
 }
 #endif
 
-// The top-p stream of a row with penalties from the token-state table (its bitmap staged in
-// LDS, every history token buffered): out of line, so that the common stream's code and
-// registers stay as they are.
+// The stream of a history row (its bitmap into LDS first: topp_hist_begin), out of line: the
+// other rows' stream keeps its code and registers.
 template <typename T>
 __device__ __noinline__ void topp_stream_hist_entry(int r, uint64_t kernarg) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
     r = __builtin_amdgcn_readfirstlane(r);
     const RowP prm = row_params(a, r);
-    topp_stream<T, true>(a, g_row_sh.t, r, prm);
+    const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
+    topp_stream<T>(a, g_row_sh.t, r, prm, fill);
 #else
     (void)r; (void)kernarg;
+#endif
+}
+
+// A history row's buffers after its stream (topp_hist_prepare), out of line: rows without a
+// history keep the finish's registers.
+template <typename T>
+__device__ __noinline__ int topp_hist_entry(int r, uint64_t kernarg, uint32_t tauk, float xmaxr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KArgs a = kargs_at(kernarg);
+    r = __builtin_amdgcn_readfirstlane(r);
+    const RowP prm = row_params(a, r);
+    return topp_hist_prepare<T>(a, g_row_sh.t, r, prm, tp_u(tauk), tp_uf(xmaxr));
+#else
+    (void)r; (void)kernarg; (void)tauk; (void)xmaxr;
+    return 0;
 #endif
 }
 
@@ -1866,8 +1881,13 @@ __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logit
         // a top-p row in progress may open a cooperative pass
         if (threadIdx.x == 0 && a.coop) ag_add64(&a.coop->wgs, kCoopPending);
         const RowP prm = row_params(a, r);
-        if (prm.has_hist) topp_stream_hist_entry<T>(r, kernarg);
-        else topp_stream<T, false>(a, g_row_sh.t, r, prm);
+        if (prm.has_hist) {
+            // history rows: their bitmap into LDS first (a copy of the stream of its own)
+            const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
+            topp_stream<T>(a, g_row_sh.t, r, prm, fill);
+        } else {
+            topp_stream<T>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+        }
         why = topp_finish<T>(a, g_row_sh.t, r, prm, kernarg);
         // done with it: no longer pending, and no longer holding slots (thread 0 set the mark)
         if (threadIdx.x == 0 && a.coop)

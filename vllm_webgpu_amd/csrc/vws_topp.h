@@ -24,11 +24,12 @@
 //     logprobs come from the candidates (top-L, rank) and the sums (log-sum-exp); a sampled
 //     token below the candidates is ranked by one more pass.
 // Rows with penalties from a token-state table that comes with its bitmap of non-zero words
-// stage that bitmap in LDS and buffer every history token whatever its value, so that nothing
-// outside the buffers is penalised (the sums see raw values, which are then the processed ones);
-// the finish gives the buffered history tokens their processed values from their words.  Rows
-// with penalties from id lists, logits processors, an allowed mask or the soft cap, rows whose
-// buffers overflow (ties) and the rare rows listed under VWS_FALLBACK_* take the multi-pass path
+// stream their raw values like any other row; the finish stages the bitmap in LDS, adds the
+// history tokens the stream did not buffer to the buffers (taking their terms out of the sums),
+// so that nothing outside the buffers is penalised, and gives every history token its processed
+// value from its word.  Rows with penalties from id lists, logits processors, an allowed mask or
+// the soft cap, rows whose buffers overflow (ties) and the rare rows listed under VWS_FALLBACK_*
+// take the multi-pass path
 // instead; nothing is written for them here.
 #pragma once
 
@@ -92,7 +93,7 @@ struct TopPSmem {
     uint32_t ck[kTpWaves][kTpSlots];
     int32_t ci[kTpWaves][kTpSlots];
     union {
-        uint32_t hb[kTpHistWords];        // stream of a history row: bit t = token t's word is non-zero
+        uint32_t hb[kTpHistWords];        // finish of a history row, before the masses: bit t = token t's word is non-zero
         struct {
             uint64_t hmass[kTpBuckets];   // finish: exact masses of the surviving candidates
             uint32_t hcnt[kTpBuckets];    // and the number of candidates per bucket (top-L logprobs)
@@ -100,6 +101,7 @@ struct TopPSmem {
     };
     union {
         uint32_t rhist[kTpWaves][256];    // stream: per-wave radix-select scratch
+        uint32_t hl[2 * kTpGather];       // finish of a history row: unbuffered history tokens
         struct {
             uint64_t key[kTpGather];      // boundary bucket: key(y) << 32 | index
         } g;
@@ -123,6 +125,8 @@ struct TopPSmem {
     uint32_t wMax[kTpWaves];              // largest buffered key (raw values)
     uint32_t wMaxP[kTpWaves];             // history rows: largest processed key
     float wS0h[kTpWaves];                 // history rows: their history tokens' raw normaliser terms
+    double wSub[kTpWaves], wSRsub[kTpWaves];  // history rows: stream terms of the tokens added after it
+    uint32_t hl_n;
     // history rows with raw logprobs: the history tokens at or above the threshold by raw value
     // (their buffered entries hold processed values): raw keys and indices
     uint32_t rl_key[kTpRawCap];
@@ -161,7 +165,7 @@ struct TpDrop {
 };
 
 // Out of line (compaction is rare); defined next to the LDS it works on.
-__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw, int hist);
+__device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, float c, int want_raw);
 
 // Whether the single-pass top-p path may serve the row.
 __device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
@@ -220,15 +224,15 @@ struct TpBuf {
         }
     }
     // Stores the candidates of one vector of every lane (elements v[j] >= tauf of a vector in
-    // the row, okv, and history tokens: bit j of hb; first index i0; bal[j] the wave's ballot of
-    // element j's test), with one capacity check for the whole vector: every lane writes,
-    // without branches, a candidate into its slot (placed by mbcnt) and anything else into its
-    // spare slot past the capacity.  Wave-uniform call.  A full buffer marks the row for the
-    // multi-pass path (the stream compacts every half iteration, from kTpSoft entries on, so
-    // this takes more than kTpCapW - kTpSoft candidates in half an iteration of one wave).
+    // the row, okv; first index i0; bal[j] the wave's ballot of element j's test), with one
+    // capacity check for the whole vector: every lane writes, without branches, a candidate into
+    // its slot (placed by mbcnt) and anything else into its spare slot past the capacity.
+    // Wave-uniform call.  A full buffer marks the row for the multi-pass path (the stream
+    // compacts every half iteration, from kTpSoft entries on, so this takes more than
+    // kTpCapW - kTpSoft candidates in half an iteration of one wave).
     template <int VEC>
     __device__ __forceinline__ void append_vec(TopPSmem& sm, const float* v, const uint64_t* bal,
-                                               bool okv, int i0, uint32_t hb) {
+                                               bool okv, int i0) {
         int tot = 0;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) tot += __popcll(bal[j]);
@@ -243,11 +247,10 @@ struct TpBuf {
         for (int j = 0; j < VEC; ++j) {
             const int at = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[j] >> 32),
                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal[j], (uint32_t)base));
-            const bool hj = ((hb >> j) & 1u) != 0u;
-            const bool c = okv & ((v[j] >= tauf) | hj);  // the lanes of bal[j] (no short-circuit branch)
+            const bool c = okv & (v[j] >= tauf);  // the lanes of bal[j] (no short-circuit branch)
             const int pos = c ? at : spare;
             sm.ck[w][pos] = f2u(v[j]);
-            sm.ci[w][pos] = (int32_t)((uint32_t)(i0 + j) | (hj ? kTpHist : 0u));
+            sm.ci[w][pos] = i0 + j;
             base += __popcll(bal[j]);
         }
         cnt = base;
@@ -289,23 +292,17 @@ __device__ __forceinline__ void topp_rank_members(TopPSmem& sm, uint32_t ng, flo
 // Out of line (defined next to the LDS it works on).
 __device__ __noinline__ void topp_rank_members_entry(uint32_t ng, float m);
 
-// Keeps the kTpKeep largest values (ties included) of wave w's buffer, and its history tokens,
-// and raises its threshold to the smallest kept value; the dropped entries are returned as terms
-// of the approximate sum.
+// Keeps the kTpKeep largest values (ties included) of wave w's buffer and raises its threshold
+// to the smallest kept value; the dropped entries are returned as terms of the approximate sum.
 __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, float aw, float c,
-                                               bool want_raw, bool hist) {
+                                               bool want_raw) {
     TpDrop d{0.0, 0.0, 0.0f, 0u, 0};
     const int lane = lane_id();
     uint32_t* ck = sm.ck[w];
     int32_t* ci = sm.ci[w];
-    int nh = 0;  // history tokens (kept whatever their value: the rest make up kTpKeep)
-    for (int base = 0; base < cnt; base += kWave) {
-        const int i = base + lane;
-        if (i < cnt) ck[i] = key_of(u2f(ck[i]));  // raw bits -> keys
-        if (hist) nh += __popcll(wave_ballot(i < cnt && ((uint32_t)ci[i] & kTpHist)));
-    }
+    for (int i = lane; i < cnt; i += kWave) ck[i] = key_of(u2f(ck[i]));  // raw bits -> keys
     wave_sync();
-    const uint32_t kth = wave_kth_largest(ck, cnt, kTpKeep - nh > 1 ? kTpKeep - nh : 1, sm.rhist[w]);
+    const uint32_t kth = wave_kth_largest(ck, cnt, kTpKeep, sm.rhist[w]);
     int out = 0;
     for (int base = 0; base < cnt; base += kWave) {
         const int i = base + lane;
@@ -315,7 +312,7 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
         if (i < cnt) {
             kk = ck[i];
             ii = ci[i];
-            keep = kk >= kth || (hist && ((uint32_t)ii & kTpHist));  // history tokens stay buffered
+            keep = kk >= kth;
             if (!keep) {
                 const float x = val_of(kk);
                 float z;
@@ -343,10 +340,11 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
 }
 
 // The stream over row r.  Publishes each wave's results into sm; topp_finish completes the row.
-// HIST: a row with penalties from the token-state table; its bitmap is staged in sm.hb and every
-// history token is buffered.
-template <typename T, bool HIST>
-__device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r, const RowP& prm) {
+// fill: the entries per wave the seed threshold aims at (less than kTpFill of the slots when
+// history tokens will need some).
+template <typename T>
+__device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
+                                            float fill) {
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int U = 32 / VEC;
@@ -369,28 +367,9 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
-    // history rows: the bitmap's words are read first (their stores into LDS wait only for them)
-    constexpr int kHbPer = (kTpHistWords + NT - 1) / NT;
-    uint32_t hbw[HIST ? kHbPer : 1];
-    const int nhw = (V + 31) >> 5;
-    if (HIST) {
-        const uint32_t* brow = a.tbits + (size_t)prm.trow * (size_t)a.tbstride;
-#pragma unroll
-        for (int q = 0; q < kHbPer; ++q) {
-            const int i = q * NT + tid;
-            hbw[q] = i < nhw ? brow[i] : 0u;
-            if (i == nhw - 1 && (V & 31)) hbw[q] &= (1u << (V & 31)) - 1u;  // no token past V
-        }
-    }
     float A[U][VEC], Bq[U][VEC];
     load_iter(A, 0);
     load_iter(Bq, 1);
-    if (HIST) {
-#pragma unroll
-        for (int q = 0; q < kHbPer; ++q)
-            if (q * NT + tid < kTpHistWords) sm.hb[q * NT + tid] = hbw[q];
-    }
-
     // seed: a threshold from the lane maxima over the first iteration.  A lane's maximum over its
     // E elements reaches tau with probability 1 - (1 - phi)^E when a fraction phi of the
     // elements does, so a wave's m-th largest lane maximum, m = 64 (1 - (1 - phi)^E), admits
@@ -405,21 +384,6 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         for (int j = 0; j < VEC; ++j) lmax = ok ? __builtin_fmaxf(lmax, A[q][j]) : lmax;
     }
     const float share = (float)V / (float)kTpWaves;
-    float fill = kTpFill * (float)kTpCapW;
-    if (HIST) {
-        // history tokens take slots of their own: the estimate of a wave's share of them (from
-        // the bitmap words this wave staged, a 1/16 sample of the row's) leaves the fill target
-        uint32_t nb = 0u, nwd = 0u;
-#pragma unroll
-        for (int q = 0; q < kHbPer; ++q) {
-            nb += (uint32_t)__popc(hbw[q]);
-            nwd += (q * NT + tid < nhw) ? 1u : 0u;
-        }
-        nb = (uint32_t)wave_sum_u64(nb);
-        nwd = (uint32_t)wave_sum_u64(nwd);
-        const float est = nwd ? (float)nb * (float)nhw / (float)nwd : 0.0f;  // the row's
-        fill = __builtin_fmaxf(fill - est / (float)kTpWaves, (float)kWave);
-    }
     const float phi = __builtin_fminf(1.0f, fill / share);
     const bool seeded = phi < 1.0f && nbody > 0;
     uint32_t tw = 0u;
@@ -432,7 +396,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     }
     if (tid == 0) sm.status = 0u;
     if (lane == 0) sm.bc[wave] = tw;  // bc is free until the finish's first barrier
-    __syncthreads();  // (also publishes the history bitmap)
+    __syncthreads();
     uint32_t tau0 = 0u;
     if (seeded) tau0 = wave_mth_largest64(lane < kTpWaves ? sm.bc[lane] : 0u, kTpWaves / 2);
     if (tau0 <= 0x007FFFFFu || tau0 >= 0xFF800000u) tau0 = 0u;  // -inf, or +inf (degenerate row)
@@ -451,28 +415,21 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     // term for NaN and -inf).  The ballots of the element tests decide whether any lane appends
     // (no separate vector test: a wave almost always has a candidate somewhere in a vector
     // position).
-    auto consume = [&](const float* v, int i0, bool okv, uint32_t hv) __attribute__((always_inline)) {
-        uint32_t hb = 0u;
-        if (HIST) {
-            // bits i0 .. i0 + VEC - 1 of the bitmap (i0 need not be aligned: a 64-bit window)
-            const uint32_t w = okv ? ((uint32_t)i0 >> 5) : 0u;
-            const uint64_t win = (uint64_t)sm.hb[w] | ((uint64_t)sm.hb[w + 1] << 32);
-            hb = (uint32_t)(win >> ((uint32_t)i0 & 31u)) & hv;
-        }
+    auto consume = [&](const float* v, int i0, bool okv) __attribute__((always_inline)) {
         uint64_t bal[VEC];
         uint64_t any = 0ull;
         // ballots of single compares (the compiler takes their lane masks as they are)
         const uint64_t okm = wave_ballot(okv);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            bal[j] = wave_ballot((v[j] >= cb.tauf) || (HIST && ((hb >> j) & 1u))) & okm;
+            bal[j] = wave_ballot(v[j] >= cb.tauf) & okm;
             any |= bal[j];
         }
-        if (any) cb.append_vec<VEC>(sm, v, bal, okv, i0, hb);
+        if (any) cb.append_vec<VEC>(sm, v, bal, okv, i0);
         float s = 0.0f, z = 0.0f, sr = 0.0f;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            const bool inc = okv && !(v[j] >= cb.tauf) && !(HIST && ((hb >> j) & 1u));
+            const bool inc = okv && !(v[j] >= cb.tauf);
             float zj;
             const float t = tp_term(v[j], aw, c, zj);
             const float tt = inc ? t : 0.0f;
@@ -491,7 +448,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     // keeps the buffer's fill at most kTpSoft every half iteration: the dropped entries join the sum
     auto shrink = [&]() __attribute__((always_inline)) {
         if (cb.cnt > kTpSoft && !cb.ovf) {
-            const TpDrop d = topp_compact_entry(wave, cb.cnt, aw, c, want_raw ? 1 : 0, HIST ? 1 : 0);
+            const TpDrop d = topp_compact_entry(wave, cb.cnt, aw, c, want_raw ? 1 : 0);
             acc += d.s;
             accr += d.sr;
             accz += d.z;
@@ -505,7 +462,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         for (int q = 0; q < U; ++q) {
             if (q == U / 2) shrink();
             const int vi = (it * U + q) * NT + t;
-            consume(buf[q], sl.a + vi * VEC, vi < nbody, (1u << VEC) - 1u);
+            consume(buf[q], sl.a + vi * VEC, vi < nbody);
         }
     };
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
@@ -524,14 +481,10 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         int i0 = 0;
         if (tid <= 1) i0 = sl.load_edge(tid, v);
         const int end = tid == 0 ? sl.a : V;
-        uint32_t hv = 0u;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-            const bool in = tid <= 1 && i0 + j < end;
-            if (!in) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
-            hv |= in ? (1u << j) : 0u;
-        }
-        consume(v, i0, true, hv);
+        for (int j = 0; j < VEC; ++j)
+            if (!(tid <= 1 && i0 + j < end)) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
+        consume(v, i0, true);
     }
 
     // publish the wave's results
@@ -973,6 +926,10 @@ template <typename T>
 __device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
 template <typename T>
 __device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
+template <typename T>
+__device__ __noinline__ int topp_hist_entry(int r, uint64_t kernarg, uint32_t tauk, float xmaxr);
+template <typename T>
+__device__ __noinline__ void topp_stream_hist_entry(int r, uint64_t kernarg);
 
 // Whether a pass of `kind` over row r reads the rows' token-state words (penalties from the
 // table, exact and wide passes): such passes run in topp_range_hist_entry.
@@ -982,6 +939,179 @@ __device__ __forceinline__ bool tp_pass_pen(const KArgs& a, int r, int kind) {
     const float pr = a.pres ? a.pres[r] : 0.0f;
     const float fr = a.freq ? a.freq[r] : 0.0f;
     return __builtin_amdgcn_readfirstlane((rp == 1.0f && pr == 0.0f && fr == 0.0f) ? 0 : 1) != 0;
+}
+
+// History rows, before the stream: the row's bitmap of history tokens into LDS (sm.hb, kept
+// through the stream), and the seed's fill target less the history tokens' share of the
+// slots (the finish adds every history token the stream does not buffer).  Uniform result.
+__device__ __forceinline__ float topp_hist_begin(const KArgs& a, TopPSmem& sm, const RowP& prm) {
+    constexpr int NT = kGenThreads;
+    const int tid = threadIdx.x;
+    const int V = a.V;
+    const int nhw = (V + 31) >> 5;
+    const uint32_t* brow = a.tbits + (size_t)prm.trow * (size_t)a.tbstride;
+    uint32_t n = 0u;
+    for (int i = tid; i < nhw; i += NT) {
+        uint32_t b = brow[i];
+        if (i == nhw - 1 && (V & 31)) b &= (1u << (V & 31)) - 1u;  // no token past V
+        sm.hb[i] = b;
+        n += (uint32_t)__popc(b);
+    }
+    n = (uint32_t)wave_sum_u64(n);
+    if (tid == 0) sm.bc[0] = 0u;
+    __syncthreads();
+    if ((tid & 63) == 0) atomicAdd(&sm.bc[0], n);
+    __syncthreads();
+    const float nh = (float)tp_u(sm.bc[0]);
+    __syncthreads();  // bc is the stream's from here on
+    return __builtin_fmaxf(kTpFill * (float)kTpCapW - 1.1f * nh / (float)kTpWaves, (float)kWave);
+}
+
+// History rows (penalties from the token-state table with its bitmap), after the stream (the
+// bitmap is in LDS: topp_hist_begin): the buffered history tokens are marked (bit 18 of the index word is
+// free: V <= kTpHistMaxV) and take their processed values from their token-state words, in
+// place; the others, which the stream summed, join the buffers with their processed values and
+// their terms come out of the sums (wSub, wSRsub).  With raw logprobs, the history tokens' raw
+// normaliser terms are added up (wS0h) and those at or above the threshold by raw value are
+// listed (rl_*: the raw top-L and rank need them).  Leaves the waves' largest processed keys in
+// wMaxP.  Returns 0, or the reason the row takes the multi-pass path (uniform).
+template <typename T>
+__device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
+                                                 uint32_t tauk, float xmaxr) {
+    constexpr int NT = kGenThreads;
+    constexpr int G = 16;  // buffered entries per lane whose words are gathered together
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int L = a.L;
+    const bool greedy = prm.greedy;
+    const int V = a.V;
+    const uint32_t* trw = a.tstate + (size_t)prm.trow * (size_t)a.tstride;
+    // a history token: its processed value, and with raw logprobs its raw normaliser term and
+    // (at or above the threshold by raw value) its listing
+    float s0h = 0.0f;
+    uint32_t mx = 0u;
+    auto history = [&](float x, uint32_t wd, uint32_t t) __attribute__((always_inline)) {
+        const float y = apply_hashed(x, wd & kStateMask, 0.0f, prm.rep, prm.inv_rep, prm.freq, prm.pres);
+        if (L >= 0) {
+            s0h += exp_det(x - xmaxr);
+            const uint32_t kx = key_of(x);
+            if (kx >= tauk) {
+                const uint32_t pos = atomicAdd(&sm.rl_n, 1u);
+                if (pos < (uint32_t)kTpRawCap) {
+                    sm.rl_key[pos] = kx;
+                    sm.rl_idx[pos] = (int32_t)t;
+                }
+            }
+        }
+        return y;
+    };
+    // (the row's bitmap of history tokens was staged in LDS before the stream)
+    const int nhw = (V + 31) >> 5;
+    if (tid == 0) {
+        sm.rl_n = 0u;
+        sm.hl_n = 0u;
+    }
+    __syncthreads();
+    // the buffered history tokens: marked, their bits cleared, their words gathered (G entries
+    // per lane at a time) and their processed values written in place
+    const int cnt0 = (int)tp_u(sm.wCnt[wave]);
+    for (int base = 0; base < cnt0; base += G * kWave) {
+        uint32_t cw[G], wd[G];
+        bool h[G];
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            const int i = base + q * kWave + lane;
+            cw[q] = i < cnt0 ? (uint32_t)sm.ci[wave][i] : 0u;
+            const uint32_t bit = 1u << (cw[q] & 31u);
+            h[q] = i < cnt0 && (sm.hb[(cw[q] & kTpIdxMask) >> 5] & bit) != 0u;
+            if (h[q]) atomicAnd(&sm.hb[(cw[q] & kTpIdxMask) >> 5], ~bit);
+        }
+#pragma unroll
+        for (int q = 0; q < G; ++q) wd[q] = h[q] ? trw[cw[q] & kTpIdxMask] : 0u;
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            const int i = base + q * kWave + lane;
+            if (i >= cnt0) continue;
+            float y = u2f(sm.ck[wave][i]);
+            if (h[q]) {
+                y = history(y, wd[q], cw[q] & kTpIdxMask);
+                sm.ck[wave][i] = f2u(y);
+                sm.ci[wave][i] = (int32_t)(cw[q] | kTpHist);
+            }
+            const uint32_t ky = key_of(y);
+            mx = ky > mx ? ky : mx;
+        }
+    }
+    __syncthreads();
+    // the others were summed by the stream: listed (a chunk of NT bitmap words at a time) and,
+    // once the list holds half its capacity or the bitmap is done, their logits and words
+    // gathered together; their exact terms (of the approximate sum and of the raw one, as the
+    // stream computed them) come out of the sums, and they join the buffers with their processed
+    // values, consecutive entries in different waves
+    const T* lrow = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
+    const float cz = greedy ? kLog2e : kLog2e / prm.T;
+    const bool want_raw = L >= 0 && !greedy && prm.T != 1.0f;
+    const float aws = tp_uf(sm.anchor);
+    constexpr uint32_t kCap = 2u * (uint32_t)kTpGather;
+    double sub = 0.0, subr = 0.0;
+    int cntw = cnt0;
+    for (int w0 = 0; w0 < nhw; w0 += NT) {
+        if (w0 + tid < nhw) {
+            uint32_t b = sm.hb[w0 + tid];
+            while (b) {
+                const uint32_t j = (uint32_t)__builtin_ctz(b);
+                b &= b - 1u;
+                const uint32_t pos = atomicAdd(&sm.hl_n, 1u);
+                if (pos < kCap) sm.hl[pos] = (uint32_t)(w0 + tid) * 32u + j;
+            }
+        }
+        __syncthreads();
+        const uint32_t nl = tp_u(sm.hl_n);
+        if (nl > kCap) return VWS_FALLBACK_OVERFLOW;
+        if (nl < kCap / 2 && w0 + NT < nhw) continue;  // (uniform)
+        for (uint32_t base = 0; base < nl; base += NT) {
+            const uint32_t j = base + (uint32_t)(lane * kTpWaves + wave);
+            const bool in = j < nl;
+            const uint32_t t = in ? sm.hl[j] : 0u;
+            const float x = in ? Elem<T>::load1(lrow + t) : 0.0f;
+            const uint32_t wd = in ? trw[t] : 0u;
+            float y = 0.0f;
+            if (in) {
+                float z;
+                sub += (double)tp_term(x, aws, cz, z);
+                if (want_raw) subr += (double)tp_term(x, aws, kLog2e, z);
+                y = history(x, wd, t);
+                const uint32_t ky = key_of(y);
+                mx = ky > mx ? ky : mx;
+            }
+            const uint64_t bal = wave_ballot(in);
+            const int pos = cntw + lane_prefix(bal);
+            if (in && pos < kTpCapW) {
+                sm.ck[wave][pos] = f2u(y);
+                sm.ci[wave][pos] = (int32_t)(t | kTpHist);
+            }
+            cntw += __popcll(bal);
+        }
+        __syncthreads();  // the list's last readers are done
+        if (tid == 0) sm.hl_n = 0u;
+        __syncthreads();
+    }
+    sub = tp_wave_sum_f64(sub);
+    subr = tp_wave_sum_f64(subr);
+    mx = wave_max_u32(mx);
+    s0h = (float)tp_wave_sum_f64((double)s0h);
+    if (lane == 0) {
+        sm.wSub[wave] = sub;
+        sm.wSRsub[wave] = subr;
+        sm.wMaxP[wave] = mx;
+        sm.wS0h[wave] = s0h;
+        sm.wCnt[wave] = (uint32_t)(cntw < kTpCapW ? cntw : kTpCapW);
+        if (cntw > kTpCapW) atomicOr(&sm.status, 1u);
+    }
+    __syncthreads();
+    if (sm.status != 0u) return VWS_FALLBACK_OVERFLOW;
+    if (tp_u(sm.rl_n) > (uint32_t)kTpRawCap) return VWS_FALLBACK_TOPL;
+    return 0;
 }
 
 // Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
@@ -1019,60 +1149,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     const float xmaxr = val_of(maxr);  // raw maximum (the raw logprobs)
     uint32_t maxk = maxr;
     if (hist) {
-        // the buffered history tokens take their processed values from their token-state words
-        // (gathered G entries per lane at a time), in place, keeping their mark; with raw
-        // logprobs, their raw normaliser terms are added up here and those at or above the
-        // threshold by raw value are listed (the raw top-L and rank need them)
-        const uint32_t* trw = a.tstate + (size_t)prm.trow * (size_t)a.tstride;
-        const int cnt0 = (int)tp_u(sm.wCnt[wave]);
-        uint32_t mx = 0u;
-        float s0h = 0.0f;
-        if (tid == 0) sm.rl_n = 0u;
-        __syncthreads();
-        constexpr int G = 8;
-        for (int base = 0; base < cnt0; base += G * kWave) {
-            uint32_t cw[G], wd[G];
-#pragma unroll
-            for (int q = 0; q < G; ++q) {
-                const int i = base + q * kWave + lane;
-                cw[q] = i < cnt0 ? (uint32_t)sm.ci[wave][i] : 0u;
-            }
-#pragma unroll
-            for (int q = 0; q < G; ++q)
-                wd[q] = (cw[q] & kTpHist) ? (trw[cw[q] & (kTpHist - 1u)] & kStateMask) : 0u;
-#pragma unroll
-            for (int q = 0; q < G; ++q) {
-                const int i = base + q * kWave + lane;
-                if (i >= cnt0) continue;
-                const float x = u2f(sm.ck[wave][i]);
-                float y = x;
-                if (cw[q] & kTpHist) {
-                    y = apply_hashed(x, wd[q], 0.0f, prm.rep, prm.inv_rep, prm.freq, prm.pres);
-                    sm.ck[wave][i] = f2u(y);
-                    if (L >= 0) {
-                        s0h += exp_det(x - xmaxr);
-                        const uint32_t kx = key_of(x);
-                        if (kx >= tauk) {
-                            const uint32_t pos = atomicAdd(&sm.rl_n, 1u);
-                            if (pos < (uint32_t)kTpRawCap) {
-                                sm.rl_key[pos] = kx;
-                                sm.rl_idx[pos] = (int32_t)(cw[q] & (kTpHist - 1u));
-                            }
-                        }
-                    }
-                }
-                const uint32_t ky = key_of(y);
-                mx = ky > mx ? ky : mx;
-            }
-        }
-        mx = wave_max_u32(mx);
-        s0h = (float)tp_wave_sum_f64((double)s0h);
-        if (lane == 0) {
-            sm.wMaxP[wave] = mx;
-            sm.wS0h[wave] = s0h;
-        }
-        __syncthreads();
-        if (tp_u(sm.rl_n) > (uint32_t)kTpRawCap) return VWS_FALLBACK_TOPL;
+        // every history token into the buffers with its processed value (out of line)
+        if (const int why = topp_hist_entry<T>(r, kernarg, tauk, xmaxr)) return why;
         maxk = 0u;
 #pragma unroll
         for (int w = 0; w < kTpWaves; ++w) maxk = sm.wMaxP[w] > maxk ? sm.wMaxP[w] : maxk;
@@ -1111,6 +1189,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     // raw entries at or above the threshold) come from the pre-pass
     {
         const float mr = (greedy || Tt == 1.0f) ? xmaxr : xmaxr / Tt;  // history rows: raw buckets
+        const bool same_max = maxk == maxr;  // x - max x is then what the rows without a history use
         uint64_t wc = 0ull, sx = 0ull;
         uint32_t nxs = 0u;
         float s0b = 0.0f;
@@ -1131,7 +1210,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                 const uint64_t w = surv ? mass_of(e) : 0ull;
                 // raw logprobs' normaliser: x - max x is d itself for greedy rows and T = 1
                 // (without a history)
-                if (L >= 0 && !hm) s0b += H ? exp_det(x - xmaxr) : (decltype(unit)::value ? e : exp_det(x - xmax));
+                if (L >= 0 && !hm) s0b += (H && !same_max) ? exp_det(x - xmaxr) : (decltype(unit)::value ? e : exp_det(x - xmax));
                 const int b = tp_bucket(d);
                 const bool below = kk < tauk;
                 sm.ck[wave][i] = kk;
@@ -1235,7 +1314,10 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             const double k1 = ((Tt != 1.0f ? 2.0 : 1.0) + 4.0) * ln2 * 0x1p-24;
             const double ws = lane < kTpWaves ? sm.wS[lane] : 0.0;
             const double wz = lane < kTpWaves ? (double)sm.wZ[lane] : 0.0;
-            const double sap = tp_wave_sum_f64(mw * ws);
+            // history rows: the terms of the tokens added to the buffers after the stream come
+            // out of the centre (the error bound stays that of the stream's sum)
+            const double wsub = (hist && lane < kTpWaves) ? sm.wSub[lane] : 0.0;
+            const double sap = tp_wave_sum_f64(mw * (ws - wsub));
             const double err0 = tp_wave_sum_f64(mw * (k0 * ws + k1 * wz * (1.0 + 0x1p-8)));
             if (lane == 0) {
                 uint64_t Sx = 0ull;  // exact mass of the survivors buffered below the threshold
@@ -1646,7 +1728,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             if (lane == 0) sm.red[wave][3] = rk;
             if (wave == 0) {
                 // log-sum-exp of the raw logits: the buffered part plus the stream's terms
-                const double sw = lane < kTpWaves ? ((greedy || Tt == 1.0f) ? sm.wS[lane] : sm.wSR[lane]) : 0.0;
+                const bool u1 = greedy || Tt == 1.0f;
+                const double sw = lane < kTpWaves ? ((u1 ? sm.wS[lane] : sm.wSR[lane]) -
+                                                     (hist ? (u1 ? sm.wSub[lane] : sm.wSRsub[lane]) : 0.0)) : 0.0;
                 const double s0 = sm.tot_s0b + tp_wave_sum_f64(sw) * exp((double)aw - (double)sm.xr);
                 if (lane == 0) sm.bc64[8] = (uint64_t)__double_as_longlong(s0);
             }
