@@ -174,21 +174,6 @@ __device__ __forceinline__ KArgs kargs_at(uint64_t kernarg) {
 }
 #endif
 
-// The stream of a history row (its bitmap into LDS first: topp_hist_begin), out of line: the
-// other rows' stream keeps its code and registers.
-template <typename T>
-__device__ __noinline__ void topp_stream_hist_entry(int r, uint64_t kernarg) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const KArgs a = kargs_at(kernarg);
-    r = __builtin_amdgcn_readfirstlane(r);
-    const RowP prm = row_params(a, r);
-    const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
-    topp_stream<T>(a, g_row_sh.t, r, prm, fill);
-#else
-    (void)r; (void)kernarg;
-#endif
-}
-
 // A history row's buffers after its stream (topp_hist_prepare), out of line: rows without a
 // history keep the finish's registers.
 template <typename T>

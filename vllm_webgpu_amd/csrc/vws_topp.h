@@ -928,8 +928,6 @@ template <typename T>
 __device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
 template <typename T>
 __device__ __noinline__ int topp_hist_entry(int r, uint64_t kernarg, uint32_t tauk, float xmaxr);
-template <typename T>
-__device__ __noinline__ void topp_stream_hist_entry(int r, uint64_t kernarg);
 
 // Whether a pass of `kind` over row r reads the rows' token-state words (penalties from the
 // table, exact and wide passes): such passes run in topp_range_hist_entry.
