@@ -351,7 +351,7 @@ def pmc_traffic_bytes(config: int):
         text = open(path).read()
     except OSError:
         return None
-    m = re.search(r"^\| `void vws::row_kernel<[a-z ]+>\([^`]*` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
+    m = re.search(r"^\| `void vws::row_kernel<[a-z ,]+>\([^`]*` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
                   text, re.M)
     return None if m is None else float(m.group(1)) * 1e6
 

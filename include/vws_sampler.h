@@ -40,6 +40,7 @@ extern "C" {
 #define VWS_ERR_WORKSPACE_TOO_SMALL 3
 #define VWS_ERR_HIP 4
 #define VWS_ERR_LIMIT 5
+#define VWS_ERR_UNSUPPORTED 6   /* a call only the trace build serves (vws_trace_set) */
 
 /* logits element types */
 #define VWS_DTYPE_F32 0
@@ -277,6 +278,33 @@ int32_t vws_set_coop_wait_polls(int32_t polls);
 #define VWS_KERNEL_KINDS 6
 int vws_profile_begin(int32_t max_launches);
 int vws_profile_end(double* ms, int32_t* count);
+
+/* Phase trace of the sampling kernel (no counterpart in the reference: a diagnostic for the
+ * people who tune this library).  Only the trace build records (vllm_webgpu_amd/_vws_trace.so,
+ * `make -C vllm_webgpu_amd/csrc trace`, the same kernels compiled with -DVWS_TRACE); this build
+ * returns VWS_ERR_UNSUPPORTED.  vws_trace_set(buf, max_workgroups) makes every later vws_sample
+ * launch of the process write, for each of its first max_workgroups workgroups, the
+ * VWS_TRACE_SLOTS 64-bit words buf[wg * VWS_TRACE_SLOTS + slot] (device memory the caller owns
+ * and keeps alive): s_memrealtime stamps (a 100 MHz device clock) at the phase boundaries
+ * below, by the first thread of the workgroup's last wave, and the XCD and row the workgroup
+ * ran.  Each stamp delays the stamping wave by the clock read (the trace build's launches take
+ * a few percent longer than the product build's).  A phase a
+ * row does not reach keeps whatever the buffer held (clear it first).  vws_trace_set(NULL, 0)
+ * turns it off.  Launches that overlap on one buffer overwrite each other's records. */
+#define VWS_TRACE_SLOTS 16
+#define VWS_TRACE_ENTRY 0    /* the workgroup's first instruction */
+#define VWS_TRACE_PARAMS 1   /* single pass: the row's parameters are read (last wave) */
+#define VWS_TRACE_FIRST 2    /* single pass: the last wave holds its first iteration */
+#define VWS_TRACE_SEED 3     /* the seed threshold is published to every wave */
+#define VWS_TRACE_STREAM 4   /* every wave has streamed the row (single pass: and packed its
+                                candidates) */
+#define VWS_TRACE_ROW 5      /* the row is done (results written, or handed to another path) */
+#define VWS_TRACE_EXIT 6     /* the workgroup is done, after any help with other rows' passes */
+#define VWS_TRACE_WAVE_LOOP 7 /* single pass: the last wave has examined its share */
+#define VWS_TRACE_WAVE_PACK 8 /* single pass: the last wave has packed its candidates */
+#define VWS_TRACE_XCC 14     /* value: the XCD (XCC id) the workgroup ran on */
+#define VWS_TRACE_ROWID 15   /* value: the row the workgroup served */
+int vws_trace_set(uint64_t* buf, int32_t max_workgroups);
 
 /* Device self-test of the sampler arithmetic: evaluates fn (0 = exp_det, 1 = log_det,
  * 2 = the logit soft cap at cap 1, i.e. its tanh, 3 = fp32 -> f16 -> fp32 rounding) at

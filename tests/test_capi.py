@@ -55,6 +55,11 @@ def test_abi_constants_match_header(L):
     assert define("VWS_ERR_UNSUPPORTED_DTYPE") == _lib.ERR_UNSUPPORTED_DTYPE
     assert define("VWS_ERR_WORKSPACE_TOO_SMALL") == _lib.ERR_WORKSPACE_TOO_SMALL
     assert define("VWS_ERR_LIMIT") == _lib.ERR_LIMIT
+    assert define("VWS_ERR_UNSUPPORTED") == _lib.ERR_UNSUPPORTED
+    assert define("VWS_TRACE_SLOTS") == _lib.TRACE_SLOTS
+    for n in ("ENTRY", "PARAMS", "FIRST", "SEED", "STREAM", "ROW", "EXIT", "WAVE_LOOP", "WAVE_PACK",
+              "XCC", "ROWID"):
+        assert define(f"VWS_TRACE_{n}") == getattr(_lib, f"TRACE_{n}"), n
     assert define("VWS_MAX_VOCAB") == _lib.MAX_VOCAB
     assert define("VWS_MAX_LOGPROBS") == _lib.MAX_LOGPROBS
 
@@ -189,6 +194,24 @@ def test_coop_wait_polls_hook(L):
         assert L.vws_set_coop_wait_polls(7) == 0
     finally:
         L.vws_set_coop_wait_polls(prev)
+
+
+def test_trace_set_only_in_the_trace_build(L):
+    """The product library refuses vws_trace_set; the trace build (same ABI, same exports)
+    takes a buffer or turns recording off, and rejects a count without a buffer."""
+    assert L.vws_trace_set(None, 0) == _lib.ERR_UNSUPPORTED
+    assert "trace build" in _lib.last_error()
+    if not os.path.exists(_lib.TRACE_LIB_PATH):
+        subprocess.run(["make", "-s", "-j4", "-C", os.path.join(ROOT, "vllm_webgpu_amd", "csrc"),
+                        "trace"], check=True)
+    T = _lib.load(_lib.TRACE_LIB_PATH)
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.TRACE_LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    assert set(_declared()) <= set(re.findall(r"\bT (vws_\w+)", out))
+    assert T.vws_trace_set(None, 0) == _lib.OK
+    assert T.vws_trace_set(None, 4) == _lib.ERR_INVALID_ARGUMENT
+    assert T.vws_trace_set(ctypes.c_void_p(4096), -1) == _lib.ERR_INVALID_ARGUMENT
+    assert T.vws_trace_set(None, 0) == _lib.OK
 
 
 def test_greedy_batches_need_no_uniforms(L):

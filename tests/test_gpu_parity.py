@@ -115,6 +115,34 @@ def test_softmax(cuda):
         np.testing.assert_allclose(q.cpu().numpy(), p, rtol=2e-4, atol=1e-9)
 
 
+def test_softmax_long_rows(cuda):
+    """Rows longer than 32 values per thread (the two-read path: an online max and normaliser,
+    then the write), with -inf and NaN elements (exp_det is 0 for NaN: their probability is 0),
+    a row of one finite value, and a row in ascending order (every thread's running maximum
+    rises at each of its values)."""
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(19)
+    B, V = 5, 150001
+    x = (rng.normal(size=(B, V)) * 3).astype(np.float32)
+    x[1, ::7] = -np.inf
+    x[2, 1234] = np.nan
+    x[3, :] = -np.inf
+    x[3, 77] = 2.5
+    x[4] = np.sort(x[4])
+    T = np.array([1.0, 0.7, 1.5, 1.0, 0.9], np.float32)
+    p, rm, ls = ops.softmax(torch.from_numpy(x).to(cuda), torch.from_numpy(T))
+    p, rm, ls = p.cpu().numpy(), rm.cpu().numpy(), ls.cpu().numpy()
+    for b in range(B):
+        rp, rrm, rls = O.softmax(x[b:b + 1], float(T[b]))
+        np.testing.assert_allclose(p[b], rp[0], rtol=1e-5, atol=1e-12, equal_nan=True)
+        assert rm[b] == rrm[0]
+        np.testing.assert_allclose(ls[b], rls[0], rtol=1e-6)
+    assert p[3, 77] == 1.0 and not p[3, :77].any()
+
+
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("scale", [0.05, 0.25])
 def test_config_scaled(cuda, cfg, scale):

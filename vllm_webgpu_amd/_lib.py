@@ -13,6 +13,8 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_vws.so")
+# the same kernels built with per-workgroup phase stamps (vws_trace_set; vllm_webgpu_amd/trace.py)
+TRACE_LIB_PATH = os.path.join(_HERE, "_vws_trace.so")
 
 ABI_VERSION = 7
 OK = 0
@@ -21,6 +23,7 @@ ERR_UNSUPPORTED_DTYPE = 2
 ERR_WORKSPACE_TOO_SMALL = 3
 ERR_HIP = 4
 ERR_LIMIT = 5
+ERR_UNSUPPORTED = 6
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -43,12 +46,19 @@ STATE_OUTPUT = 0
 STATE_PROMPT = 1
 STATE_PROMPT_FLAG = 0x80000000
 
+TRACE_SLOTS = 16
+(TRACE_ENTRY, TRACE_PARAMS, TRACE_FIRST, TRACE_SEED, TRACE_STREAM, TRACE_ROW, TRACE_EXIT,
+ TRACE_WAVE_LOOP, TRACE_WAVE_PACK) = range(9)
+TRACE_XCC = 14
+TRACE_ROWID = 15
+
 EXPORTED = (
     "vws_abi_version", "vws_last_error", "vws_sample_workspace_size", "vws_workspace_init",
     "vws_validate_sample_args", "vws_sample", "vws_sample_noalloc", "vws_argmax",
     "vws_topk_workspace_size",
     "vws_topk", "vws_softmax", "vws_apply_penalties", "vws_math_selftest",
     "vws_profile_begin", "vws_profile_end", "vws_set_coop_wait_polls", "vws_token_state_update",
+    "vws_trace_set",
 )
 
 KERNEL_KINDS = ("sample", "topk", "argmax", "softmax", "penalties", "other")
@@ -129,28 +139,55 @@ def _declare(L):
     L.vws_profile_end.argtypes = [_P, _P]
     L.vws_set_coop_wait_polls.restype = _I32
     L.vws_set_coop_wait_polls.argtypes = [_I32]
+    L.vws_trace_set.restype = ctypes.c_int
+    L.vws_trace_set.argtypes = [_P, _I32]
     L.vws_token_state_update.restype = ctypes.c_int
     L.vws_token_state_update.argtypes = [_P, _I64, _P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P]
 
 
+def load(path: str) -> ctypes.CDLL:
+    """Loads a build of the library (after torch), declares it and checks its ABI version."""
+    import torch  # noqa: F401  (HIP runtime first, see module docstring)
+
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is not built: run `make -C vllm_webgpu_amd/csrc` (`... trace` for the trace "
+            "build) or `python -c 'import __graft_entry__ as g; g.build()'`")
+    L = ctypes.CDLL(path)
+    _declare(L)
+    v = L.vws_abi_version()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"{os.path.basename(path)} ABI version {v} != {ABI_VERSION}")
+    return L
+
+
 def lib() -> ctypes.CDLL:
-    """Loads _vws.so (after torch) and checks its ABI version; raises if it is not built."""
+    """The library every entry point of this package calls: _vws.so, loaded on first use (or the
+    build `use()` selected); raises if it is not built."""
     global _lib
     with _lock:
         if _lib is None:
-            import torch  # noqa: F401  (HIP runtime first, see module docstring)
-
-            if not os.path.exists(LIB_PATH):
-                raise RuntimeError(
-                    f"{LIB_PATH} is not built: run `make -C vllm_webgpu_amd/csrc` or "
-                    "`python -c 'import __graft_entry__ as g; g.build()'`")
-            L = ctypes.CDLL(LIB_PATH)
-            _declare(L)
-            v = L.vws_abi_version()
-            if v != ABI_VERSION:
-                raise RuntimeError(f"_vws.so ABI version {v} != {ABI_VERSION}")
-            _lib = L
+            _lib = load(LIB_PATH)
     return _lib
+
+
+class use:
+    """``with _lib.use(path):`` makes the package's entry points call that build of the library
+    (the trace build, say) inside the block, in this thread and every other."""
+
+    def __init__(self, path: str):
+        self.L = load(path)
+
+    def __enter__(self) -> ctypes.CDLL:
+        global _lib
+        with _lock:
+            self.prev, _lib = _lib, self.L
+        return self.L
+
+    def __exit__(self, *exc) -> None:
+        global _lib
+        with _lock:
+            _lib = self.prev
 
 
 def last_error() -> str:

@@ -42,6 +42,13 @@ thread_local std::string g_err;
 // (vws_set_coop_wait_polls), read at every launch.
 std::atomic<int> g_coop_wait_polls{kCoopWaitPolls};
 
+#ifdef VWS_TRACE
+// Trace build: the record buffer of vws_trace_set and its workgroup count, read at every launch.
+std::mutex g_trace_mu;
+uint64_t* g_trace_buf = nullptr;
+int g_trace_wgs = 0;
+#endif
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -379,6 +386,13 @@ int vws_sample(const vws_sample_args* a) {
         else if (a->batch > d.cus * d.row_blocks_per_cu) k.coop_count = 1;
     }
     k.coop_wait_polls = g_coop_wait_polls.load(std::memory_order_relaxed);
+#ifdef VWS_TRACE
+    {
+        std::lock_guard<std::mutex> lock(g_trace_mu);
+        k.trace = g_trace_buf;
+        k.trace_wgs = g_trace_wgs;
+    }
+#endif
     const int cf = (k.coop ? 1 : 0) | (k.coop_count ? 2 : 0) |
                    ((k.coop_count && a->batch <= kRowOrderMaxBatch) ? 4 : 0);
     hipStream_t s = (hipStream_t)a->stream;
@@ -584,6 +598,22 @@ int32_t vws_set_coop_wait_polls(int32_t polls) {
         return -1;
     }
     return g_coop_wait_polls.exchange(polls);
+}
+
+int vws_trace_set(uint64_t* buf, int32_t max_workgroups) {
+#ifdef VWS_TRACE
+    if (max_workgroups < 0 || (max_workgroups > 0 && !buf))
+        return fail(VWS_ERR_INVALID_ARGUMENT, "trace: a buffer of max_workgroups >= 0 records");
+    std::lock_guard<std::mutex> lock(g_trace_mu);
+    g_trace_buf = max_workgroups > 0 ? buf : nullptr;
+    g_trace_wgs = max_workgroups;
+    return ok();
+#else
+    (void)buf;
+    (void)max_workgroups;
+    return fail(VWS_ERR_UNSUPPORTED, "vws_trace_set: not the trace build of the library "
+                                     "(vllm_webgpu_amd/_vws_trace.so records phase stamps)");
+#endif
 }
 
 int vws_profile_begin(int32_t max_launches) {

@@ -146,6 +146,8 @@ struct KArgs {
     CoopState* coop;        // cooperative passes (sampling workspace), or null
     int coop_count;         // B exceeds the workgroups resident at once: count them in coop->wgs
     int coop_wait_polls;    // bound of an owner's wait for the chunks helpers run (>= 0)
+    uint64_t* trace;        // trace build: [trace_wgs][VWS_TRACE_SLOTS] phase stamps, or null
+    int trace_wgs;
 };
 
 // Workspace layout (bytes, 256-aligned sections).

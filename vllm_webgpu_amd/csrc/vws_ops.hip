@@ -63,9 +63,11 @@ __global__ __launch_bounds__(kOpThreads) void argmax_kernel(const T* logits, int
 // probs = exp_det(x/T - m) / S, m = max x/T, S = sum exp_det(x/T - m); one workgroup per row.
 // Rows of up to 32 values per thread (V <= 32768: 8 chunks of fp32, 4 of 16-bit values) are
 // read once: each thread keeps its chunks in registers through the max, the sum and the write
-// (one read and one write of the row);
-// longer rows are read three times (max, sum, write).  S is summed in double, in a different
-// order than the sequential oracle (the probabilities agree to within a few fp32 ulps).
+// (one read and one write of the row).  Longer rows are read twice: the maximum and S together
+// (an online merge of per-thread running maxima and sums), then the write.  S is summed in
+// double, in a different order than the sequential oracle (and, for long rows, with rescaled
+// partial sums); each probability is e * fl64(1 / S): the probabilities agree with the oracle's
+// to within a few fp32 ulps.
 template <typename T>
 __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, int64_t stride, int V,
                                                               const float* temperature, float* probs,
@@ -90,6 +92,8 @@ __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, in
     float m;
     double S;
     if (nch <= kSoftmaxRegs * kOpThreads) {
+        // the row in registers: y = fl(x / T) once, then e = exp(y - m) in place of y, then
+        // the probabilities e * fl64(1 / S) (within an ulp of e / S)
         float v[kSoftmaxRegs][VEC];
 #pragma unroll
         for (int q = 0; q < kSoftmaxRegs; ++q) {
@@ -101,17 +105,31 @@ __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, in
                 for (int j = 0; j < VEC; ++j) v[q][j] = __builtin_nanf("");
             }
         }
+        if (Tt != 1.0f) {
+#pragma unroll
+            for (int q = 0; q < kSoftmaxRegs; ++q)
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[q][j] = v[q][j] / Tt;
+        }
 #pragma unroll
         for (int q = 0; q < kSoftmaxRegs; ++q)
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[q][j] / Tt); mk = mk > k ? mk : k; }
+            for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[q][j]); mk = mk > k ? mk : k; }
         mk = op_block_max(mk, red);
         m = val_of((uint32_t)mk);
 #pragma unroll
         for (int q = 0; q < kSoftmaxRegs; ++q)
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) if (v[q][j] == v[q][j]) s += (double)exp_det(v[q][j] / Tt - m);
+            for (int j = 0; j < VEC; ++j) {
+                // exp_det is 0 for NaN (NaN logits, padding, y - m of infinities)
+                const float e = exp_det(v[q][j] - m);
+                v[q][j] = e;
+                const int c = threadIdx.x + q * kOpThreads;
+                const int i0 = c == 0 ? 0 : sl.a + (c - 1) * VEC;
+                if (c < nch && inside(c, i0 + j)) s += (double)e;
+            }
         S = op_block_sum_f64(s, redd);
+        const double inv = 1.0 / S;
 #pragma unroll
         for (int q = 0; q < kSoftmaxRegs; ++q) {
             const int c = threadIdx.x + q * kOpThreads;
@@ -119,31 +137,45 @@ __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, in
             const int i0 = c == 0 ? 0 : sl.a + (c - 1) * VEC;
 #pragma unroll
             for (int j = 0; j < VEC; ++j)
-                if (c < nch && inside(c, i0 + j))
-                    out[i0 + j] = (float)((double)exp_det(v[q][j] / Tt - m) / S);
+                if (c < nch && inside(c, i0 + j)) out[i0 + j] = (float)((double)v[q][j] * inv);
         }
     } else {
+        // longer rows: the maximum and the normaliser in one pass (each thread keeps a running
+        // maximum mt of its finite values and its sum st of exp(y - mt), rescaled when mt
+        // rises; the workgroup merges them as sum st * exp(mt - m)), then a second pass writes
+        // the probabilities.  Only finite values add a term: exp_det is 0 for NaN, for -inf
+        // and for y - m of infinities, so S is 0 when m is not finite.
+        float mt = -__builtin_inff();
+        double st = 0.0;
         for (int c = threadIdx.x; c < nch; c += kOpThreads) {
             float v[VEC];
-            sl.load(c, v);
+            const int i0 = sl.load(c, v);
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[j] / Tt); mk = mk > k ? mk : k; }
+            for (int j = 0; j < VEC; ++j) {
+                const float y = v[j] / Tt;
+                const uint64_t k = key_of(y);
+                mk = mk > k ? mk : k;
+                if (!inside(c, i0 + j)) continue;  // padding of the head and tail chunks
+                if (!(__builtin_fabsf(y) < __builtin_inff())) continue;
+                if (y > mt) {
+                    st = st * (double)exp_det(mt - y) + 1.0;
+                    mt = y;
+                } else {
+                    st += (double)exp_det(y - mt);
+                }
+            }
         }
         mk = op_block_max(mk, red);
         m = val_of((uint32_t)mk);
-        for (int c = threadIdx.x; c < nch; c += kOpThreads) {
-            float v[VEC];
-            sl.load(c, v);
-#pragma unroll
-            for (int j = 0; j < VEC; ++j) if (v[j] == v[j]) s += (double)exp_det(v[j] / Tt - m);
-        }
-        S = op_block_sum_f64(s, redd);
+        const bool mfin = __builtin_fabsf(m) < __builtin_inff();
+        S = op_block_sum_f64(mfin && mt > -__builtin_inff() ? st * (double)exp_det(mt - m) : 0.0, redd);
+        const double inv = 1.0 / S;
         for (int c = threadIdx.x; c < nch; c += kOpThreads) {
             float v[VEC];
             const int i0 = sl.load(c, v);
 #pragma unroll
             for (int j = 0; j < VEC; ++j)
-                if (inside(c, i0 + j)) out[i0 + j] = (float)((double)exp_det(v[j] / Tt - m) / S);
+                if (inside(c, i0 + j)) out[i0 + j] = (float)((double)exp_det(v[j] / Tt - m) * inv);
         }
     }
     if (threadIdx.x == 0) {

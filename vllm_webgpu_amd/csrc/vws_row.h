@@ -8,6 +8,42 @@
 
 namespace vws {
 
+// Trace build (-DVWS_TRACE) only: lane 0 of the workgroup's last wave stores the device clock
+// (s_memrealtime, 100 MHz) or a value into slot s of the workgroup's record (vws_trace_set).
+// The last wave, because the wait for the clock read delays the wave that stores it: wave 0
+// does the workgroup's serial work (edges, selections) and more often sets a phase's end.
+// VWS_TRACE_MARK_AFTER first waits for dep, a value the phase produced, so that the stamp
+// cannot be taken before the phase's loads have landed.
+#ifdef VWS_TRACE
+__device__ __forceinline__ bool trace_lane(const KArgs& a) {
+    return a.trace && threadIdx.x == blockDim.x - 64u && (int)blockIdx.x < a.trace_wgs;
+}
+__device__ __forceinline__ void trace_put(const KArgs& a, int s, uint64_t v) {
+    if (trace_lane(a)) a.trace[(size_t)blockIdx.x * VWS_TRACE_SLOTS + s] = v;
+}
+// the clock is read by the stamping wave alone (the others issue nothing)
+__device__ __forceinline__ void trace_mark(const KArgs& a, int s) {
+    if (trace_lane(a)) a.trace[(size_t)blockIdx.x * VWS_TRACE_SLOTS + s] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ uint64_t trace_clock() { return __builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ uint32_t trace_xcc() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xFu;
+}
+#define VWS_TRACE_MARK(a, s) ::vws::trace_mark((a), (s))
+#define VWS_TRACE_MARK_AFTER(a, s, dep)                        \
+    do {                                                       \
+        asm volatile("" : : "v"((uint32_t)(dep)));             \
+        VWS_TRACE_MARK(a, s);                                  \
+    } while (0)
+#define VWS_TRACE_PUT(a, s, v) ::vws::trace_put((a), (s), (uint64_t)(v))
+#else
+#define VWS_TRACE_MARK(a, s) ((void)0)
+#define VWS_TRACE_MARK_AFTER(a, s, dep) ((void)0)
+#define VWS_TRACE_PUT(a, s, v) ((void)0)
+#endif
+
 struct RowP {
     float T, top_p, min_p, rep, pres, freq, inv_rep;
     int k, np, no;

@@ -1194,6 +1194,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     load_mask(MB, 1);
     const RowP prm = row_params_scalar(a, r);
     const int k = fast_k(a, prm);
+    VWS_TRACE_MARK_AFTER(a, VWS_TRACE_PARAMS, k);
     if (k == 0) {
         *topp_row = topp_eligible(a, prm);
         return false;
@@ -1313,12 +1314,15 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         if (small_pool) {
             const uint32_t t4 = wave_top4(key_of(mx));
             if (lane < 4) sm.seedk[wave * 4 + lane] = t4;
+            VWS_TRACE_MARK_AFTER(a, VWS_TRACE_FIRST, t4);
         } else {
             const uint32_t sk = wave_sort_desc64(key_of(mx));
             if (lane < kSeedPerWave) sm.seedk[wave * kSeedPerWave + lane] = sk;
+            VWS_TRACE_MARK_AFTER(a, VWS_TRACE_FIRST, sk);
         }
     }
     __syncthreads();  // also publishes the hash
+    VWS_TRACE_MARK(a, VWS_TRACE_SEED);
     // the hash is complete here; a row whose history overflowed it takes the general path
     if (sm.status & 1u) return false;
     uint32_t seed = 0u;
@@ -1431,6 +1435,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         load_iter(Bq, it + 3, BoolC<false>{});
         load_mask(MB, it + 3);
     }
+    VWS_TRACE_MARK_AFTER(a, VWS_TRACE_WAVE_LOOP, cb.cnt);
     if (wave == 0) {
         // unaligned head (thread 0) and tail (thread 1), fewer than 2 vectors in total; handled
         // last, and by wave 0 alone, so no other wave waits for its loads
@@ -1557,7 +1562,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         atomicMax(&sm.tmaxk, cb.tau);
         if (cb.ovf) atomicOr(&sm.status, 2u);
     }
+    VWS_TRACE_MARK(a, VWS_TRACE_WAVE_PACK);
     __syncthreads();
+    VWS_TRACE_MARK(a, VWS_TRACE_STREAM);
     const int total = (int)sm.npack;
     if (total > kRowPack) return false;  // too many candidates
     // the single-wave finish checks the status and the thresholds once its count is running
@@ -1997,6 +2004,12 @@ __device__ __noinline__ int row_order_entry(uint64_t kernarg, int b) {
 template <typename T, bool LP, bool MASK>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
                                                           int coop, KArgs a) {
+#ifdef VWS_TRACE
+    // stored once the row is done: a store this early turns the row parameters' scalar loads
+    // into vector ones
+    uint64_t tr_entry = 0;
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x) == blockDim.x - 64u) tr_entry = trace_clock();
+#endif
     const uint64_t kernarg = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr() + 24u;
     int r = blockIdx.x;
     if (coop & 2) {
@@ -2004,7 +2017,14 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
         if (coop & 4) r = __builtin_amdgcn_readfirstlane(row_order_entry(kernarg, r));
     }
     const bool long_row = row_one<T, LP, MASK>(a, r, logits, lstride, V, kernarg);
+    VWS_TRACE_MARK(a, VWS_TRACE_ROW);
+#ifdef VWS_TRACE
+    trace_put(a, VWS_TRACE_ENTRY, tr_entry);
+    trace_put(a, VWS_TRACE_XCC, trace_xcc());
+    trace_put(a, VWS_TRACE_ROWID, (uint64_t)r);
+#endif
     if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T>(kernarg, long_row ? 1 : 0);
+    VWS_TRACE_MARK(a, VWS_TRACE_EXIT);
 }
 
 }  // namespace vws

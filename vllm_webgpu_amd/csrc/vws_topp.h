@@ -397,6 +397,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     if (tid == 0) sm.status = 0u;
     if (lane == 0) sm.bc[wave] = tw;  // bc is free until the finish's first barrier
     __syncthreads();
+    VWS_TRACE_MARK(a, VWS_TRACE_SEED);
     uint32_t tau0 = 0u;
     if (seeded) tau0 = wave_mth_largest64(lane < kTpWaves ? sm.bc[lane] : 0u, kTpWaves / 2);
     if (tau0 <= 0x007FFFFFu || tau0 >= 0xFF800000u) tau0 = 0u;  // -inf, or +inf (degenerate row)
@@ -1130,6 +1131,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         sm.coop_fail = 0u;
     }
     __syncthreads();  // every wave's stream results are published
+    VWS_TRACE_MARK(a, VWS_TRACE_STREAM);
     if (sm.status != 0u) return (sm.status & 1u) ? VWS_FALLBACK_OVERFLOW : VWS_FALLBACK_SUM;
     const bool hist = prm.has_hist;
     // an entry's element index (history rows mark their history tokens in bit 18)

@@ -96,18 +96,41 @@ class SampleResult:
     logprob_ranks: torch.Tensor | None   # [B] int32
 
 
-def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p=None,
-           repetition_penalty=None, presence_penalty=None, frequency_penalty=None,
-           prompt_ids=None, prompt_lens=None, output_ids=None, output_lens=None,
-           uniforms: torch.Tensor | None = None, num_logprobs: int | None = None,
-           allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
-           adjust_lens=None, logit_softcap: float | None = None,
-           logit_softcap_f16: bool = False, rng_seeds: torch.Tensor | None = None,
-           rng_offsets: torch.Tensor | None = None, token_state: torch.Tensor | None = None,
-           token_state_rows: torch.Tensor | None = None,
-           token_state_bits: torch.Tensor | None = None) -> SampleResult:
+class PreparedSample:
+    """One ``vws_sample`` call with its arguments validated and packed once (``prepare_sample``):
+    ``launch()`` issues it again on the current stream with one C call, reading the same input
+    tensors (their current contents) and writing the same ``result`` tensors.  The object keeps
+    every tensor it points at alive."""
+
+    def __init__(self, args, result: SampleResult, keep: tuple):
+        self.args = args
+        self.result = result
+        self._keep = keep
+
+    def launch(self) -> SampleResult:
+        self.args.stream = _stream_ptr()
+        _lib.check(_lib.lib().vws_sample(ctypes.byref(self.args)))
+        return self.result
+
+
+def sample(logits: torch.Tensor, *args, **kwargs) -> SampleResult:
     """Samples one token per row of ``logits`` [B, V] (float32, bfloat16 or float16, on the
-    GPU; each widened exactly to fp32).
+    GPU; each widened exactly to fp32).  Arguments: those of ``prepare_sample``."""
+    return prepare_sample(logits, *args, **kwargs).launch()
+
+
+def prepare_sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p=None,
+                   repetition_penalty=None, presence_penalty=None, frequency_penalty=None,
+                   prompt_ids=None, prompt_lens=None, output_ids=None, output_lens=None,
+                   uniforms: torch.Tensor | None = None, num_logprobs: int | None = None,
+                   allowed_mask: torch.Tensor | None = None, adjust_ids=None, adjust_vals=None,
+                   adjust_lens=None, logit_softcap: float | None = None,
+                   logit_softcap_f16: bool = False, rng_seeds: torch.Tensor | None = None,
+                   rng_offsets: torch.Tensor | None = None, token_state: torch.Tensor | None = None,
+                   token_state_rows: torch.Tensor | None = None,
+                   token_state_bits: torch.Tensor | None = None) -> PreparedSample:
+    """Validates and packs one sampling call over ``logits`` [B, V] (float32, bfloat16 or
+    float16, on the GPU; each widened exactly to fp32) without launching it.
 
     Per-row parameters are scalars or [B] tensors; ``None`` means off (temperature None = every
     row greedy).  Histories are padded int32 [B, W] (ids outside [0, V) are padding).
@@ -239,10 +262,9 @@ def sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=None, min_p
     a.num_logprobs = L
     a.logprob_ids, a.logprob_vals, a.logprob_ranks = _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    a.stream = _stream_ptr()
-    _lib.check(L_lib.vws_sample(ctypes.byref(a)))
-    # keep the argument tensors alive until the work is enqueued (it is, on return)
-    return SampleResult(sampled, flags, nkept, lp_ids, lp_vals, ranks)
+    keep = (logits, T, K, P, MP, R, PR, FR, pid, plens, oid, olens, aid, aval, alens, TS, TR,
+            token_state_bits, AM, U, SEED, OFF, ws)
+    return PreparedSample(a, SampleResult(sampled, flags, nkept, lp_ids, lp_vals, ranks), keep)
 
 
 def token_state_update(state: torch.Tensor, tokens: torch.Tensor, rows=None, prompt: bool = False,
