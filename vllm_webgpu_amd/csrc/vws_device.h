@@ -402,6 +402,18 @@ __device__ __forceinline__ uint32_t wave_mth_largest64(uint32_t v, int m) {
     return ans;
 }
 
+// The same by counting, for one wave that selects for the workgroup: every lane counts the
+// keys >= its own (64 lane reads, no dependent chain), and the answer is the largest key with
+// at least m of them.
+// N: the keys of lanes [0, N) take part (the others must hold 0).
+template <int N = kWave>
+__device__ __forceinline__ uint32_t wave_mth_largest64_count(uint32_t v, int m) {
+    uint32_t cge = 0u;
+#pragma unroll
+    for (int j = 0; j < N; ++j) cge += __builtin_amdgcn_readlane(v, j) >= v ? 1u : 0u;
+    return wave_max_u32(cge >= (uint32_t)m ? v : 0u);
+}
+
 // k-th largest key (1-based, with multiplicity) of at most 256 keys held 4 per lane by one
 // whole wave (missing entries passed as 0): an in-register bitonic sort into descending order
 // across the wave (element e = 4 * lane + i), then a read of element k - 1.

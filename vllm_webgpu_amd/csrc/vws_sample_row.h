@@ -1284,8 +1284,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const float lam = (float)(kc - 1) * (float)sample / (float)V;
     const int m_seed = sample > 0 ? min(kc, (int)__builtin_ceilf(lam + 5.0f * __builtin_sqrtf(lam) + 3.0f)) : 0;
     const bool seeded = sample > 0 && m_seed <= kRowWaves * kSeedPerWave;
-    // m <= 64: the pool is every wave's 4 largest lane maxima, and every wave selects the m-th
-    // largest of it for itself; otherwise the 16 largest of every wave, selected by wave 0
+    // m <= 64: the pool is every wave's 4 largest lane maxima, otherwise the 16 largest of every
+    // wave, whose m-th largest wave 0 selects
     const bool small_pool = m_seed <= kRowWaves * 4;
     // LP: the wave's anchor, its largest value over the first iteration (0 when it has none
     // that is finite), so that its sum of exp(x - anchor) starts near 1 and cannot overflow
@@ -1325,9 +1325,17 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     VWS_TRACE_MARK(a, VWS_TRACE_SEED);
     // the hash is complete here; a row whose history overflowed it takes the general path
     if (sm.status & 1u) return false;
+    // Rows whose stream waits for later iterations: every wave selects a small pool's seed for
+    // itself while those land.  Rows held in the first two iterations wait for nothing else:
+    // wave 0 selects and the others read it after a barrier (16 waves selecting at once cost
+    // their CU's issue slots, ~1.5 us).
+    const bool sel0 = !small_pool || nit <= 2;
     uint32_t seed = 0u;
-    if (seeded && small_pool) {
+    if (seeded && !sel0) {
         seed = wave_mth_largest64(sm.seedk[lane], m_seed);
+    } else if (seeded && small_pool && wave == 0) {
+        const uint32_t t0 = wave_mth_largest64_count(sm.seedk[lane], m_seed);
+        if (lane == 0) sm.bc[0] = t0;
     } else if (seeded && wave == 0) {
         const uint32_t t0 = wave_kth_largest_256(sm.seedk[4 * lane], sm.seedk[4 * lane + 1],
                                                  sm.seedk[4 * lane + 2], sm.seedk[4 * lane + 3], m_seed);
@@ -1350,9 +1358,9 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             }
         }
     }
-    if (gather || (seeded && !small_pool)) {
+    if (gather || (seeded && sel0)) {
         __syncthreads();
-        if (seeded && !small_pool) seed = sm.bc[0];
+        if (seeded && sel0) seed = sm.bc[0];
     }
 
     // 4. stream; 5. the k-th largest candidate, checked against every threshold used.  A seeded

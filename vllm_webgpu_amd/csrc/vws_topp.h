@@ -399,7 +399,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     __syncthreads();
     VWS_TRACE_MARK(a, VWS_TRACE_SEED);
     uint32_t tau0 = 0u;
-    if (seeded) tau0 = wave_mth_largest64(lane < kTpWaves ? sm.bc[lane] : 0u, kTpWaves / 2);
+    if (seeded) tau0 = wave_mth_largest64_count<kTpWaves>(lane < kTpWaves ? sm.bc[lane] : 0u, kTpWaves / 2);
     if (tau0 <= 0x007FFFFFu || tau0 >= 0xFF800000u) tau0 = 0u;  // -inf, or +inf (degenerate row)
     const float aw = tau0 ? val_of(tau0) : 0.0f;
     const bool greedy = prm.greedy;
