@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define VWS_ABI_VERSION 7
+#define VWS_ABI_VERSION 8
 
 /* status codes */
 #define VWS_OK 0
@@ -144,7 +144,8 @@ typedef struct vws_sample_args {
     const int32_t* adjust_lens;
 
     /* Uniforms in (0, 1), fp32 [B, V] (row stride in elements); read only at surviving
-     * tokens.  Required when temperature is non-NULL, unless rng_seeds is given. */
+     * tokens.  Required when temperature is non-NULL, unless rng_seeds or rng_key_set is
+     * given. */
     const float* uniforms;
     int64_t uniforms_row_stride;
     /* Generated uniforms instead (when uniforms is NULL): device u64 [B] keys and offsets
@@ -154,6 +155,11 @@ typedef struct vws_sample_args {
      * buffer is read or needs to be written. */
     const uint64_t* rng_seeds;
     const uint64_t* rng_offsets;
+    /* Or one key for the whole launch (uniforms and rng_seeds NULL, rng_key_set non-zero): row
+     * r generates as with seed rng_key and offset r.  A by-value key: a sampling step needs no
+     * upload of per-row keys (no extra copy ahead of the kernel on the stream). */
+    uint64_t rng_key;
+    int32_t rng_key_set;
 
     /* Outputs */
     int32_t* sampled;    /* [B] token ids */

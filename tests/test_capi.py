@@ -218,6 +218,13 @@ def test_greedy_batches_need_no_uniforms(L):
     assert _status(L, _args(L, temperature=None, uniforms=None)) == _lib.OK
 
 
+def test_launch_key_replaces_uniforms(L):
+    """A by-value key for the launch stands in for uniforms or per-row keys."""
+    assert _status(L, _args(L, uniforms=None, rng_key=0x1234, rng_key_set=1)) == _lib.OK
+    assert _status(L, _args(L, uniforms=None, rng_key=0x1234, rng_key_set=0)) == _lib.ERR_INVALID_ARGUMENT
+    assert "rng_key_set" in _lib.last_error()
+
+
 def test_errors_raise_with_library_text(L):
     assert _status(L, _args(L, dtype=9)) != 0
     with pytest.raises(_lib.VwsError, match="unsupported logits dtype 9"):

@@ -114,3 +114,44 @@ def test_offsets_and_seeds_change_the_draws(cuda):
     # flat rows: the winner is the largest uniform of the row
     u = O.philox_uniforms(seeds.view(np.uint64), V, offsets.view(np.uint64))
     assert np.array_equal(a, np.argmax(u, axis=1))
+
+
+def _run_key(w, cuda, key, num_logprobs=None):
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    if w.dtype == "bf16":
+        logits = torch.from_numpy(w.logits.view(np.int16)).to(cuda).view(torch.bfloat16)
+    else:
+        logits = torch.from_numpy(w.logits).to(cuda)
+    hist = torch.from_numpy(w.output_ids) if w.output_ids is not None else None
+    res = ops.sample(logits, temperature=torch.from_numpy(w.temperature),
+                     top_k=torch.from_numpy(w.top_k), top_p=torch.from_numpy(w.top_p),
+                     min_p=torch.from_numpy(w.min_p),
+                     repetition_penalty=torch.from_numpy(w.repetition),
+                     presence_penalty=torch.from_numpy(w.presence),
+                     frequency_penalty=torch.from_numpy(w.frequency), output_ids=hist,
+                     rng_key=key, num_logprobs=num_logprobs)
+    torch.cuda.synchronize()
+    out = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
+               n_kept=res.num_kept.cpu().numpy())
+    if num_logprobs is not None:
+        out.update(lp_ids=res.logprob_ids.cpu().numpy(), lp_vals=res.logprob_vals.cpu().numpy(),
+                   ranks=res.logprob_ranks.cpu().numpy())
+    return out
+
+
+@pytest.mark.parametrize("cfg,scale,L", [(3, 0.25, None), (4, 0.1, None), (5, 0.1, 20)])
+def test_launch_key(cuda, cfg, scale, L):
+    """One by-value key for the launch: row r draws as with seed key and offset r -- the same
+    tokens as those per-row keys passed as arrays, and as the oracle with their uniforms."""
+    w = W.config(cfg, scale)
+    w.num_logprobs = L
+    B = w.shape[0]
+    key = 0xC0FFEE1234567 + cfg  # above 2^32: both key words matter
+    seeds = np.full(B, key, np.int64)
+    offsets = np.arange(B, dtype=np.int64)
+    g = _run_key(w, cuda, key, num_logprobs=L)
+    assert_same(g, _run_gen(w, cuda, seeds, offsets, num_logprobs=L), f"C{cfg} key vs arrays")
+    assert_same(g, oracle_run(_with_generated(w, seeds, offsets), num_logprobs=L), f"C{cfg} key")

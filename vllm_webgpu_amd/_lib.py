@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, "_vws.so")
 # the same kernels built with per-workgroup phase stamps (vws_trace_set; vllm_webgpu_amd/trace.py)
 TRACE_LIB_PATH = os.path.join(_HERE, "_vws_trace.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 OK = 0
 ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED_DTYPE = 2
@@ -87,6 +87,7 @@ class SampleArgs(ctypes.Structure):
         ("adjust_ids", _P), ("adjust_vals", _P), ("adjust_row_stride", _I64), ("adjust_width", _I32),
         ("adjust_lens", _P),
         ("uniforms", _P), ("uniforms_row_stride", _I64), ("rng_seeds", _P), ("rng_offsets", _P),
+        ("rng_key", ctypes.c_uint64), ("rng_key_set", _I32),
         ("sampled", _P), ("row_flags", _P), ("num_kept", _P),
         ("num_logprobs", _I32), ("logprob_ids", _P), ("logprob_vals", _P), ("logprob_ranks", _P),
         ("workspace", _P), ("workspace_bytes", _SZ), ("stream", _P),

@@ -229,8 +229,9 @@ int validate_sample(const vws_sample_args* a) {
     if (st) return st;
     if (!a->sampled) return fail(VWS_ERR_INVALID_ARGUMENT, "sampled is NULL");
     if (a->temperature) {
-        if (!a->uniforms && !a->rng_seeds)
-            return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms or rng_seeds are required when temperature is given");
+        if (!a->uniforms && !a->rng_seeds && !a->rng_key_set)
+            return fail(VWS_ERR_INVALID_ARGUMENT,
+                        "uniforms, rng_seeds or rng_key_set is required when temperature is given");
         if (a->uniforms && a->uniforms_row_stride < a->vocab)
             return fail(VWS_ERR_INVALID_ARGUMENT, "uniforms_row_stride < vocab");
     }
@@ -367,6 +368,7 @@ int vws_sample(const vws_sample_args* a) {
     k.ustride = a->uniforms_row_stride;
     k.rng_seed = a->uniforms ? nullptr : a->rng_seeds;
     k.rng_offset = a->uniforms ? nullptr : a->rng_offsets;
+    k.rng_key = a->rng_key;
     k.sampled = a->sampled;
     k.flags = a->row_flags;
     k.nkept = a->num_kept;

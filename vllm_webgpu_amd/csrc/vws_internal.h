@@ -120,6 +120,7 @@ struct KArgs {
     int64_t ustride;
     const uint64_t* rng_seed;   // [B] keys of the generated uniforms (when u is NULL)
     const uint64_t* rng_offset; // [B] their counter offsets, or NULL (0)
+    uint64_t rng_key;           // launch-wide key (u and rng_seed NULL): row r's offset is r
     int32_t* sampled;
     uint32_t* flags;
     int32_t* nkept;

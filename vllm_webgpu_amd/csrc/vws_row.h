@@ -86,10 +86,17 @@ __device__ __forceinline__ uint32_t state_word(const KArgs& a, int trow, int t) 
 }
 
 // The race's uniform of token t in row r: the caller's [B, V] uniforms, or the generated one
-// (philox_uniform of the row's key and offset) when the caller passes keys instead.
+// (philox_uniform of the row's key and offset) when the caller passes keys instead, or one key
+// for the launch (offset r).
+__device__ __forceinline__ uint64_t row_rng_seed(const KArgs& a, int r) {
+    return a.rng_seed ? a.rng_seed[r] : a.rng_key;
+}
+__device__ __forceinline__ uint64_t row_rng_offset(const KArgs& a, int r) {
+    return a.rng_seed ? (a.rng_offset ? a.rng_offset[r] : 0ull) : (uint64_t)(uint32_t)r;
+}
 __device__ __forceinline__ float row_uniform(const KArgs& a, int r, int t) {
     if (a.u) return a.u[(size_t)r * a.ustride + t];
-    return philox_uniform(a.rng_seed[r], a.rng_offset ? a.rng_offset[r] : 0ull, (uint32_t)t);
+    return philox_uniform(row_rng_seed(a, r), row_rng_offset(a, r), (uint32_t)t);
 }
 
 // k served by the single-pass kernel for this row, or 0 when the row needs another path (top-k

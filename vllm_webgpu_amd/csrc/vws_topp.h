@@ -771,8 +771,8 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
     } else if (d.kind == kTpPassWideRace) {
         const uint32_t ksv = d.ksv, kkeep = d.kkeep, kmem = d.kmem;
         // gen: the uniforms are generated (at the kept elements only) instead of streamed
-        const uint64_t gseed = a.u ? 0ull : a.rng_seed[r];
-        const uint64_t goff = (a.u || !a.rng_offset) ? 0ull : a.rng_offset[r];
+        const uint64_t gseed = a.u ? 0ull : row_rng_seed(a, r);
+        const uint64_t goff = a.u ? 0ull : row_rng_offset(a, r);
         auto body = [&](const float* v, const float* u, int i0, bool ok, bool gen) __attribute__((always_inline)) {
             // generated uniforms: one Philox block per 4 tokens when the vector starts on a
             // block (the body's vectors all do when the row's aligned start does), else token

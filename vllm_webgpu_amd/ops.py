@@ -24,7 +24,8 @@ _ws_cache: dict[int, torch.Tensor] = {}
 
 
 def _stream_ptr() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    # the raw handle of the current stream, without building a Stream object
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device())
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -51,7 +52,8 @@ def _row_param(x, B: int, dtype, device, name: str) -> torch.Tensor | None:
         return None
     if not torch.is_tensor(x):
         x = torch.full((B,), x, dtype=dtype)
-    x = x.to(device=device, dtype=dtype).contiguous()
+    if not (x.dtype == dtype and x.device == device and x.is_contiguous()):
+        x = x.to(device=device, dtype=dtype).contiguous()
     if x.shape != (B,):
         raise ValueError(f"{name} must have shape ({B},), got {tuple(x.shape)}")
     return x
@@ -128,7 +130,8 @@ def prepare_sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=Non
                    logit_softcap_f16: bool = False, rng_seeds: torch.Tensor | None = None,
                    rng_offsets: torch.Tensor | None = None, token_state: torch.Tensor | None = None,
                    token_state_rows: torch.Tensor | None = None,
-                   token_state_bits: torch.Tensor | None = None) -> PreparedSample:
+                   token_state_bits: torch.Tensor | None = None,
+                   rng_key: int | None = None) -> PreparedSample:
     """Validates and packs one sampling call over ``logits`` [B, V] (float32, bfloat16 or
     float16, on the GPU; each widened exactly to fp32) without launching it.
 
@@ -136,9 +139,10 @@ def prepare_sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=Non
     row greedy).  Histories are padded int32 [B, W] (ids outside [0, V) are padding).
     ``uniforms`` [B, V] float32 in (0, 1) drive the exponential race; instead, ``rng_seeds``
     [B] int64 (and optionally ``rng_offsets`` [B] int64) let the kernel generate them
-    (Philox-4x32-10 keyed per row, evaluated only where a token races).  One of the two is
-    required whenever ``temperature`` is given.  Logits processors (before the penalties): ``allowed_mask``
-    int32 [B, ceil(V/32)] bit words (bit set = token allowed, see ``pack_allowed``), and the
+    (Philox-4x32-10 keyed per row, evaluated only where a token races), or ``rng_key`` (a
+    Python int) does for the whole launch: row r as with seed ``rng_key`` and offset r.  One of
+    them is required whenever ``temperature`` is given.  Logits processors (before the
+    penalties): ``allowed_mask`` int32 [B, ceil(V/32)] bit words (bit set = token allowed, see ``pack_allowed``), and the
     sparse ``adjust_ids`` int32 / ``adjust_vals`` float32 [B, W]: -inf bans a token, a finite
     value is added to its logit.  ``logit_softcap`` > 0: ``logits`` are the lm_head output
     before Gemma's final soft cap, which is applied first (cap * tanh(x / cap)); with
@@ -222,11 +226,10 @@ def prepare_sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=Non
     if rng_seeds is not None and U is None:
         SEED = _row_param(rng_seeds, B, torch.int64, dev, "rng_seeds")
         OFF = _row_param(rng_offsets, B, torch.int64, dev, "rng_offsets")
-    if T is not None and U is None and SEED is None:
-        raise ValueError("uniforms or rng_seeds are required when temperature is given")
-    sampled = torch.empty(B, dtype=torch.int32, device=dev)
-    flags = torch.empty(B, dtype=torch.int32, device=dev)
-    nkept = torch.empty(B, dtype=torch.int32, device=dev)
+    if T is not None and U is None and SEED is None and rng_key is None:
+        raise ValueError("uniforms, rng_seeds or rng_key is required when temperature is given")
+    out3 = torch.empty((3, B), dtype=torch.int32, device=dev)  # one allocation for the three
+    sampled, flags, nkept = out3[0], out3[1], out3[2]
     L = -1 if num_logprobs is None else int(num_logprobs)
     lp_ids = lp_vals = ranks = None
     if L >= 0:
@@ -258,6 +261,8 @@ def prepare_sample(logits: torch.Tensor, temperature=None, top_k=None, top_p=Non
     a.uniforms = _ptr(U)
     a.uniforms_row_stride = U.stride(0) if U is not None else 0
     a.rng_seeds, a.rng_offsets = _ptr(SEED), _ptr(OFF)
+    if U is None and SEED is None and rng_key is not None:
+        a.rng_key, a.rng_key_set = int(rng_key) & 0xFFFFFFFFFFFFFFFF, 1
     a.sampled, a.row_flags, a.num_kept = sampled.data_ptr(), flags.data_ptr(), nkept.data_ptr()
     a.num_logprobs = L
     a.logprob_ids, a.logprob_vals, a.logprob_ranks = _ptr(lp_ids), _ptr(lp_vals), _ptr(ranks)

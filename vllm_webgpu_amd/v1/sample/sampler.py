@@ -12,9 +12,10 @@ processor lists (bad-word matches, min-tokens bans, biases) are built on the hos
 
 Random rows race with the key ``p / (-ln u)``: an exponential race, as vLLM's
 ``random_sample`` (``probs / q.exponential_()``).  The uniforms ``u`` are generated inside the
-launch (Philox-4x32-10, only where a token races) from one 64-bit key per row and step, drawn
-here with torch's generators -- the request's own generator for seeded rows -- so no ``[B, V]``
-tensor is drawn or read.
+launch (Philox-4x32-10, only where a token races), so no ``[B, V]`` tensor is drawn or read:
+from one 64-bit key per launch, drawn from torch's default generator and passed by value,
+when no request is seeded; otherwise from one key per row and step (the request's own stream
+for seeded rows), uploaded with one copy.
 
 There is no host fallback: without the HIP library, or for logits that are not on a ROCm device,
 ``forward`` raises.
@@ -67,13 +68,51 @@ class KeyStream:
         return k
 
 
-def draw_seeds(B: int, generators: dict, device: torch.device) -> torch.Tensor:
+class SeedStaging:
+    """Reusable buffers for ``draw_seeds``: a ring of pinned host buffers and one device buffer,
+    so that a step's keys take no allocation.  A host buffer is written again only once the
+    copy that last read it has completed (an event per buffer); the device buffer is rewritten
+    by the next step's copy, which the stream orders after this step's kernel.  One staging
+    object per stream."""
+
+    RING = 4
+
+    def __init__(self) -> None:
+        self.cap = 0
+        self.host = self.dev = None
+        self.events = []
+        self.i = 0
+
+    def acquire(self, B: int, device: torch.device):
+        if B > self.cap or self.dev is None or self.dev.device != device:
+            self.cap = max(B, 2 * self.cap, 64)
+            self.host = torch.empty((self.RING, self.cap), dtype=torch.int64, pin_memory=True)
+            self.dev = torch.empty(self.cap, dtype=torch.int64, device=device)
+            # (waiting on an event never recorded returns at once)
+            self.events = [torch.cuda.Event() for _ in range(self.RING)]
+        self.i = (self.i + 1) % self.RING
+        self.events[self.i].synchronize()
+        return self.host[self.i, :B], self.dev[:B]
+
+    def copied(self) -> None:
+        self.events[self.i].record()
+
+
+def draw_seeds(B: int, generators: dict, device: torch.device,
+               staging: SeedStaging | None = None) -> torch.Tensor:
     """int64 ``[B]`` keys of the race's generated uniforms, one fresh draw per row and step: row
     ``i`` draws from ``generators[i]`` if present (a seeded request samples the same tokens
     again), the others from torch's default CPU generator.  ``KeyStream`` entries (the
     persistent batch's seeded requests) are computed together on the host; a ``torch.Generator``
-    entry draws from its own stream.  One host-to-device copy."""
-    keys = torch.randint(_SEED_LO, _SEED_HI, (B,), dtype=torch.int64)
+    entry draws from its own stream.  One host-to-device copy; with ``staging`` (device
+    tensors only) no allocation, and the returned tensor is the staging's device buffer, valid
+    until the next draw on it."""
+    use = staging is not None and device.type == "cuda"
+    if use:
+        keys, dev_keys = staging.acquire(B, device)
+        torch.randint(_SEED_LO, _SEED_HI, (B,), dtype=torch.int64, out=keys)
+    else:
+        keys = torch.randint(_SEED_LO, _SEED_HI, (B,), dtype=torch.int64)
     ks = [(i, g) for i, g in generators.items() if isinstance(g, KeyStream)]
     if ks:
         rows = np.array([i for i, _ in ks], np.int64)
@@ -86,6 +125,10 @@ def draw_seeds(B: int, generators: dict, device: torch.device) -> torch.Tensor:
         if not isinstance(g, KeyStream):
             keys[i] = torch.randint(_SEED_LO, _SEED_HI, (1,), dtype=torch.int64,
                                     device=g.device, generator=g)[0].cpu()
+    if use:
+        dev_keys.copy_(keys, non_blocking=True)
+        staging.copied()
+        return dev_keys
     if device.type == "cuda":
         keys = keys.pin_memory()
     return keys.to(device, non_blocking=True)
@@ -164,6 +207,7 @@ class Sampler:
         self.logprobs_mode = logprobs_mode
         self.logit_softcap = logit_softcap
         self.logit_softcap_f16 = bool(logit_softcap_f16)
+        self._seeds = SeedStaging()
 
     def __call__(self, logits: torch.Tensor, sampling_metadata: SamplingMetadata) -> SamplerOutput:
         return self.forward(logits, sampling_metadata)
@@ -176,9 +220,14 @@ class Sampler:
         dev = logits.device
 
         temperature = None if m.all_greedy else m.temperature
-        seeds = None
+        seeds = key = None
         if temperature is not None:
-            seeds = draw_seeds(B, m.generators, dev)
+            if m.generators:
+                seeds = draw_seeds(B, m.generators, dev, self._seeds)
+            else:
+                # no seeded request: one key for the launch, from torch's default generator,
+                # passed by value (row r draws as with that seed and offset r)
+                key = int(torch.randint(_SEED_LO, _SEED_HI, (1,), dtype=torch.int64))
 
         penalties = {}
         if not m.no_penalties and m.token_state is not None:
@@ -211,7 +260,8 @@ class Sampler:
                               adjust_vals=vals.to(dev, non_blocking=True))
 
         res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
-                         min_p=m.min_p, rng_seeds=seeds, num_logprobs=m.max_num_logprobs,
+                         min_p=m.min_p, rng_seeds=seeds, rng_key=key,
+                         num_logprobs=m.max_num_logprobs,
                          logit_softcap=self.logit_softcap,
                          logit_softcap_f16=self.logit_softcap_f16, **penalties, **processors)
         lp = None
