@@ -553,6 +553,16 @@ def main():
         R.fill_(1.0)
         PR.fill_(0.0)
         FR.fill_(0.0)
+        # C5 without logprobs, and the same with one row restricted to 20 tokens (an allowed
+        # mask for the whole launch, all-ones on the other rows)
+        one_masked5 = np.ones((B, V), bool)
+        one_masked5[3] = False
+        one_masked5[3, np.random.default_rng(68).choice(V, 20, replace=False)] = True
+        variants["no_logprobs"] = variant_timing(_lib, L, w, sets, T, K, P, MP, R, PR, FR, out,
+                                                 flags, nkept, ws, stream, vsteps, vwarm)
+        variants["no_logprobs_one_masked_row"] = variant_timing(
+            _lib, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, stream, vsteps,
+            vwarm, allowed=one_masked5)
     if variants:
         log("variants: " + ", ".join(
             f"{k} {v['kernel_us']:.2f} us ({v['mismatches']} mismatches in {v['parity_rows']} rows, "

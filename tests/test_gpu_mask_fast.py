@@ -139,3 +139,77 @@ def test_unaligned_rows_and_processors(cuda):
     assert_same(g, ref, w.name)
     g2, ref2 = _run(w, allowed, cuda, adjust_ids=aid, adjust_vals=aval)
     assert_same(g2, ref2, w.name + " aligned")
+
+
+STREAM_TOPP = 0x200
+
+
+def test_c5_topp_rows_with_masks(cuda):
+    """C5's top-p rows (1024 x 151936 fp32, T 1, top-p 0.95, no top-k; without logprobs) with an
+    allowed mask on every row -- one token, 5, 50, 1000, half the vocabulary, everything, 300:
+    the top-p stream masks as it loads, so the rows stay on it."""
+    w = W.config(5)
+    w.num_logprobs = None
+    B, V = w.shape
+    rng = np.random.default_rng(67)
+    allowed = _allowed_sets(rng, B, V)
+    g, ref = _run(w, allowed, cuda)
+    assert_same(g, ref, "C5 + masks")
+    on = (g["flags"] & STREAM_TOPP) != 0
+    assert on.mean() > 0.95, f"{int((~on).sum())} of {B} rows left the top-p stream"
+
+
+def test_c5_one_masked_row(cuda):
+    """The bench's variant: C5 (no logprobs) with one row restricted to 20 tokens."""
+    w = W.config(5)
+    w.num_logprobs = None
+    B, V = w.shape
+    allowed = np.ones((B, V), bool)
+    allowed[3] = False
+    allowed[3, np.random.default_rng(68).choice(V, 20, replace=False)] = True
+    g, ref = _run(w, allowed, cuda)
+    assert_same(g, ref, "C5 one masked row")
+    # (the further passes some rows need mask their logits too)
+    assert (g["flags"] & STREAM_TOPP).all()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_topp_masks_small_rows_flat_rows_and_tails(cuda, dt):
+    """Top-p rows with masks at every density, T != 1, min-p, greedy rows, flat rows whose
+    nucleus reaches below the candidates (further passes over the masked logits, shared with
+    other workgroups), an odd vocabulary (the tail element by element), and a row with nothing
+    allowed."""
+    rng = np.random.default_rng(69)
+    B, V = 42, 60001
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    x[::6] = rng.normal(0, 0.3, (7, V)).astype(np.float32)  # flat rows
+    T = np.where(np.arange(B) % 7 == 3, 0.0, np.where(np.arange(B) % 2 == 0, 1.0, 0.8)).astype(np.float32)
+    mp = np.where(np.arange(B) % 5 == 1, 0.05, 0.0).astype(np.float32)
+    w = _wl(f"{dt} top-p masks", x, T, k=0, p=0.92, mp=mp, seed=70)
+    if dt == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        w.logits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    elif dt == "f16":
+        w.logits = x.astype(np.float16)
+    w.dtype = dt
+    allowed = _allowed_sets(rng, B, V)
+    allowed[:, V - 1] = rng.random(B) < 0.5
+    allowed[41] = False
+    g, ref = _run(w, allowed, cuda)
+    assert_same(g, ref, w.name)
+
+
+def test_topp_masks_flat_rows_take_the_passes(cuda):
+    """Flat rows with half their vocabulary allowed: the nucleus reaches below the candidates,
+    so the exact recount and the wide race run over the masked logits, in chunks shared with
+    other workgroups; a few steeper rows in the same launch."""
+    rng = np.random.default_rng(73)
+    B, V = 40, 120000
+    x = rng.normal(0, 0.4, (B, V)).astype(np.float32)
+    x[::5] *= 8.0
+    w = _wl("flat + masks", x, 0.9, k=0, p=0.97, seed=74)
+    allowed = rng.random((B, V)) < 0.5
+    g, ref = _run(w, allowed, cuda)
+    assert_same(g, ref, w.name)
+    assert (g["flags"] & STREAM_TOPP).all()
+    assert (g["flags"] & (0x400 | 0x800)).any(), "no masked row took a further pass"

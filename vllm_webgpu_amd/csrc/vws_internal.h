@@ -120,7 +120,6 @@ struct KArgs {
     int64_t ustride;
     const uint64_t* rng_seed;   // [B] keys of the generated uniforms (when u is NULL)
     const uint64_t* rng_offset; // [B] their counter offsets, or NULL (0)
-    uint64_t rng_key;           // launch-wide key (u and rng_seed NULL): row r's offset is r
     int32_t* sampled;
     uint32_t* flags;
     int32_t* nkept;
@@ -149,6 +148,7 @@ struct KArgs {
     int coop_wait_polls;    // bound of an owner's wait for the chunks helpers run (>= 0)
     uint64_t* trace;        // trace build: [trace_wgs][VWS_TRACE_SLOTS] phase stamps, or null
     int trace_wgs;
+    uint64_t rng_key;       // launch-wide key (u and rng_seed NULL): row r's offset is r
 };
 
 // Workspace layout (bytes, 256-aligned sections).

@@ -192,7 +192,7 @@ __device__ __noinline__ int topp_hist_entry(int r, uint64_t kernarg, uint32_t ta
 // The pass sm.pd over row r's body vectors [v0, v1) (and the edges): without, and with the
 // penalties from the token-state table (separate functions, so that the plain pass keeps its
 // registers).
-template <typename T, bool PEN>
+template <typename T, bool PEN, bool MSK>
 __device__ __forceinline__ void topp_range_body(int r, uint64_t kernarg, int v0, int v1, int edges) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
@@ -212,7 +212,7 @@ __device__ __forceinline__ void topp_range_body(int r, uint64_t kernarg, int v0,
     d.kkeep = tp_u(sm.pd.kkeep);
     d.kmem = tp_u(sm.pd.kmem);
     TpPassAcc acc;
-    tp_pass_range<T, PEN>(a, sm, r, d, v0, v1, edges != 0, acc);
+    tp_pass_range<T, PEN, MSK>(a, sm, r, d, v0, v1, edges != 0, acc);
     tp_pass_reduce(sm, d.kind, acc);
 #else
     (void)r; (void)kernarg; (void)v0; (void)v1; (void)edges;
@@ -221,15 +221,39 @@ __device__ __forceinline__ void topp_range_body(int r, uint64_t kernarg, int v0,
 
 template <typename T>
 __device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
-    topp_range_body<T, false>(r, kernarg, v0, v1, edges);
+    topp_range_body<T, false, false>(r, kernarg, v0, v1, edges);
 }
 
 template <typename T>
 __device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
-    topp_range_body<T, true>(r, kernarg, v0, v1, edges);
+    topp_range_body<T, true, false>(r, kernarg, v0, v1, edges);
 }
 
-template <typename T, bool PEN>
+// the same for launches with an allowed mask (elements outside it are -inf)
+template <typename T>
+__device__ __noinline__ void topp_range_mask_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
+    topp_range_body<T, false, true>(r, kernarg, v0, v1, edges);
+}
+
+template <typename T>
+__device__ __noinline__ void topp_range_mask_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
+    topp_range_body<T, true, true>(r, kernarg, v0, v1, edges);
+}
+
+// A range of a pass over row r: with the row's penalties (pen) and the launch's mask (MSK).
+template <typename T, bool MSK>
+__device__ __forceinline__ void topp_range_any(bool pen, int r, uint64_t kernarg, int v0, int v1,
+                                               int edges) {
+    if (MSK) {
+        if (pen) topp_range_mask_hist_entry<T>(r, kernarg, v0, v1, edges);
+        else topp_range_mask_entry<T>(r, kernarg, v0, v1, edges);
+    } else {
+        if (pen) topp_range_hist_entry<T>(r, kernarg, v0, v1, edges);
+        else topp_range_entry<T>(r, kernarg, v0, v1, edges);
+    }
+}
+
+template <typename T, bool PEN, bool MSK>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -294,8 +318,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     const uint32_t slot = tp_u(sm.cp[4]);
     const bool pen = PEN && tp_pass_pen(a, r, kind);
     if (slot == kCoopNone) {
-        if (pen) topp_range_hist_entry<T>(r, kernarg, 0, nbody, 1);
-        else topp_range_entry<T>(r, kernarg, 0, nbody, 1);
+        topp_range_any<T, MSK>(pen, r, kernarg, 0, nbody, 1);
         return;
     }
     CoopSlot& S = st->slot[slot];
@@ -346,8 +369,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     for (int k = 0; c != kCoopNone; ++k) {
         const int v0 = (int)c * cvecs;
         const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
-        if (pen) topp_range_hist_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
-        else topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        topp_range_any<T, MSK>(pen, r, kernarg, v0, v1, c == 0u ? 1 : 0);
         __syncthreads();
         if (tid == 0) {
             ++own;
@@ -468,7 +490,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
 // launch is left to start, so no row waits for this workgroup's CU); otherwise return once no
 // chunk is open.  PEN: the launch has penalties from a token-state table with its bitmap (some
 // chunks are of penalised passes; without, the function calls only the plain range function).
-template <typename T, bool PEN>
+template <typename T, bool PEN, bool MSK>
 __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int NT = kGenThreads;
@@ -566,8 +588,7 @@ __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
         const int nbody = __builtin_amdgcn_readfirstlane(sl.nbody);
         const int v0 = (int)c * cvecs;
         const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
-        if (PEN && tp_pass_pen(a, r, kind)) topp_range_hist_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
-        else topp_range_entry<T>(r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        topp_range_any<T, MSK>(PEN && tp_pass_pen(a, r, kind), r, kernarg, v0, v1, c == 0u ? 1 : 0);
         __syncthreads();
         // the next chunk, claimed while this one's totals go out (before this one counts as
         // done, so the pass cannot have been replaced meanwhile)
@@ -1196,7 +1217,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const int k = fast_k(a, prm);
     VWS_TRACE_MARK_AFTER(a, VWS_TRACE_PARAMS, k);
     if (k == 0) {
-        *topp_row = topp_eligible(a, prm);
+        // MASK: the top-p stream masks by whole words only for rows that start 16-byte aligned
+        *topp_row = topp_eligible(a, prm) && !(MASK && sl.a != 0);
         return false;
     }
     // raw logprobs are of the capped logits, which the stream does not compute
@@ -1884,11 +1906,11 @@ __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logit
         if (prm.has_hist) {
             // history rows: their bitmap into LDS first (a copy of the stream of its own)
             const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
-            topp_stream<T>(a, g_row_sh.t, r, prm, fill);
+            topp_stream<T, MASK>(a, g_row_sh.t, r, prm, fill);
         } else {
-            topp_stream<T>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+            topp_stream<T, MASK>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
         }
-        why = topp_finish<T>(a, g_row_sh.t, r, prm, kernarg);
+        why = topp_finish<T, MASK>(a, g_row_sh.t, r, prm, kernarg);
         // done with it: no longer pending, and no longer holding slots (thread 0 set the mark)
         if (threadIdx.x == 0 && a.coop)
             ag_add64(&a.coop->wgs, 0ull - kCoopPending - (g_row_sh.t.coop_hold ? kCoopActive : 0ull));
@@ -1907,7 +1929,7 @@ __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logit
 // workgroup counts itself finished; once every workgroup has started it polls while top-p rows
 // are in progress, before that it only runs chunks already open (so that it keeps no row from
 // starting).  Out of line: nothing but the kernarg address stays live across the row.
-template <typename T>
+template <typename T, bool MASK>
 __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
@@ -1916,8 +1938,8 @@ __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
     if (!a.coop_count) {
         if (long_row) {
             __syncthreads();
-            if (a.tbits) coop_help_entry<T, true>(kernarg, 1);
-            else coop_help_entry<T, false>(kernarg, 1);
+            if (a.tbits) coop_help_entry<T, true, MASK>(kernarg, 1);
+            else coop_help_entry<T, false, MASK>(kernarg, 1);
         }
         return;
     }
@@ -1934,8 +1956,8 @@ __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
     const uint32_t how = tp_u(sm.cp[6]);
     if (how) {
         __syncthreads();
-        if (a.tbits) coop_help_entry<T, true>(kernarg, how == 2u ? 1 : 0);
-        else coop_help_entry<T, false>(kernarg, how == 2u ? 1 : 0);
+        if (a.tbits) coop_help_entry<T, true, MASK>(kernarg, how == 2u ? 1 : 0);
+        else coop_help_entry<T, false, MASK>(kernarg, how == 2u ? 1 : 0);
     }
 #else
     (void)kernarg;
@@ -2031,7 +2053,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
     trace_put(a, VWS_TRACE_XCC, trace_xcc());
     trace_put(a, VWS_TRACE_ROWID, (uint64_t)r);
 #endif
-    if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T>(kernarg, long_row ? 1 : 0);
+    if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T, MASK>(kernarg, long_row ? 1 : 0);
     VWS_TRACE_MARK(a, VWS_TRACE_EXIT);
 }
 

@@ -153,6 +153,7 @@ struct TopPSmem {
     uint32_t cp[19];
     uint32_t coop_hold;
     uint32_t coop_fail;                   // a cooperative pass of the row was not completed
+    uint32_t ninf;                        // masked rows: -inf elements left out of the buffers
 };
 
 // Entries dropped by a compaction, as terms of the approximate sum (per lane), and the new
@@ -169,7 +170,10 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
 
 // Whether the single-pass top-p path may serve the row.
 __device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
-    if (p.need_hash || a.allowed || a.softcap > 0.0f) return false;
+    if (p.need_hash || a.softcap > 0.0f) return false;
+    // an allowed mask: the stream masks as it loads (rows starting 16-byte aligned, checked by
+    // the caller); with raw logprobs such launches take the multi-pass path
+    if (a.allowed && a.L >= 0) return false;
     // penalties: from the token-state table with its bitmap (need_hash covers the lists)
     if (p.has_hist && !(p.tab && a.tbits && a.V <= kTpHistMaxV)) return false;
     if (p.greedy) return a.L >= 0;
@@ -342,7 +346,7 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
 // The stream over row r.  Publishes each wave's results into sm; topp_finish completes the row.
 // fill: the entries per wave the seed threshold aims at (less than kTpFill of the slots when
 // history tokens will need some).
-template <typename T>
+template <typename T, bool MASK>
 __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
                                             float fill) {
     constexpr int NT = kGenThreads;
@@ -367,9 +371,39 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
             Elem<T>::from_words((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], buf[q]);
         }
     };
+    // MASK: the row's allowed-token words, one per lane and iteration (lane l: word l % (2 VEC)
+    // of the wave's vector group l / (2 VEC)); elements outside the mask become -inf as they
+    // are loaded (the row starts 16-byte aligned, so the words line up with the vectors)
+    const uint32_t* mrow = MASK ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(mrow, MASK ? 4u * (uint32_t)((V + 31) >> 5) : 0u);
+    auto load_mask = [&](uint32_t& mw, int it) __attribute__((always_inline)) {
+        if (MASK) {
+            const int ln = lane_now();
+            const uint32_t wi = (uint32_t)((((it * U + ln / (2 * VEC)) * NT + wave * kWave) * VEC) >> 5) +
+                                (uint32_t)(ln % (2 * VEC));
+            mw = __builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * wi, 0u, 0);
+        }
+    };
+    auto mask_iter = [&](float (&buf)[U][VEC], uint32_t mw) __attribute__((always_inline)) {
+        if (MASK) {
+            const int ln = lane_now();
+#pragma unroll
+            for (int q = 0; q < U; ++q) {
+                const int src = q * 2 * VEC + ((ln * VEC) >> 5);
+                const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mw);
+                const uint32_t bits = w >> ((ln * VEC) & 31);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) buf[q][j] = ((bits >> j) & 1u) ? buf[q][j] : -__builtin_inff();
+            }
+        }
+    };
     float A[U][VEC], Bq[U][VEC];
+    uint32_t MA = 0u, MB = 0u;
     load_iter(A, 0);
+    load_mask(MA, 0);
     load_iter(Bq, 1);
+    load_mask(MB, 1);
+    mask_iter(A, MA);
     // seed: a threshold from the lane maxima over the first iteration.  A lane's maximum over its
     // E elements reaches tau with probability 1 - (1 - phi)^E when a fraction phi of the
     // elements does, so a wave's m-th largest lane maximum, m = 64 (1 - (1 - phi)^E), admits
@@ -394,7 +428,10 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         const int msel = min(64, max(1, (int)__builtin_ceilf(64.0f * pl)));
         tw = wave_mth_largest64(key_of(lmax), msel);
     }
-    if (tid == 0) sm.status = 0u;
+    if (tid == 0) {
+        sm.status = 0u;
+        if (MASK) sm.ninf = 0u;
+    }
     if (lane == 0) sm.bc[wave] = tw;  // bc is free until the finish's first barrier
     __syncthreads();
     VWS_TRACE_MARK(a, VWS_TRACE_SEED);
@@ -411,6 +448,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     cb.set_tau(tau0);
     double acc = 0.0, accr = 0.0;
     float accz = 0.0f;
+    uint64_t ninf = 0ull;  // MASK: -inf elements kept out of the buffers (some lane had one)
     // one vector of VEC elements starting at element i0 (okv: in the row; hv: the elements whose
     // history bit counts): candidates into the buffer, every other element into the sums (a zero
     // term for NaN and -inf).  The ballots of the element tests decide whether any lane appends
@@ -423,7 +461,11 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         const uint64_t okm = wave_ballot(okv);
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-            bal[j] = wave_ballot(v[j] >= cb.tauf) & okm;
+            // MASK: only finite values are candidates (a heavily masked row leaves no seed, and
+            // its -inf elements would fill the buffers); they are survivors of zero mass, noted
+            // for the finish
+            bal[j] = wave_ballot(v[j] >= cb.tauf && (!MASK || v[j] > -__builtin_inff())) & okm;
+            if (MASK) ninf |= wave_ballot(v[j] == -__builtin_inff()) & okm;
             any |= bal[j];
         }
         if (any) cb.append_vec<VEC>(sm, v, bal, okv, i0);
@@ -467,11 +509,17 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         }
     };
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
+        if (it > 0) mask_iter(A, MA);  // (the first iteration was masked before the seed)
         examine(A, it);
         load_iter(A, it + 2);
+        load_mask(MA, it + 2);
         shrink();
-        if (it + 1 < nit && !cb.ovf) examine(Bq, it + 1);
+        if (it + 1 < nit && !cb.ovf) {
+            mask_iter(Bq, MB);
+            examine(Bq, it + 1);
+        }
         load_iter(Bq, it + 3);
+        load_mask(MB, it + 3);
         shrink();
     }
     if (wave == 0 && !cb.ovf) {
@@ -483,8 +531,13 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         if (tid <= 1) i0 = sl.load_edge(tid, v);
         const int end = tid == 0 ? sl.a : V;
 #pragma unroll
-        for (int j = 0; j < VEC; ++j)
-            if (!(tid <= 1 && i0 + j < end)) v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
+        for (int j = 0; j < VEC; ++j) {
+            if (!(tid <= 1 && i0 + j < end)) {
+                v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
+            } else if (MASK && !((mrow[(i0 + j) >> 5] >> ((i0 + j) & 31)) & 1u)) {
+                v[j] = -__builtin_inff();
+            }
+        }
         consume(v, i0, true);
     }
 
@@ -511,6 +564,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         sm.wCnt[wave] = (uint32_t)cb.cnt;
         sm.wMax[wave] = kmax;
         if (wave == 0) sm.anchor = aw;
+        if (MASK && ninf) atomicOr(&sm.ninf, 1u);
         const bool finite = (s == s) && s < 1e300 && (z == z) && z < 3e38f && (sr == sr) && sr < 1e300;
         if (!finite) atomicOr(&sm.status, 2u);
     }
@@ -569,8 +623,10 @@ struct TpPen {
 // (a range is a chunk of a few steps: the second load overlaps the first step's work).  f(v, u, i0, ok) gets the VEC elements of one vector from element i0 on (ok: the
 // vector lies in the range; head and tail are NaN-padded) and, with WITH_U, their uniforms
 // (dword-aligned 16-byte loads).  PEN: the elements are penalised first from their token-state
-// words (streamed like the uniforms), so that f sees processed values.
-template <typename T, bool WITH_U, bool PEN, typename F>
+// words (streamed like the uniforms), so that f sees processed values.  MSK: elements outside
+// the row's allowed mask become -inf first (one mask word per vector; the row starts 16-byte
+// aligned, so a vector's bits lie in one word).
+template <typename T, bool WITH_U, bool PEN, bool MSK, typename F>
 __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int v1, bool edges,
                                              const TpPen& pen, F&& f) {
     constexpr int NT = kGenThreads;
@@ -593,6 +649,9 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
                                                  WITH_U ? 4u * (uint32_t)(nv * VEC) : 0u);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(PEN ? (const void*)(pen.wrow + e0) : (const void*)row,
                                                  PEN ? 4u * (uint32_t)(nv * VEC) : 0u);
+    const uint32_t* arow = MSK ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(MSK ? (const void*)arow : (const void*)row,
+                                                 MSK ? 4u * (uint32_t)((V + 31) >> 5) : 0u);
     auto tid_now = [&]() __attribute__((always_inline)) { return wave * kWave + lane_now(); };
     using W4 = decltype(__builtin_amdgcn_raw_buffer_load_b128(lrs, 0u, 0u, 0));
     // a history token's processed value (a zero word: the value itself)
@@ -602,13 +661,16 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
     };
     // vectors (it * UP + q) * NT + tid lie past the range for every thread once
     // (it * UP + q) * NT >= nv: such loads and their work are skipped (a uniform test)
-    auto load = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], W4 (&ww)[UP][WW > 0 ? WW : 1], int it)
-                    __attribute__((always_inline)) {
+    auto load = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], W4 (&ww)[UP][WW > 0 ? WW : 1],
+                    uint32_t (&mw)[UP], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < UP; ++q) {
             if ((it * UP + q) * NT >= nv) break;
             const uint32_t vi = (uint32_t)(tid_now() + (it * UP + q) * NT);
             lw[q] = __builtin_amdgcn_raw_buffer_load_b128(lrs, 16u * vi, 0u, 2 /* nt */);
+            if (MSK)
+                mw[q] = __builtin_amdgcn_raw_buffer_load_b32(
+                    mrs, 4u * (((uint32_t)e0 + vi * (uint32_t)VEC) >> 5), 0u, 0);
 #pragma unroll
             for (int g = 0; g < UW; ++g)
                 uw[q][g] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -619,8 +681,8 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
                     wrs, 4u * (vi * (uint32_t)VEC + 4u * (uint32_t)g), 0u, 2);
         }
     };
-    auto consume = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], W4 (&ww)[UP][WW > 0 ? WW : 1], int it)
-                       __attribute__((always_inline)) {
+    auto consume = [&](W4 (&lw)[UP], W4 (&uw)[UP][UW > 0 ? UW : 1], W4 (&ww)[UP][WW > 0 ? WW : 1],
+                       const uint32_t (&mw)[UP], int it) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < UP; ++q) {
             if ((it * UP + q) * NT >= nv) break;
@@ -630,6 +692,11 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
                                 (uint32_t)lw[q][3], v);
 #pragma unroll
             for (int j = 0; j < VEC; ++j) u[j] = WITH_U ? u2f((uint32_t)uw[q][j / 4][j % 4]) : 0.0f;
+            if (MSK) {
+                const uint32_t bits = mw[q] >> ((uint32_t)(e0 + vi * VEC) & 31u);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) v[j] = ((bits >> j) & 1u) ? v[j] : -__builtin_inff();
+            }
             if (PEN) {
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) v[j] = penal(v[j], (uint32_t)ww[q][j / 4][j % 4]);
@@ -640,13 +707,14 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
     W4 la[UP], lb[UP];
     W4 ua[UP][UW > 0 ? UW : 1], ub[UP][UW > 0 ? UW : 1];
     W4 wa[UP][WW > 0 ? WW : 1], wb[UP][WW > 0 ? WW : 1];
-    load(la, ua, wa, 0);
-    load(lb, ub, wb, 1);
+    uint32_t ma[UP] = {}, mb[UP] = {};
+    load(la, ua, wa, ma, 0);
+    load(lb, ub, wb, mb, 1);
     for (int it = 0; it < nit; it += 2) {
-        consume(la, ua, wa, it);
-        load(la, ua, wa, it + 2);
-        if (it + 1 < nit) consume(lb, ub, wb, it + 1);
-        load(lb, ub, wb, it + 3);
+        consume(la, ua, wa, ma, it);
+        load(la, ua, wa, ma, it + 2);
+        if (it + 1 < nit) consume(lb, ub, wb, mb, it + 1);
+        load(lb, ub, wb, mb, it + 3);
     }
     if (edges && wave == 0) {
         float v[VEC], u[VEC];
@@ -661,6 +729,8 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             u[j] = (WITH_U && i0 + j < end) ? urow[i0 + j] : 0.0f;
+            if (MSK && i0 + j < end && !((arow[(i0 + j) >> 5] >> ((i0 + j) & 31)) & 1u))
+                v[j] = -__builtin_inff();
             if (PEN && i0 + j < end) v[j] = penal(v[j], pen.wrow[i0 + j]);
         }
         f(v, u, i0, tid <= 1);
@@ -736,7 +806,7 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
 //     candidate) into acc.n.
 // PEN (rows with penalties from the token-state table, exact and wide passes only): the pass
 // sees processed values (the rank pass ranks raw ones).
-template <typename T, bool PEN>
+template <typename T, bool PEN, bool MSK>
 __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int r, const TpPassDesc& d,
                                               int v0, int v1, bool edges, TpPassAcc& acc) {
     constexpr int VEC = Elem<T>::kVec;
@@ -751,7 +821,7 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
         pen.wrow = a.tstate + (size_t)(a.trows ? a.trows[r] : r) * (size_t)a.tstride;
     }
     auto range = [&](auto with_u, auto&& f) __attribute__((always_inline)) {
-        tp_row_range<T, decltype(with_u)::value, PEN>(a, r, v0, v1, edges, pen, f);
+        tp_row_range<T, decltype(with_u)::value, PEN, MSK>(a, r, v0, v1, edges, pen, f);
     };
     if (d.kind == kTpPassExact) {
         range(BoolC<false>{}, [&](const float* v, const float*, int, bool ok)
@@ -816,7 +886,7 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
                                       __attribute__((always_inline)) { body(v, u, i0, ok, true); });
         }
     } else {
-        tp_row_range<T, false, false>(a, r, v0, v1, edges, pen, [&](const float* v, const float*, int, bool ok)
+        tp_row_range<T, false, false, MSK>(a, r, v0, v1, edges, pen, [&](const float* v, const float*, int, bool ok)
                                                                    __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) acc.n += (ok && key_of(v[j]) >= tauk) ? 1ull : 0ull;
@@ -920,7 +990,7 @@ __device__ __forceinline__ uint32_t coop_chunk_of(uint64_t x) {
 //     functions that call them, so that the others keep their registers);
 //   topp_range_entry: the pass sm.pd over the body vectors [v0, v1) of row r (and the edges),
 //     its workgroup totals into sm.bc64[10..13] as tp_pass_reduce leaves them.
-template <typename T, bool PEN>
+template <typename T, bool PEN, bool MSK>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar);
 template <typename T>
@@ -985,6 +1055,8 @@ __device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, i
     const bool greedy = prm.greedy;
     const int V = a.V;
     const uint32_t* trw = a.tstate + (size_t)prm.trow * (size_t)a.tstride;
+    // the row's allowed-token words (a masked history token's raw value is -inf), or null
+    const uint32_t* arow = a.allowed ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
     // a history token: its processed value, and with raw logprobs its raw normaliser term and
     // (at or above the threshold by raw value) its listing
     float s0h = 0.0f;
@@ -1072,7 +1144,8 @@ __device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, i
             const uint32_t j = base + (uint32_t)(lane * kTpWaves + wave);
             const bool in = j < nl;
             const uint32_t t = in ? sm.hl[j] : 0u;
-            const float x = in ? Elem<T>::load1(lrow + t) : 0.0f;
+            float x = in ? Elem<T>::load1(lrow + t) : 0.0f;
+            if (in && arow && !((arow[t >> 5] >> (t & 31)) & 1u)) x = -__builtin_inff();  // masked
             const uint32_t wd = in ? trw[t] : 0u;
             float y = 0.0f;
             if (in) {
@@ -1116,7 +1189,7 @@ __device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, i
 // Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
 // take the multi-pass path (VWS_FALLBACK_*).  Every return decision is uniform over the
 // workgroup: values that decide are read from LDS after a barrier, or are scalars.
-template <typename T>
+template <typename T, bool MASK>
 __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
                                            uint64_t kernarg) {
     constexpr int NT = kGenThreads;
@@ -1168,8 +1241,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     // a cooperative pass that was not completed marks sm.coop_fail; the row is handed over right
     // after it, before anything is written
     auto pass = [&](int kind, uint32_t key, int bs) __attribute__((always_inline)) {
-        if (hist) topp_pass_entry<T, true>(kind, r, kernarg, Tt, m, lp_min, key, bs);
-        else topp_pass_entry<T, false>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        if (hist) topp_pass_entry<T, true, MASK>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        else topp_pass_entry<T, false, MASK>(kind, r, kernarg, Tt, m, lp_min, key, bs);
         __syncthreads();
     };
     for (int i = tid; i < kTpBuckets; i += NT) {
@@ -1341,7 +1414,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
                     const double lo = floor(sap - err) - nterms;
                     nlo = lo > 0.0 ? (uint64_t)lo : 0ull;
                     nhi = (uint64_t)ceil(sap + err);
-                    sm.bc[9] = tauk > 0x007FFFFFu ? 1u : 0u;  // elements below the candidates survive
+                    // elements below the candidates survive (masked rows: the -inf elements
+                    // outside the buffers are survivors of zero mass)
+                    sm.bc[9] = (tauk > 0x007FFFFFu || (MASK && sm.ninf != 0u)) ? 1u : 0u;
                 }
                 sm.bc[8] = (uint32_t)why;
                 sm.bc64[0] = nlo + Sx;
