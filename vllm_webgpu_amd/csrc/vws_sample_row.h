@@ -1884,6 +1884,28 @@ __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
 }
 
 // One row: the single pass, the single-pass top-p path or the multi-pass path.  Returns whether
+// The single-pass top-p path of a row in a launch with an allowed mask (stream and finish);
+// returns 0 or the reason the row takes the multi-pass path.
+template <typename T>
+__device__ __noinline__ int topp_row_mask_entry(int r, uint64_t kernarg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const KArgs a = kargs_at(kernarg);
+    r = __builtin_amdgcn_readfirstlane(r);
+    const RowP prm = row_params(a, r);
+    if (prm.has_hist) {
+        const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
+        topp_stream<T, true>(a, g_row_sh.t, r, prm, fill);
+    } else {
+        topp_stream<T, true>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+    }
+    return topp_finish<T, true>(a, g_row_sh.t, r, prm, kernarg);
+#else
+    (void)r;
+    (void)kernarg;
+    return 0;
+#endif
+}
+
 // the row took one of the longer paths (top-p or multi-pass), whose workgroup then looks for
 // chunks of other rows' passes.
 template <typename T, bool LP, bool MASK>
@@ -1902,15 +1924,21 @@ __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logit
         __syncthreads();
         // a top-p row in progress may open a cooperative pass
         if (threadIdx.x == 0 && a.coop) ag_add64(&a.coop->wgs, kCoopPending);
-        const RowP prm = row_params(a, r);
-        if (prm.has_hist) {
-            // history rows: their bitmap into LDS first (a copy of the stream of its own)
-            const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
-            topp_stream<T, MASK>(a, g_row_sh.t, r, prm, fill);
+        if (MASK) {
+            // launches with an allowed mask: out of line, so that the kernel's single pass keeps
+            // the registers it has without the masked top-p path
+            why = topp_row_mask_entry<T>(r, kernarg);
         } else {
-            topp_stream<T, MASK>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+            const RowP prm = row_params(a, r);
+            if (prm.has_hist) {
+                // history rows: their bitmap into LDS first (a copy of the stream of its own)
+                const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
+                topp_stream<T, false>(a, g_row_sh.t, r, prm, fill);
+            } else {
+                topp_stream<T, false>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+            }
+            why = topp_finish<T, false>(a, g_row_sh.t, r, prm, kernarg);
         }
-        why = topp_finish<T, MASK>(a, g_row_sh.t, r, prm, kernarg);
         // done with it: no longer pending, and no longer holding slots (thread 0 set the mark)
         if (threadIdx.x == 0 && a.coop)
             ag_add64(&a.coop->wgs, 0ull - kCoopPending - (g_row_sh.t.coop_hold ? kCoopActive : 0ull));
