@@ -642,8 +642,10 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": gbps_kern / PEAK_HBM_GBPS, "traffic": pmc_traffic_bytes(args.config),
-            "kernel": ("vws::row_kernel<unsigned short>" if w.dtype == "bf16"
-                       else "vws::row_kernel<float>"),
+            # the instantiation the launch ran: element type, raw logprobs, allowed mask
+            "kernel": "vws::row_kernel<{}, {}, false>".format(
+                "unsigned short" if w.dtype == "bf16" else "float",
+                "true" if w.num_logprobs is not None else "false"),
         },
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "cpu_baseline_reference_ops": cpu_ref_ops,
