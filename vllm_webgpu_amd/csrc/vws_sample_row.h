@@ -1401,8 +1401,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     double lacc = 0.0;
     // One vector (VEC elements per lane) at a time: the lane maximum against the threshold
     // decides for the whole wave whether any element of the vector is examined one by one.
+    // MASK: the first iteration was masked whole (the seed needs it); later ones are masked
+    // only where a vector passes the threshold by its raw values (a masked value is at most
+    // its raw one), which on rows the mask leaves mostly open is a few vectors per iteration
     auto examine = [&](float (&buf)[U][VEC], uint32_t mw, int it) __attribute__((always_inline)) {
-        mask_iter(buf, mw);
         cb.refresh();
         const int t = tid_now();
         float lit = 0.0f;
@@ -1419,8 +1421,21 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             float mq = buf[q][0];
 #pragma unroll
             for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
-            const uint64_t hm = wave_ballot(ok && mq >= cb.tauf);
+            uint64_t hm = wave_ballot(ok && mq >= cb.tauf);
             if (__builtin_expect(hm == 0ull, 1)) continue;
+            if (MASK && it > 0) {
+                const int ln = lane_now();
+                const int src = q * 2 * VEC + ((ln * VEC) >> 5);
+                const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mw);
+                const uint32_t bits = w >> ((ln * VEC) & 31);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) buf[q][j] = ((bits >> j) & 1u) ? buf[q][j] : -__builtin_inff();
+                mq = buf[q][0];
+#pragma unroll
+                for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
+                hm = wave_ballot(ok && mq >= cb.tauf);
+                if (hm == 0ull) continue;
+            }
             cb.template append_vec<VEC>(buf[q], sl.a + vi * VEC, hm);
         }
         if (LP) lacc += (double)lit;
@@ -1837,15 +1852,22 @@ __device__ __noinline__ int row_logprobs_entry(int r, uint64_t kernarg) {
     const uint64_t me = ((uint64_t)rk << 32) | (0x7FFFFFFFu - ix);
     if (mine) keys[tid] = me;
     const float A = val_of(km);  // the row maximum: the largest candidate
-    if (tid == 0) {
-        double S = 0.0;
-        for (int w = 0; w < kRowWaves; ++w)
-            if (sm.lpS[w] > 0.0) S += sm.lpS[w] * exp2((double)sm.lpA[w] - (double)A * (double)kLog2e);
-        sm.lplog = (float)log(S);
+    if (tid < kWave) {
+        // the waves' sums rescaled to the row maximum, one lane per wave (double exp2 and log
+        // in parallel rather than one after another in one thread), summed by a butterfly
+        double t = 0.0;
+        if (lane < kRowWaves && sm.lpS[lane] > 0.0)
+            t = sm.lpS[lane] * exp2((double)sm.lpA[lane] - (double)A * (double)kLog2e);
+#pragma unroll
+        for (int o = 1; o < kRowWaves; o <<= 1)
+            t += __builtin_bit_cast(double, lane_xor64(__builtin_bit_cast(uint64_t, t), o));
+        if (lane == 0) sm.lplog = (float)log(t);
     }
     __syncthreads();
     uint32_t pos = 0u;
     if (mine && rk >= tmax) {
+        // (eight independent LDS reads in flight per step)
+#pragma unroll 8
         for (int j = 0; j < total; ++j) pos += keys[j] > me ? 1u : 0u;
     }
     const float logS = sm.lplog;

@@ -2,6 +2,7 @@
 library (``_vws_trace.so``, ``vws_trace_set``), aggregated per phase and per XCD.
 
     python -m vllm_webgpu_amd.trace --config 3 [--launches 24] [--table-history]
+                                    [--logprobs L] [--mask-rows N]
 
 Runs ``--launches`` back-to-back ``vws_sample`` launches of one of the BASELINE workloads (three
 input sets rotated, as ``bench.py`` does) after warm-up launches, each launch writing its own
@@ -35,7 +36,7 @@ PATHS = {"single pass": lambda f: (f & (_lib.FLAG_GENERAL_PATH | _lib.FLAG_STREA
 TICKS_PER_US = 100.0
 
 
-def _inputs(cfg: int, dev, table_history: bool, sets: int):
+def _inputs(cfg: int, dev, table_history: bool, sets: int, logprobs=-1, mask_rows: int = 0):
     import torch
 
     from . import ops
@@ -59,6 +60,20 @@ def _inputs(cfg: int, dev, table_history: bool, sets: int):
               uniforms=None if w.uniforms is None else torch.from_numpy(w.uniforms).to(dev),
               num_logprobs=w.num_logprobs)
     name = w.name
+    if logprobs is None or logprobs >= 0:
+        kw["num_logprobs"] = logprobs
+        name += " (no logprobs)" if logprobs is None else f" ({logprobs} logprobs)"
+    if mask_rows:
+        # the first mask_rows rows restricted to 20 tokens each, the others allowed everything
+        from . import ops
+
+        allowed = torch.ones((B, V), dtype=torch.bool)
+        rng = np.random.default_rng(62)
+        for i in range(mask_rows):
+            allowed[i] = False
+            allowed[i, torch.from_numpy(rng.choice(V, 20, replace=False))] = True
+        kw["allowed_mask"] = ops.pack_allowed(allowed.to(dev))
+        name += f" ({mask_rows} masked rows)"
     if table_history:
         # the workload's history ids (or, without one, C3's penalties from a 512-token output
         # history per row) as the token-state table and its bitmap
@@ -78,7 +93,7 @@ def _inputs(cfg: int, dev, table_history: bool, sets: int):
 
 
 def collect(cfg: int, launches: int = 24, warmup: int = 10, sets: int = 3,
-            table_history: bool = False):
+            table_history: bool = False, logprobs=-1, mask_rows: int = 0):
     """Runs the launches through the trace build, then the same sequence through the product
     build; returns (records [launches, B, slots] int64, flags [launches, B] uint32, (trace,
     product) kernel us per launch, workload name, batch)."""
@@ -87,7 +102,7 @@ def collect(cfg: int, launches: int = 24, warmup: int = 10, sets: int = 3,
     from . import ops
 
     dev = torch.device("cuda:0")
-    w, xs, kw, name = _inputs(cfg, dev, table_history, sets)
+    w, xs, kw, name = _inputs(cfg, dev, table_history, sets, logprobs, mask_rows)
     B = w.shape[0]
     # every launch prepared up front, so that the launches run back to back (a host that falls
     # behind would start each one from an idle device, which changes its timing)
@@ -214,9 +229,15 @@ def main(argv=None) -> int:
     ap.add_argument("--table-history", action="store_true",
                     help="the history as the token-state table and bitmap (C3's penalties for "
                          "workloads without a history)")
+    ap.add_argument("--logprobs", type=int, default=-1,
+                    help="raw logprobs per row (0..64) instead of the workload's; -2: none")
+    ap.add_argument("--mask-rows", type=int, default=0,
+                    help="an allowed mask with the first N rows restricted to 20 tokens")
     args = ap.parse_args(argv)
+    lp = None if args.logprobs == -2 else args.logprobs
     rec, fl, kus, name, B = collect(args.config, args.launches, args.warmup,
-                                    table_history=args.table_history)
+                                    table_history=args.table_history, logprobs=lp,
+                                    mask_rows=args.mask_rows)
     print(report(rec, fl, kus, name, B))
     return 0
 
