@@ -194,11 +194,12 @@ def token_state_timing(lib_mod, L, W, w, sets, T, K, P, MP, R, PR, FR, out, flag
 
 def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, stream,
                    steps: int, warmup: int, num_logprobs=None, parity_rows: int = 16,
-                   allowed=None, hist=None, table: bool = False) -> dict:
+                   allowed=None, hist=None, table: bool = False, adjust=None) -> dict:
     """The launch with one thing changed (raw logprobs requested, an allowed mask [B, V] bool,
-    or a [B, H] output history replacing the workload's: as padded id lists, or with `table` as
-    the token-state table and its bitmap the runner keeps, built by vws_token_state_update),
-    timed with kernel-stamped events and checked against the oracle on its first rows."""
+    a [B, H] output history replacing the workload's: as padded id lists, or with `table` as
+    the token-state table and its bitmap the runner keeps, built by vws_token_state_update; or
+    `adjust` = (ids, vals, lens), a sparse processor list), timed with kernel-stamped events and
+    checked against the oracle on its first rows."""
     import torch
 
     from oracle import sampler as O  # checker only
@@ -228,6 +229,7 @@ def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkep
               torch.empty((B, num_logprobs + 1), dtype=torch.float32, device=out.device),
               torch.empty(B, dtype=torch.int32, device=out.device))
     argv, keep = [], []
+    adj_d = None if adjust is None else tuple(torch.from_numpy(t).to(out.device) for t in adjust)
     for i, (lg, u, h) in enumerate(sets):
         trows = None
         if table:
@@ -245,6 +247,10 @@ def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkep
             a.token_state_bits, a.token_state_bits_stride = bits.data_ptr(), bits.stride(0)
         if words is not None:
             a.allowed_mask, a.allowed_row_stride = words_d.data_ptr(), words_d.stride(0)
+        if adj_d is not None:
+            a.adjust_ids, a.adjust_vals = adj_d[0].data_ptr(), adj_d[1].data_ptr()
+            a.adjust_row_stride, a.adjust_width = adj_d[0].stride(0), adj_d[0].shape[1]
+            a.adjust_lens = adj_d[2].data_ptr()
         a.stream = stream.cuda_stream
         argv.append(a)
     lib_mod.check(L.vws_sample(ctypes.byref(argv[0])))
@@ -255,7 +261,9 @@ def variant_timing(lib_mod, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkep
                         w.repetition[:n], w.presence[:n], w.frequency[:n])
     ref = O.sample(w.logits_f32()[:n], prm, w.uniforms[:n],
                    output_ids=None if out_ids is None else out_ids[:n],
-                   num_logprobs=num_logprobs, allowed=None if words is None else words[:n])
+                   num_logprobs=num_logprobs, allowed=None if words is None else words[:n],
+                   adjust_ids=None if adjust is None else adjust[0][:n],
+                   adjust_vals=None if adjust is None else adjust[1][:n])
     mism = int((out.cpu().numpy()[:n] != ref["token"]).sum())
     if lp is not None:
         mism += int((lp[1].cpu().numpy()[:n] != ref["lp_ids"]).any(axis=1).sum())
@@ -563,6 +571,18 @@ def main():
         variants["no_logprobs_one_masked_row"] = variant_timing(
             _lib, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws, stream, vsteps,
             vwarm, allowed=one_masked5)
+        # one row with a processor list (four banned ids: a min-tokens request), lengths given
+        # so that the other rows carry none: that row takes the multi-pass path
+        ids5 = np.full((B, 8), V, np.int32)
+        vals5 = np.zeros((B, 8), np.float32)
+        lens5 = np.zeros(B, np.int32)
+        ids5[3, :4] = [11, 222, 3333, 44444]
+        vals5[3, :4] = -np.inf
+        lens5[3] = 4
+        ws5b = ops.workspace(L.vws_sample_workspace_size(B, V, 8), dev)
+        variants["one_row_with_bans"] = variant_timing(
+            _lib, L, w, sets, T, K, P, MP, R, PR, FR, out, flags, nkept, ws5b, stream, vsteps,
+            vwarm, num_logprobs=w.num_logprobs, adjust=(ids5, vals5, lens5))
     if variants:
         log("variants: " + ", ".join(
             f"{k} {v['kernel_us']:.2f} us ({v['mismatches']} mismatches in {v['parity_rows']} rows, "

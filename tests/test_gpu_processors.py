@@ -131,3 +131,35 @@ def test_long_processor_lists(cuda):
     vals = rng.uniform(-3.0, -0.1, (B, width)).astype(np.float32)
     vals[:, ::7] = -np.inf
     _run(cuda, w, w.logits, ids, vals)
+
+
+def test_processor_lengths_keep_other_rows_on_their_paths(cuda):
+    """With per-row lengths, only the rows that carry processor entries leave the top-p path
+    (the others of a launch with a list are not counted as carrying one); parity throughout."""
+    rng = np.random.default_rng(131)
+    B, V = 32, 50000
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    ids = np.full((B, 6), V, np.int32)
+    vals = np.zeros((B, 6), np.float32)
+    lens = np.zeros(B, np.int32)
+    for b in (3, 17):
+        ids[b, :4] = np.argsort(-x[b])[:4]     # ban the row's four largest logits
+        vals[b, :4] = -np.inf
+        lens[b] = 4
+    T = np.full(B, 0.9, np.float32)
+    p = np.full(B, 0.92, np.float32)
+    u = rng.random((B, V), dtype=np.float32).clip(2 ** -24, 1 - 2 ** -24)
+    prm = O.make_params(B, T, np.zeros(B, np.int32), p, np.zeros(B, np.float32),
+                        np.ones(B, np.float32), np.zeros(B, np.float32), np.zeros(B, np.float32))
+    ref = O.sample(x, prm, u, adjust_ids=ids, adjust_vals=vals, adjust_lens=lens)
+    res = ops.sample(torch.from_numpy(x).to(cuda), temperature=torch.from_numpy(T),
+                     top_p=torch.from_numpy(p), uniforms=torch.from_numpy(u).to(cuda),
+                     adjust_ids=torch.from_numpy(ids), adjust_vals=torch.from_numpy(vals),
+                     adjust_lens=torch.from_numpy(lens))
+    torch.cuda.synchronize()
+    tok = res.sampled.cpu().numpy()
+    fl = res.flags.cpu().numpy().view(np.uint32)
+    assert np.array_equal(tok, ref["token"])
+    assert np.array_equal(fl & FLAG_MASK, ref["flags"] & FLAG_MASK)
+    general = (fl & 0x100) != 0
+    assert general[[3, 17]].all() and general.sum() == 2

@@ -211,7 +211,7 @@ def test_runner_logits_processors_match_oracle(cuda):
         for i, r in enumerate(active):
             pr[i, :len(prompts[r])] = prompts[r]
             ou[i, :len(outputs[r])] = outputs[r]
-        ids, vals = processor_lists(md, B, V)
+        ids, vals, _ = processor_lists(md, B, V)
         allowed = ~md.allowed_token_ids_mask.cpu().numpy()
         words = np.zeros((B, (V + 31) // 32 * 32), np.uint64)
         words[:, :V] = allowed

@@ -147,7 +147,7 @@ def test_processor_lists_bad_words_min_tokens_and_bias():
                                    1: [[9, 14], [8, 15]]},
               min_tokens={0: (2, {0}), 1: (3, {0, 2})},
               logit_bias=[None, {4: 1.5, 20: -2.0}])
-    ids, vals = processor_lists(m, 2, V)
+    ids, vals, lens = processor_lists(m, 2, V)
     rows = [{(int(t), float(v)) for t, v in zip(ids[i].tolist(), vals[i].tolist()) if t < V}
             for i in range(2)]
     ninf = float("-inf")
@@ -157,6 +157,7 @@ def test_processor_lists_bad_words_min_tokens_and_bias():
     # row 1: [9, 14] matches, [8, 15] does not; min_tokens 3 not reached -> stop ids 0, 2; bias
     assert rows[1] == {(14, ninf), (0, ninf), (2, ninf), (4, 1.5), (20, -2.0)}
     assert ids.shape[1] == 5 and (ids[0, 2:] == V).all()          # padded with V
+    assert lens.tolist() == [2, 5]
     assert processor_lists(_meta(), 2, V) is None
 
 

@@ -150,7 +150,9 @@ def pad_output_ids(output_token_ids: list[list[int]], vocab_size: int,
 
 
 def processor_lists(m: SamplingMetadata, B: int, V: int):
-    """Host-side (ids, vals) int32/float32 [B, W] of the sparse logits processors, or None.
+    """Host-side (ids, vals, lens): int32/float32 [B, W] of the sparse logits processors and
+    int32 [B] entries per row, or None.  The lengths let rows without an entry keep their
+    paths (a row counts as carrying processors only when its length is non-zero).
 
     Bad words follow vLLM-v1's ``apply_bad_words``: a sequence bans its last token when the
     row's output ends with the rest of it (single-token sequences always).  Min-tokens bans the
@@ -180,11 +182,12 @@ def processor_lists(m: SamplingMetadata, B: int, V: int):
         return None
     ids = torch.full((B, width), V, dtype=torch.int32)
     vals = torch.zeros((B, width), dtype=torch.float32)
+    lens = torch.tensor([len(r) for r in rows], dtype=torch.int32)
     for i, r in enumerate(rows):
         if r:
             ids[i, :len(r)] = torch.tensor([t for t, _ in r], dtype=torch.int32)
             vals[i, :len(r)] = torch.tensor([v for _, v in r], dtype=torch.float32)
-    return ids, vals
+    return ids, vals, lens
 
 
 class Sampler:
@@ -255,9 +258,10 @@ class Sampler:
                                           else processors["allowed_mask"] & w)
         adj = processor_lists(m, B, V)
         if adj is not None:
-            ids, vals = adj
+            ids, vals, lens = adj
             processors.update(adjust_ids=ids.to(dev, non_blocking=True),
-                              adjust_vals=vals.to(dev, non_blocking=True))
+                              adjust_vals=vals.to(dev, non_blocking=True),
+                              adjust_lens=lens.to(dev, non_blocking=True))
 
         res = ops.sample(logits, temperature=temperature, top_k=m.top_k, top_p=m.top_p,
                          min_p=m.min_p, rng_seeds=seeds, rng_key=key,
