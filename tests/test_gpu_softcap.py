@@ -13,6 +13,7 @@ import pytest
 from oracle import sampler as O
 from tests.cases import _wl
 from tests.common import FLAG_MASK, assert_same, gpu_run, oracle_run
+from vllm_webgpu_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 
@@ -94,8 +95,8 @@ def test_values_too_close_to_settle(cuda):
 
 
 def test_general_path_rows(cuda):
-    """No top-k, top-k past the single pass, min-p, and a raising (negative) presence
-    penalty: all served by the multi-pass kernel with the cap on every logit."""
+    """No top-k with a history from id lists, top-k past the single pass, min-p, and a raising
+    (negative) presence penalty: served by the multi-pass kernel with the cap on every logit."""
     rng = np.random.default_rng(26)
     B, V = 8, 60000
     x = (rng.standard_normal((B, V)) * 10.0).astype(np.float32)
@@ -170,3 +171,48 @@ def test_cap_off_is_unchanged(cuda):
     for key in ("token", "flags", "n_kept"):
         assert np.array_equal(a[key], b[key])
     assert np.array_equal(a["flags"] & FLAG_MASK, oracle_run(w)["flags"] & FLAG_MASK)
+
+
+STREAM_TOPP = 0x200
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_topp_rows_with_the_cap(cuda, f16):
+    """Top-p rows without top-k under the cap (Gemma's sampling): the top-p stream caps every
+    logit as it loads it (and its f16 store when asked), so the rows stay on it; T != 1, min-p,
+    greedy rows with logprobs, 20 raw logprobs of the capped logits, saturated logits."""
+    rng = np.random.default_rng(141)
+    B, V = 48, 262144 // 4
+    x = (rng.standard_normal((B, V)) * 10.0).astype(np.float32)
+    x[::9, :50] = 400.0                                     # saturated at +cap
+    T = np.where(np.arange(B) % 6 == 5, 0.0, np.where(np.arange(B) % 2 == 0, 1.0, 0.8)).astype(np.float32)
+    mp = np.where(np.arange(B) % 4 == 1, 0.02, 0.0).astype(np.float32)
+    w = _wl("cap_topp", x, T, k=0, p=0.95, mp=mp, seed=142, L=20)
+    g = gpu_run(w, cuda, softcap=30.0, softcap_f16=f16)
+    assert_same(g, oracle_run(w, softcap=30.0, softcap_f16=f16), w.name)
+    on = (g["flags"] & STREAM_TOPP) != 0
+    assert on.mean() > 0.9, f"{int((~on).sum())} of {B} rows left the top-p stream"
+
+
+def test_topp_capped_flat_rows_take_the_passes(cuda):
+    """Flat rows under the cap: the exact and wide passes cap each element as they load it,
+    in chunks shared with other workgroups."""
+    rng = np.random.default_rng(143)
+    B, V = 40, 120000
+    x = (rng.normal(0, 0.4, (B, V))).astype(np.float32)
+    x[::5] *= 60.0
+    w = _wl("cap flat", x, 0.9, k=0, p=0.97, seed=144)
+    g = gpu_run(w, cuda, softcap=30.0)
+    assert_same(g, oracle_run(w, softcap=30.0), w.name)
+    assert (g["flags"] & STREAM_TOPP).all()
+    assert (g["flags"] & (0x400 | 0x800)).any(), "no capped row took a further pass"
+
+
+def test_c4_shape_with_the_cap(cuda):
+    """C4 (512 x 262144 bf16, mixed rows) under Gemma's cap of 30 with the f16 store: (nearly)
+    every row served by the single-pass paths."""
+    w = W.config(4)
+    g = gpu_run(w, cuda, softcap=30.0, softcap_f16=True)
+    assert_same(g, oracle_run(w, softcap=30.0, softcap_f16=True), "C4 + cap")
+    gen = (g["flags"] & GENERAL) != 0
+    assert gen.mean() < 0.03, f"{int(gen.sum())} of 512 rows took the multi-pass path"

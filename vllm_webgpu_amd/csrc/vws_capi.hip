@@ -16,7 +16,7 @@
 namespace vws {
 template <typename T> __global__ void fast_kernel(KArgs);
 template <typename T> __global__ void general_kernel(KArgs);
-template <typename T, bool LP, bool MASK> __global__ void row_kernel(const void*, int64_t, int, int, KArgs);
+template <typename T, bool LP, int XF> __global__ void row_kernel(const void*, int64_t, int, int, KArgs);
 template <typename T> __global__ void argmax_kernel(const T*, int64_t, int, int32_t*);
 template <typename T>
 __global__ void softmax_kernel(const T*, int64_t, int, const float*, float*, float*, float*);
@@ -91,7 +91,7 @@ DeviceInfo device_info() {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fast_kernel<float>, kFastThreads, 0) != hipSuccess || n <= 0) n = 4;
         d.fast_blocks_per_cu = n;
         int nr = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nr, row_kernel<float, false, false>, kGenThreads, 0) != hipSuccess || nr <= 0) nr = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nr, row_kernel<float, false, kXfNone>, kGenThreads, 0) != hipSuccess || nr <= 0) nr = 1;
         d.row_blocks_per_cu = nr;
         (void)hipGetLastError();
     }
@@ -399,17 +399,27 @@ int vws_sample(const vws_sample_args* a) {
                    ((k.coop_count && a->batch <= kRowOrderMaxBatch) ? 4 : 0);
     hipStream_t s = (hipStream_t)a->stream;
     // the kernel with the raw-logprob epilogue only for launches that ask for logprobs, the one
-    // that masks as it streams only for launches with an allowed mask (and no logprobs)
+    // that masks as it streams only for launches with an allowed mask (and no logprobs), the one
+    // whose top-p path caps as it streams only for launches with the soft cap (and no mask)
     const int K = VWS_KERNEL_SAMPLE;
-    const int var = a->num_logprobs >= 0 ? 1 : (a->allowed_mask ? 2 : 0);
+    const bool lp = a->num_logprobs >= 0;
+    const bool cap = a->logit_softcap > 0.0f && !a->allowed_mask;
+    const int var = (lp ? 1 : 0) | (!lp && a->allowed_mask ? 2 : 0) | (cap ? 4 : 0);
     using Kern = void (*)(const void*, int64_t, int, int, KArgs);
+    auto pick = [var](auto tag) -> Kern {
+        using T = decltype(tag);
+        switch (var) {
+        case 1: return row_kernel<T, true, kXfNone>;
+        case 2: return row_kernel<T, false, kXfMask>;
+        case 4: return row_kernel<T, false, kXfCap>;
+        case 5: return row_kernel<T, true, kXfCap>;
+        default: return row_kernel<T, false, kXfNone>;
+        }
+    };
     Kern kern;
-    if (a->dtype == VWS_DTYPE_F32)
-        kern = var == 1 ? row_kernel<float, true, false> : var == 2 ? row_kernel<float, false, true> : row_kernel<float, false, false>;
-    else if (a->dtype == VWS_DTYPE_BF16)
-        kern = var == 1 ? row_kernel<uint16_t, true, false> : var == 2 ? row_kernel<uint16_t, false, true> : row_kernel<uint16_t, false, false>;
-    else
-        kern = var == 1 ? row_kernel<_Float16, true, false> : var == 2 ? row_kernel<_Float16, false, true> : row_kernel<_Float16, false, false>;
+    if (a->dtype == VWS_DTYPE_F32) kern = pick(float{});
+    else if (a->dtype == VWS_DTYPE_BF16) kern = pick(uint16_t{});
+    else kern = pick(_Float16{});
     launch(K, kern, dim3(grid), dim3(kGenThreads), s, k.logits, k.lstride, k.V, cf, k);
     if ((st = check_launch("vws_sample"))) return st;
     return ok();

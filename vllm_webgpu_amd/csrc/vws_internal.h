@@ -26,6 +26,14 @@ constexpr int kBuckets = 4096;                    // d-buckets of width 1/128 ov
 constexpr int kGatherCap = 2048;                  // boundary-bucket entries resolved in LDS
 constexpr int kLpCapW = 192;                      // per-wave top-L candidate slots
 
+// The sampling kernel's instantiations by what the top-p path does to each logit as it loads it
+// (the single pass caps candidates only and masks as it streams): nothing, the launch's allowed
+// mask (masked elements become -inf), or the launch's soft cap (cap * tanh(x / cap), with its
+// f16 store when asked); the same in every pass over a row.
+constexpr int kXfNone = 0;
+constexpr int kXfMask = 1;
+constexpr int kXfCap = 2;
+
 // Row states written by the fast path for the general path.
 constexpr uint32_t kRowNeedsGeneral = 1u;
 

@@ -192,7 +192,7 @@ __device__ __noinline__ int topp_hist_entry(int r, uint64_t kernarg, uint32_t ta
 // The pass sm.pd over row r's body vectors [v0, v1) (and the edges): without, and with the
 // penalties from the token-state table (separate functions, so that the plain pass keeps its
 // registers).
-template <typename T, bool PEN, bool MSK>
+template <typename T, bool PEN, int XF>
 __device__ __forceinline__ void topp_range_body(int r, uint64_t kernarg, int v0, int v1, int edges) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
@@ -212,48 +212,29 @@ __device__ __forceinline__ void topp_range_body(int r, uint64_t kernarg, int v0,
     d.kkeep = tp_u(sm.pd.kkeep);
     d.kmem = tp_u(sm.pd.kmem);
     TpPassAcc acc;
-    tp_pass_range<T, PEN, MSK>(a, sm, r, d, v0, v1, edges != 0, acc);
+    tp_pass_range<T, PEN, XF>(a, sm, r, d, v0, v1, edges != 0, acc);
     tp_pass_reduce(sm, d.kind, acc);
 #else
     (void)r; (void)kernarg; (void)v0; (void)v1; (void)edges;
 #endif
 }
 
-template <typename T>
+// A range of a pass over row r (PEN: with the row's penalties; XF: what each logit goes through
+// as it loads, the launch's mask or soft cap); one out-of-line function per combination, so
+// that plain launches keep their registers.
+template <typename T, bool PEN, int XF>
 __device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
-    topp_range_body<T, false, false>(r, kernarg, v0, v1, edges);
+    topp_range_body<T, PEN, XF>(r, kernarg, v0, v1, edges);
 }
 
-template <typename T>
-__device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
-    topp_range_body<T, true, false>(r, kernarg, v0, v1, edges);
-}
-
-// the same for launches with an allowed mask (elements outside it are -inf)
-template <typename T>
-__device__ __noinline__ void topp_range_mask_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
-    topp_range_body<T, false, true>(r, kernarg, v0, v1, edges);
-}
-
-template <typename T>
-__device__ __noinline__ void topp_range_mask_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges) {
-    topp_range_body<T, true, true>(r, kernarg, v0, v1, edges);
-}
-
-// A range of a pass over row r: with the row's penalties (pen) and the launch's mask (MSK).
-template <typename T, bool MSK>
+template <typename T, int XF>
 __device__ __forceinline__ void topp_range_any(bool pen, int r, uint64_t kernarg, int v0, int v1,
                                                int edges) {
-    if (MSK) {
-        if (pen) topp_range_mask_hist_entry<T>(r, kernarg, v0, v1, edges);
-        else topp_range_mask_entry<T>(r, kernarg, v0, v1, edges);
-    } else {
-        if (pen) topp_range_hist_entry<T>(r, kernarg, v0, v1, edges);
-        else topp_range_entry<T>(r, kernarg, v0, v1, edges);
-    }
+    if (pen) topp_range_entry<T, true, XF>(r, kernarg, v0, v1, edges);
+    else topp_range_entry<T, false, XF>(r, kernarg, v0, v1, edges);
 }
 
-template <typename T, bool PEN, bool MSK>
+template <typename T, bool PEN, int XF>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -318,7 +299,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     const uint32_t slot = tp_u(sm.cp[4]);
     const bool pen = PEN && tp_pass_pen(a, r, kind);
     if (slot == kCoopNone) {
-        topp_range_any<T, MSK>(pen, r, kernarg, 0, nbody, 1);
+        topp_range_any<T, XF>(pen, r, kernarg, 0, nbody, 1);
         return;
     }
     CoopSlot& S = st->slot[slot];
@@ -369,7 +350,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
     for (int k = 0; c != kCoopNone; ++k) {
         const int v0 = (int)c * cvecs;
         const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
-        topp_range_any<T, MSK>(pen, r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        topp_range_any<T, XF>(pen, r, kernarg, v0, v1, c == 0u ? 1 : 0);
         __syncthreads();
         if (tid == 0) {
             ++own;
@@ -490,7 +471,7 @@ __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, 
 // launch is left to start, so no row waits for this workgroup's CU); otherwise return once no
 // chunk is open.  PEN: the launch has penalties from a token-state table with its bitmap (some
 // chunks are of penalised passes; without, the function calls only the plain range function).
-template <typename T, bool PEN, bool MSK>
+template <typename T, bool PEN, int XF>
 __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int NT = kGenThreads;
@@ -588,7 +569,7 @@ __device__ __noinline__ void coop_help_entry(uint64_t kernarg, int spin) {
         const int nbody = __builtin_amdgcn_readfirstlane(sl.nbody);
         const int v0 = (int)c * cvecs;
         const int v1 = nbody < v0 + cvecs ? nbody : v0 + cvecs;
-        topp_range_any<T, MSK>(PEN && tp_pass_pen(a, r, kind), r, kernarg, v0, v1, c == 0u ? 1 : 0);
+        topp_range_any<T, XF>(PEN && tp_pass_pen(a, r, kind), r, kernarg, v0, v1, c == 0u ? 1 : 0);
         __syncthreads();
         // the next chunk, claimed while this one's totals go out (before this one counts as
         // done, so the pass cannot have been replaced meanwhile)
@@ -1221,8 +1202,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         *topp_row = topp_eligible(a, prm) && !(MASK && sl.a != 0);
         return false;
     }
-    // raw logprobs are of the capped logits, which the stream does not compute
-    if (LP && a.softcap > 0.0f) return false;
+    // raw logprobs are of the capped logits, which this stream does not compute (the top-p
+    // path's does: greedy rows with logprobs go there)
+    if (LP && a.softcap > 0.0f) {
+        *topp_row = topp_eligible(a, prm);
+        return false;
+    }
     // MASK: the mask words line up with the vectors only when the row starts 16-byte aligned
     if (MASK && sl.a != 0) return false;
     // the threshold keeps at least kc candidates: the top-L raw logits must be among them
@@ -1906,21 +1891,21 @@ __device__ __noinline__ void row_general(int r, uint64_t kernarg) {
 }
 
 // One row: the single pass, the single-pass top-p path or the multi-pass path.  Returns whether
-// The single-pass top-p path of a row in a launch with an allowed mask (stream and finish);
-// returns 0 or the reason the row takes the multi-pass path.
-template <typename T>
-__device__ __noinline__ int topp_row_mask_entry(int r, uint64_t kernarg) {
+// The single-pass top-p path of a row in a launch with an allowed mask or the soft cap (stream
+// and finish, XF); returns 0 or the reason the row takes the multi-pass path.
+template <typename T, int XF>
+__device__ __noinline__ int topp_row_xf_entry(int r, uint64_t kernarg) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
     r = __builtin_amdgcn_readfirstlane(r);
     const RowP prm = row_params(a, r);
     if (prm.has_hist) {
         const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
-        topp_stream<T, true>(a, g_row_sh.t, r, prm, fill);
+        topp_stream<T, XF>(a, g_row_sh.t, r, prm, fill);
     } else {
-        topp_stream<T, true>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+        topp_stream<T, XF>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
     }
-    return topp_finish<T, true>(a, g_row_sh.t, r, prm, kernarg);
+    return topp_finish<T, XF>(a, g_row_sh.t, r, prm, kernarg);
 #else
     (void)r;
     (void)kernarg;
@@ -1930,13 +1915,13 @@ __device__ __noinline__ int topp_row_mask_entry(int r, uint64_t kernarg) {
 
 // the row took one of the longer paths (top-p or multi-pass), whose workgroup then looks for
 // chunks of other rows' passes.
-template <typename T, bool LP, bool MASK>
+template <typename T, bool LP, int XF>
 __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logits, int64_t lstride,
                                         int V, uint64_t kernarg) {
     bool topp = false;
     if (a.nofast) {
         topp = topp_eligible(a, row_params(a, r));
-    } else if (row_fast<T, LP, MASK>(a, g_row_sh.f, r, logits, lstride, V, &topp)) {
+    } else if (row_fast<T, LP, XF == kXfMask>(a, g_row_sh.f, r, logits, lstride, V, &topp)) {
         if (!LP || row_logprobs_entry(r, kernarg)) return false;
     }
     int why = 0;
@@ -1946,20 +1931,20 @@ __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logit
         __syncthreads();
         // a top-p row in progress may open a cooperative pass
         if (threadIdx.x == 0 && a.coop) ag_add64(&a.coop->wgs, kCoopPending);
-        if (MASK) {
-            // launches with an allowed mask: out of line, so that the kernel's single pass keeps
-            // the registers it has without the masked top-p path
-            why = topp_row_mask_entry<T>(r, kernarg);
+        if (XF != kXfNone) {
+            // launches with an allowed mask or the soft cap: out of line, so that the kernel's
+            // single pass keeps the registers it has without these top-p paths
+            why = topp_row_xf_entry<T, XF>(r, kernarg);
         } else {
             const RowP prm = row_params(a, r);
             if (prm.has_hist) {
                 // history rows: their bitmap into LDS first (a copy of the stream of its own)
                 const float fill = tp_uf(topp_hist_begin(a, g_row_sh.t, prm));
-                topp_stream<T, false>(a, g_row_sh.t, r, prm, fill);
+                topp_stream<T, kXfNone>(a, g_row_sh.t, r, prm, fill);
             } else {
-                topp_stream<T, false>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
+                topp_stream<T, kXfNone>(a, g_row_sh.t, r, prm, kTpFill * (float)kTpCapW);
             }
-            why = topp_finish<T, false>(a, g_row_sh.t, r, prm, kernarg);
+            why = topp_finish<T, kXfNone>(a, g_row_sh.t, r, prm, kernarg);
         }
         // done with it: no longer pending, and no longer holding slots (thread 0 set the mark)
         if (threadIdx.x == 0 && a.coop)
@@ -1979,17 +1964,22 @@ __device__ __forceinline__ bool row_one(const KArgs& a, int r, const void* logit
 // workgroup counts itself finished; once every workgroup has started it polls while top-p rows
 // are in progress, before that it only runs chunks already open (so that it keeps no row from
 // starting).  Out of line: nothing but the kernarg address stays live across the row.
-template <typename T, bool MASK>
+template <typename T, int XF>
 __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const KArgs a = kargs_at(kernarg);
     long_row = __builtin_amdgcn_readfirstlane(long_row);
     if (!a.coop) return;
+    // chunks of other rows' passes, run as the launch loads its logits (mask, soft cap or as
+    // they are) and with penalties from the token-state table where the launch has them
+    auto help = [&](int spin) __attribute__((always_inline)) {
+        if (a.tbits) coop_help_entry<T, true, XF>(kernarg, spin);
+        else coop_help_entry<T, false, XF>(kernarg, spin);
+    };
     if (!a.coop_count) {
         if (long_row) {
             __syncthreads();
-            if (a.tbits) coop_help_entry<T, true, MASK>(kernarg, 1);
-            else coop_help_entry<T, false, MASK>(kernarg, 1);
+            help(1);
         }
         return;
     }
@@ -2006,8 +1996,7 @@ __device__ __noinline__ void row_kernel_rest(uint64_t kernarg, int long_row) {
     const uint32_t how = tp_u(sm.cp[6]);
     if (how) {
         __syncthreads();
-        if (a.tbits) coop_help_entry<T, true, MASK>(kernarg, how == 2u ? 1 : 0);
-        else coop_help_entry<T, false, MASK>(kernarg, how == 2u ? 1 : 0);
+        help(how == 2u ? 1 : 0);
     }
 #else
     (void)kernarg;
@@ -2081,7 +2070,7 @@ __device__ __noinline__ int row_order_entry(uint64_t kernarg, int b) {
 // region is present; bit 1, the workgroups are counted (KArgs::coop_count); bit 2, the rows are
 // served longest first (row_order_entry: every workgroup scans the batch's parameters, so the
 // launcher asks for it only up to kRowOrderMaxBatch rows).
-template <typename T, bool LP, bool MASK>
+template <typename T, bool LP, int XF>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, int64_t lstride, int V,
                                                           int coop, KArgs a) {
 #ifdef VWS_TRACE
@@ -2096,14 +2085,14 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const void* logits, in
         if (threadIdx.x == 0) ag_add64(&a.coop->wgs, kCoopStarted);
         if (coop & 4) r = __builtin_amdgcn_readfirstlane(row_order_entry(kernarg, r));
     }
-    const bool long_row = row_one<T, LP, MASK>(a, r, logits, lstride, V, kernarg);
+    const bool long_row = row_one<T, LP, XF>(a, r, logits, lstride, V, kernarg);
     VWS_TRACE_MARK(a, VWS_TRACE_ROW);
 #ifdef VWS_TRACE
     trace_put(a, VWS_TRACE_ENTRY, tr_entry);
     trace_put(a, VWS_TRACE_XCC, trace_xcc());
     trace_put(a, VWS_TRACE_ROWID, (uint64_t)r);
 #endif
-    if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T, MASK>(kernarg, long_row ? 1 : 0);
+    if ((coop & 2) || ((coop & 1) && long_row)) row_kernel_rest<T, XF>(kernarg, long_row ? 1 : 0);
     VWS_TRACE_MARK(a, VWS_TRACE_EXIT);
 }
 

@@ -66,6 +66,7 @@ constexpr int VWS_FALLBACK_GATHER = 7;      // the boundary bucket holds too man
 constexpr int VWS_FALLBACK_TOPL = 8;        // the top-L logprobs reach below the candidates
 constexpr int VWS_FALLBACK_COOP = 9;        // a cooperative pass was not completed in time
 
+
 // The finish's further passes over the row (the rarer cases; tp_pass_range).
 constexpr int kTpPassExact = 0;     // exact masses below the candidates
 constexpr int kTpPassWideRace = 1;  // the race and the boundary members below the candidates
@@ -170,10 +171,11 @@ __device__ __noinline__ TpDrop topp_compact_entry(int w, int cnt, float aw, floa
 
 // Whether the single-pass top-p path may serve the row.
 __device__ __forceinline__ bool topp_eligible(const KArgs& a, const RowP& p) {
-    if (p.need_hash || a.softcap > 0.0f) return false;
+    if (p.need_hash) return false;
     // an allowed mask: the stream masks as it loads (rows starting 16-byte aligned, checked by
-    // the caller); with raw logprobs such launches take the multi-pass path
-    if (a.allowed && a.L >= 0) return false;
+    // the caller); with raw logprobs such launches take the multi-pass path.  The soft cap: the
+    // stream caps as it loads (not together with a mask)
+    if (a.allowed && (a.L >= 0 || a.softcap > 0.0f)) return false;
     // penalties: from the token-state table with its bitmap (need_hash covers the lists)
     if (p.has_hist && !(p.tab && a.tbits && a.V <= kTpHistMaxV)) return false;
     if (p.greedy) return a.L >= 0;
@@ -346,9 +348,10 @@ __device__ __forceinline__ TpDrop topp_compact(TopPSmem& sm, int w, int cnt, flo
 // The stream over row r.  Publishes each wave's results into sm; topp_finish completes the row.
 // fill: the entries per wave the seed threshold aims at (less than kTpFill of the slots when
 // history tokens will need some).
-template <typename T, bool MASK>
+template <typename T, int XF>
 __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
                                             float fill) {
+    constexpr bool MASK = XF == kXfMask, CAP = XF == kXfCap;
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int U = 32 / VEC;
@@ -384,7 +387,15 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
             mw = __builtin_amdgcn_raw_buffer_load_b32(mrs, 4u * wi, 0u, 0);
         }
     };
-    auto mask_iter = [&](float (&buf)[U][VEC], uint32_t mw) __attribute__((always_inline)) {
+    // CAP: every element of the iteration capped
+    auto xf_iter = [&](float (&buf)[U][VEC], uint32_t mw) __attribute__((always_inline)) {
+        if (CAP) {
+            const bool f16 = a.softcap_f16 != 0;
+#pragma unroll
+            for (int q = 0; q < U; ++q)
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) buf[q][j] = softcap_out(buf[q][j], a.inv_softcap, a.softcap, f16);
+        }
         if (MASK) {
             const int ln = lane_now();
 #pragma unroll
@@ -403,7 +414,7 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
     load_mask(MA, 0);
     load_iter(Bq, 1);
     load_mask(MB, 1);
-    mask_iter(A, MA);
+    xf_iter(A, MA);
     // seed: a threshold from the lane maxima over the first iteration.  A lane's maximum over its
     // E elements reaches tau with probability 1 - (1 - phi)^E when a fraction phi of the
     // elements does, so a wave's m-th largest lane maximum, m = 64 (1 - (1 - phi)^E), admits
@@ -509,13 +520,13 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
         }
     };
     for (int it = 0; it < nit && !cb.ovf; it += 2) {
-        if (it > 0) mask_iter(A, MA);  // (the first iteration was masked before the seed)
+        if (it > 0) xf_iter(A, MA);  // (the first iteration was handled before the seed)
         examine(A, it);
         load_iter(A, it + 2);
         load_mask(MA, it + 2);
         shrink();
         if (it + 1 < nit && !cb.ovf) {
-            mask_iter(Bq, MB);
+            xf_iter(Bq, MB);
             examine(Bq, it + 1);
         }
         load_iter(Bq, it + 3);
@@ -536,6 +547,8 @@ __device__ __forceinline__ void topp_stream(const KArgs& a, TopPSmem& sm, int r,
                 v[j] = __builtin_nanf("");  // NaN: neither stored nor summed
             } else if (MASK && !((mrow[(i0 + j) >> 5] >> ((i0 + j) & 31)) & 1u)) {
                 v[j] = -__builtin_inff();
+            } else if (CAP) {
+                v[j] = softcap_out(v[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
             }
         }
         consume(v, i0, true);
@@ -623,12 +636,13 @@ struct TpPen {
 // (a range is a chunk of a few steps: the second load overlaps the first step's work).  f(v, u, i0, ok) gets the VEC elements of one vector from element i0 on (ok: the
 // vector lies in the range; head and tail are NaN-padded) and, with WITH_U, their uniforms
 // (dword-aligned 16-byte loads).  PEN: the elements are penalised first from their token-state
-// words (streamed like the uniforms), so that f sees processed values.  MSK: elements outside
-// the row's allowed mask become -inf first (one mask word per vector; the row starts 16-byte
-// aligned, so a vector's bits lie in one word).
-template <typename T, bool WITH_U, bool PEN, bool MSK, typename F>
+// words (streamed like the uniforms), so that f sees processed values.  XF = kXfMask: elements
+// outside the row's allowed mask become -inf first (one mask word per vector; the row starts
+// 16-byte aligned, so a vector's bits lie in one word); kXfCap: every element is capped first.
+template <typename T, bool WITH_U, bool PEN, int XF, typename F>
 __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int v1, bool edges,
                                              const TpPen& pen, F&& f) {
+    constexpr bool MSK = XF == kXfMask, CAP = XF == kXfCap;
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int UW = WITH_U ? VEC / 4 : 0;  // uniform loads per vector
@@ -697,6 +711,11 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) v[j] = ((bits >> j) & 1u) ? v[j] : -__builtin_inff();
             }
+            if (CAP) {
+#pragma unroll
+                for (int j = 0; j < VEC; ++j)
+                    v[j] = softcap_out(v[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
+            }
             if (PEN) {
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) v[j] = penal(v[j], (uint32_t)ww[q][j / 4][j % 4]);
@@ -731,6 +750,7 @@ __device__ __forceinline__ void tp_row_range(const KArgs& a, int r, int v0, int 
             u[j] = (WITH_U && i0 + j < end) ? urow[i0 + j] : 0.0f;
             if (MSK && i0 + j < end && !((arow[(i0 + j) >> 5] >> ((i0 + j) & 31)) & 1u))
                 v[j] = -__builtin_inff();
+            if (CAP && i0 + j < end) v[j] = softcap_out(v[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
             if (PEN && i0 + j < end) v[j] = penal(v[j], pen.wrow[i0 + j]);
         }
         f(v, u, i0, tid <= 1);
@@ -806,7 +826,7 @@ __device__ __forceinline__ void tp_wide_keys(const TpPassDesc& d, uint32_t* out)
 //     candidate) into acc.n.
 // PEN (rows with penalties from the token-state table, exact and wide passes only): the pass
 // sees processed values (the rank pass ranks raw ones).
-template <typename T, bool PEN, bool MSK>
+template <typename T, bool PEN, int XF>
 __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int r, const TpPassDesc& d,
                                               int v0, int v1, bool edges, TpPassAcc& acc) {
     constexpr int VEC = Elem<T>::kVec;
@@ -821,7 +841,7 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
         pen.wrow = a.tstate + (size_t)(a.trows ? a.trows[r] : r) * (size_t)a.tstride;
     }
     auto range = [&](auto with_u, auto&& f) __attribute__((always_inline)) {
-        tp_row_range<T, decltype(with_u)::value, PEN, MSK>(a, r, v0, v1, edges, pen, f);
+        tp_row_range<T, decltype(with_u)::value, PEN, XF>(a, r, v0, v1, edges, pen, f);
     };
     if (d.kind == kTpPassExact) {
         range(BoolC<false>{}, [&](const float* v, const float*, int, bool ok)
@@ -886,7 +906,7 @@ __device__ __forceinline__ void tp_pass_range(const KArgs& a, TopPSmem& sm, int 
                                       __attribute__((always_inline)) { body(v, u, i0, ok, true); });
         }
     } else {
-        tp_row_range<T, false, false, MSK>(a, r, v0, v1, edges, pen, [&](const float* v, const float*, int, bool ok)
+        tp_row_range<T, false, false, XF>(a, r, v0, v1, edges, pen, [&](const float* v, const float*, int, bool ok)
                                                                    __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) acc.n += (ok && key_of(v[j]) >= tauk) ? 1ull : 0ull;
@@ -987,21 +1007,18 @@ __device__ __forceinline__ uint32_t coop_chunk_of(uint64_t x) {
 //     results are in sm.bc64[10..13] after a barrier; sets sm.coop_fail when a cooperative
 //     pass was not completed (the row then takes the multi-pass path).  PEN: a row with
 //     penalties from the token-state table (its range functions are separate, and so are the
-//     functions that call them, so that the others keep their registers);
-//   topp_range_entry: the pass sm.pd over the body vectors [v0, v1) of row r (and the edges),
-//     its workgroup totals into sm.bc64[10..13] as tp_pass_reduce leaves them.
-template <typename T, bool PEN, bool MSK>
+//     functions that call them, so that the others keep their registers); XF: the launch's
+//     transform of each loaded logit (kXfNone, kXfMask, kXfCap);
+//   topp_range_entry<T, PEN, XF>: the pass sm.pd over the body vectors [v0, v1) of row r (and
+//     the edges), its workgroup totals into sm.bc64[10..13] as tp_pass_reduce leaves them.
+template <typename T, bool PEN, int XF>
 __device__ __noinline__ void topp_pass_entry(int kind, int r, uint64_t kernarg, float Tt, float m,
                                              float lp_min, uint32_t key, int bstar);
-template <typename T>
-__device__ __noinline__ void topp_range_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
-template <typename T>
-__device__ __noinline__ void topp_range_hist_entry(int r, uint64_t kernarg, int v0, int v1, int edges);
 template <typename T>
 __device__ __noinline__ int topp_hist_entry(int r, uint64_t kernarg, uint32_t tauk, float xmaxr);
 
 // Whether a pass of `kind` over row r reads the rows' token-state words (penalties from the
-// table, exact and wide passes): such passes run in topp_range_hist_entry.
+// table, exact and wide passes): such passes run in topp_range_entry<T, true, XF>.
 __device__ __forceinline__ bool tp_pass_pen(const KArgs& a, int r, int kind) {
     if (!a.tstate || kind == kTpPassRank) return false;
     const float rp = a.rep ? a.rep[r] : 1.0f;
@@ -1146,6 +1163,7 @@ __device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, i
             const uint32_t t = in ? sm.hl[j] : 0u;
             float x = in ? Elem<T>::load1(lrow + t) : 0.0f;
             if (in && arow && !((arow[t >> 5] >> (t & 31)) & 1u)) x = -__builtin_inff();  // masked
+            if (in && a.softcap > 0.0f) x = softcap_out(x, a.inv_softcap, a.softcap, a.softcap_f16 != 0);
             const uint32_t wd = in ? trw[t] : 0u;
             float y = 0.0f;
             if (in) {
@@ -1189,9 +1207,10 @@ __device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, i
 // Completes a row after topp_stream.  Returns 0, or (nothing written) the reason the row must
 // take the multi-pass path (VWS_FALLBACK_*).  Every return decision is uniform over the
 // workgroup: values that decide are read from LDS after a barrier, or are scalars.
-template <typename T, bool MASK>
+template <typename T, int XF>
 __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, const RowP& prm,
                                            uint64_t kernarg) {
+    constexpr bool MASK = XF == kXfMask;
     constexpr int NT = kGenThreads;
     constexpr int VEC = Elem<T>::kVec;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1241,8 +1260,8 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     // a cooperative pass that was not completed marks sm.coop_fail; the row is handed over right
     // after it, before anything is written
     auto pass = [&](int kind, uint32_t key, int bs) __attribute__((always_inline)) {
-        if (hist) topp_pass_entry<T, true, MASK>(kind, r, kernarg, Tt, m, lp_min, key, bs);
-        else topp_pass_entry<T, false, MASK>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        if (hist) topp_pass_entry<T, true, XF>(kind, r, kernarg, Tt, m, lp_min, key, bs);
+        else topp_pass_entry<T, false, XF>(kind, r, kernarg, Tt, m, lp_min, key, bs);
         __syncthreads();
     };
     for (int i = tid; i < kTpBuckets; i += NT) {
@@ -1769,7 +1788,9 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     uint32_t rank = 0u;
     if (L >= 0) {
         const T* row = reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride;
-        xs = tp_uf(Elem<T>::load1(row + token));
+        xs = Elem<T>::load1(row + token);
+        if (a.softcap > 0.0f) xs = softcap_out(xs, a.inv_softcap, a.softcap, a.softcap_f16 != 0);
+        xs = tp_uf(xs);
         const uint32_t ks = key_of(xs);
         // a sampled token below the candidates (wide rows) is ranked by a pass over the row
         const bool rank_pass = ks < tauk;
