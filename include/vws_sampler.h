@@ -271,6 +271,13 @@ int vws_apply_penalties(float* logits, int32_t batch, int32_t vocab, int64_t row
  * previous bound, or -1 (with vws_last_error) for polls < 0. */
 int32_t vws_set_coop_wait_polls(int32_t polls);
 
+/* Test hook (no counterpart in the reference): 0 keeps every row of later vws_sample launches
+ * off the single pass (greedy and top-k rows take the multi-pass path, top-p rows still the
+ * single-pass top-p path), 1 (the default) lets rows take it again; process-wide, read by each
+ * launch.  Both paths give the same results, which tests compare.  Returns the previous
+ * setting, or -1 (with vws_last_error) for any other value. */
+int32_t vws_set_single_pass(int32_t enabled);
+
 /* Per-kernel timing.  vws_profile_begin(n) makes the next n kernel launches of this library
  * (on any stream) carry a hipEvent pair that the runtime stamps when the kernel itself begins
  * and ends (hipExtLaunchKernel; no marker packets between launches, so the sum is the kernels'

@@ -196,6 +196,17 @@ def test_coop_wait_polls_hook(L):
         L.vws_set_coop_wait_polls(prev)
 
 
+def test_single_pass_hook(L):
+    prev = L.vws_set_single_pass(0)
+    try:
+        assert prev == 1
+        assert L.vws_set_single_pass(2) == -1
+        assert "enabled" in _lib.last_error()
+        assert L.vws_set_single_pass(1) == 0
+    finally:
+        L.vws_set_single_pass(prev)
+
+
 def test_trace_set_only_in_the_trace_build(L):
     """The product library refuses vws_trace_set; the trace build (same ABI, same exports)
     takes a buffer or turns recording off, and rejects a count without a buffer."""

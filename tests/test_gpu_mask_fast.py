@@ -1,6 +1,8 @@
-"""GPU parity of allowed-token masks on the single pass: a launch with an allowed mask (and no
-logprobs) masks every element as it streams -- one mask word per lane and iteration, shared
-across the wave -- so its top-k and greedy rows no longer take the multi-pass path.
+"""GPU parity of allowed-token masks on the single passes: a launch with an allowed mask and no
+logprobs masks every element as it streams -- one mask word per lane and iteration, shared
+across the wave -- so its top-k, greedy and top-p rows no longer take the multi-pass path; a
+launch with an allowed mask and raw logprobs streams raw values and masks the candidates of its
+top-k and greedy rows.
 
 Tokens, flags and survivor counts are compared bit for bit with the oracle."""
 import numpy as np
@@ -24,7 +26,7 @@ def _bits(allowed):
     return (words.reshape(B, -1, 32) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
 
 
-def _run(w, allowed, device, logits_t=None, **kw):
+def _run(w, allowed, device, logits_t=None, num_logprobs=None, softcap=None, **kw):
     import torch
 
     from vllm_webgpu_amd import ops
@@ -33,7 +35,7 @@ def _run(w, allowed, device, logits_t=None, **kw):
     prm = O.make_params(w.shape[0], w.temperature, w.top_k, w.top_p, w.min_p, w.repetition,
                         w.presence, w.frequency)
     ref = O.sample(w.logits_f32(), prm, w.uniforms, output_ids=w.output_ids, allowed=bits,
-                   **{k: v for k, v in kw.items()})
+                   num_logprobs=num_logprobs, softcap=softcap, **{k: v for k, v in kw.items()})
     if logits_t is None:
         if w.dtype == "bf16":
             logits_t = torch.from_numpy(w.logits.view(np.int16)).to(device).view(torch.bfloat16)
@@ -49,10 +51,14 @@ def _run(w, allowed, device, logits_t=None, **kw):
         frequency_penalty=torch.from_numpy(w.frequency),
         output_ids=None if w.output_ids is None else torch.from_numpy(w.output_ids),
         uniforms=torch.from_numpy(w.uniforms).to(device),
-        allowed_mask=torch.from_numpy(bits.view(np.int32)).to(device), **tk)
+        allowed_mask=torch.from_numpy(bits.view(np.int32)).to(device), num_logprobs=num_logprobs,
+        logit_softcap=softcap, **tk)
     torch.cuda.synchronize()
     g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
              n_kept=res.num_kept.cpu().numpy())
+    if num_logprobs is not None:
+        g.update(lp_ids=res.logprob_ids.cpu().numpy(), lp_vals=res.logprob_vals.cpu().numpy(),
+                 ranks=res.logprob_ranks.cpu().numpy())
     return g, ref
 
 
@@ -213,3 +219,37 @@ def test_topp_masks_flat_rows_take_the_passes(cuda):
     assert_same(g, ref, w.name)
     assert (g["flags"] & STREAM_TOPP).all()
     assert (g["flags"] & (0x400 | 0x800)).any(), "no masked row took a further pass"
+
+
+@pytest.mark.parametrize("case", ["c3_L20", "c4_bf16_L5"])
+def test_logprob_launches_with_masks(cuda, case):
+    """Raw logprobs and an allowed mask in one launch: the top-k and greedy rows mask their
+    candidates on the single pass (the logprobs are of the raw logits); rows whose masked
+    candidates reach the top k, and top-p rows, take the multi-pass path.  C3 (penalties,
+    k 50, 20 logprobs) and a quarter of C4 (bf16, mixed rows, 5 logprobs), with masks of every
+    density and half the rows left open; then the same launch with the single pass switched
+    off (vws_set_single_pass), every top-k row on the multi-pass path, with the same results."""
+    from vllm_webgpu_amd import _lib
+
+    rng = np.random.default_rng(171)
+    if case == "c3_L20":
+        w, L = W.config(3), 20
+    else:
+        w, L = W.config(4, scale=0.25), 5
+    B, V = w.shape
+    allowed = _allowed_sets(rng, B, V)
+    allowed[rng.random(B) < 0.5] = True                      # half the rows left open
+    g, ref = _run(w, allowed, cuda, num_logprobs=L)
+    assert_same(g, ref, case)
+    open_rows = allowed.all(axis=1) & (w.top_k > 0) & (w.top_k <= 256)
+    assert open_rows.sum() > 10
+    gen = (g["flags"][open_rows] & GENERAL) != 0
+    assert not gen.any(), f"{int(gen.sum())} open top-k rows took the multi-pass path"
+    lib = _lib.lib()
+    prev = lib.vws_set_single_pass(0)
+    try:
+        g2, _ = _run(w, allowed, cuda, num_logprobs=L)
+    finally:
+        lib.vws_set_single_pass(prev)
+    assert_same(g2, ref, case + ", single pass off")
+    assert ((g2["flags"][w.top_k > 0] & GENERAL) != 0).all()

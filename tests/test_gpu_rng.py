@@ -82,7 +82,8 @@ def test_generated_large_k_and_wide_rows(cuda):
 
 
 def test_generated_multi_pass(cuda):
-    """An allowed mask sends every row to the multi-pass kernel (with logprobs)."""
+    """A launch with an allowed mask and logprobs: its top-p rows and k > 256 rows take the
+    multi-pass kernel (its k = 20 rows the single pass, which masks their candidates)."""
     rng = np.random.default_rng(42)
     B, V = 8, 20000
     x = rng.normal(0, 3, (B, V)).astype(np.float32)

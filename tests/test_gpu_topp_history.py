@@ -31,7 +31,7 @@ def bits_from_table(st):
     return w.view(np.int32)
 
 
-def _run(w, device, prompt=None, output=None, plens=None, olens=None, bits=True):
+def _run(w, device, prompt=None, output=None, plens=None, olens=None, bits=True, softcap=None):
     import torch
 
     from vllm_webgpu_amd import ops
@@ -40,7 +40,8 @@ def _run(w, device, prompt=None, output=None, plens=None, olens=None, bits=True)
     prm = O.make_params(B, w.temperature, w.top_k, w.top_p, w.min_p, w.repetition, w.presence,
                         w.frequency)
     ref = O.sample(w.logits_f32(), prm, w.uniforms, prompt_ids=prompt, output_ids=output,
-                   prompt_lens=plens, output_lens=olens, num_logprobs=w.num_logprobs)
+                   prompt_lens=plens, output_lens=olens, num_logprobs=w.num_logprobs,
+                   softcap=softcap)
     st = table_from_lists(B, V, prompt, output, plens, olens)
     if w.dtype == "bf16":
         x = torch.from_numpy(w.logits.view(np.int16)).to(device).view(torch.bfloat16)
@@ -55,7 +56,8 @@ def _run(w, device, prompt=None, output=None, plens=None, olens=None, bits=True)
         frequency_penalty=torch.from_numpy(w.frequency),
         uniforms=torch.from_numpy(w.uniforms).to(device), num_logprobs=w.num_logprobs,
         token_state=torch.from_numpy(st.view(np.int32)).to(device),
-        token_state_bits=torch.from_numpy(bits_from_table(st)).to(device) if bits else None)
+        token_state_bits=torch.from_numpy(bits_from_table(st)).to(device) if bits else None,
+        logit_softcap=softcap)
     torch.cuda.synchronize()
     g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
              n_kept=res.num_kept.cpu().numpy())
@@ -136,6 +138,22 @@ def test_flat_rows_take_the_passes_with_penalties(cuda):
     assert_same(g, ref, w.name)
     assert not (g["flags"] & GENERAL).any()
     assert (g["flags"] & (RECOUNT | WIDE)).any(), "no row took a further pass"
+
+
+def test_capped_rows_with_penalties(cuda):
+    """Under the soft cap (30): the stream caps as it loads, the history tokens' gathered logits
+    are capped before their words apply, and flat rows take the capped passes; T 0.9, 3 raw
+    logprobs, a few saturated rows."""
+    rng = np.random.default_rng(111)
+    B, V = 40, 90000
+    x = rng.normal(0, 12, (B, V)).astype(np.float32)
+    x[1::5] = rng.normal(0, 0.5, (8, V))
+    x[::7, :30] = 500.0
+    prompt, out = _hist(rng, x, 300, 200, top_share=60)
+    w = _wl("cap + penalties", x, 0.9, k=0, p=0.95, rep=1.2, pres=0.4, freq=0.2, seed=112, L=3)
+    g, ref = _run(w, cuda, prompt=prompt, output=out, softcap=30.0)
+    assert_same(g, ref, w.name)
+    assert ((g["flags"] & STREAM_TOPP) != 0).mean() > 0.9, f"rows left the top-p path: {g['flags']}"
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])

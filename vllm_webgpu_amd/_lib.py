@@ -57,8 +57,8 @@ EXPORTED = (
     "vws_validate_sample_args", "vws_sample", "vws_sample_noalloc", "vws_argmax",
     "vws_topk_workspace_size",
     "vws_topk", "vws_softmax", "vws_apply_penalties", "vws_math_selftest",
-    "vws_profile_begin", "vws_profile_end", "vws_set_coop_wait_polls", "vws_token_state_update",
-    "vws_trace_set",
+    "vws_profile_begin", "vws_profile_end", "vws_set_coop_wait_polls", "vws_set_single_pass",
+    "vws_token_state_update", "vws_trace_set",
 )
 
 KERNEL_KINDS = ("sample", "topk", "argmax", "softmax", "penalties", "other")
@@ -140,6 +140,8 @@ def _declare(L):
     L.vws_profile_end.argtypes = [_P, _P]
     L.vws_set_coop_wait_polls.restype = _I32
     L.vws_set_coop_wait_polls.argtypes = [_I32]
+    L.vws_set_single_pass.restype = _I32
+    L.vws_set_single_pass.argtypes = [_I32]
     L.vws_trace_set.restype = ctypes.c_int
     L.vws_trace_set.argtypes = [_P, _I32]
     L.vws_token_state_update.restype = ctypes.c_int

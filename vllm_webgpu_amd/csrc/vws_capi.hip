@@ -41,6 +41,8 @@ thread_local std::string g_err;
 // Bound of a top-p row's wait for the chunks of its cooperative passes run by other workgroups
 // (vws_set_coop_wait_polls), read at every launch.
 std::atomic<int> g_coop_wait_polls{kCoopWaitPolls};
+// Whether rows may take the single pass (vws_set_single_pass), read at every launch.
+std::atomic<int> g_single_pass{1};
 
 #ifdef VWS_TRACE
 // Trace build: the record buffer of vws_trace_set and its workgroup count, read at every launch.
@@ -378,7 +380,6 @@ int vws_sample(const vws_sample_args* a) {
     k.lp_ranks = a->logprob_ranks;
     // every row would leave the single-pass kernel at once: rows go straight to the top-p
     // stream or the general path, without the single pass's first loads
-    k.nofast = (a->allowed_mask && a->num_logprobs >= 0) ? 1 : 0;
     // more rows than workgroups resident at once: the kernel counts its workgroups, so that one
     // whose row is done waits for other rows' passes only once no workgroup is left to start
     const int grid = a->batch;
@@ -388,6 +389,7 @@ int vws_sample(const vws_sample_args* a) {
         else if (a->batch > d.cus * d.row_blocks_per_cu) k.coop_count = 1;
     }
     k.coop_wait_polls = g_coop_wait_polls.load(std::memory_order_relaxed);
+    k.nofast = g_single_pass.load(std::memory_order_relaxed) ? 0 : 1;
 #ifdef VWS_TRACE
     {
         std::lock_guard<std::mutex> lock(g_trace_mu);
@@ -398,19 +400,21 @@ int vws_sample(const vws_sample_args* a) {
     const int cf = (k.coop ? 1 : 0) | (k.coop_count ? 2 : 0) |
                    ((k.coop_count && a->batch <= kRowOrderMaxBatch) ? 4 : 0);
     hipStream_t s = (hipStream_t)a->stream;
-    // the kernel with the raw-logprob epilogue only for launches that ask for logprobs, the one
-    // that masks as it streams only for launches with an allowed mask (and no logprobs), the one
-    // whose top-p path caps as it streams only for launches with the soft cap (and no mask)
+    // the kernels with the raw-logprob epilogue only for launches that ask for logprobs, those
+    // with an allowed mask only for launches that have one (without logprobs it masks as it
+    // streams, with them it masks the candidates of the single pass), those whose top-p path
+    // caps as it streams only for launches with the soft cap and no mask
     const int K = VWS_KERNEL_SAMPLE;
     const bool lp = a->num_logprobs >= 0;
     const bool cap = a->logit_softcap > 0.0f && !a->allowed_mask;
-    const int var = (lp ? 1 : 0) | (!lp && a->allowed_mask ? 2 : 0) | (cap ? 4 : 0);
+    const int var = (lp ? 1 : 0) | (a->allowed_mask ? 2 : 0) | (cap ? 4 : 0);
     using Kern = void (*)(const void*, int64_t, int, int, KArgs);
     auto pick = [var](auto tag) -> Kern {
         using T = decltype(tag);
         switch (var) {
         case 1: return row_kernel<T, true, kXfNone>;
         case 2: return row_kernel<T, false, kXfMask>;
+        case 3: return row_kernel<T, true, kXfMask>;
         case 4: return row_kernel<T, false, kXfCap>;
         case 5: return row_kernel<T, true, kXfCap>;
         default: return row_kernel<T, false, kXfNone>;
@@ -610,6 +614,14 @@ int32_t vws_set_coop_wait_polls(int32_t polls) {
         return -1;
     }
     return g_coop_wait_polls.exchange(polls);
+}
+
+int32_t vws_set_single_pass(int32_t enabled) {
+    if (enabled != 0 && enabled != 1) {
+        fail(VWS_ERR_INVALID_ARGUMENT, "enabled must be 0 or 1 (got %d)", enabled);
+        return -1;
+    }
+    return g_single_pass.exchange(enabled);
 }
 
 int vws_trace_set(uint64_t* buf, int32_t max_workgroups) {

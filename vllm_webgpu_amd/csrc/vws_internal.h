@@ -144,7 +144,7 @@ struct KArgs {
     int hs_row;             // history hash slots per row (power of two) or 0
     int S;                  // parts per row
     int part_len;           // elements per part (multiple of 64)
-    int nofast;             // no row can take the single-pass kernel (logprobs, allowed mask)
+    int nofast;             // no row takes the single pass (vws_set_single_pass(0))
     int topk_k;             // k of the top-k operation
     float softcap;          // > 0: Gemma's soft cap applied to every logit first
     float inv_softcap;      // fl(1 / softcap)

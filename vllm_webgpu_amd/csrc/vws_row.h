@@ -103,8 +103,11 @@ __device__ __forceinline__ float row_uniform(const KArgs& a, int r, int t) {
 // off or above kKMax; an allowed mask together with logprobs).  With raw logprobs the single
 // pass keeps at least L candidates and finishes the logprobs from them (row_logprobs_entry);
 // with an allowed mask it masks every element as it streams.
+// CM: the kernel masks the candidates of its single pass (launches with an allowed mask and raw
+// logprobs); no other kernel serves such a launch's rows on the single pass.
+template <bool CM>
 __device__ __forceinline__ int fast_k(const KArgs& a, const RowP& p) {
-    if (a.allowed && a.L >= 0) return 0;
+    if (!CM && a.allowed && a.L >= 0) return 0;
     if (p.greedy) return 1;
     if (p.k > 0 && p.k < a.V && p.k <= kKMax) return p.k;
     return 0;

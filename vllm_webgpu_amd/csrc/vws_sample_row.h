@@ -1082,17 +1082,20 @@ __device__ __forceinline__ bool row_tail_small(const KArgs& a, RowSmem& sm, int 
 // the row instead.  LP (launches with raw logprobs): the stream also sums exp(x - a) over every
 // element (a the wave's largest value of its first iteration), the candidates keep their raw
 // keys, and the threshold keeps at least max(k, L) candidates, so that row_logprobs_entry can
-// finish the logprobs from the candidates.  MASK (launches with an allowed-token mask and no
-// logprobs): every element outside the row's mask becomes -inf as it is loaded, before the seed
+// finish the logprobs from the candidates.  MASK (launches with an allowed-token mask) without
+// LP (SM): every element outside the row's mask becomes -inf as it is loaded, before the seed
 // and the threshold see it.  One mask word per lane and iteration covers the wave's whole
 // iteration (U vectors of 64 lanes x VEC elements = 64 words; row starts 16-byte aligned), and
-// each lane takes its vector's bits from the lane that loaded them (ds_bpermute).
+// each lane takes its vector's bits from the lane that loaded them (ds_bpermute).  MASK with LP
+// (CM): the stream keeps raw values (the logprobs are of the raw logits), and each candidate is
+// masked at its pack.
 template <typename T, bool LP, bool MASK>
 __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, const void* logits,
                                          int64_t lstride, int V, bool* topp_row) {
     constexpr int NT = kRowThreads;
     constexpr int VEC = Elem<T>::kVec;
     constexpr int U = 32 / VEC;  // 16-byte loads in flight per lane per iteration
+    constexpr bool SM = MASK && !LP, CM = MASK && LP;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const T* row = reinterpret_cast<const T*>(logits) + (size_t)r * lstride;
@@ -1113,7 +1116,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // Without logprobs the first loads wait for no argument read.
     if (LP) {
         const RowP p0 = row_params_scalar(a, r);
-        if (fast_k(a, p0) == 0) {
+        if (fast_k<CM>(a, p0) == 0) {
             *topp_row = topp_eligible(a, p0);
             return false;
         }
@@ -1164,12 +1167,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     const float ha_val = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(avs, 4u * (uint32_t)tid, 0u, 0));
     __builtin_amdgcn_sched_barrier(0);
     load_part(A, 0, BoolC<true>{}, U / 2, U);
-    // MASK: the row's allowed-token words; lane l loads word l of the wave's share of an
+    // SM: the row's allowed-token words; lane l loads word l of the wave's share of an
     // iteration (vector l / (2 VEC), word l % (2 VEC) of it); words past the mask read 0
-    const uint32_t* mrow = MASK ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
-    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(mrow, MASK ? 4u * (uint32_t)((V + 31) >> 5) : 0u);
+    const uint32_t* mrow = SM ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(mrow, SM ? 4u * (uint32_t)((V + 31) >> 5) : 0u);
     auto load_mask = [&](uint32_t& mw, int it) __attribute__((always_inline)) {
-        if (MASK) {
+        if (SM) {
             const int ln = lane_now();
             const uint32_t wi = (uint32_t)((((it * U + ln / (2 * VEC)) * NT + wave * kWave) * VEC) >> 5) +
                                 (uint32_t)(ln % (2 * VEC));
@@ -1178,7 +1181,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     };
     // elements of buf outside the mask become -inf (mw: this lane's word of the iteration)
     auto mask_iter = [&](float (&buf)[U][VEC], uint32_t mw) __attribute__((always_inline)) {
-        if (MASK) {
+        if (SM) {
             const int ln = lane_now();
 #pragma unroll
             for (int q = 0; q < U; ++q) {
@@ -1195,11 +1198,11 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     load_iter(Bq, 1, BoolC<false>{});
     load_mask(MB, 1);
     const RowP prm = row_params_scalar(a, r);
-    const int k = fast_k(a, prm);
+    const int k = fast_k<CM>(a, prm);
     VWS_TRACE_MARK_AFTER(a, VWS_TRACE_PARAMS, k);
     if (k == 0) {
-        // MASK: the top-p stream masks by whole words only for rows that start 16-byte aligned
-        *topp_row = topp_eligible(a, prm) && !(MASK && sl.a != 0);
+        // SM: the top-p stream masks by whole words only for rows that start 16-byte aligned
+        *topp_row = topp_eligible(a, prm) && !(SM && sl.a != 0);
         return false;
     }
     // raw logprobs are of the capped logits, which this stream does not compute (the top-p
@@ -1208,8 +1211,8 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         *topp_row = topp_eligible(a, prm);
         return false;
     }
-    // MASK: the mask words line up with the vectors only when the row starts 16-byte aligned
-    if (MASK && sl.a != 0) return false;
+    // SM: the mask words line up with the vectors only when the row starts 16-byte aligned
+    if (SM && sl.a != 0) return false;
     // the threshold keeps at least kc candidates: the top-L raw logits must be among them
     const int kc = LP ? max(k, a.L) : k;
     const bool hh = prm.has_hist;     // penalties
@@ -1360,7 +1363,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             if (kk) {
                 const uint32_t hv = sm.hval[s] | (tabrow ? tabrow[kk - 1u] & kStateMask : 0u);
                 float xr = Elem<T>::load1(row + (kk - 1u));
-                if (MASK && !((mrow[(kk - 1u) >> 5] >> ((kk - 1u) & 31u)) & 1u)) xr = -__builtin_inff();
+                if (SM && !((mrow[(kk - 1u) >> 5] >> ((kk - 1u) & 31u)) & 1u)) xr = -__builtin_inff();
                 sm.hpen[s] = apply_hashed(xr, hv, sm.hadj[s], prm.rep, prm.inv_rep, prm.freq, prm.pres);
             }
         }
@@ -1386,7 +1389,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     double lacc = 0.0;
     // One vector (VEC elements per lane) at a time: the lane maximum against the threshold
     // decides for the whole wave whether any element of the vector is examined one by one.
-    // MASK: the first iteration was masked whole (the seed needs it); later ones are masked
+    // SM: the first iteration was masked whole (the seed needs it); later ones are masked
     // only where a vector passes the threshold by its raw values (a masked value is at most
     // its raw one), which on rows the mask leaves mostly open is a few vectors per iteration
     auto examine = [&](float (&buf)[U][VEC], uint32_t mw, int it) __attribute__((always_inline)) {
@@ -1408,7 +1411,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
             uint64_t hm = wave_ballot(ok && mq >= cb.tauf);
             if (__builtin_expect(hm == 0ull, 1)) continue;
-            if (MASK && it > 0) {
+            if (SM && it > 0) {
                 const int ln = lane_now();
                 const int src = q * 2 * VEC + ((ln * VEC) >> 5);
                 const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mw);
@@ -1435,16 +1438,16 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
     // it by twice the margin in capped units.
     if (capped && seed > 0x007FFFFFu)
         seed = key_of(softcap_lower(val_of(seed), a.inv_softcap, a.softcap));
-    // MASK: the elements outside the mask are -inf; the threshold admits finite values only
+    // SM: the elements outside the mask are -inf; the threshold admits finite values only
     // (the smallest key above -inf), so that they never become candidates
-    if (MASK && seed < 0x00800000u) seed = 0x00800000u;
+    if (SM && seed < 0x00800000u) seed = 0x00800000u;
     // Fewer candidates than k are exact when no threshold was used.  With the finite-only
-    // threshold alone (MASK), every finite value is a candidate and the top k also holds every
+    // threshold alone (SM), every finite value is a candidate and the top k also holds every
     // -inf element (y = -inf >= the k-th value): those have zero mass, fail min-p, are removed
     // by top-p when it is on (their cumulative mass 0 is at most the cut; the near-tie term they
     // would add needs 1 - p within 2e-6 of 0, which is left to the multi-pass path), and lose
     // every race, so they change nothing when min-p or top-p is on.
-    const bool short_ok = MASK && seed == 0x00800000u &&
+    const bool short_ok = SM && seed == 0x00800000u &&
                           (prm.min_p > 0.0f || (1.0f - prm.top_p) > 2e-6f);
     cb.init(wave, kc, !capped);
     cb.set_tau(seed);
@@ -1475,7 +1478,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         int i0 = 0;
         if (tid <= 1) i0 = sl.load_edge(tid, v);
         const int end = tid == 0 ? sl.a : V;
-        if (MASK && tid <= 1) {
+        if (SM && tid <= 1) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) {
                 const int t = i0 + j;
@@ -1520,6 +1523,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         // the presence bits with one LDS read per candidate.
         const uint32_t pmode = sm.pmode;
         uint32_t ymx = 0u;
+        // CM: the row's mask lowers each masked candidate to -inf at its pack.  A mask only
+        // lowers values, so every element below the thresholds stays below them; a masked
+        // candidate that reaches the top k fails the exactness check (multi-pass path).
+        const uint32_t* cmrow = CM ? a.allowed + (size_t)r * (size_t)a.astride : nullptr;
         // one candidate: its processed value (cap, then the hashed processors and penalties
         // unless a compaction has applied them) and its packed entry at slot pos
         auto pack_one = [&](int pos, uint32_t kx, int32_t ii, bool fixed, bool first)
@@ -1528,6 +1535,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             // values never occur with LP; a compaction that processed keys set status bit 8)
             if (LP) reinterpret_cast<uint32_t*>(sm.hpen)[pos] = kx;
             if (capped) kx = key_of(softcap_out(val_of(kx), a.inv_softcap, a.softcap, a.softcap_f16 != 0));
+            if (CM && !((cmrow[(uint32_t)ii >> 5] >> (ii & 31)) & 1u)) kx = key_of(-__builtin_inff());
             if (!fixed) {
                 const int hs = (hx && rhash_maybe(sm, ii)) ? rhash_find(sm, ii) : -1;
                 uint32_t hv = hs >= 0 ? sm.hval[hs] : 0u;
