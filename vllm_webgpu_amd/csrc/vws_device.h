@@ -332,6 +332,43 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     VWS_BUTTERFLY(v, lane_xor64, vws_max64);
     return v;
 }
+
+// Wave-aggregated LDS atomics, for per-element counters that many lanes of a wave may hit at
+// once (elements that share a key or a bucket: the -inf elements of a masked row, a flat row's
+// masses): LDS serialises the lanes of one atomic instruction that address one word, so such a
+// wave costs 64 LDS cycles per instruction where one atomic of the sum would do.  Each helper
+// may be called in divergent code; it covers the lanes active at the call.
+//
+// base[idx] += 1 for each active lane: one atomic when every active lane has the same idx.
+__device__ __forceinline__ void agg_count(uint32_t* base, uint32_t idx) {
+    const uint64_t act = wave_ballot(true);
+    const uint32_t i0 = __builtin_amdgcn_readfirstlane(idx);
+    if (wave_ballot(idx == i0) == act) {
+        if (lane_id() == (int)__builtin_ctzll(act)) atomicAdd(&base[i0], (uint32_t)__popcll(act));
+    } else {
+        atomicAdd(&base[idx], 1u);
+    }
+}
+// base[idx] += w for each active lane: one atomic of the wave's sum when all 64 lanes are
+// active and share idx (the sum needs every lane's value).
+__device__ __forceinline__ void agg_add64(uint64_t* base, uint32_t idx, uint64_t w) {
+    const uint64_t act = wave_ballot(true);
+    const uint32_t i0 = __builtin_amdgcn_readfirstlane(idx);
+    if (act == ~0ull && wave_ballot(idx == i0) == act) {
+        const uint64_t sum = wave_sum_u64(w);
+        if (lane_id() == 0 && sum)
+            atomicAdd(reinterpret_cast<unsigned long long*>(&base[i0]), (unsigned long long)sum);
+    } else if (w) {
+        atomicAdd(reinterpret_cast<unsigned long long*>(&base[idx]), (unsigned long long)w);
+    }
+}
+// A slot of the counter *ctr for each active lane (ascending with the lane), one atomic per wave.
+__device__ __forceinline__ uint32_t agg_reserve(uint32_t* ctr) {
+    const uint64_t act = wave_ballot(true);
+    uint32_t b = 0u;
+    if (lane_id() == (int)__builtin_ctzll(act)) b = atomicAdd(ctr, (uint32_t)__popcll(act));
+    return __builtin_amdgcn_readfirstlane(b) + (uint32_t)lane_prefix(act);
+}
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     VWS_BUTTERFLY(v, lane_xor64, vws_min64);
     return v;

@@ -412,7 +412,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             const uint32_t kk = key_of(v[j]);
             if (kk) {
                 nvalid++;
-                if (topk_try) atomicAdd(&sm.hcnt[kk >> 20], 1u);
+                if (topk_try) agg_count(sm.hcnt, kk >> 20);
             }
             if (kk > mk) { mk = kk; mi = i0 + j; mxi = i0 + j; }
             else if (kk == mk && kk != 0u) { mi = min(mi, i0 + j); mxi = max(mxi, i0 + j); }
@@ -447,7 +447,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             for (int i = lane; i < n; i += 64) {
                 const uint32_t kk = sm.u.lp.key[wave][i];
                 if (kk >= kth && kk != 0u) {
-                    const uint32_t pos = atomicAdd(&sm.nsel, 1u);
+                    const uint32_t pos = agg_reserve(&sm.nsel);
                     if (pos < 128u) { sm.lp_sel_key[pos] = kk; sm.lp_sel_idx[pos] = sm.u.lp.idx[wave][i]; }
                 }
             }
@@ -497,7 +497,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
                     const uint32_t kk = key_of(v[j]);
-                    if (kk && (kk >> 20) == (uint32_t)b1) atomicAdd(&sm.hcnt[(kk >> 8) & 0xFFFu], 1u);
+                    if (kk && (kk >> 20) == (uint32_t)b1) agg_count(sm.hcnt, (kk >> 8) & 0xFFFu);
                 }
             });
             __syncthreads();
@@ -512,7 +512,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
                     const uint32_t kk = key_of(v[j]);
-                    if (kk && (kk >> 8) == pre) atomicAdd(&sm.hcnt[kk & 0xFFu], 1u);
+                    if (kk && (kk >> 8) == pre) agg_count(sm.hcnt, kk & 0xFFu);
                 }
             });
             __syncthreads();
@@ -585,7 +585,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                         const uint64_t w = mass_of(e);
                         wl += w;
                         nkl++;
-                        if (w) atomicAdd((unsigned long long*)&sm.hmass[bucket_of(d)], (unsigned long long)w);
+                        if (w) agg_add64(sm.hmass, (uint32_t)bucket_of(d), w);
                     } else if (share_lse && v[j] == v[j]) {
                         s0_shared += (double)exp_det(d);
                     }
@@ -614,7 +614,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                         const uint32_t ky = key_of(y);
                         kmin = min(kmin, ky);
                         kmax = max(kmax, ky);
-                        const uint32_t pos = atomicAdd(&sm.gcount, 1u);
+                        const uint32_t pos = agg_reserve(&sm.gcount);
                         if (pos < (uint32_t)kGatherCap) sm.u.gather[pos] = ((uint64_t)ky << 32) | (uint32_t)(i0 + j);
                     }
                 }
@@ -652,8 +652,8 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                             if (ky < klo || ky > khi) continue;
                             const int s = kBuckets - 1 - (int)(((uint64_t)(ky - klo) * kBuckets) / span);
                             const uint64_t w = mass_of(exp_det(d));
-                            if (w) atomicAdd((unsigned long long*)&sm.hmass[s], (unsigned long long)w);
-                            atomicAdd(&sm.hcnt[s], 1u);
+                            if (w) agg_add64(sm.hmass, (uint32_t)s, w);
+                            agg_count(sm.hcnt, (uint32_t)s);
                         }
                     });
                     __syncthreads();
@@ -689,7 +689,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                         for (int j = 0; j < VEC; ++j) {
                             float y, d;
                             if (in_bstar(v[j], y, d) && key_of(y) == klo)
-                                atomicAdd(&sm.hcnt[1023 - ((i0 + j) >> 9)], 1u);
+                                agg_count(sm.hcnt, 1023u - (uint32_t)((i0 + j) >> 9));
                         }
                     });
                     __syncthreads();
@@ -707,7 +707,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                             float y, d;
                             const int ix = i0 + j;
                             if ((ix >> 9) == hi_bits && in_bstar(v[j], y, d) && key_of(y) == klo)
-                                atomicAdd(&sm.hcnt[1023 - (ix & 511)], 1u);
+                                agg_count(sm.hcnt, 1023u - (uint32_t)(ix & 511));
                         }
                     });
                     __syncthreads();
@@ -732,7 +732,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                             if (tie_rule) {
                                 if ((uint32_t)ix >= idx_thr) race.add(exp_det(d), ky, ix, urow ? uc[j] : row_uniform(a, r, ix));
                             } else {
-                                const uint32_t pos = atomicAdd(&sm.gcount, 1u);
+                                const uint32_t pos = agg_reserve(&sm.gcount);
                                 if (pos < (uint32_t)kGatherCap) sm.u.gather[pos] = ((uint64_t)ky << 32) | (uint32_t)ix;
                             }
                         }
@@ -957,7 +957,7 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const uint32_t kk = key_of(v[j]);
-            if (kk) { nvalid++; atomicAdd(&sm.hcnt[kk >> 20], 1u); }
+            if (kk) { nvalid++; agg_count(sm.hcnt, kk >> 20); }
         }
     });
     const uint32_t nval = (uint32_t)gblock_sum(nvalid, sm);
@@ -973,7 +973,7 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const uint32_t kk = key_of(v[j]);
-            if (kk && (kk >> 20) == (uint32_t)b1) atomicAdd(&sm.hcnt[(kk >> 8) & 0xFFFu], 1u);
+            if (kk && (kk >> 20) == (uint32_t)b1) agg_count(sm.hcnt, (kk >> 8) & 0xFFFu);
         }
     });
     __syncthreads();
@@ -987,7 +987,7 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const uint32_t kk = key_of(v[j]);
-            if (kk && (kk >> 8) == pre) atomicAdd(&sm.hcnt[kk & 0xFFu], 1u);
+            if (kk && (kk >> 8) == pre) agg_count(sm.hcnt, kk & 0xFFu);
         }
     });
     __syncthreads();
@@ -1001,7 +1001,7 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
     for_rows([&](float* v, int i0) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j)
-            if (key_of(v[j]) == kth) atomicAdd(&sm.hcnt[1023 - ((i0 + j) >> 9)], 1u);
+            if (key_of(v[j]) == kth) agg_count(sm.hcnt, 1023u - (uint32_t)((i0 + j) >> 9));
     });
     __syncthreads();
     uint64_t rank = rem;
@@ -1015,7 +1015,7 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
             const int ix = i0 + j;
-            if ((ix >> 9) == hi_bits && key_of(v[j]) == kth) atomicAdd(&sm.hcnt[1023 - (ix & 511)], 1u);
+            if ((ix >> 9) == hi_bits && key_of(v[j]) == kth) agg_count(sm.hcnt, 1023u - (uint32_t)(ix & 511));
         }
     });
     __syncthreads();
@@ -1030,7 +1030,7 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
             const uint32_t kk = key_of(v[j]);
             const int ix = i0 + j;
             if (kk > kth || (kk == kth && (uint32_t)ix <= idx_last)) {
-                const uint32_t pos = atomicAdd(&sm.gcount, 1u);
+                const uint32_t pos = agg_reserve(&sm.gcount);
                 if (pos < (uint32_t)kGatherCap) sm.u.gather[pos] = ((uint64_t)(~kk) << 32) | (uint32_t)ix;
             }
         }
