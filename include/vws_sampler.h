@@ -134,9 +134,10 @@ typedef struct vws_sample_args {
      * value -inf bans the token (bad words, min-tokens stop ids), a finite value is added to
      * its logit (logit bias; at most one finite entry per token and row).  Ids outside [0, V)
      * are padding; adjust_lens (device [B]) may be NULL, meaning the full width.  With an
-     * allowed mask every row is masked as its logits stream in (top-k, greedy and top-p rows
-     * alike); rows that do not start 16-byte aligned and launches that also ask for raw
-     * logprobs take the multi-pass path. */
+     * allowed mask and no raw logprobs every row is masked as its logits stream in (top-k,
+     * greedy and top-p rows alike; rows that do not start 16-byte aligned take the multi-pass
+     * path); with raw logprobs (of the unmasked logits) top-k and greedy rows mask their
+     * candidates and top-p rows take the multi-pass path. */
     const uint32_t* allowed_mask;
     int64_t allowed_row_stride;
     const int32_t* adjust_ids;
