@@ -318,6 +318,11 @@ int vws_profile_end(double* ms, int32_t* count);
 #define VWS_TRACE_EXIT 6     /* the workgroup is done, after any help with other rows' passes */
 #define VWS_TRACE_WAVE_LOOP 7 /* single pass: the last wave has examined its share */
 #define VWS_TRACE_WAVE_PACK 8 /* single pass: the last wave has packed its candidates */
+#define VWS_TRACE_TP_HIST 9   /* top-p path, history rows: every history token is buffered */
+#define VWS_TRACE_TP_MASS 10  /* top-p path: the candidates' exact masses are in */
+#define VWS_TRACE_TP_CUT 11   /* top-p path: the cut is decided (any further pass run) */
+#define VWS_TRACE_TP_RACE 12  /* top-p path: the race is done */
+#define VWS_TRACE_TP_LOGPROBS 13 /* top-p path: the raw logprobs are done */
 #define VWS_TRACE_XCC 14     /* value: the XCD (XCC id) the workgroup ran on */
 #define VWS_TRACE_ROWID 15   /* value: the row the workgroup served */
 int vws_trace_set(uint64_t* buf, int32_t max_workgroups);

@@ -58,7 +58,7 @@ def test_abi_constants_match_header(L):
     assert define("VWS_ERR_UNSUPPORTED") == _lib.ERR_UNSUPPORTED
     assert define("VWS_TRACE_SLOTS") == _lib.TRACE_SLOTS
     for n in ("ENTRY", "PARAMS", "FIRST", "SEED", "STREAM", "ROW", "EXIT", "WAVE_LOOP", "WAVE_PACK",
-              "XCC", "ROWID"):
+              "TP_HIST", "TP_MASS", "TP_CUT", "TP_RACE", "TP_LOGPROBS", "XCC", "ROWID"):
         assert define(f"VWS_TRACE_{n}") == getattr(_lib, f"TRACE_{n}"), n
     assert define("VWS_MAX_VOCAB") == _lib.MAX_VOCAB
     assert define("VWS_MAX_LOGPROBS") == _lib.MAX_LOGPROBS

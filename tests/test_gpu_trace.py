@@ -32,6 +32,18 @@ def test_trace_records_and_results(cuda):
     text = trace.report(rec, fl, kus, name, B)
     assert "Per XCD" in text and "single pass" in text
 
+    # the top-p path's finish stamps, in order, on C5's rows (sampled, 20 logprobs)
+    rec5, fl5, _, _, B5 = trace.collect(5, launches=2, warmup=1)
+    for i in range(2):
+        r = rec5[i]
+        on = (fl5[i][r[:, _lib.TRACE_ROWID]] & _lib.FLAG_STREAM_TOPP) != 0
+        assert on.mean() > 0.9
+        seq = [_lib.TRACE_STREAM, _lib.TRACE_TP_MASS, _lib.TRACE_TP_CUT, _lib.TRACE_TP_RACE,
+               _lib.TRACE_TP_LOGPROBS, _lib.TRACE_ROW]
+        for s0, s1 in zip(seq, seq[1:]):
+            assert (r[on, s0] > 0).all() and (r[on, s1] >= r[on, s0]).all(), (s0, s1)
+    assert "top-p: masses -> cut decided" in trace.report(rec5, fl5, (1.0, 1.0), "C5", B5)
+
     # the same tokens from both builds
     w, xs, kw, _ = trace._inputs(2, cuda, False, 1)
     a = ops.sample(xs[0], **kw).sampled.cpu().numpy()

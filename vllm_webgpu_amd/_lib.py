@@ -48,7 +48,8 @@ STATE_PROMPT_FLAG = 0x80000000
 
 TRACE_SLOTS = 16
 (TRACE_ENTRY, TRACE_PARAMS, TRACE_FIRST, TRACE_SEED, TRACE_STREAM, TRACE_ROW, TRACE_EXIT,
- TRACE_WAVE_LOOP, TRACE_WAVE_PACK) = range(9)
+ TRACE_WAVE_LOOP, TRACE_WAVE_PACK, TRACE_TP_HIST, TRACE_TP_MASS, TRACE_TP_CUT, TRACE_TP_RACE,
+ TRACE_TP_LOGPROBS) = range(14)
 TRACE_XCC = 14
 TRACE_ROWID = 15
 

@@ -1243,6 +1243,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
     if (hist) {
         // every history token into the buffers with its processed value (out of line)
         if (const int why = topp_hist_entry<T>(r, kernarg, tauk, xmaxr)) return why;
+        VWS_TRACE_MARK(a, VWS_TRACE_TP_HIST);
         maxk = 0u;
 #pragma unroll
         for (int w = 0; w < kTpWaves; ++w) maxk = sm.wMaxP[w] > maxk ? sm.wMaxP[w] : maxk;
@@ -1387,6 +1388,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         token = (int32_t)(0x7FFFFFFFu - tp_u((uint32_t)best));
         flags |= VWS_FLAG_GREEDY;
     } else {
+        VWS_TRACE_MARK(a, VWS_TRACE_TP_MASS);
         // ---- wave 0: the interval of the exact mass below the candidates (the anchor's
         // scale, then the error bound of the terms), and whether survivors lie below them
         const float q32 = 1.0f - prm.top_p;  // in (0, 1)
@@ -1651,6 +1653,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
             go_exact = true;  // ambiguous: once more on the exact masses
         }
 
+        VWS_TRACE_MARK(a, VWS_TRACE_TP_CUT);
         // ---- race over the kept survivors: candidates above the boundary bucket, and the
         // boundary bucket's members from the cut on
         RowRace rs;
@@ -1783,6 +1786,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         nkept = (int32_t)tp_u(sm.bc[14]);
     }
 
+    VWS_TRACE_MARK(a, VWS_TRACE_TP_RACE);
     // ---- raw logprobs: every element at or above the sampled one is a candidate
     float logS = 0.0f, xs = 0.0f;
     uint32_t rank = 0u;
@@ -1874,6 +1878,7 @@ __device__ __forceinline__ int topp_finish(const KArgs& a, TopPSmem& sm, int r, 
         }
     }
 
+    VWS_TRACE_MARK(a, VWS_TRACE_TP_LOGPROBS);
     // ---- outputs (nothing was written before this point)
     if (tid == 0) {
         a.sampled[r] = token;

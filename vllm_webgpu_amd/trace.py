@@ -174,6 +174,12 @@ def report(rec, fl, kernel_us, name: str, B: int) -> str:
               ("every wave streamed", rel(_lib.TRACE_STREAM)),
               ("row done", rel(_lib.TRACE_ROW)),
               ("finish: streamed -> row done", rel(_lib.TRACE_ROW, _lib.TRACE_STREAM)),
+              ("  top-p: streamed -> history tokens buffered", rel(_lib.TRACE_TP_HIST, _lib.TRACE_STREAM)),
+              ("  top-p: streamed -> exact masses in", rel(_lib.TRACE_TP_MASS, _lib.TRACE_STREAM)),
+              ("  top-p: masses -> cut decided", rel(_lib.TRACE_TP_CUT, _lib.TRACE_TP_MASS)),
+              ("  top-p: cut -> race done", rel(_lib.TRACE_TP_RACE, _lib.TRACE_TP_CUT)),
+              ("  top-p: race -> raw logprobs done", rel(_lib.TRACE_TP_LOGPROBS, _lib.TRACE_TP_RACE)),
+              ("  top-p: logprobs -> row done", rel(_lib.TRACE_ROW, _lib.TRACE_TP_LOGPROBS)),
               ("help after the row", rel(_lib.TRACE_EXIT, _lib.TRACE_ROW))]
     for pname, pick in PATHS.items():
         sel = pick(rflags)
