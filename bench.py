@@ -359,7 +359,7 @@ def pmc_traffic_bytes(config: int):
         text = open(path).read()
     except OSError:
         return None
-    m = re.search(r"^\| `void vws::row_kernel<[a-z ,]+>\([^`]*` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
+    m = re.search(r"^\| `void vws::row_kernel<[a-z0-9 ,]+>\([^`]*` \|(?:[^|\n]*\|){5} *([0-9.]+) *\|$",
                   text, re.M)
     return None if m is None else float(m.group(1)) * 1e6
 
@@ -662,8 +662,9 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": gbps_kern, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": gbps_kern / PEAK_HBM_GBPS, "traffic": pmc_traffic_bytes(args.config),
-            # the instantiation the launch ran: element type, raw logprobs, allowed mask
-            "kernel": "vws::row_kernel<{}, {}, false>".format(
+            # the instantiation the launch ran: element type, raw logprobs, logit transform
+            # (0: none; the bench's workloads have no allowed mask and no soft cap)
+            "kernel": "vws::row_kernel<{}, {}, 0>".format(
                 "unsigned short" if w.dtype == "bf16" else "float",
                 "true" if w.num_logprobs is not None else "false"),
         },
