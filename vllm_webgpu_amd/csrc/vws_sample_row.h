@@ -1428,6 +1428,40 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         }
         if (LP) lacc += (double)lit;
     };
+    // SM: the same examination, after which each vector's registers take vector q of iteration
+    // nxt at once (run: examine iteration it at all), so the next loads leave as soon as their
+    // registers are free; measured faster for masked launches only
+    auto examine_pv = [&](float (&buf)[U][VEC], uint32_t mw, int it, int nxt, bool run) __attribute__((always_inline)) {
+        if (run) cb.refresh();
+        const int t = tid_now();
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+            if (run) do {
+                const int vi = (it * U + q) * NT + t;
+                const bool ok = vi < nbody;
+                float mq = buf[q][0];
+#pragma unroll
+                for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
+                uint64_t hm = wave_ballot(ok && mq >= cb.tauf);
+                if (__builtin_expect(hm == 0ull, 1)) continue;
+                if (it > 0) {
+                    const int ln = lane_now();
+                    const int src = q * 2 * VEC + ((ln * VEC) >> 5);
+                    const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mw);
+                    const uint32_t bits = w >> ((ln * VEC) & 31);
+#pragma unroll
+                    for (int j = 0; j < VEC; ++j) buf[q][j] = ((bits >> j) & 1u) ? buf[q][j] : -__builtin_inff();
+                    mq = buf[q][0];
+#pragma unroll
+                    for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
+                    hm = wave_ballot(ok && mq >= cb.tauf);
+                    if (hm == 0ull) continue;
+                }
+                cb.template append_vec<VEC>(buf[q], sl.a + vi * VEC, hm);
+            } while (0);
+            load_part(buf, nxt, BoolC<false>{}, q, q + 1);
+        }
+    };
     const bool sampling = !prm.greedy;
     // With the soft cap the buffer keeps raw values throughout (the cap is applied at the pack),
     // so it is never cut by processed values: a full buffer sends the row to the general path.
@@ -1460,13 +1494,22 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)((kk - 1u) | 0x80000000u));
         }
     }
-    for (int it = 0; it < nit && !cb.ovf; it += 2) {
-        examine(A, MA, it);
-        load_iter(A, it + 2, BoolC<false>{});
-        load_mask(MA, it + 2);
-        if (it + 1 < nit && !cb.ovf) examine(Bq, MB, it + 1);
-        load_iter(Bq, it + 3, BoolC<false>{});
-        load_mask(MB, it + 3);
+    if (SM) {
+        for (int it = 0; it < nit && !cb.ovf; it += 2) {
+            examine_pv(A, MA, it, it + 2, true);
+            load_mask(MA, it + 2);
+            examine_pv(Bq, MB, it + 1, it + 3, it + 1 < nit && !cb.ovf);
+            load_mask(MB, it + 3);
+        }
+    } else {
+        for (int it = 0; it < nit && !cb.ovf; it += 2) {
+            examine(A, MA, it);
+            load_iter(A, it + 2, BoolC<false>{});
+            load_mask(MA, it + 2);
+            if (it + 1 < nit && !cb.ovf) examine(Bq, MB, it + 1);
+            load_iter(Bq, it + 3, BoolC<false>{});
+            load_mask(MB, it + 3);
+        }
     }
     VWS_TRACE_MARK_AFTER(a, VWS_TRACE_WAVE_LOOP, cb.cnt);
     if (wave == 0) {
