@@ -1428,9 +1428,12 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         }
         if (LP) lacc += (double)lit;
     };
-    // SM: the same examination, after which each vector's registers take vector q of iteration
-    // nxt at once (run: examine iteration it at all), so the next loads leave as soon as their
-    // registers are free; measured faster for masked launches only
+    // The same examination, after which each vector's registers take vector q of iteration nxt
+    // at once (run: examine iteration it at all), so the next loads leave as soon as their
+    // registers are free.  Used by the masked kernel and the 16-bit kernels without logprobs:
+    // measured faster there (C3 with one masked row 36.5 -> 34.0 us, C4 164.2 -> 161.0 us) and
+    // slower in the fp32 plain and logprob kernels (C3 +0.8 us, C3 + 20 logprobs +2.7 us).
+    constexpr bool REFILL = SM || (!LP && VEC == 8);
     auto examine_pv = [&](float (&buf)[U][VEC], uint32_t mw, int it, int nxt, bool run) __attribute__((always_inline)) {
         if (run) cb.refresh();
         const int t = tid_now();
@@ -1444,7 +1447,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
                 for (int j = 1; j < VEC; ++j) mq = fmaxf(mq, buf[q][j]);
                 uint64_t hm = wave_ballot(ok && mq >= cb.tauf);
                 if (__builtin_expect(hm == 0ull, 1)) continue;
-                if (it > 0) {
+                if (SM && it > 0) {
                     const int ln = lane_now();
                     const int src = q * 2 * VEC + ((ln * VEC) >> 5);
                     const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mw);
@@ -1494,7 +1497,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             cb.append(pk != 0u && pk >= cb.tau, pk, (int32_t)((kk - 1u) | 0x80000000u));
         }
     }
-    if (SM) {
+    if (REFILL) {
         for (int it = 0; it < nit && !cb.ovf; it += 2) {
             examine_pv(A, MA, it, it + 2, true);
             load_mask(MA, it + 2);
