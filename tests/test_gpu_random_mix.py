@@ -1,0 +1,190 @@
+"""Randomised mixed launches against the oracle: every option the sampling call takes, combined
+at random in one launch -- fp32, bf16 or f16 logits; greedy rows, top-k (1 to 300, off),
+top-p, min-p; penalties from padded id lists or from the token-state table with its bitmap;
+raw logprobs (0, 3 or 20); an allowed mask of random density per row; bans and biases with
+per-row lengths; Gemma's soft cap with and without its f16 store; odd vocabularies.  Each
+launch's rows take whichever paths their parameters pick (single pass, single-pass top-p with
+its further passes, multi-pass), so the paths' hand-overs are exercised together.
+
+Token ids, flags and survivor counts must match the oracle bit for bit; logprob ids and ranks
+bit for bit, values within the tolerances of tests/common.py."""
+import numpy as np
+import pytest
+
+from oracle import sampler as O
+from tests.cases import _u
+from tests.common import assert_same
+from tests.test_gpu_topp_history import bits_from_table
+from tests.test_gpu_token_state import table_from_lists
+
+pytestmark = pytest.mark.gpu
+
+
+def _words(allowed):
+    B, V = allowed.shape
+    w = np.zeros((B, (V + 31) // 32 * 32), np.uint64)
+    w[:, :V] = allowed
+    return (w.reshape(B, -1, 32) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
+
+
+def _launch(rng, dt):
+    B = int(rng.integers(8, 72))
+    V = int(rng.choice([4099, 32000, 50021, 128256, 151936]))
+    x = rng.normal(0, rng.uniform(0.5, 5.0), (B, V)).astype(np.float32)
+    x[rng.random(B) < 0.15] *= 0.05                                   # flat rows
+    spikes = rng.integers(0, V, (B, 6))
+    np.put_along_axis(x, spikes, x.max(axis=1, keepdims=True) + rng.uniform(0, 4, (B, 6)).astype(np.float32), 1)
+    if rng.random() < 0.3:
+        x = np.round(x * 4) / 4                                       # coarse grid: ties
+    if dt == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        raw = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        xf = (raw.astype(np.uint32) << 16).view(np.float32)
+    elif dt == "f16":
+        raw = x.astype(np.float16)
+        xf = raw.astype(np.float32)
+    else:
+        raw = xf = x
+    T = np.where(rng.random(B) < 0.15, 0.0, rng.uniform(0.3, 1.5, B)).astype(np.float32)
+    k = rng.choice(np.array([0, 0, 0, 1, 20, 50, 256, 300], np.int32), B).astype(np.int32)
+    p = np.where(rng.random(B) < 0.3, 1.0, rng.uniform(0.5, 0.99, B)).astype(np.float32)
+    mp = np.where(rng.random(B) < 0.2, 0.05, 0.0).astype(np.float32)
+    cfg = dict(B=B, V=V, dt=dt, raw=raw, xf=xf, T=T, k=k, p=p, mp=mp,
+               rep=np.ones(B, np.float32), pres=np.zeros(B, np.float32),
+               freq=np.zeros(B, np.float32), prompt=None, output=None, table=False, L=None,
+               allowed=None, aid=None, aval=None, alen=None, cap=None, cap16=False)
+    if rng.random() < 0.6:
+        cfg["rep"] = np.where(rng.random(B) < 0.7, rng.uniform(0.8, 1.3, B), 1.0).astype(np.float32)
+        cfg["pres"] = np.where(rng.random(B) < 0.5, rng.uniform(-0.5, 0.8, B), 0.0).astype(np.float32)
+        cfg["freq"] = np.where(rng.random(B) < 0.5, rng.uniform(0.0, 0.5, B), 0.0).astype(np.float32)
+        W = int(rng.choice([16, 128, 512]))
+        out = rng.integers(0, V, (B, W)).astype(np.int32)
+        top = np.argsort(-xf, axis=1)[:, :8].astype(np.int32)         # hit the rows' top tokens
+        out[:, :8] = top
+        out[rng.random((B, W)) < 0.1] = V                             # padding
+        cfg["output"] = out
+        if rng.random() < 0.5:
+            cfg["prompt"] = rng.integers(0, V, (B, 64)).astype(np.int32)
+        cfg["table"] = rng.random() < 0.5
+    cfg["L"] = [None, 0, 3, 20][int(rng.integers(0, 4))]
+    if rng.random() < 0.3:
+        dens = rng.choice([0.001, 0.1, 0.5, 1.0], B)
+        allowed = rng.random((B, V)) < dens[:, None]
+        allowed[np.arange(B), rng.integers(0, V, B)] = True
+        cfg["allowed"] = allowed
+    if rng.random() < 0.25:
+        Wa = 6
+        aid = rng.integers(0, V, (B, Wa)).astype(np.int32)
+        aid[:, :2] = np.argsort(-xf, axis=1)[:, :2]                   # ban or bias the top two
+        aval = np.where(rng.random((B, Wa)) < 0.5, -np.inf, rng.uniform(-2, 2, (B, Wa))).astype(np.float32)
+        cfg.update(aid=aid, aval=aval, alen=rng.integers(0, Wa + 1, B).astype(np.int32))
+    if rng.random() < 0.25:
+        cfg["cap"] = 30.0
+        cfg["cap16"] = bool(rng.random() < 0.5)
+    return cfg
+
+
+@pytest.mark.parametrize("seed", range(36))
+def test_random_mixed_launch(cuda, seed):
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(5000 + seed)
+    c = _launch(rng, ["f32", "bf16", "f16"][seed % 3])
+    B, V = c["B"], c["V"]
+    u = _u(rng, (B, V))
+    prm = O.make_params(B, c["T"], c["k"], c["p"], c["mp"], c["rep"], c["pres"], c["freq"])
+    bits = None if c["allowed"] is None else _words(c["allowed"])
+    ref = O.sample(c["xf"], prm, u, prompt_ids=c["prompt"], output_ids=c["output"],
+                   num_logprobs=c["L"], allowed=bits, adjust_ids=c["aid"],
+                   adjust_vals=c["aval"], adjust_lens=c["alen"], softcap=c["cap"],
+                   softcap_f16=c["cap16"])
+    dev = cuda
+    if c["dt"] == "bf16":
+        x = torch.from_numpy(c["raw"].view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        x = torch.from_numpy(c["raw"]).to(dev)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    hist = {}
+    if c["output"] is not None:
+        if c["table"]:
+            st = table_from_lists(B, V, c["prompt"], c["output"])
+            hist = dict(token_state=t(st.view(np.int32)))
+            if V <= 196608:
+                hist["token_state_bits"] = t(bits_from_table(st))
+        else:
+            hist = dict(prompt_ids=t(c["prompt"]), output_ids=t(c["output"]))
+    greedy_all = bool(np.all(~(c["T"] >= np.float32(1e-5))))
+    res = ops.sample(
+        x, temperature=None if greedy_all else torch.from_numpy(c["T"]),
+        top_k=torch.from_numpy(c["k"]), top_p=torch.from_numpy(c["p"]),
+        min_p=torch.from_numpy(c["mp"]), repetition_penalty=torch.from_numpy(c["rep"]),
+        presence_penalty=torch.from_numpy(c["pres"]), frequency_penalty=torch.from_numpy(c["freq"]),
+        uniforms=t(u), num_logprobs=c["L"],
+        allowed_mask=None if bits is None else t(bits.view(np.int32)),
+        adjust_ids=t(c["aid"]), adjust_vals=t(c["aval"]), adjust_lens=t(c["alen"]),
+        logit_softcap=c["cap"], logit_softcap_f16=c["cap16"], **hist)
+    torch.cuda.synchronize()
+    g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
+             n_kept=res.num_kept.cpu().numpy())
+    if c["L"] is not None:
+        g.update(lp_ids=res.logprob_ids.cpu().numpy(), lp_vals=res.logprob_vals.cpu().numpy(),
+                 ranks=res.logprob_ranks.cpu().numpy())
+    label = (f"seed {seed}: {c['dt']} B={B} V={V} L={c['L']} pen={c['output'] is not None} "
+             f"table={c['table']} mask={bits is not None} adj={c['aid'] is not None} cap={c['cap']}")
+    print(label, flush=True)
+    assert_same(g, ref, label)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_multi_pass_edges_are_not_duplicated(cuda, dt):
+    """Multi-pass rows whose every element survives (no top-k, top-p 1), with the allowed mask
+    masking the first and last tokens and penalties on them: the padding of the unaligned
+    head, of the tail and of the chunks past the tail must not be processed into copies of
+    those tokens (each would count as a survivor, and carry mass on top-p rows).  Odd
+    vocabularies and a row view that starts unaligned, so that both edges are partial."""
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(77)
+    B, V = 12, 4099
+    x = rng.normal(0, 2, (B, V + 3)).astype(np.float32)
+    T = np.full(B, 0.9, np.float32)
+    k = np.zeros(B, np.int32)
+    p = np.where(np.arange(B) % 3 == 2, 0.97, 1.0).astype(np.float32)
+    rep = np.full(B, 1.2, np.float32)
+    pres = np.full(B, 0.4, np.float32)
+    out = np.tile(np.array([0, 1, 2, 3, 5, 7, V - 1, V - 2, V - 3], np.int32), (B, 1))
+    allowed = rng.random((B, V)) < 0.5
+    allowed[:, :8] = False
+    allowed[:, V - 8:] = False
+    allowed[:, 100] = True
+    bits = _words(allowed)
+    u = _u(rng, (B, V))
+    for off in (0, 1):                                   # aligned rows, then rows off by one
+        xv = x[:, off:off + V]
+        if dt == "bf16":
+            uu = np.ascontiguousarray(xv).view(np.uint32).astype(np.uint64)
+            raw = ((uu + 0x7FFF + ((uu >> 16) & 1)) >> 16).astype(np.uint16)
+            xf = (raw.astype(np.uint32) << 16).view(np.float32)
+            full = torch.from_numpy(np.ascontiguousarray(
+                np.pad(raw, ((0, 0), (off, 3 - off)))).view(np.int16)).to(cuda).view(torch.bfloat16)
+        else:
+            xf = np.ascontiguousarray(xv)
+            full = torch.from_numpy(np.ascontiguousarray(np.pad(xf, ((0, 0), (off, 3 - off))))).to(cuda)
+        xt = full[:, off:off + V]
+        prm = O.make_params(B, T, k, p, 0.0, rep, pres, 0.0)
+        ref = O.sample(xf, prm, u, output_ids=out, allowed=bits)
+        res = ops.sample(xt, temperature=torch.from_numpy(T), top_k=torch.from_numpy(k),
+                         top_p=torch.from_numpy(p), repetition_penalty=torch.from_numpy(rep),
+                         presence_penalty=torch.from_numpy(pres),
+                         output_ids=torch.from_numpy(out).to(cuda),
+                         uniforms=torch.from_numpy(u).to(cuda),
+                         allowed_mask=torch.from_numpy(bits.view(np.int32)).to(cuda))
+        torch.cuda.synchronize()
+        g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
+                 n_kept=res.num_kept.cpu().numpy())
+        assert_same(g, ref, f"{dt} offset {off}")
+        assert (g["n_kept"][p == 1.0] == V).all()

@@ -310,13 +310,24 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
         __threadfence();
         __syncthreads();
     }
+    // Elements of the chunk being visited that belong to the row: the first cur_nv (a body
+    // vector all VEC; the unaligned head and tail fewer, their other slots NaN padding whose
+    // indices are other elements'; chunks past the tail none).  Only those are processed, so
+    // padding never turns into a masked or penalised copy of another element.
+    int cur_nv = VEC;
+    auto chunk_nv = [&](int c) -> int {
+        if (c >= 1 && c <= sl.nbody) return VEC;
+        if (c == 0) return sl.a - sl.lo;
+        if (c == sl.nbody + 1) return sl.hi - sl.body_end();
+        return 0;
+    };
     // processed values of a chunk: hashed tokens (processors, then penalties), then the
     // allowed-token mask (masked tokens are -inf whatever the hash did to them)
     auto finalize = [&](float* v, int i0) {
         if (hh || tb) {
             const uint32_t w = (uint32_t)i0 >> 5, sh = (uint32_t)i0 & 31u;
             const uint64_t win = (uint64_t)sm.bitmap[w] | ((uint64_t)sm.bitmap[w + 1] << 32);
-            const uint32_t bits = (uint32_t)(win >> sh) & ((1u << VEC) - 1u);
+            const uint32_t bits = (uint32_t)(win >> sh) & ((1u << cur_nv) - 1u);
             if (bits) {
 #pragma unroll
                 for (int j = 0; j < VEC; ++j) {
@@ -336,7 +347,7 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
             const uint32_t bits = (uint32_t)(win >> sh);
 #pragma unroll
             for (int j = 0; j < VEC; ++j)
-                if (!((bits >> j) & 1u) && i0 + j < V) v[j] = -__builtin_inff();
+                if (!((bits >> j) & 1u) && j < cur_nv) v[j] = -__builtin_inff();
         }
     };
     // every pass visits the same chunks in the same order: 2 chunks per thread per iteration
@@ -353,7 +364,9 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     v1[j] = softcap_out(v1[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 }
             }
+            cur_nv = chunk_nv(c0);
             f(v0, i0);
+            cur_nv = chunk_nv(c0 + NT);
             f(v1, i1);
         }
     };
@@ -377,7 +390,9 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
                     v1[j] = softcap_out(v1[j], a.inv_softcap, a.softcap, a.softcap_f16 != 0);
                 }
             }
+            cur_nv = chunk_nv(c0);
             f(v0, i0, u0);
+            cur_nv = chunk_nv(c0 + NT);
             f(v1, i1, u1);
         }
     };
