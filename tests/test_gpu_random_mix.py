@@ -27,9 +27,9 @@ def _words(allowed):
     return (w.reshape(B, -1, 32) << np.arange(32, dtype=np.uint64)).sum(axis=2).astype(np.uint32)
 
 
-def _launch(rng, dt):
-    B = int(rng.integers(8, 72))
-    V = int(rng.choice([4099, 32000, 50021, 128256, 151936]))
+def _launch(rng, dt, big=False):
+    B = int(rng.integers(300, 700)) if big else int(rng.integers(8, 72))
+    V = int(rng.choice([4099, 32000, 50021] if big else [4099, 32000, 50021, 128256, 151936]))
     x = rng.normal(0, rng.uniform(0.5, 5.0), (B, V)).astype(np.float32)
     x[rng.random(B) < 0.15] *= 0.05                                   # flat rows
     spikes = rng.integers(0, V, (B, 6))
@@ -74,8 +74,14 @@ def _launch(rng, dt):
         cfg["allowed"] = allowed
     if rng.random() < 0.25:
         Wa = 6
-        aid = rng.integers(0, V, (B, Wa)).astype(np.int32)
-        aid[:, :2] = np.argsort(-xf, axis=1)[:, :2]                   # ban or bias the top two
+        # distinct ids per row (at most one finite entry per token is the call's contract):
+        # the row's top two, then four others
+        top2 = np.argsort(-xf, axis=1)[:, :2]
+        aid = np.empty((B, Wa), np.int32)
+        for b in range(B):
+            rest = rng.choice(V - 2, Wa - 2, replace=False)
+            rest = np.setdiff1d(np.arange(V), top2[b])[rest]
+            aid[b] = np.concatenate([top2[b], rest])
         aval = np.where(rng.random((B, Wa)) < 0.5, -np.inf, rng.uniform(-2, 2, (B, Wa))).astype(np.float32)
         cfg.update(aid=aid, aval=aval, alen=rng.integers(0, Wa + 1, B).astype(np.int32))
     if rng.random() < 0.25:
@@ -84,16 +90,22 @@ def _launch(rng, dt):
     return cfg
 
 
-@pytest.mark.parametrize("seed", range(36))
+@pytest.mark.parametrize("seed", range(60))
 def test_random_mixed_launch(cuda, seed):
+    """Seeds 48 and above use larger batches (up to 700 rows: more rows than workgroups resident
+    at once) and the kernel's own uniforms (a launch-wide generator key)."""
     import torch
 
     from vllm_webgpu_amd import ops
 
     rng = np.random.default_rng(5000 + seed)
-    c = _launch(rng, ["f32", "bf16", "f16"][seed % 3])
+    c = _launch(rng, ["f32", "bf16", "f16"][seed % 3], big=seed >= 48)
     B, V = c["B"], c["V"]
-    u = _u(rng, (B, V))
+    key = int(rng.integers(1, 2 ** 62)) if seed >= 48 else None
+    if key is None:
+        u = _u(rng, (B, V))
+    else:
+        u = O.philox_uniforms(np.full(B, key, np.uint64), V, np.arange(B, dtype=np.uint64))
     prm = O.make_params(B, c["T"], c["k"], c["p"], c["mp"], c["rep"], c["pres"], c["freq"])
     bits = None if c["allowed"] is None else _words(c["allowed"])
     ref = O.sample(c["xf"], prm, u, prompt_ids=c["prompt"], output_ids=c["output"],
@@ -121,7 +133,7 @@ def test_random_mixed_launch(cuda, seed):
         top_k=torch.from_numpy(c["k"]), top_p=torch.from_numpy(c["p"]),
         min_p=torch.from_numpy(c["mp"]), repetition_penalty=torch.from_numpy(c["rep"]),
         presence_penalty=torch.from_numpy(c["pres"]), frequency_penalty=torch.from_numpy(c["freq"]),
-        uniforms=t(u), num_logprobs=c["L"],
+        uniforms=None if key is not None else t(u), rng_key=key, num_logprobs=c["L"],
         allowed_mask=None if bits is None else t(bits.view(np.int32)),
         adjust_ids=t(c["aid"]), adjust_vals=t(c["aval"]), adjust_lens=t(c["alen"]),
         logit_softcap=c["cap"], logit_softcap_f16=c["cap16"], **hist)
