@@ -200,3 +200,84 @@ def test_multi_pass_edges_are_not_duplicated(cuda, dt):
                  n_kept=res.num_kept.cpu().numpy())
         assert_same(g, ref, f"{dt} offset {off}")
         assert (g["n_kept"][p == 1.0] == V).all()
+
+
+def _edge_launch(rng):
+    """Extreme parameters: tiny and odd vocabularies, strided rows that start unaligned, NaN and
+    infinite logits, extreme temperatures, k around V, p at 0 and near 1, min-p up to 1,
+    histories with lengths, rows that allow nothing."""
+    B = int(rng.integers(1, 40))
+    V = int(rng.choice([1, 2, 7, 63, 64, 65, 100, 1000, 3001, 8191, 8193, 20000]))
+    off = int(rng.integers(0, 4))
+    full = rng.normal(0, rng.choice([0.01, 1.0, 8.0]), (B, V + 4)).astype(np.float32)
+    x = full[:, off:off + V]
+    sp = rng.random((B, V))
+    x = np.where(sp < 0.002, np.nan, x)
+    x = np.where((sp >= 0.002) & (sp < 0.004), -np.inf, x)
+    x = np.where((sp >= 0.004) & (sp < 0.0045), np.inf, x).astype(np.float32)
+    if rng.random() < 0.3:
+        x = np.round(x).astype(np.float32)                            # many ties
+    T = rng.choice(np.array([0.0, 1e-3, 0.05, 1.0, 3.0, 10.0], np.float32), B).astype(np.float32)
+    k = rng.choice(np.array([0, 1, 2, max(V - 1, 0), V, V + 5, 64, 65, 256, 257], np.int32), B).astype(np.int32)
+    p = rng.choice(np.array([1.0, 0.999999, 0.5, 1e-6, 0.0, 0.3], np.float32), B).astype(np.float32)
+    mp = rng.choice(np.array([0.0, 0.0, 0.5, 0.99, 1.0], np.float32), B).astype(np.float32)
+    c = dict(B=B, V=V, off=off, x=x, T=T, k=k, p=p, mp=mp, rep=np.ones(B, np.float32),
+             pres=np.zeros(B, np.float32), freq=np.zeros(B, np.float32), prompt=None,
+             output=None, plens=None, olens=None, L=None, allowed=None)
+    if rng.random() < 0.5:
+        c["rep"] = rng.uniform(0.5, 2.0, B).astype(np.float32)
+        c["pres"] = rng.uniform(-1.0, 1.0, B).astype(np.float32)
+        c["freq"] = rng.uniform(-0.5, 0.5, B).astype(np.float32)
+        W = int(rng.integers(1, 40))
+        c["output"] = rng.integers(-2, V + 2, (B, W)).astype(np.int32)
+        c["olens"] = rng.integers(0, W + 1, B).astype(np.int32)
+        if rng.random() < 0.5:
+            c["prompt"] = rng.integers(0, V, (B, W)).astype(np.int32)
+            c["plens"] = rng.integers(0, W + 1, B).astype(np.int32)
+    if rng.random() < 0.5:
+        c["L"] = int(min(V, rng.choice([0, 1, 5, 20])))
+    if rng.random() < 0.3:
+        allowed = rng.random((B, V)) < rng.choice([0.0, 0.01, 0.5, 1.0], B)[:, None]
+        c["allowed"] = allowed
+    return c
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_edge_launch(cuda, seed):
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(9000 + seed)
+    c = _edge_launch(rng)
+    B, V = c["B"], c["V"]
+    u = _u(rng, (B, V))
+    prm = O.make_params(B, c["T"], c["k"], c["p"], c["mp"], c["rep"], c["pres"], c["freq"])
+    bits = None if c["allowed"] is None else _words(c["allowed"])
+    ref = O.sample(c["x"], prm, u, prompt_ids=c["prompt"], output_ids=c["output"],
+                   prompt_lens=c["plens"], output_lens=c["olens"], num_logprobs=c["L"],
+                   allowed=bits)
+    # the logits as a strided view of a wider buffer, starting c["off"] elements in
+    buf = np.full((B, V + 4), np.float32(7.0))
+    buf[:, c["off"]:c["off"] + V] = c["x"]
+    xt = torch.from_numpy(buf).to(cuda)[:, c["off"]:c["off"] + V]
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    greedy_all = bool(np.all(~(c["T"] >= np.float32(1e-5))))
+    res = ops.sample(
+        xt, temperature=None if greedy_all else torch.from_numpy(c["T"]),
+        top_k=torch.from_numpy(c["k"]), top_p=torch.from_numpy(c["p"]),
+        min_p=torch.from_numpy(c["mp"]), repetition_penalty=torch.from_numpy(c["rep"]),
+        presence_penalty=torch.from_numpy(c["pres"]), frequency_penalty=torch.from_numpy(c["freq"]),
+        prompt_ids=t(c["prompt"]), prompt_lens=t(c["plens"]), output_ids=t(c["output"]),
+        output_lens=t(c["olens"]), uniforms=t(u), num_logprobs=c["L"],
+        allowed_mask=None if bits is None else t(bits.view(np.int32)))
+    torch.cuda.synchronize()
+    g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
+             n_kept=res.num_kept.cpu().numpy())
+    if c["L"] is not None:
+        g.update(lp_ids=res.logprob_ids.cpu().numpy(), lp_vals=res.logprob_vals.cpu().numpy(),
+                 ranks=res.logprob_ranks.cpu().numpy())
+    label = (f"edge seed {seed}: B={B} V={V} off={c['off']} L={c['L']} "
+             f"pen={c['output'] is not None} mask={bits is not None}")
+    print(label, flush=True)
+    assert_same(g, ref, label)

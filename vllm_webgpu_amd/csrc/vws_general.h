@@ -540,7 +540,9 @@ __device__ __forceinline__ void general_row(const KArgs& a, GenSmem& sm, int r, 
         const float q32 = 1.0f - prm.top_p;
         const bool topp = q32 > 0.0f;
         const bool abl = topp && !(q32 < 1.0f);
-        const bool share_lse = (L >= 0) && !hh && !tb && Tt == 1.0f && kth_y == -__builtin_inff() &&
+        // (raw logprobs are of the unmasked, unpenalised logits: the sampling sum serves them
+        // only when nothing changes a logit)
+        const bool share_lse = (L >= 0) && !hh && !tb && !mrow && Tt == 1.0f && kth_y == -__builtin_inff() &&
                                lp_min == -__builtin_inff();
         auto survivor = [&](float x, float& y, float& d) -> bool {
             y = (Tt == 1.0f) ? x : x / Tt;
@@ -890,6 +892,31 @@ logprobs:
             a.lp_vals[(size_t)r * stride] = (raw_s - m0) - logS;
             a.lp_ranks[r] = (int32_t)rk;
         }
+        // Fewer than L elements that are not NaN: the rest of the top L are the row's NaN
+        // elements in index order (a sort by key puts them last, lowest index first), found by
+        // wave 0 a block of 64 at a time (it stops once it has them: such a row is short or
+        // mostly NaN), then -1 / NaN past the row's end
+        auto fill_rest = [&](int n) {
+            if (n >= L || wave != 0) return;
+            const int need = L - n;
+            int found = 0;
+            for (int base = 0; base < V && found < need; base += kWave) {
+                const int i = base + lane;
+                const float xi = i < V ? Elem<T>::load1(row + i) : 0.0f;
+                const bool isn = i < V && !(xi == xi);
+                const uint64_t bal = wave_ballot(isn);
+                const int pos = found + lane_prefix(bal);
+                if (isn && pos < need) {
+                    a.lp_ids[(size_t)r * stride + 1 + n + pos] = i;
+                    a.lp_vals[(size_t)r * stride + 1 + n + pos] = __builtin_nanf("");
+                }
+                found += __popcll(bal);
+            }
+            for (int j = n + min(found, need) + lane; j < L; j += kWave) {
+                a.lp_ids[(size_t)r * stride + 1 + j] = -1;
+                a.lp_vals[(size_t)r * stride + 1 + j] = __builtin_nanf("");
+            }
+        };
         // the buffered top-L candidates overflowed (ties) or their cut holds more than the 128
         // gathered: the exact selection over the row
         const bool exact_sel = L > 0 && (sm.bc32[2] != 0u || sm.nsel > 128u);
@@ -900,10 +927,7 @@ logprobs:
                 a.lp_ids[(size_t)r * stride + 1 + j] = (int32_t)(uint32_t)g;
                 a.lp_vals[(size_t)r * stride + 1 + j] = (val_of(~(uint32_t)(g >> 32)) - m0) - logS;
             }
-            for (int j = (int)n + tid; j < L; j += NT) {
-                a.lp_ids[(size_t)r * stride + 1 + j] = -1;
-                a.lp_vals[(size_t)r * stride + 1 + j] = __builtin_nanf("");
-            }
+            fill_rest((int)n);
         } else if (L > 0) {
             const uint32_t n = min(sm.nsel, 128u);
             for (uint32_t j = tid; j < n; j += NT) {
@@ -919,10 +943,7 @@ logprobs:
                     a.lp_vals[(size_t)r * stride + 1 + pos] = (val_of(kj) - m0) - logS;
                 }
             }
-            for (int j = (int)n + tid; j < L; j += NT) {
-                a.lp_ids[(size_t)r * stride + 1 + j] = -1;
-                a.lp_vals[(size_t)r * stride + 1 + j] = __builtin_nanf("");
-            }
+            fill_rest((int)n);
         }
     }
     // the workspace is left as it was found (zeros): other operations that share it, such as
