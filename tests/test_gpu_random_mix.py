@@ -205,7 +205,8 @@ def test_multi_pass_edges_are_not_duplicated(cuda, dt):
 def _edge_launch(rng):
     """Extreme parameters: tiny and odd vocabularies, strided rows that start unaligned, NaN and
     infinite logits, extreme temperatures, k around V, p at 0 and near 1, min-p up to 1,
-    histories with lengths, rows that allow nothing."""
+    histories with lengths (as lists, or as a token-state table reached through a row map),
+    rows that allow nothing, bans and biases, the soft cap at 1 and 30."""
     B = int(rng.integers(1, 40))
     V = int(rng.choice([1, 2, 7, 63, 64, 65, 100, 1000, 3001, 8191, 8193, 20000]))
     off = int(rng.integers(0, 4))
@@ -223,7 +224,8 @@ def _edge_launch(rng):
     mp = rng.choice(np.array([0.0, 0.0, 0.5, 0.99, 1.0], np.float32), B).astype(np.float32)
     c = dict(B=B, V=V, off=off, x=x, T=T, k=k, p=p, mp=mp, rep=np.ones(B, np.float32),
              pres=np.zeros(B, np.float32), freq=np.zeros(B, np.float32), prompt=None,
-             output=None, plens=None, olens=None, L=None, allowed=None)
+             output=None, plens=None, olens=None, L=None, allowed=None, table=False,
+             aid=None, aval=None, alen=None, cap=None, cap16=False)
     if rng.random() < 0.5:
         c["rep"] = rng.uniform(0.5, 2.0, B).astype(np.float32)
         c["pres"] = rng.uniform(-1.0, 1.0, B).astype(np.float32)
@@ -239,6 +241,19 @@ def _edge_launch(rng):
     if rng.random() < 0.3:
         allowed = rng.random((B, V)) < rng.choice([0.0, 0.01, 0.5, 1.0], B)[:, None]
         c["allowed"] = allowed
+    if c["output"] is not None and rng.random() < 0.5:
+        c["table"] = True
+    if rng.random() < 0.25:
+        Wa = 4
+        aid = np.full((B, Wa), -1, np.int32)
+        for b in range(B):
+            n = min(Wa, V)
+            aid[b, :n] = rng.choice(V, n, replace=False)
+        aval = np.where(rng.random((B, Wa)) < 0.4, -np.inf, rng.uniform(-3, 3, (B, Wa))).astype(np.float32)
+        c.update(aid=aid, aval=aval, alen=rng.integers(0, Wa + 1, B).astype(np.int32))
+    if rng.random() < 0.25:
+        c["cap"] = float(rng.choice([1.0, 30.0]))
+        c["cap16"] = bool(rng.random() < 0.5)
     return c
 
 
@@ -256,21 +271,36 @@ def test_random_edge_launch(cuda, seed):
     bits = None if c["allowed"] is None else _words(c["allowed"])
     ref = O.sample(c["x"], prm, u, prompt_ids=c["prompt"], output_ids=c["output"],
                    prompt_lens=c["plens"], output_lens=c["olens"], num_logprobs=c["L"],
-                   allowed=bits)
+                   allowed=bits, adjust_ids=c["aid"], adjust_vals=c["aval"],
+                   adjust_lens=c["alen"], softcap=c["cap"], softcap_f16=c["cap16"])
     # the logits as a strided view of a wider buffer, starting c["off"] elements in
     buf = np.full((B, V + 4), np.float32(7.0))
     buf[:, c["off"]:c["off"] + V] = c["x"]
     xt = torch.from_numpy(buf).to(cuda)[:, c["off"]:c["off"] + V]
     t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    if c["table"]:
+        # the histories as a token-state table of B + 3 rows, reached through a row map; the
+        # rows no launch row maps to hold junk
+        R = B + 3
+        rows = rng.permutation(R)[:B].astype(np.int32)
+        st = rng.integers(0, 2 ** 31, (R, V)).astype(np.uint32)
+        st[rows] = table_from_lists(B, V, c["prompt"], c["output"], c["plens"], c["olens"])
+        hist = dict(token_state=t(st.view(np.int32)), token_state_rows=t(rows))
+        if V <= 196608:
+            hist["token_state_bits"] = t(bits_from_table(st))
+    else:
+        hist = dict(prompt_ids=t(c["prompt"]), prompt_lens=t(c["plens"]),
+                    output_ids=t(c["output"]), output_lens=t(c["olens"]))
     greedy_all = bool(np.all(~(c["T"] >= np.float32(1e-5))))
     res = ops.sample(
         xt, temperature=None if greedy_all else torch.from_numpy(c["T"]),
         top_k=torch.from_numpy(c["k"]), top_p=torch.from_numpy(c["p"]),
         min_p=torch.from_numpy(c["mp"]), repetition_penalty=torch.from_numpy(c["rep"]),
         presence_penalty=torch.from_numpy(c["pres"]), frequency_penalty=torch.from_numpy(c["freq"]),
-        prompt_ids=t(c["prompt"]), prompt_lens=t(c["plens"]), output_ids=t(c["output"]),
-        output_lens=t(c["olens"]), uniforms=t(u), num_logprobs=c["L"],
-        allowed_mask=None if bits is None else t(bits.view(np.int32)))
+        uniforms=t(u), num_logprobs=c["L"],
+        allowed_mask=None if bits is None else t(bits.view(np.int32)),
+        adjust_ids=t(c["aid"]), adjust_vals=t(c["aval"]), adjust_lens=t(c["alen"]),
+        logit_softcap=c["cap"], logit_softcap_f16=c["cap16"], **hist)
     torch.cuda.synchronize()
     g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
              n_kept=res.num_kept.cpu().numpy())
@@ -278,6 +308,7 @@ def test_random_edge_launch(cuda, seed):
         g.update(lp_ids=res.logprob_ids.cpu().numpy(), lp_vals=res.logprob_vals.cpu().numpy(),
                  ranks=res.logprob_ranks.cpu().numpy())
     label = (f"edge seed {seed}: B={B} V={V} off={c['off']} L={c['L']} "
-             f"pen={c['output'] is not None} mask={bits is not None}")
+             f"pen={c['output'] is not None} table={c['table']} mask={bits is not None} "
+             f"adj={c['aid'] is not None} cap={c['cap']}/{c['cap16']}")
     print(label, flush=True)
     assert_same(g, ref, label)
