@@ -312,3 +312,73 @@ def test_random_edge_launch(cuda, seed):
              f"adj={c['aid'] is not None} cap={c['cap']}/{c['cap16']}")
     print(label, flush=True)
     assert_same(g, ref, label)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_ops(cuda, seed):
+    """The standalone operations on random edge inputs: argmax, top-k (k from 1 to min(V, 256)),
+    softmax at a random temperature (fp32, bf16 or f16 logits), and the in-place penalties --
+    tiny and odd vocabularies, NaN and infinite logits, heavy ties, strided rows."""
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(7000 + seed)
+    B = int(rng.integers(1, 30))
+    V = int(rng.choice([1, 2, 7, 64, 65, 1000, 4099, 32000, 40001]))
+    x = rng.normal(0, rng.choice([0.01, 1.0, 8.0]), (B, V)).astype(np.float32)
+    if rng.random() < 0.4:
+        x = np.round(x * 2) / 2                                       # ties
+    sp = rng.random((B, V))
+    x = np.where(sp < 0.003, np.nan, x)
+    x = np.where((sp >= 0.003) & (sp < 0.006), -np.inf, x)
+    x = np.where((sp >= 0.006) & (sp < 0.007), np.inf, x).astype(np.float32)
+    dt = ["f32", "bf16", "f16"][seed % 3]
+    if dt == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        raw = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        xf = (raw.astype(np.uint32) << 16).view(np.float32)
+        xt = torch.from_numpy(raw.view(np.int16)).to(cuda).view(torch.bfloat16)
+    elif dt == "f16":
+        raw = x.astype(np.float16)
+        xf = raw.astype(np.float32)
+        xt = torch.from_numpy(raw).to(cuda)
+    else:
+        xf = x
+        wide = np.zeros((B, V + 3), np.float32)
+        wide[:, 1:V + 1] = x
+        xt = torch.from_numpy(wide).to(cuda)[:, 1:V + 1]            # strided, unaligned rows
+    label = f"ops seed {seed}: {dt} B={B} V={V}"
+    print(label, flush=True)
+
+    assert np.array_equal(ops.argmax(xt).cpu().numpy(), O.argmax(xf)), label + " argmax"
+
+    k = int(rng.integers(1, min(V, 256) + 1))
+    vals, ids = ops.topk(xt, k)
+    rv, ri = O.topk(xf, k)
+    assert np.array_equal(ids.cpu().numpy(), ri), f"{label} topk ids (k={k})"
+    # (values equal as floats: NaN to NaN, and -0 to +0, the keys the ordering uses)
+    np.testing.assert_array_equal(vals.cpu().numpy(), rv, err_msg=f"{label} topk values")
+
+    T = np.float32(rng.choice([0.05, 0.7, 1.0, 3.0]))
+    p, rm, ls = ops.softmax(xt, torch.full((B,), float(T)))
+    p, rm, ls = p.cpu().numpy(), rm.cpu().numpy(), ls.cpu().numpy()
+    for b in range(B):
+        rp, rrm, rls = O.softmax(xf[b:b + 1], float(T))
+        np.testing.assert_allclose(p[b], rp[0], rtol=1e-5, atol=1e-12, equal_nan=True,
+                                   err_msg=f"{label} softmax row {b}")
+        assert rm[b] == rrm[0] or (np.isnan(rm[b]) and np.isnan(rrm[0])), f"{label} row max {b}"
+
+    if dt == "f32":
+        W = int(rng.integers(1, 30))
+        pr = rng.integers(-1, V + 1, (B, W)).astype(np.int32)
+        ou = rng.integers(-1, V + 1, (B, W)).astype(np.int32)
+        rep = rng.uniform(0.5, 2.0, B).astype(np.float32)
+        pres = rng.uniform(-1, 1, B).astype(np.float32)
+        freq = rng.uniform(-1, 1, B).astype(np.float32)
+        ref = O.apply_penalties(xf, pr, ou, rep, pres, freq)
+        got = torch.from_numpy(xf.copy()).to(cuda)
+        ops.apply_penalties(got, torch.from_numpy(rep), torch.from_numpy(pres),
+                            torch.from_numpy(freq), prompt_ids=torch.from_numpy(pr).to(cuda),
+                            output_ids=torch.from_numpy(ou).to(cuda))
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32)), label + " penalties"

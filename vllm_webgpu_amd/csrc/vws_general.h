@@ -1092,6 +1092,31 @@ __device__ __forceinline__ uint32_t general_topk_select(const KArgs& a, GenSmem&
     return n < (uint32_t)k ? n : (uint32_t)k;
 }
 
+// The top k of a row with fewer than k elements that are not NaN (positions [0, n) written):
+// positions [n, k) take the row's NaN elements in index order (a sort by key puts them last,
+// lowest index first); the caller has set every position to -1 / NaN before.  Called by one
+// whole wave, which scans the row 64 elements at a time and stops once it has them (such a row
+// is short or mostly NaN).
+template <typename T>
+__device__ __forceinline__ void topk_fill_nan(const T* row, int V, int n, int k, float* vals,
+                                              int32_t* ids) {
+    const int lane = threadIdx.x & 63;
+    const int need = k - n;
+    int found = 0;
+    for (int base = 0; base < V && found < need; base += kWave) {
+        const int i = base + lane;
+        const float xi = i < V ? Elem<T>::load1(row + i) : 0.0f;
+        const bool isn = i < V && !(xi == xi);
+        const uint64_t bal = wave_ballot(isn);
+        const int pos = found + lane_prefix(bal);
+        if (isn && pos < need) {
+            vals[n + pos] = __builtin_nanf("");
+            ids[n + pos] = i;
+        }
+        found += __popcll(bal);
+    }
+}
+
 // Exact top-k ids/values of a row for the topk operation, when its single-pass list
 // overflowed (ties).
 template <typename T>
@@ -1107,6 +1132,9 @@ __device__ __forceinline__ void general_topk_row(const KArgs& a, GenSmem& sm, in
         a.topk_vals[(size_t)r * k + j] = val_of(~(uint32_t)(g >> 32));
         a.topk_ids[(size_t)r * k + j] = (int32_t)(uint32_t)g;
     }
+    if ((int)n < k && threadIdx.x < kWave)
+        topk_fill_nan<T>(reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride, a.V, (int)n,
+                         k, a.topk_vals + (size_t)r * k, a.topk_ids + (size_t)r * k);
 }
 
 }  // namespace vws

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, in
 #pragma unroll
             for (int j = 0; j < VEC; ++j) { const uint64_t k = key_of(v[q][j]); mk = mk > k ? mk : k; }
         mk = op_block_max(mk, red);
-        m = val_of((uint32_t)mk);
+        m = mk ? val_of((uint32_t)mk) : -__builtin_inff();  // (a row of NaN: the empty maximum)
 #pragma unroll
         for (int q = 0; q < kSoftmaxRegs; ++q)
 #pragma unroll
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kOpThreads) void softmax_kernel(const T* logits, in
             }
         }
         mk = op_block_max(mk, red);
-        m = val_of((uint32_t)mk);
+        m = mk ? val_of((uint32_t)mk) : -__builtin_inff();  // (a row of NaN: the empty maximum)
         const bool mfin = __builtin_fabsf(m) < __builtin_inff();
         S = op_block_sum_f64(mfin && mt > -__builtin_inff() ? st * (double)exp_det(mt - m) : 0.0, redd);
         const double inv = 1.0 / S;

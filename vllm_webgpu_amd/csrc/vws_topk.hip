@@ -289,7 +289,9 @@ __device__ __forceinline__ void fast_hand_to_general(const KArgs& a, int r) {
     if (threadIdx.x == 0) a.row_state[r] = kRowNeedsGeneral;
 }
 
-__device__ __forceinline__ void fast_topk_merge(const KArgs& a, FastSmem& sm, int r, int k) {
+// Returns the positions of the row's top k written from the lists (k, or every candidate when
+// the row has fewer than k that are not NaN), or -1 when the row was handed over.
+__device__ __forceinline__ int fast_topk_merge(const KArgs& a, FastSmem& sm, int r, int k) {
     constexpr int NT = kFastThreads;
     constexpr int NSPEC = (kMaxParts * kSpec) / NT;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -321,7 +323,7 @@ __device__ __forceinline__ void fast_topk_merge(const KArgs& a, FastSmem& sm, in
         if (off > (uint32_t)kMergeCap) sm.status |= 8u;
     }
     __syncthreads();
-    if (sm.status) { fast_hand_to_general(a, r); return; }
+    if (sm.status) { fast_hand_to_general(a, r); return -1; }
     const int N = (int)sm.poff[S];
 #pragma unroll
     for (int s = 0; s < NSPEC; ++s) {
@@ -371,6 +373,16 @@ __device__ __forceinline__ void fast_topk_merge(const KArgs& a, FastSmem& sm, in
             a.topk_ids[(size_t)r * k + rank] = ij;
         }
     }
+    if (kth != 0u) return k;
+    // fewer than k candidates that are not NaN: every one of them was written
+    if (wave == 0) {
+        uint64_t c = 0;
+        for (int j = lane; j < N; j += kWave) c += mk[j] != 0u ? 1u : 0u;
+        c = wave_sum_u64(c);
+        if (lane == 0) sm.bcast[1] = (uint32_t)c;
+    }
+    __syncthreads();
+    return (int)sm.bcast[1];
 }
 
 template <typename T>
@@ -392,7 +404,10 @@ __global__ __launch_bounds__(kFastThreads) void fast_kernel(KArgs a) {
     __syncthreads();
     if (!sm.last) return;
     if (threadIdx.x == 0) ag_store32(&a.row_counter[r], 0u);
-    fast_topk_merge(a, sm, r, k);
+    const int nv = fast_topk_merge(a, sm, r, k);
+    if (nv >= 0 && nv < k && threadIdx.x < kWave)
+        topk_fill_nan<T>(reinterpret_cast<const T*>(a.logits) + (size_t)r * a.lstride, a.V, nv, k,
+                         a.topk_vals + (size_t)r * k, a.topk_ids + (size_t)r * k);
 }
 
 // The rows fast_kernel handed over (row_state), selected exactly by the multi-pass path's radix
