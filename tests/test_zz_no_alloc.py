@@ -104,3 +104,57 @@ def test_noalloc_rejects_batches_beyond_the_scratch(cuda):
     assert L.vws_sample_workspace_size(4096, 1000, 2048) > _lib.NOALLOC_SCRATCH_BYTES
     assert L.vws_sample_noalloc(ctypes.byref(a)) == _lib.ERR_LIMIT
     assert "static scratch" in _lib.last_error()
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_noalloc_matches_the_workspace_entry_on_random_launches(cuda, seed):
+    """Random mixed launches (every sampling option; see tests/test_gpu_random_mix.py) prepared
+    once, run through vws_sample and then through vws_sample_noalloc with the same arguments:
+    tokens, flags, survivor counts, logprob ids and ranks identical, logprob values within
+    1e-6 (the device's double sums may finish in another order)."""
+    import torch
+
+    from tests.cases import _u
+    from tests.test_gpu_random_mix import _launch, _words
+    from vllm_webgpu_amd import _lib, ops
+
+    L = _lib.lib()
+    rng = np.random.default_rng(31000 + seed)
+    c = _launch(rng, ["f32", "bf16", "f16"][seed % 3], big=seed % 5 == 4)
+    B, V = c["B"], c["V"]
+    u = _u(rng, (B, V))
+    bits = None if c["allowed"] is None else _words(c["allowed"])
+    if c["dt"] == "bf16":
+        x = torch.from_numpy(c["raw"].view(np.int16)).to(cuda).view(torch.bfloat16)
+    else:
+        x = torch.from_numpy(c["raw"]).to(cuda)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    greedy_all = bool(np.all(~(c["T"] >= np.float32(1e-5))))
+    prep = ops.prepare_sample(
+        x, temperature=None if greedy_all else torch.from_numpy(c["T"]),
+        top_k=torch.from_numpy(c["k"]), top_p=torch.from_numpy(c["p"]),
+        min_p=torch.from_numpy(c["mp"]), repetition_penalty=torch.from_numpy(c["rep"]),
+        presence_penalty=torch.from_numpy(c["pres"]), frequency_penalty=torch.from_numpy(c["freq"]),
+        prompt_ids=t(c["prompt"]), output_ids=t(c["output"]), uniforms=t(u),
+        num_logprobs=c["L"], allowed_mask=None if bits is None else t(bits.view(np.int32)),
+        adjust_ids=t(c["aid"]), adjust_vals=t(c["aval"]), adjust_lens=t(c["alen"]),
+        logit_softcap=c["cap"], logit_softcap_f16=c["cap16"])
+    if L.vws_sample_workspace_size(B, V, prep.args.prompt_width + prep.args.output_width) > _lib.NOALLOC_SCRATCH_BYTES:
+        pytest.skip("beyond the static scratch")
+    res = prep.launch()
+    outs = [res.sampled, res.flags, res.num_kept]
+    if c["L"] is not None:
+        outs += [res.logprob_ids, res.logprob_ranks, res.logprob_vals]
+    torch.cuda.synchronize()
+    ref = [o.cpu().numpy().copy() for o in outs]
+    for o in outs:
+        o.fill_(-7)
+    prep.args.stream = ops._stream_ptr()
+    _lib.check(L.vws_sample_noalloc(ctypes.byref(prep.args)))
+    torch.cuda.synchronize()
+    got = [o.cpu().numpy() for o in outs]
+    label = f"seed {seed}: {c['dt']} B={B} V={V} L={c['L']}"
+    for g, r in zip(got[:-1] if c["L"] is not None else got, ref):
+        assert np.array_equal(g, r), label
+    if c["L"] is not None:
+        np.testing.assert_allclose(got[-1], ref[-1], rtol=1e-6, atol=0, equal_nan=True, err_msg=label)
