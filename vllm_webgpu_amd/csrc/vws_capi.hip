@@ -378,8 +378,6 @@ int vws_sample(const vws_sample_args* a) {
     k.lp_ids = a->logprob_ids;
     k.lp_vals = a->logprob_vals;
     k.lp_ranks = a->logprob_ranks;
-    // every row would leave the single-pass kernel at once: rows go straight to the top-p
-    // stream or the general path, without the single pass's first loads
     // more rows than workgroups resident at once: the kernel counts its workgroups, so that one
     // whose row is done waits for other rows' passes only once no workgroup is left to start
     const int grid = a->batch;
@@ -389,6 +387,8 @@ int vws_sample(const vws_sample_args* a) {
         else if (a->batch > d.cus * d.row_blocks_per_cu) k.coop_count = 1;
     }
     k.coop_wait_polls = g_coop_wait_polls.load(std::memory_order_relaxed);
+    // the single pass switched off (vws_set_single_pass(0)): rows go straight to the top-p
+    // stream or the general path, without the single pass's first loads
     k.nofast = g_single_pass.load(std::memory_order_relaxed) ? 0 : 1;
 #ifdef VWS_TRACE
     {

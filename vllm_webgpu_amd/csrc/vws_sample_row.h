@@ -1439,6 +1439,7 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
         const int t = tid_now();
 #pragma unroll
         for (int q = 0; q < U; ++q) {
+            // (a continue leaves the do-while: the vector has nothing at or above the threshold)
             if (run) do {
                 const int vi = (it * U + q) * NT + t;
                 const bool ok = vi < nbody;
