@@ -257,7 +257,9 @@ def _edge_launch(rng):
     return c
 
 
-@pytest.mark.parametrize("seed", range(60))
+# 10285 and 10663: short history rows with 20 raw logprobs whose stream keeps every element,
+# with a NaN history token (the top-p path listed it among the raw top L)
+@pytest.mark.parametrize("seed", list(range(60)) + [10285, 10663])
 def test_random_edge_launch(cuda, seed):
     import torch
 

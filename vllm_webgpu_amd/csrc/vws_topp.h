@@ -1114,7 +1114,10 @@ __device__ __forceinline__ int topp_hist_prepare(const KArgs& a, TopPSmem& sm, i
         if (L >= 0) {
             s0h += exp_det(x - xmaxr);
             const uint32_t kx = key_of(x);
-            if (kx >= tauk) {
+            // NaN (key 0) sorts after every value: never listed, also when a short row keeps
+            // every element (threshold key 0); a row with fewer than L other candidates falls
+            // back to the multi-pass path, which lists its NaN elements last
+            if (kx >= tauk && kx != 0u) {
                 const uint32_t pos = atomicAdd(&sm.rl_n, 1u);
                 if (pos < (uint32_t)kTpRawCap) {
                     sm.rl_key[pos] = kx;
