@@ -384,3 +384,41 @@ def test_random_ops(cuda, seed):
                             torch.from_numpy(freq), prompt_ids=torch.from_numpy(pr).to(cuda),
                             output_ids=torch.from_numpy(ou).to(cuda))
         assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32)), label + " penalties"
+
+
+@pytest.mark.parametrize("V,k", [(7, 6), (65, 64), (1000, 256)])
+def test_banned_nan_logits(cuda, V, k):
+    """A ban turns a NaN logit into -inf, which counts as a survivor when the top k reaches
+    -inf (rows with fewer than k values that are not NaN), as the oracle's assignment does."""
+    import torch
+
+    from vllm_webgpu_amd import ops
+
+    rng = np.random.default_rng(V)
+    B = 4
+    x = rng.normal(0, 1, (B, V)).astype(np.float32)
+    x[rng.random((B, V)) < 0.6] = np.nan
+    aid = np.full((B, 3), -1, np.int32)
+    aval = np.full((B, 3), -np.inf, np.float32)
+    for b in range(B):
+        nan_ids = np.flatnonzero(np.isnan(x[b]))
+        aid[b, 0] = nan_ids[0]                          # a banned NaN
+        aid[b, 1] = np.flatnonzero(~np.isnan(x[b]))[0]  # a banned value
+        aid[b, 2] = nan_ids[-1]
+        aval[b, 2] = 1.5                                 # a biased NaN stays NaN
+    alen = np.array([3, 2, 1, 3], np.int32)
+    T = np.array([1.0, 0.5, 0.0, 2.0], np.float32)
+    kk = np.full(B, k, np.int32)
+    p = np.ones(B, np.float32)
+    zero, one = np.zeros(B, np.float32), np.ones(B, np.float32)
+    u = _u(rng, (B, V))
+    prm = O.make_params(B, T, kk, p, zero, one, zero, zero)
+    ref = O.sample(x, prm, u, adjust_ids=aid, adjust_vals=aval, adjust_lens=alen)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    res = ops.sample(t(x), temperature=torch.from_numpy(T), top_k=torch.from_numpy(kk),
+                     top_p=torch.from_numpy(p), uniforms=t(u), adjust_ids=t(aid),
+                     adjust_vals=t(aval), adjust_lens=t(alen))
+    torch.cuda.synchronize()
+    g = dict(token=res.sampled.cpu().numpy(), flags=res.flags.cpu().numpy().view(np.uint32),
+             n_kept=res.num_kept.cpu().numpy())
+    assert_same(g, ref, f"banned NaN logits V={V} k={k}")

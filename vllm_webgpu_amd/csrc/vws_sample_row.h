@@ -1272,6 +1272,10 @@ __device__ __forceinline__ bool row_fast(const KArgs& a, RowSmem& sm, int r, con
             if (t < 0 || t >= V) return;
             if (bv == -__builtin_inff()) {
                 rhash_insert(sm, t, kHBan);
+                // a ban turns a NaN logit into -inf, an element that the candidates (chosen by
+                // raw value) never hold: such a row leaves for the multi-pass path (bit 1, as a
+                // hash overflow), which bans every listed element whatever its value
+                if (key_of(Elem<T>::load1(row + t)) == 0u) atomicOr(&sm.status, 1u);
             } else {
                 rhash_insert(sm, t, kHBias, bv);
                 if (bv > 0.0f) sm.adjraise = 1u;
